@@ -1,0 +1,250 @@
+/*
+ * iam.h - C ABI of the MI355X (gfx950) input-adaptive sparse decode library.
+ *
+ * This is the boundary that replaces the reference's OpenCL runtime
+ * (gpu.hpp) and the OpenCL bodies of its operator wrappers.  Every entry
+ * point is extern "C", takes plain pointers and sizes, and returns an int
+ * status: 0 on success, a negative IAM_E* code on failure, with a message in
+ * iam_last_error() (thread-local).  The C++ headers under
+ * input-adaptive-matrix-inference-optimization_amd/cpp/ keep the reference's
+ * class and method surface on top of these calls and turn non-zero statuses
+ * into std::runtime_error, as the reference does.
+ *
+ * Execution model: one HIP stream per context, in order.  Every call is
+ * asynchronous except iam_write / iam_read (blocking, like the reference's
+ * writeBuffer/readBuffer) and iam_sync (the reference's eval()).  A context
+ * is not thread-safe.  Device pointers come from iam_alloc; "_dev" arguments
+ * point to device memory.
+ *
+ * Citations are to files of the reference repository.
+ */
+#ifndef IAM_H
+#define IAM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define IAM_OK 0
+#define IAM_E_INVALID (-1)    /* bad argument or shape */
+#define IAM_E_HIP (-2)        /* HIP runtime error */
+#define IAM_E_NOMEM (-3)      /* allocation failed or over the byte budget */
+#define IAM_E_STATE (-4)      /* call out of order (e.g. mul before calc_dispatch) */
+#define IAM_E_IO (-5)         /* file missing, truncated or malformed */
+
+#define IAM_PROBES_COUNT 4096 /* bucketMul.cl:18, bucket_mul.hpp:101 */
+
+typedef struct iam_ctx iam_ctx;
+
+/* ------------------------------------------------------------------ runtime */
+
+/* Gpu::Gpu() (gpu.hpp:109-159): one device, one in-order queue. */
+int iam_ctx_create(int device, iam_ctx** out);
+/* Gpu::~Gpu() (gpu.hpp:161-188); frees everything allocated through the context. */
+int iam_ctx_destroy(iam_ctx* ctx);
+/* Gpu::eval() (gpu.hpp:399-447): wait for the queue, fold kernel timings. */
+int iam_sync(iam_ctx* ctx);
+/* Gpu::checkError message (gpu.hpp:581-587), thread-local. */
+const char* iam_last_error(void);
+/* device name / CU count / global memory (gpu.hpp:123-135, :28-31) */
+int iam_device_info(iam_ctx* ctx, char* name, size_t name_len, int* compute_units,
+                    size_t* global_mem_bytes);
+/* MemoryTracker (gpu.hpp:21-60): byte budget = device memory - margin. */
+int iam_mem_status(iam_ctx* ctx, size_t* allocated, size_t* usable);
+
+/* Gpu::createBuffer (gpu.hpp:236-262) */
+int iam_alloc(iam_ctx* ctx, size_t bytes, void** out_dev);
+/* Gpu::releaseBuffer (gpu.hpp:264-269) */
+int iam_free(iam_ctx* ctx, void* dev);
+/* BufferWrapper::zero (bucket_mul.hpp:34-38): a fill kernel, safe under graph capture. */
+int iam_zero(iam_ctx* ctx, void* dev, size_t offset_bytes, size_t bytes);
+/* Gpu::writeBuffer (gpu.hpp:464-469), blocking. */
+int iam_write(iam_ctx* ctx, void* dst_dev, size_t dst_offset, const void* src_host, size_t bytes);
+/* Gpu::readBuffer (gpu.hpp:457-462), blocking (waits for prior work). */
+int iam_read(iam_ctx* ctx, void* dst_host, const void* src_dev, size_t src_offset, size_t bytes);
+/* Gpu::copyBuffer (gpu.hpp:449-455), asynchronous device-to-device. */
+int iam_copy(iam_ctx* ctx, void* dst_dev, size_t dst_offset, const void* src_dev,
+             size_t src_offset, size_t bytes);
+
+/* Per-kernel profiling (gpu.hpp:104-106, :275-290, :411-432): when enabled each
+ * launch is bracketed by HIP events and iam_sync folds the durations. */
+int iam_profiling(iam_ctx* ctx, int enable);
+/* Gpu::printKernelStats (gpu.hpp:190-234) into a text buffer. */
+int iam_kernel_stats(iam_ctx* ctx, char* buf, size_t len);
+int iam_kernel_stats_reset(iam_ctx* ctx);
+/* total time (ms) and launch count of one kernel name since the last reset */
+int iam_kernel_stat(iam_ctx* ctx, const char* name, double* total_ms, int* calls);
+
+/* --------------------------------------------------------------- bucketMul */
+
+/* One weight matrix in the reference's bucket layout
+ * (preprocess_layer_fixed_gpu.py:110-242, binary_loader.hpp:30-37):
+ *   buckets  fp16 [n_experts * expert_rows][bucket_cols], packed value|position
+ *   stats    fp16, stats_stride values per row; selection reads
+ *            stats[row * stats_stride + stats_channel]
+ *            (reference files: stride 4, channel 3, bucketMul.cl:372)
+ *   probes   fp16, at least (expert_no + 1) * 4096 values (bucketMul.cl:103-109)
+ *   expert_rows = 16 * in_dim, bucket_cols = out_dim / 16. */
+typedef struct {
+    const uint16_t* buckets;
+    const uint16_t* stats;
+    const uint16_t* probes;
+    int expert_rows;
+    int bucket_cols;
+    int stats_stride;
+    int stats_channel;
+} iam_bucket_matrix;
+
+/* BucketMul::calcDispatch (bucket_mul.hpp:147-191): cutoff search
+ * (findCutoffBinarySearch, bucketMul.cl:68-214) and row selection
+ * (prepareDispatch, bucketMul.cl:351-386) for x against stats/probes in the
+ * reference's 4-channel stats layout.  The dispatch is kept in the context,
+ * like the BucketMul singleton's scratch (bucket_mul.hpp:125-144).
+ * expert_size is the row count R of one expert; rows with r/16 >= in_size
+ * are skipped, as in the reference.  x must hold at least max(4096, in_size)
+ * floats, because the cutoff always reads x[0:4096] (bucketMul.cl:102-110). */
+int iam_bucketmul_calc_dispatch(iam_ctx* ctx, const float* x_dev, const uint16_t* stats_dev,
+                                const uint16_t* probes_dev, int expert_no, int in_size,
+                                int bucket_cols, int expert_size, float effort);
+/* BucketMul::mul (bucket_mul.hpp:193-252): walk the rows selected by the last
+ * calc_dispatch and write y[16 * bucket_cols] (overwritten). */
+int iam_bucketmul_mul(iam_ctx* ctx, const uint16_t* buckets_dev, int bucket_cols, float* y_dev);
+/* BucketMul::fullMul (bucket_mul.hpp:254-267) */
+int iam_bucketmul_full(iam_ctx* ctx, const float* x_dev, const uint16_t* stats_dev,
+                       const uint16_t* probes_dev, const uint16_t* buckets_dev, int expert_no,
+                       int in_size, int bucket_cols, int expert_size, float effort, float* y_dev);
+/* Up to 3 independent matrices in one cutoff launch and one walk launch
+ * (the q/k/v and gate/up calls of attention.hpp:160-170 and
+ * feedforward.hpp:60-68 share an input).  xs[i] may repeat. */
+int iam_bucketmul_multi(iam_ctx* ctx, int n, const iam_bucket_matrix* mats,
+                        const float* const* xs_dev, const int* in_sizes, float* const* ys_dev,
+                        int expert_no, float effort);
+/* Parity outputs of the last calc_dispatch / multi call for matrix slot
+ * `slot`: the cutoff (fp32, as written by findCutoffBinarySearch) and the
+ * selected-row count S.  Blocking. */
+int iam_bucketmul_dispatch_info(iam_ctx* ctx, int slot, float* cutoff, uint32_t* count);
+/* The selected rows (expert-local row ids, ascending) of slot `slot`; writes
+ * min(S, cap) ids into rows_host.  Blocking. */
+int iam_bucketmul_dispatch_rows(iam_ctx* ctx, int slot, uint32_t* rows_host, size_t cap,
+                                uint32_t* count);
+/* effort -> quantile exactly as bucket_mul.hpp:164 */
+int iam_effort_quantile(float effort);
+/* Derive a compact copy stats3[r] = stats[r*4 + 3] (device), so the
+ * selection reads 2 bytes per row instead of 8.  The file layout is unchanged. */
+int iam_stats_compact(iam_ctx* ctx, const uint16_t* stats_dev, size_t rows, int stride,
+                      int channel, uint16_t* out_dev);
+
+/* ------------------------------------------------------------ layer ops */
+
+/* rmsNorm32fast (aux.cl:156-196) then the fp16 gain mul16x32 (aux.cl:434-440) /
+ * mulVec32by16 (aux.cl:301-306).  n must be a multiple of 256. */
+int iam_rmsnorm_gain(iam_ctx* ctx, const float* in_dev, const uint16_t* gain_dev, int n,
+                     float eps, float* out_dev);
+/* add32 (bucketMul.cl:517-520) into h, then rmsnorm_gain of the sum
+ * (transformer_layer.hpp:108-112 fused).  h_dev is updated in place. */
+int iam_add_rmsnorm_gain(iam_ctx* ctx, float* h_dev, const float* delta_dev,
+                         const uint16_t* gain_dev, int n, float eps, float* out_dev);
+/* add32 (bucketMul.cl:517-520): out = a + b */
+int iam_add(iam_ctx* ctx, const float* a_dev, const float* b_dev, int n, float* out_dev);
+/* silu32 (matrix.cl:27-32): out = up * gate / (1 + exp(-gate)) */
+int iam_silu_mul(iam_ctx* ctx, const float* gate_dev, const float* up_dev, int n,
+                 float* out_dev);
+/* precompute_rope_cache (attention.hpp:207-235): host table
+ * [max_pos][head_dim/2][2] of (cos, sin) in float. */
+int iam_rope_table(double theta, int head_dim, int max_pos, float* table_host);
+/* rope_mx (aux.cl:227-248) on n_heads heads; table row = *pos_dev. */
+int iam_rope(iam_ctx* ctx, const float* in_dev, const float* table_dev, const int* pos_dev,
+             int n_heads, int head_dim, float* out_dev);
+/* RoPE of q (n_heads) and k (n_kv heads), then the KV append
+ * (attention.hpp:172-189 and :281-309) into fp16 caches laid out
+ * [max_ctx][n_kv][head_dim] at position *pos_dev. */
+int iam_rope_kv_append(iam_ctx* ctx, const float* q_dev, const float* k_dev, const float* v_dev,
+                       const float* table_dev, const int* pos_dev, int n_heads, int n_kv,
+                       int head_dim, float* q_out_dev, uint16_t* kcache_dev,
+                       uint16_t* vcache_dev);
+/* Decode attention over positions 0..*pos_dev of an fp16 GQA cache
+ * (dotSetScore2 aux.cl:497-540, sum_of_exps32_mx :204-210, softmax_add32_mx
+ * :219-225, sumScores32 :370-384; driver attention.hpp:311-404), split over
+ * the context.  Query head h reads KV head h*n_kv/n_heads (repeat4x32). */
+int iam_attention_decode(iam_ctx* ctx, const float* q_dev, const uint16_t* kcache_dev,
+                         const uint16_t* vcache_dev, const int* pos_dev, int n_heads, int n_kv,
+                         int head_dim, int max_ctx, float* out_dev);
+/* fetchRow16to32 (aux.cl:442-452): out = (float) table[*token_dev][:] */
+int iam_embed_gather(iam_ctx* ctx, const uint16_t* table_dev, int cols, const int* token_dev,
+                     float* out_dev);
+/* greedy pick (test_generation.cpp:235, :276): first index of the maximum */
+int iam_argmax(iam_ctx* ctx, const float* v_dev, int n, int* out_dev);
+
+/* -------------------------------------------------------- synthetic data */
+
+/* Counter-based generator shared with the CPU oracle: element n of tensor
+ * `tensor_id` = mean + sigma * (sum of 12 uniform uint32 - 6*2^32) / 2^32,
+ * rounded to float (and then to fp16 for the f16 variant). */
+int iam_gen_f16(iam_ctx* ctx, uint64_t seed, uint64_t tensor_id, size_t count, double mean,
+                double sigma, uint16_t* out_dev);
+int iam_gen_f32(iam_ctx* ctx, uint64_t seed, uint64_t tensor_id, size_t count, double mean,
+                double sigma, float* out_dev);
+/* GPU bucketizer, byte-identical to bucketize_fp16_packed
+ * (preprocess_layer_fixed_gpu.py:110-242): W fp16 [out_dim][in_dim] ->
+ * buckets [16*in][out/16], stats [16*in][4], probes [in]. */
+int iam_bucketize(iam_ctx* ctx, const uint16_t* w_dev, int out_dim, int in_dim,
+                  uint16_t* buckets_dev, uint16_t* stats_dev, uint16_t* probes_dev);
+
+/* ----------------------------------------------------------------- model */
+
+/* Mistral-shaped decoder (model.hpp:15-30, attention.hpp:21-27): dims,
+ * heads, vocabulary, KV capacity and RoPE theta are parameters. */
+typedef struct {
+    int n_layers;
+    int dim;
+    int ffn_dim;
+    int n_heads;
+    int n_kv_heads;
+    int head_dim;
+    int vocab;
+    int max_ctx;
+    double rope_theta;
+    float norm_eps;
+} iam_model_config;
+
+typedef struct iam_model iam_model;
+
+/* MistralModel::MistralModel (model.hpp:84-127): allocates weights (bucket
+ * layout, LM head included), fp16 KV caches [n_layers][max_ctx][n_kv][hd],
+ * activations and the RoPE table. */
+int iam_model_create(iam_ctx* ctx, const iam_model_config* cfg, iam_model** out);
+int iam_model_destroy(iam_model* m);
+/* Fill every weight from the synthetic generator: matrices N(0, 0.02^2)
+ * bucketized on the GPU, gains 1 + N(0, 0.01^2), embedding N(0, 0.02^2). */
+int iam_model_synthesize(iam_model* m, uint64_t seed);
+/* MistralModel::forward (model.hpp:152-231): one token at position pos;
+ * logits (vocab floats, device) are written; the KV cache at pos is filled. */
+int iam_model_forward(iam_model* m, int token, int pos, float effort, float* logits_dev);
+/* Like forward, but the token and position are read from device memory
+ * (token_dev, pos_dev) and the next token (first argmax) is written back to
+ * token_dev and pos is advanced, so a captured step replays without host
+ * involvement.  hidden_override_dev, if non-NULL, replaces the embedding. */
+int iam_model_step_device(iam_model* m, float effort, const float* hidden_override_dev);
+/* Greedy decode (test_generation.cpp:197-276): feeds the prompt token by
+ * token, then generates n_new tokens with first-max argmax.  With use_graph
+ * the per-token step is captured once as a HIP graph and replayed.
+ * out_tokens receives n_new ids. */
+int iam_model_generate(iam_model* m, const int* prompt, int n_prompt, int n_new, float effort,
+                       int use_graph, int* out_tokens);
+/* MistralModel::reset_caches (model.hpp:233-237) */
+int iam_model_reset_caches(iam_model* m);
+/* Device pointer and size of a named model tensor, e.g. "layer3.w1.buckets",
+ * "layer0.attn_gain", "embed", "final_gain", "lm_head.stats", "kcache",
+ * "vcache", "rope", "logits", "token", "pos", "hidden". */
+int iam_model_tensor(iam_model* m, const char* name, void** dev, size_t* bytes);
+/* The bucket-matrix descriptor of "layer{L}.{wq,wk,wv,wo,w1,w3,w2}" or "lm_head". */
+int iam_model_matrix(iam_model* m, const char* name, iam_bucket_matrix* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,136 @@
+// Internal declarations shared by the HIP translation units of libiam.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <map>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/iam.h"
+
+namespace iam {
+
+// ---------------------------------------------------------------- errors ---
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+
+#define IAM_CHECK_HIP(call)                                                         \
+    do {                                                                            \
+        hipError_t e_ = (call);                                                     \
+        if (e_ != hipSuccess)                                                       \
+            return ::iam::fail(IAM_E_HIP, std::string(#call) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+#define IAM_REQUIRE(cond, msg)                                                      \
+    do {                                                                            \
+        if (!(cond)) return ::iam::fail(IAM_E_INVALID, (msg));                      \
+    } while (0)
+
+#define IAM_TRY(expr)                                                               \
+    do {                                                                            \
+        int rc_ = (expr);                                                           \
+        if (rc_ != IAM_OK) return rc_;                                              \
+    } while (0)
+
+// ------------------------------------------------------------- constants ---
+constexpr int kProbes = IAM_PROBES_COUNT;   // bucketMul.cl:18
+constexpr int kChunkInputs = 256;           // inputs per selection chunk (one per thread)
+constexpr int kChunkRows = kChunkInputs * 16;
+constexpr int kMaxChunks = 256;             // in_dim up to 65536 per expert
+constexpr int kMaxMulti = 3;                // matrices per fused launch
+
+// ------------------------------------------------------- dispatch state ---
+// Selected rows of one matrix: per chunk of 4096 rows, the selected rows in
+// ascending order as {row id, bits of x[row/16]}, plus the chunk counts.
+struct DispatchSlot {
+    uint2* list = nullptr;       // [G][kChunkRows]
+    uint32_t* counts = nullptr;  // [kMaxChunks]
+    float* cutoff = nullptr;     // [1]
+    size_t cap_chunks = 0;
+    int G = 0;                   // chunks in the last dispatch
+    int rows = 0;                // expert rows R
+    int bucket_cols = 0;
+    int expert_no = 0;
+    float effort = 1.0f;
+    bool valid = false;
+};
+
+struct KernelStat {
+    int calls = 0;
+    double total_ms = 0.0;
+    double max_ms = 0.0;
+};
+
+struct PendingEvent {
+    const char* name;
+    hipEvent_t start, stop;
+};
+
+struct Ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    size_t total_mem = 0;
+    size_t usable = 0;
+    size_t allocated = 0;
+    std::map<uintptr_t, size_t> allocs;   // base -> bytes
+    bool profiling = false;
+    bool capturing = false;
+    std::vector<PendingEvent> pending;
+    std::vector<hipEvent_t> event_pool;
+    std::map<std::string, KernelStat> stats;
+    DispatchSlot slots[kMaxMulti];
+    float* zero_scratch = nullptr;
+};
+
+int ctx_alloc(Ctx* c, size_t bytes, void** out);
+// IAM_OK if [p, p+bytes) lies inside one allocation of this context
+int check_dev_range(Ctx* c, const void* p, size_t bytes, const char* what);
+int ctx_free(Ctx* c, void* p);
+int ensure_slot(Ctx* c, int slot, int chunks);
+
+// Launch bookkeeping: with profiling on (and no graph capture in progress)
+// each launch is bracketed by a pair of pooled events.
+int begin_launch(Ctx* c, const char* name, PendingEvent* ev);
+int end_launch(Ctx* c, PendingEvent* ev, bool have_ev);
+
+template <typename Kernel, typename... Args>
+int launch(Ctx* c, const char* name, Kernel k, dim3 grid, dim3 block, size_t shmem,
+           Args... args)
+{
+    if (grid.x == 0 || grid.y == 0 || grid.z == 0) return IAM_OK;
+    PendingEvent ev{};
+    bool have = false;
+    if (c->profiling && !c->capturing) {
+        IAM_TRY(begin_launch(c, name, &ev));
+        have = true;
+    }
+    hipLaunchKernelGGL(k, grid, block, shmem, c->stream, args...);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return fail(IAM_E_HIP, std::string("launch ") + name + ": " + hipGetErrorString(e));
+    return end_launch(c, &ev, have);
+}
+
+int zero_async(Ctx* c, void* p, size_t bytes);
+
+// ------------------------------------------------------------- bucketMul ---
+struct MatOp {
+    iam_bucket_matrix mat;
+    const float* x;
+    int in_size;
+    float* y;        // may be null for dispatch-only
+};
+// cutoff + selection (+ zero y when zero_y) for n matrices into slots 0..n-1
+int bucketmul_dispatch(Ctx* c, int n, const MatOp* ops, int expert_no, float effort, bool zero_y);
+// walk for slots 0..n-1 (y must be zero, or zeroed by the dispatch)
+int bucketmul_walk(Ctx* c, int n, const MatOp* ops);
+
+int quantile_of(float effort);
+int est_slices(int rows, float effort);
+
+}  // namespace iam
+
+struct iam_ctx : iam::Ctx {};

@@ -1,0 +1,339 @@
+// Context, memory, errors and per-kernel profiling: the HIP replacement of
+// the reference's OpenCL runtime class (gpu.hpp:21-588).
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <sstream>
+#include <iomanip>
+
+#include "internal.h"
+
+namespace iam {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int fail(int code, const std::string& msg)
+{
+    set_error(msg);
+    return code;
+}
+
+int ctx_alloc(Ctx* c, size_t bytes, void** out)
+{
+    if (!out) return fail(IAM_E_INVALID, "alloc: null output pointer");
+    *out = nullptr;
+    if (bytes == 0) bytes = 1;
+    // MemoryTracker::can_allocate (gpu.hpp:40-44)
+    if (c->allocated + bytes > c->usable)
+        return fail(IAM_E_NOMEM, "VRAM allocation failed - insufficient memory! (budget " +
+                                     std::to_string(c->usable) + " bytes, in use " +
+                                     std::to_string(c->allocated) + ", asked " +
+                                     std::to_string(bytes) + ")");
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(IAM_E_NOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
+    }
+    c->allocs[(uintptr_t)p] = bytes;
+    c->allocated += bytes;
+    *out = p;
+    return IAM_OK;
+}
+
+int ctx_free(Ctx* c, void* p)
+{
+    if (!p) return IAM_OK;
+    auto it = c->allocs.find((uintptr_t)p);
+    if (it == c->allocs.end()) return fail(IAM_E_INVALID, "free: pointer not allocated by this context");
+    IAM_CHECK_HIP(hipFree(p));
+    c->allocated -= it->second;
+    c->allocs.erase(it);
+    return IAM_OK;
+}
+
+int check_dev_range(Ctx* c, const void* p, size_t bytes, const char* what)
+{
+    // interior pointers of tracked allocations are accepted
+    uintptr_t a = (uintptr_t)p;
+    auto it = c->allocs.upper_bound(a);
+    if (it != c->allocs.begin()) {
+        --it;
+        if (a >= it->first && a + bytes <= it->first + it->second) return IAM_OK;
+    }
+    return fail(IAM_E_INVALID, std::string(what) + ": range not inside an allocation of this context");
+}
+
+int ensure_slot(Ctx* c, int slot, int chunks)
+{
+    DispatchSlot& s = c->slots[slot];
+    if (!s.counts) {
+        IAM_TRY(ctx_alloc(c, sizeof(uint32_t) * kMaxChunks, (void**)&s.counts));
+        IAM_TRY(ctx_alloc(c, sizeof(float) * 4, (void**)&s.cutoff));
+    }
+    if ((size_t)chunks > s.cap_chunks) {
+        if (c->capturing) return fail(IAM_E_STATE, "dispatch buffer growth during graph capture");
+        if (s.list) IAM_TRY(ctx_free(c, s.list));
+        s.list = nullptr;
+        IAM_TRY(ctx_alloc(c, sizeof(uint2) * (size_t)chunks * kChunkRows, (void**)&s.list));
+        s.cap_chunks = (size_t)chunks;
+    }
+    return IAM_OK;
+}
+
+int begin_launch(Ctx* c, const char* name, PendingEvent* ev)
+{
+    for (int i = 0; i < 2; i++) {
+        hipEvent_t e;
+        if (!c->event_pool.empty()) {
+            e = c->event_pool.back();
+            c->event_pool.pop_back();
+        } else {
+            IAM_CHECK_HIP(hipEventCreate(&e));
+        }
+        (i == 0 ? ev->start : ev->stop) = e;
+    }
+    ev->name = name;
+    IAM_CHECK_HIP(hipEventRecord(ev->start, c->stream));
+    return IAM_OK;
+}
+
+int end_launch(Ctx* c, PendingEvent* ev, bool have_ev)
+{
+    if (!have_ev) return IAM_OK;
+    IAM_CHECK_HIP(hipEventRecord(ev->stop, c->stream));
+    c->pending.push_back(*ev);
+    return IAM_OK;
+}
+
+// fill kernel used instead of hipMemsetAsync so that zeroing is safe inside
+// captured graphs
+__global__ void k_zero(uint32_t* p, size_t n_words)
+{
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (; i < n_words; i += stride) p[i] = 0u;
+}
+
+__global__ void k_zero_bytes(uint8_t* p, size_t n)
+{
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+int zero_async(Ctx* c, void* p, size_t bytes)
+{
+    if (bytes == 0) return IAM_OK;
+    uintptr_t a = (uintptr_t)p;
+    if ((a & 3) == 0 && (bytes & 3) == 0) {
+        size_t words = bytes / 4;
+        size_t blocks = std::min<size_t>((words + 255) / 256, 4096);
+        return launch(c, "zero32", k_zero, dim3((unsigned)blocks), dim3(256), 0, (uint32_t*)p, words);
+    }
+    return launch(c, "zero8", k_zero_bytes, dim3((unsigned)((bytes + 255) / 256)), dim3(256), 0,
+                  (uint8_t*)p, bytes);
+}
+
+static int fold_events(Ctx* c)
+{
+    for (auto& ev : c->pending) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, ev.start, ev.stop) == hipSuccess) {
+            KernelStat& s = c->stats[ev.name];
+            s.calls++;
+            s.total_ms += ms;
+            if (ms > s.max_ms) s.max_ms = ms;
+        }
+        c->event_pool.push_back(ev.start);
+        c->event_pool.push_back(ev.stop);
+    }
+    c->pending.clear();
+    return IAM_OK;
+}
+
+}  // namespace iam
+
+using namespace iam;
+
+extern "C" {
+
+const char* iam_last_error(void) { return g_last_error.c_str(); }
+
+int iam_ctx_create(int device, iam_ctx** out)
+{
+    if (!out) return fail(IAM_E_INVALID, "ctx_create: null output");
+    *out = nullptr;
+    int n = 0;
+    IAM_CHECK_HIP(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n)
+        return fail(IAM_E_INVALID, "ctx_create: device " + std::to_string(device) + " of " +
+                                       std::to_string(n));
+    IAM_CHECK_HIP(hipSetDevice(device));
+    iam_ctx* c = new iam_ctx();
+    c->device = device;
+    // default priority stream
+    hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete c;
+        return fail(IAM_E_HIP, std::string("hipStreamCreate: ") + hipGetErrorString(e));
+    }
+    size_t free_b = 0, total_b = 0;
+    IAM_CHECK_HIP(hipMemGetInfo(&free_b, &total_b));
+    c->total_mem = total_b;
+    const size_t margin = 512ull << 20;   // gpu.hpp:28 safety margin
+    c->usable = total_b > margin ? total_b - margin : total_b;
+    *out = c;
+    return IAM_OK;
+}
+
+int iam_ctx_destroy(iam_ctx* c)
+{
+    if (!c) return IAM_OK;
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    for (auto& kv : c->allocs) (void)hipFree((void*)kv.first);
+    c->allocs.clear();
+    for (auto& ev : c->pending) {
+        (void)hipEventDestroy(ev.start);
+        (void)hipEventDestroy(ev.stop);
+    }
+    for (auto e : c->event_pool) (void)hipEventDestroy(e);
+    (void)hipStreamDestroy(c->stream);
+    delete c;
+    return IAM_OK;
+}
+
+int iam_sync(iam_ctx* c)
+{
+    if (!c) return fail(IAM_E_INVALID, "sync: null context");
+    IAM_CHECK_HIP(hipStreamSynchronize(c->stream));
+    return fold_events(c);
+}
+
+int iam_device_info(iam_ctx* c, char* name, size_t name_len, int* cus, size_t* mem)
+{
+    if (!c) return fail(IAM_E_INVALID, "device_info: null context");
+    hipDeviceProp_t p;
+    IAM_CHECK_HIP(hipGetDeviceProperties(&p, c->device));
+    if (name && name_len) {
+        std::snprintf(name, name_len, "%s (%s)", p.name, p.gcnArchName);
+    }
+    if (cus) *cus = p.multiProcessorCount;
+    if (mem) *mem = p.totalGlobalMem;
+    return IAM_OK;
+}
+
+int iam_mem_status(iam_ctx* c, size_t* allocated, size_t* usable)
+{
+    if (!c) return fail(IAM_E_INVALID, "mem_status: null context");
+    if (allocated) *allocated = c->allocated;
+    if (usable) *usable = c->usable;
+    return IAM_OK;
+}
+
+int iam_alloc(iam_ctx* c, size_t bytes, void** out)
+{
+    if (!c) return fail(IAM_E_INVALID, "alloc: null context");
+    return ctx_alloc(c, bytes, out);
+}
+
+int iam_free(iam_ctx* c, void* p)
+{
+    if (!c) return fail(IAM_E_INVALID, "free: null context");
+    IAM_CHECK_HIP(hipStreamSynchronize(c->stream));
+    return ctx_free(c, p);
+}
+
+static int check_range(Ctx* c, const void* p, size_t off, size_t bytes, const char* what)
+{
+    return check_dev_range(c, (const uint8_t*)p + off, bytes, what);
+}
+
+int iam_zero(iam_ctx* c, void* p, size_t off, size_t bytes)
+{
+    if (!c || !p) return fail(IAM_E_INVALID, "zero: null argument");
+    IAM_TRY(check_range(c, p, off, bytes, "zero"));
+    return zero_async(c, (uint8_t*)p + off, bytes);
+}
+
+int iam_write(iam_ctx* c, void* dst, size_t off, const void* src, size_t bytes)
+{
+    if (!c || !dst || (!src && bytes)) return fail(IAM_E_INVALID, "write: null argument");
+    IAM_TRY(check_range(c, dst, off, bytes, "write"));
+    IAM_CHECK_HIP(hipMemcpyAsync((uint8_t*)dst + off, src, bytes, hipMemcpyHostToDevice, c->stream));
+    IAM_CHECK_HIP(hipStreamSynchronize(c->stream));
+    return IAM_OK;
+}
+
+int iam_read(iam_ctx* c, void* dst, const void* src, size_t off, size_t bytes)
+{
+    if (!c || !src || (!dst && bytes)) return fail(IAM_E_INVALID, "read: null argument");
+    IAM_TRY(check_range(c, src, off, bytes, "read"));
+    IAM_CHECK_HIP(hipMemcpyAsync(dst, (const uint8_t*)src + off, bytes, hipMemcpyDeviceToHost, c->stream));
+    IAM_CHECK_HIP(hipStreamSynchronize(c->stream));
+    return IAM_OK;
+}
+
+int iam_copy(iam_ctx* c, void* dst, size_t doff, const void* src, size_t soff, size_t bytes)
+{
+    if (!c || !dst || !src) return fail(IAM_E_INVALID, "copy: null argument");
+    IAM_TRY(check_range(c, dst, doff, bytes, "copy dst"));
+    IAM_TRY(check_range(c, src, soff, bytes, "copy src"));
+    IAM_CHECK_HIP(hipMemcpyAsync((uint8_t*)dst + doff, (const uint8_t*)src + soff, bytes,
+                                 hipMemcpyDeviceToDevice, c->stream));
+    return IAM_OK;
+}
+
+int iam_profiling(iam_ctx* c, int enable)
+{
+    if (!c) return fail(IAM_E_INVALID, "profiling: null context");
+    c->profiling = enable != 0;
+    return IAM_OK;
+}
+
+int iam_kernel_stats(iam_ctx* c, char* buf, size_t len)
+{
+    if (!c || !buf || !len) return fail(IAM_E_INVALID, "kernel_stats: bad argument");
+    std::vector<std::pair<std::string, KernelStat>> v(c->stats.begin(), c->stats.end());
+    std::sort(v.begin(), v.end(),
+              [](const auto& a, const auto& b) { return a.second.total_ms > b.second.total_ms; });
+    double total = 0;
+    for (auto& kv : v) total += kv.second.total_ms;
+    std::ostringstream os;
+    os << std::setw(28) << "Kernel" << std::setw(10) << "Calls" << std::setw(14) << "Total (ms)"
+       << std::setw(14) << "Avg (ms)" << std::setw(12) << "Max (ms)" << std::setw(12)
+       << "% of Total" << "\n";
+    for (auto& kv : v) {
+        const KernelStat& s = kv.second;
+        os << std::setw(28) << kv.first << std::setw(10) << s.calls << std::setw(14)
+           << std::fixed << std::setprecision(3) << s.total_ms << std::setw(14)
+           << std::setprecision(5) << (s.calls ? s.total_ms / s.calls : 0.0) << std::setw(12)
+           << s.max_ms << std::setw(11) << std::setprecision(1)
+           << (total > 0 ? 100.0 * s.total_ms / total : 0.0) << "%\n";
+    }
+    os << std::setw(28) << "TOTAL" << std::setw(10) << "" << std::setw(14) << std::setprecision(3)
+       << total << "\n";
+    std::string s = os.str();
+    std::snprintf(buf, len, "%s", s.c_str());
+    return IAM_OK;
+}
+
+int iam_kernel_stats_reset(iam_ctx* c)
+{
+    if (!c) return fail(IAM_E_INVALID, "kernel_stats_reset: null context");
+    c->stats.clear();
+    return IAM_OK;
+}
+
+int iam_kernel_stat(iam_ctx* c, const char* name, double* total_ms, int* calls)
+{
+    if (!c || !name) return fail(IAM_E_INVALID, "kernel_stat: bad argument");
+    auto it = c->stats.find(name);
+    if (total_ms) *total_ms = it == c->stats.end() ? 0.0 : it->second.total_ms;
+    if (calls) *calls = it == c->stats.end() ? 0 : it->second.calls;
+    return IAM_OK;
+}
+
+}  // extern "C"

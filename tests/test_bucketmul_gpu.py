@@ -1,0 +1,205 @@
+"""bucketMul on the GPU (through libiam.so) against the CPU oracle.
+
+Bar: the cutoff bits and the selected row set are bit-exact; y is within
+1e-3 relative L2 of the oracle's fp64-accumulated value.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+RTOL_L2 = 1e-3
+_cache = {}
+
+
+def make_matrix(O, out_dim, in_dim, seed=0, tid=1):
+    key = (out_dim, in_dim, seed, tid)
+    if key not in _cache:
+        W = O.gen_f16(seed, tid, out_dim * in_dim, 0.0, 0.02).reshape(out_dim, in_dim)
+        _cache[key] = O.bucketize(W)
+    return _cache[key]
+
+
+def rel_l2(a, b):
+    nb = np.linalg.norm(b)
+    return np.linalg.norm(a.astype(np.float64) - b) / (nb if nb > 0 else 1.0)
+
+
+def run_gpu(ctx, b, s, p, x, effort, in_size=None, expert_no=0, expert_rows=None, split=True):
+    R = expert_rows if expert_rows is not None else b.shape[0]
+    C = b.shape[1]
+    in_size = in_size if in_size is not None else R // 16
+    db, ds, dp, dx = ctx.upload(b), ctx.upload(s), ctx.upload(p), ctx.upload(x)
+    dy = ctx.empty(16 * C, np.float32)
+    if split:
+        ctx.calc_dispatch(dx, ds, dp, expert_no, in_size, C, R, effort)
+        ctx.mul(db, C, dy)
+    else:
+        ctx.full_mul(dx, ds, dp, db, expert_no, in_size, C, R, effort, dy)
+    y = dy.read()
+    cut, S = ctx.dispatch_info(0)
+    rows = ctx.dispatch_rows(0)
+    for d in (db, ds, dp, dx, dy):
+        d.free()
+    return y, cut, S, rows
+
+
+def check_against_oracle(O, ctx, b, s, p, x, effort, **kw):
+    y, cut, S, rows = run_gpu(ctx, b, s, p, x, effort, **kw)
+    in_size = kw.get("in_size")
+    expert_no = kw.get("expert_no", 0)
+    R = kw.get("expert_rows") or b.shape[0]
+    if in_size is None:
+        in_size = R // 16
+    q = O.effort_quantile(effort)
+    ocut = O.find_cutoff(x, p, q, exp_no=expert_no)
+    mask, oS = O.select_rows(x, s, ocut, R, in_size, exp_no=expert_no)
+    bb = b.reshape(-1, b.shape[-1])
+    oy = O.bucket_walk(bb, mask, x, R, exp_no=expert_no)
+    assert np.float32(cut).view(np.uint32) == np.float32(ocut).view(np.uint32), (cut, ocut)
+    assert S == oS
+    assert np.array_equal(rows, np.nonzero(mask)[0].astype(np.uint32))
+    assert rel_l2(y, oy) <= RTOL_L2
+    return y, oy, cut, S
+
+
+@pytest.mark.parametrize("effort", [1.0, 0.5, 0.25, 0.125, 0.05])
+def test_square_4096_parity(O, ctx, effort):
+    """One 4096x4096 matrix (wq/wo shape), x ~ N(0,1), seed 0."""
+    b, s, p = make_matrix(O, 4096, 4096)
+    x = O.gen_f32(0, 2, 4096, 0.0, 1.0)
+    y, oy, cut, S = check_against_oracle(O, ctx, b, s, p, x, effort)
+    assert rel_l2(y, oy) < 1e-5       # fp32 accumulation in another order
+
+
+def test_full_and_split_agree(O, ctx):
+    b, s, p = make_matrix(O, 4096, 4096)
+    x = O.gen_f32(0, 3, 4096, 0.0, 1.0)
+    y1, c1, S1, r1 = run_gpu(ctx, b, s, p, x, 0.25, split=True)
+    y2, c2, S2, r2 = run_gpu(ctx, b, s, p, x, 0.25, split=False)
+    assert c1 == c2 and S1 == S2 and np.array_equal(r1, r2)
+    assert rel_l2(y1, y2.astype(np.float64)) < 1e-6
+
+
+@pytest.mark.parametrize("shape", [(14336, 4096), (1024, 4096), (32000, 4096)],
+                         ids=["w1_14336x4096", "wk_1024x4096", "lmhead_32000x4096"])
+def test_mistral_shapes_parity(O, ctx, shape):
+    b, s, p = make_matrix(O, *shape, tid=5)
+    x = O.gen_f32(0, 6, 4096, 0.0, 1.0)
+    for effort in (0.25, 1.0):
+        check_against_oracle(O, ctx, b, s, p, x, effort)
+
+
+def test_down_projection_shape(O, ctx):
+    """w2: in 14336, out 4096 (R = 229376).  The cutoff sees x[0:4096] only;
+    selection covers all 14336 inputs."""
+    b, s, p = make_matrix(O, 4096, 14336, tid=7)
+    x = O.gen_f32(0, 8, 14336, 0.0, 0.3)
+    x[4096:] *= 3.0      # the tail is invisible to the cutoff but still selected against it
+    check_against_oracle(O, ctx, b, s, p, x, 0.25)
+
+
+def test_zero_input_selects_all(O, ctx):
+    b, s, p = make_matrix(O, 256, 4096, tid=9)
+    x = np.zeros(4096, np.float32)
+    y, cut, S, rows = run_gpu(ctx, b, s, p, x, 0.25)
+    assert cut == 0.0 and S == 4096 * 16 and not y.any()
+
+
+def test_skewed_channels(O, ctx):
+    b, s, p = make_matrix(O, 4096, 4096)
+    x = O.gen_f32(0, 10, 4096, 0.0, 1.0)
+    rng = np.random.default_rng(0)
+    x[rng.choice(4096, 41, replace=False)] *= 20.0
+    for effort in (0.05, 1.0):
+        check_against_oracle(O, ctx, b, s, p, x, effort)
+
+
+@pytest.mark.parametrize("out_dim", [16, 32, 48, 64, 80, 2048 + 16])
+def test_narrow_and_ragged_columns(O, ctx, out_dim):
+    """bucket_cols 1..129: the 1/2/4/8-wide load paths and a partial last tile."""
+    b, s, p = make_matrix(O, out_dim, 4096, tid=11)
+    x = O.gen_f32(0, 12, 4096, 0.0, 1.0)
+    check_against_oracle(O, ctx, b, s, p, x, 0.25)
+
+
+def test_in_size_skips_rows(O, ctx):
+    b, s, p = make_matrix(O, 256, 4096, tid=13)
+    x = O.gen_f32(0, 14, 4096, 0.0, 1.0)
+    y, oy, cut, S = check_against_oracle(O, ctx, b, s, p, x, 0.5, in_size=3000)
+    rows = ctx.dispatch_rows(0)
+    assert rows.max() < 3000 * 16
+
+
+def test_expert_offset(O, ctx):
+    b0, s0, p0 = make_matrix(O, 256, 4096, tid=15)
+    b1, s1, p1 = make_matrix(O, 256, 4096, tid=16)
+    b = np.concatenate([b0, b1])
+    s = np.concatenate([s0, s1])
+    p = np.concatenate([p0, p1])
+    x = O.gen_f32(0, 17, 4096, 0.0, 1.0)
+    y, oy, cut, S = check_against_oracle(O, ctx, b, s, p, x, 0.25, expert_no=1,
+                                         expert_rows=4096 * 16)
+    y1, cut1, S1, _ = run_gpu(ctx, b1, s1, p1, x, 0.25)
+    assert cut == cut1 and S == S1 and rel_l2(y, y1.astype(np.float64)) < 1e-6
+
+
+def test_stats_channel_three_only(O, ctx):
+    b, s, p = make_matrix(O, 256, 4096, tid=18)
+    s2 = s.copy()
+    s2[:, :3] = np.float16(60000.0).view(np.uint16)
+    x = O.gen_f32(0, 19, 4096, 0.0, 1.0)
+    y1, c1, S1, r1 = run_gpu(ctx, b, s, p, x, 0.25)
+    y2, c2, S2, r2 = run_gpu(ctx, b, s2, p, x, 0.25)
+    assert c1 == c2 and S1 == S2 and np.array_equal(r1, r2) and rel_l2(y1, y2.astype(np.float64)) < 1e-6
+
+
+def test_multi_matches_single(iam, O, ctx):
+    """q/k/v-style fused launch (shared x, three matrices, compact stats for one)."""
+    shapes = [(4096, 4096, 21), (1024, 4096, 22), (1024, 4096, 23)]
+    mats, bufs, outs, ref = [], [], [], []
+    x = O.gen_f32(0, 24, 4096, 0.0, 1.0)
+    dx = ctx.upload(x)
+    for idx, (o, i, tid) in enumerate(shapes):
+        b, s, p = make_matrix(O, o, i, tid=tid)
+        db, ds, dp = ctx.upload(b), ctx.upload(s), ctx.upload(p)
+        m = iam.BucketMatrix(db.ptr, ds.ptr, dp.ptr, b.shape[0], b.shape[1], 4, 3)
+        if idx == 2:
+            d3 = ctx.stats_compact(ds, b.shape[0])
+            bufs.append(d3)
+            m = iam.BucketMatrix(db.ptr, d3.ptr, dp.ptr, b.shape[0], b.shape[1], 1, 0)
+        mats.append(m)
+        bufs += [db, ds, dp]
+        outs.append(ctx.empty(o, np.float32))
+        ref.append(O.bucketmul(x, s, p, b, 0.25))
+    ctx.multi(mats, [dx] * 3, [4096] * 3, outs, 0.25)
+    for k in range(3):
+        y = outs[k].read()
+        oy, ocut, omask, oS = ref[k]
+        cut, S = ctx.dispatch_info(k)
+        assert np.float32(cut).view(np.uint32) == np.float32(ocut).view(np.uint32)
+        assert S == oS
+        assert np.array_equal(ctx.dispatch_rows(k), np.nonzero(omask)[0].astype(np.uint32))
+        assert rel_l2(y, oy) < 1e-5
+    for d in bufs + outs + [dx]:
+        d.free()
+
+
+def test_invalid_arguments_raise(iam, O, ctx):
+    b, s, p = make_matrix(O, 64, 4096, tid=25)
+    db, ds, dp = ctx.upload(b), ctx.upload(s), ctx.upload(p)
+    small_x = ctx.empty(1000, np.float32)          # cutoff needs 4096 inputs
+    dy = ctx.empty(64, np.float32)
+    with pytest.raises(iam.IamError) as e:
+        ctx.calc_dispatch(small_x, ds, dp, 0, 4096, 4, 65536, 0.25)
+    assert e.value.code == iam.IAM_E_INVALID
+    dx = ctx.upload(O.gen_f32(0, 1, 4096, 0, 1))
+    with pytest.raises(iam.IamError):
+        ctx.calc_dispatch(dx, ds, dp, 1, 4096, 4, 65536, 0.25)   # expert 1 does not exist
+    with pytest.raises(iam.IamError):
+        ctx.calc_dispatch(dx, ds, dp, 0, 4096, 4, 65536, float("nan"))
+    ctx.calc_dispatch(dx, ds, dp, 0, 4096, 4, 65536, 0.25)
+    with pytest.raises(iam.IamError):
+        ctx.mul(db, 8, dy)                                        # shape differs from dispatch
+    for d in (db, ds, dp, small_x, dy, dx):
+        d.free()

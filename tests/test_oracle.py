@@ -1,0 +1,409 @@
+"""Pins for the CPU oracle (oracle/oracle.c).  CPU only.
+
+Each test checks the oracle against something that fixes the answer
+independently: numpy's IEEE conversions, the reference's own known-answer
+cases and golden vectors, hand-traced search runs, closed forms and brute
+force.  A planted mistake (wrong channel, > instead of >=, a dropped term,
+a transposed index) fails at least one of them.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+GOLD = os.path.join(HERE, "golden")
+
+
+# ------------------------------------------------------------------ fp16 ---
+
+def test_f32_to_f16_matches_numpy(O):
+    rng = np.random.default_rng(0)
+    bits = rng.integers(0, 2**32, size=1 << 20, dtype=np.uint64).astype(np.uint32)
+    f = bits.view(np.float32)
+    f = f[~np.isnan(f)]
+    special = np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, 1e9, -1e9, np.inf, -np.inf,
+                        2.0**-24, 2.0**-25, 2.0**-25 * 1.0000001, 3 * 2.0**-26, 2.0**-14,
+                        2.0**-14 - 2.0**-25, 1.0 + 2.0**-11, 1.0 + 3 * 2.0**-11],
+                       dtype=np.float32)
+    sub = (rng.uniform(-1, 1, 100000) * 2.0**-13).astype(np.float32)
+    allf = np.concatenate([f, special, sub])
+    got = O.f32_to_f16(allf)
+    with np.errstate(over="ignore"):
+        want = allf.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_f16_to_f32_all_codes(O):
+    codes = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = O.f16_to_f32(codes)
+    want = codes.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_verify_packing_cases(O):
+    """preprocess_layer_fixed_gpu.py:340-361: position exact, value within 1%."""
+    import ctypes
+    cases = [(1.5, 0), (-0.5, 7), (0.0, 15), (3.14159, 8), (-2.71828, 3)]
+    for value, pos in cases:
+        packed = O.lib().orc_pack_fp16(value, pos)
+        v = ctypes.c_float()
+        p = ctypes.c_int()
+        O.lib().orc_unpack_fp16(packed, ctypes.byref(v), ctypes.byref(p))
+        assert p.value == pos
+        assert abs(v.value - value) / (abs(value) + 1e-8) < 0.01
+        # the packed code keeps the top 12 bits of the fp16 value
+        assert packed & 0xFFF0 == np.float16(value).view(np.uint16) & 0xFFF0
+
+
+# ------------------------------------------------------ bucket layout ---
+
+def _fixtures():
+    d = np.load(os.path.join(GOLD, "bucketize_fixtures.npz"))
+    meta = json.load(open(os.path.join(GOLD, "bucketize_fixtures.json")))
+    return d, meta
+
+
+@pytest.mark.parametrize("name", [c["name"] for c in _fixtures()[1]["cases"]])
+def test_bucketize_matches_reference_fixtures(O, name):
+    d, meta = _fixtures()
+    W = d[f"{name}__W"]
+    b, s, p = O.bucketize(W)
+    assert np.array_equal(b.ravel(), d[f"{name}__buckets"].ravel())
+    assert np.array_equal(s.ravel(), d[f"{name}__stats"].ravel())
+    assert np.array_equal(p.ravel(), d[f"{name}__probes"].ravel())
+
+
+def test_order_fixture_discriminates():
+    """The order fixture must fail a bucketizer that sums in another order:
+    sequential / float64 stats and pairwise / float64 probes all differ."""
+    d, _ = _fixtures()
+    W = d["orderdisc3200x7__W"].view(np.float16).astype(np.float32)
+    out, inn = W.shape
+    nb = out // 16
+    A = np.abs(W)
+    ref_p = d["orderdisc3200x7__probes"].view(np.float16).ravel()
+    p_pw = (np.add.reduce(np.ascontiguousarray(A.T), axis=1) / np.float32(out)).astype(np.float16)
+    p_64 = (A.astype(np.float64).sum(0) / out).astype(np.float16)
+    assert (p_pw != ref_p).any() or (p_64 != ref_p).any()
+    ref_s = d["orderdisc3200x7__stats"].view(np.float16).reshape(inn * 16, 4)[:, 3]
+    rows = np.ascontiguousarray((-np.sort(-A.T.reshape(inn, nb, 16), axis=2, kind="stable"))
+                                .transpose(0, 2, 1)).reshape(inn * 16, nb)
+    sq = np.zeros(inn * 16, np.float32)
+    for b in range(nb):
+        sq = sq + rows[:, b]
+    s_seq = (sq / np.float32(nb)).astype(np.float16)
+    s_64 = (rows.astype(np.float64).sum(1) / nb).astype(np.float16)
+    assert (s_seq != ref_s).any()
+    assert (s_64 != ref_s).any()
+
+
+def test_bucketize_invariants(O):
+    rng = np.random.default_rng(3)
+    W = rng.normal(0, 0.02, size=(256, 40)).astype(np.float16)
+    b, s, p = O.bucketize(W.view(np.uint16))
+    out, inn = W.shape
+    nb = out // 16
+    bb = b.reshape(inn, 16, nb)
+    # positions within each (input, bucket) column form a permutation of 0..15
+    pos = bb & 15
+    assert np.array_equal(np.sort(pos, axis=1), np.broadcast_to(np.arange(16)[None, :, None], pos.shape))
+    # the position points back at the original weight; |value| non-increasing in rank
+    Wb = W.view(np.uint16).T.reshape(inn, nb, 16)
+    orig = np.take_along_axis(Wb, pos.transpose(0, 2, 1).astype(np.int64), axis=2).transpose(0, 2, 1)
+    assert np.array_equal(orig & 0xFFF0, bb & 0xFFF0)
+    mag = np.abs(orig.view(np.float16).astype(np.float32))
+    assert (np.diff(mag, axis=1) <= 0).all()
+    # stats channels equal; stats non-increasing in rank
+    assert (s == s[:, :1]).all()
+    st = s[:, 3].view(np.float16).astype(np.float32).reshape(inn, 16)
+    assert (np.diff(st, axis=1) <= 0).all()
+
+
+def test_pairwise_sum_matches_numpy(O):
+    rng = np.random.default_rng(5)
+    for n in [0, 1, 7, 8, 9, 15, 16, 127, 128, 129, 200, 255, 256, 1000, 2000, 4097]:
+        a = (rng.exponential(1.0, n) * np.exp2(rng.uniform(-20, 10, n))).astype(np.float32)
+        got = O.lib().orc_np_pairwise_sum_f32(a, n)
+        want = np.add.reduce(a) if n else np.float32(0)
+        assert np.float32(got).view(np.uint32) == np.float32(want).view(np.uint32) or (n == 0 and got == 0)
+
+
+# ---------------------------------------------------------------- cutoff ---
+
+def test_effort_quantile_kat(O):
+    # bucket_mul.hpp:164, target = 4096 - quantile
+    kat = {1.0: 4096, 0.5: 2049, 0.25: 1025, 0.125: 513, 0.05: 206}
+    for e, target in kat.items():
+        assert 4096 - O.effort_quantile(e) == target
+
+
+def test_importance_matches_reference_harness(O):
+    """test_cutoff_binary_search.cpp:223-237 restates the importance as
+    CUTOFF_SCALE * |input * fp16_to_float(probe)| in float."""
+    rng = np.random.default_rng(1)
+    x = rng.normal(0, 1, 4096).astype(np.float32)
+    probes = rng.uniform(0, 0.05, 8192).astype(np.float16)
+    for exp_no in (0, 1):
+        got = O.importance(x, probes.view(np.uint16), exp_no)
+        pv = probes[exp_no * 4096:(exp_no + 1) * 4096].astype(np.float32)
+        want = np.float32(100000.0) * np.abs(x * pv)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_cutoff_zero_input(O):
+    # all importances 0: bound 0, count 0 < target, range 0 < 1e-5 -> 0 after 1 round
+    c, tr = O.find_cutoff_imp(np.zeros(4096, np.float32), O.effort_quantile(0.25), trace=True)
+    assert c == 0.0 and tr.rounds == 1 and tr.converged == 1
+
+
+def test_cutoff_exact_hit_round1(O):
+    imp = np.zeros(4096, np.float32)
+    imp[:1025] = 10.0
+    imp[1025:] = 1.0
+    c, tr = O.find_cutoff_imp(imp, O.effort_quantile(0.25), trace=True)
+    # min 1, max 10, bound 5.5 counts exactly 1025 = target
+    assert c == 5.5 and tr.rounds == 1 and tr.counts[0] == 1025
+
+
+def test_cutoff_ramp_gap_convergence(O):
+    """imp = 0..4095, target 1025: hand-traced; stops in round 11 when the
+    bracket counts are 1024 and 1026 (|gap| < 3) and returns the bound tested
+    in that round."""
+    imp = np.arange(4096, dtype=np.float32)
+    c, tr = O.find_cutoff_imp(imp, O.effort_quantile(0.25), trace=True)
+    want_bounds = [2047.5, 3071.25, 2559.375, 2815.3125, 2943.28125, 3007.265625, 3039.2578125,
+                   3055.25390625, 3063.251953125, 3067.2509765625, 3069.25048828125]
+    want_counts = [2048, 1024, 1536, 1280, 1152, 1088, 1056, 1040, 1032, 1028, 1026]
+    assert tr.rounds == 11 and tr.converged == 1
+    assert list(tr.bounds[:11]) == want_bounds
+    assert list(tr.counts[:11]) == want_counts
+    assert c == np.float32(3069.25048828125)
+
+
+def test_cutoff_round_limit_float_ties(O):
+    """1023 values at 1000, 5 at 500, the rest 0, target 1025.  The bracket
+    closes on 500 from below; from round 18 the float midpoints round (ties to
+    even), the bracket never shrinks below 1e-5 and the counts stay 1023/1028,
+    so all 20 rounds run and the untested midpoint 500 - 2^-11 is returned.
+    Hand-traced: bound_19 = 500 - 62*2^-15, bound_20 = 500 - 31*2^-15."""
+    imp = np.zeros(4096, np.float32)
+    imp[:1023] = 1000.0
+    imp[1023:1028] = 500.0
+    c, tr = O.find_cutoff_imp(imp, O.effort_quantile(0.25), trace=True)
+    assert tr.rounds == 20 and tr.converged == 0
+    assert tr.bounds[0] == 500.0 and tr.counts[0] == 1023
+    assert tr.bounds[1] == 250.0 and tr.counts[1] == 1028
+    assert tr.bounds[18] == np.float32(500 - 62 * 2.0**-15)
+    assert tr.bounds[19] == np.float32(500 - 31 * 2.0**-15)
+    assert c == np.float32(500 - 2.0**-11)
+
+
+def test_cutoff_bracket_invariants(O):
+    rng = np.random.default_rng(11)
+    for trial in range(40):
+        x = rng.normal(0, 1, 4096).astype(np.float32)
+        if trial % 4 == 1:
+            x[rng.choice(4096, 41, replace=False)] *= 20     # skewed channels
+        if trial % 4 == 2:
+            x = np.round(x * 4) / 4                           # many ties
+        probes = np.abs(rng.normal(0.016, 0.002, 4096)).astype(np.float16)
+        for effort in (1.0, 0.5, 0.25, 0.125, 0.05):
+            q = O.effort_quantile(effort)
+            c, tr = O.find_cutoff(x, probes.view(np.uint16), q, trace=True)
+            imp = O.importance(x, probes.view(np.uint16))
+            assert tr.init_min <= c <= tr.init_max
+            cnt = int((imp > c).sum())
+            assert tr.final_max_count <= cnt <= tr.final_min_count
+            if effort == 1.0 and tr.converged and tr.final_max - tr.final_min >= 1e-5:
+                assert (imp <= c).sum() <= 2
+
+
+def test_cutoff_constant_importance(O):
+    # every |x*p| equal: min == max, one round
+    x = np.ones(4096, np.float32)
+    probes = np.full(4096, 0.015625, np.float16)
+    c, tr = O.find_cutoff(x, probes.view(np.uint16), O.effort_quantile(0.5), trace=True)
+    assert c == np.float32(1562.5) and tr.rounds == 1
+
+
+# ------------------------------------------------------------- selection ---
+
+def test_select_rows_channel3_ge_and_in_size(O):
+    rng = np.random.default_rng(2)
+    in_dim = 64
+    R = in_dim * 16
+    x = rng.normal(0, 1, 4096).astype(np.float32)
+    stats = np.zeros((R, 4), np.float16)
+    stats[:, 3] = np.abs(rng.normal(0.02, 0.01, R)).astype(np.float16)
+    stats[:, :3] = np.float16(60000.0)     # garbage in channels 0..2
+    imp3 = np.float32(100000.0) * np.abs(np.repeat(x[:in_dim], 16) * stats[:, 3].astype(np.float32))
+    cutoff = np.float32(np.sort(imp3)[R // 2])   # an importance value: tie case included
+    mask, s = O.select_rows(x, stats.view(np.uint16), cutoff, R, in_dim)
+    want = (imp3 >= cutoff)
+    assert np.array_equal(mask.astype(bool), want)
+    assert s == want.sum()
+    assert mask[np.argmin(np.abs(imp3 - cutoff))] == 1           # >= at equality
+    mask2, _ = O.select_rows(x, stats.view(np.uint16), cutoff, R, in_dim // 2)
+    assert not mask2[R // 2:].any()                              # rows past in_size skipped
+    assert np.array_equal(mask2[:R // 2], mask[:R // 2])
+
+
+def test_select_rows_expert_offset(O):
+    rng = np.random.default_rng(4)
+    R = 32 * 16
+    x = rng.normal(0, 1, 4096).astype(np.float32)
+    stats = np.abs(rng.normal(0.02, 0.01, (2 * R, 4))).astype(np.float16)
+    m0, _ = O.select_rows(x, stats.view(np.uint16), 1000.0, R, 32, exp_no=0)
+    m1, _ = O.select_rows(x, stats.view(np.uint16), 1000.0, R, 32, exp_no=1)
+    imp1 = np.float32(100000.0) * np.abs(np.repeat(x[:32], 16) * stats[R:, 3].astype(np.float32))
+    assert np.array_equal(m1.astype(bool), imp1 >= 1000.0)
+    assert not np.array_equal(m0, m1)
+
+
+# ------------------------------------------------------------------ walk ---
+
+def _packed_dense(b, in_dim):
+    """W~[c*16 + pos, i] = value of the packed code, from the bucket layout."""
+    R, C_ = b.shape
+    Wt = np.zeros((16 * C_, in_dim), np.float64)
+    codes = b.reshape(in_dim, 16, C_)
+    vals = codes.view(np.float16).astype(np.float64)
+    for i in range(in_dim):
+        for k in range(16):
+            o = np.arange(C_) * 16 + (codes[i, k] & 15)
+            Wt[o, i] = vals[i, k]
+    return Wt
+
+
+def test_walk_all_rows_is_dense_gemv(O):
+    rng = np.random.default_rng(6)
+    out_dim, in_dim = 128, 48
+    W = rng.normal(0, 0.02, (out_dim, in_dim)).astype(np.float16)
+    b, s, p = O.bucketize(W.view(np.uint16))
+    x = rng.normal(0, 1, in_dim).astype(np.float32)
+    y = O.bucket_walk(b, np.ones(in_dim * 16, np.uint8), x, in_dim * 16)
+    Wt = _packed_dense(b, in_dim)
+    np.testing.assert_allclose(y, Wt @ x.astype(np.float64), rtol=1e-6, atol=1e-7)
+    # the packed matrix is W with 4 low mantissa bits replaced: close to W x
+    yw = W.astype(np.float64) @ x.astype(np.float64)
+    assert np.linalg.norm(y - yw) / np.linalg.norm(yw) < 1.5e-2   # 4 of 10 mantissa bits replaced
+    y32 = O.bucket_walk(b, np.ones(in_dim * 16, np.uint8), x, in_dim * 16, acc64=False)
+    np.testing.assert_allclose(y32, y, rtol=1e-4, atol=1e-6)
+
+
+def test_walk_one_hot_and_zero(O):
+    rng = np.random.default_rng(7)
+    out_dim, in_dim = 64, 32
+    W = rng.normal(0, 0.02, (out_dim, in_dim)).astype(np.float16)
+    b, s, p = O.bucketize(W.view(np.uint16))
+    x = np.zeros(in_dim, np.float32)
+    x[5] = 2.0
+    mask = np.zeros(in_dim * 16, np.uint8)
+    mask[5 * 16:5 * 16 + 16] = 1
+    y = O.bucket_walk(b, mask, x, in_dim * 16)
+    Wt = _packed_dense(b, in_dim)
+    np.testing.assert_array_equal(y, (2.0 * Wt[:, 5]).astype(np.float32))
+    mask[5 * 16 + 3:5 * 16 + 16] = 0          # only ranks 0..2 of input 5
+    y = O.bucket_walk(b, mask, x, in_dim * 16)
+    top = np.argsort(-np.abs(W[:, 5].astype(np.float32)).reshape(-1, 16), axis=1, kind="stable")[:, :3]
+    want = np.zeros(out_dim, np.float32)
+    for bk in range(out_dim // 16):
+        for pp in top[bk]:
+            want[bk * 16 + pp] = 2.0 * Wt[bk * 16 + pp, 5]
+    np.testing.assert_array_equal(y, want)
+    y0 = O.bucket_walk(b, np.ones(in_dim * 16, np.uint8), np.zeros(in_dim, np.float32), in_dim * 16)
+    assert not y0.any()
+
+
+def test_bucketmul_zero_x_selects_everything(O):
+    rng = np.random.default_rng(8)
+    W = rng.normal(0, 0.02, (64, 4096)).astype(np.float16)
+    b, s, p = O.bucketize(W.view(np.uint16))
+    y, cut, mask, S = O.bucketmul(np.zeros(4096, np.float32), s, p, b, 0.25)
+    assert cut == 0.0 and S == 4096 * 16 and not y.any()
+
+
+# ----------------------------------------------------------- layer ops ---
+
+def test_rmsnorm_gain_closed_form(O):
+    rng = np.random.default_rng(9)
+    x = rng.normal(0, 1, 4096).astype(np.float32)
+    g = (1 + rng.normal(0, 0.01, 4096)).astype(np.float16)
+    got = O.rmsnorm_gain(x, g.view(np.uint16), 1e-5)
+    xd = x.astype(np.float64)
+    want = xd / np.sqrt(np.mean(xd * xd) + 1e-5) * g.astype(np.float64)
+    np.testing.assert_allclose(got, want, rtol=2e-6, atol=1e-7)
+
+
+def test_silu_closed_form(O):
+    rng = np.random.default_rng(10)
+    g = rng.normal(0, 3, 5000).astype(np.float32)
+    u = rng.normal(0, 1, 5000).astype(np.float32)
+    want = u.astype(np.float64) * g / (1 + np.exp(-g.astype(np.float64)))
+    np.testing.assert_allclose(O.silu_mul(g, u), want, rtol=1e-6, atol=1e-9)
+
+
+def test_rope_table_and_rotation(O):
+    t = O.rope_table(10000.0, 128, 64)
+    i = np.arange(64)
+    freq = (1.0 / np.power(10000.0, 2.0 * i / 128)).astype(np.float32)
+    ang = (np.arange(64, dtype=np.float32)[:, None] * freq[None, :]).astype(np.float32)
+    np.testing.assert_allclose(t[..., 0], np.cos(ang.astype(np.float64)), atol=2e-7)
+    np.testing.assert_allclose(t[..., 1], np.sin(ang.astype(np.float64)), atol=2e-7)
+    rng = np.random.default_rng(12)
+    x = rng.normal(0, 1, 4 * 128).astype(np.float32)
+    pos = 37
+    got = O.rope(x, t[pos], 4, 128)
+    xh = x.reshape(4, 128).astype(np.float64)
+    c = np.concatenate([t[pos, :, 0], t[pos, :, 0]]).astype(np.float64)
+    s = np.concatenate([t[pos, :, 1], t[pos, :, 1]]).astype(np.float64)
+    rot = np.concatenate([-xh[:, 64:], xh[:, :64]], axis=1)     # rotate-half
+    np.testing.assert_allclose(got.reshape(4, 128), xh * c + rot * s, rtol=1e-6, atol=1e-6)
+    # rotation preserves the norm of each (d, d+64) pair
+    np.testing.assert_allclose(np.linalg.norm(got.reshape(4, 128), axis=1),
+                               np.linalg.norm(xh, axis=1), rtol=1e-5)
+
+
+def test_attention_closed_form(O):
+    rng = np.random.default_rng(13)
+    n_heads, n_kv, hd, n_tok = 8, 2, 128, 37
+    q = rng.normal(0, 1, n_heads * hd).astype(np.float32)
+    k = rng.normal(0, 1, (n_tok, n_kv, hd)).astype(np.float16)
+    v = rng.normal(0, 1, (n_tok, n_kv, hd)).astype(np.float16)
+    got = O.attention_f16kv(q, k.view(np.uint16), v.view(np.uint16), n_tok, n_heads, n_kv, hd)
+    want = np.zeros((n_heads, hd))
+    for h in range(n_heads):
+        kv = h // (n_heads // n_kv)
+        s = k[:, kv].astype(np.float64) @ q[h * hd:(h + 1) * hd].astype(np.float64) / np.sqrt(hd)
+        p = np.exp(s) / np.exp(s).sum()
+        want[h] = p @ v[:, kv].astype(np.float64)
+    np.testing.assert_allclose(got.reshape(n_heads, hd), want, rtol=1e-5, atol=1e-6)
+
+
+def test_argmax_first_max(O):
+    v = np.array([1, 5, 3, 5, 5, -1], np.float32)
+    assert O.argmax(v) == 1 == int(np.argmax(v))
+    rng = np.random.default_rng(14)
+    for _ in range(20):
+        w = rng.integers(0, 50, 1000).astype(np.float32)
+        assert O.argmax(w) == int(np.argmax(w))
+
+
+# ------------------------------------------------------------- generator ---
+
+def test_generator_statistics_and_determinism(O):
+    a = O.gen_f32(0, 7, 200000, 0.0, 1.0)
+    b = O.gen_f32(0, 7, 200000, 0.0, 1.0)
+    c = O.gen_f32(1, 7, 200000, 0.0, 1.0)
+    assert np.array_equal(a, b) and not np.array_equal(a, c)
+    assert abs(a.mean()) < 0.01 and abs(a.var() - 1.0) < 0.01
+    assert np.abs(a).max() < 6.0
+    h = O.gen_f16(0, 9, 100000, 0.0, 0.02)
+    hf = h.view(np.float16).astype(np.float32)
+    assert abs(hf.std() - 0.02) < 5e-4
+    t = O.gen_tokens(0, 3, 100000, 32000)
+    assert t.min() >= 0 and t.max() < 32000 and len(np.unique(t)) > 30000
