@@ -133,6 +133,12 @@ int iam_bucketmul_dispatch_rows(iam_ctx* ctx, int slot, uint32_t* rows_host, siz
                                 uint32_t* count);
 /* effort -> quantile exactly as bucket_mul.hpp:164 */
 int iam_effort_quantile(float effort);
+/* Device-side counters of the walk: the algorithmic weight bytes streamed
+ * (2 * S * bucket_cols summed over every matrix walked), the selected rows
+ * S and the matrices walked, since the last reset.  They are updated inside
+ * the walk kernel, so graph replays count too.  Blocking. */
+int iam_walk_counters(iam_ctx* ctx, uint64_t* weight_bytes, uint64_t* rows, uint64_t* matrices,
+                      int reset);
 /* Derive a compact copy stats3[r] = stats[r*4 + 3] (device), so the
  * selection reads 2 bytes per row instead of 8.  The file layout is unchanged. */
 int iam_stats_compact(iam_ctx* ctx, const uint16_t* stats_dev, size_t rows, int stride,
@@ -161,10 +167,11 @@ int iam_rope(iam_ctx* ctx, const float* in_dev, const float* table_dev, const in
              int n_heads, int head_dim, float* out_dev);
 /* RoPE of q (n_heads) and k (n_kv heads), then the KV append
  * (attention.hpp:172-189 and :281-309) into fp16 caches laid out
- * [max_ctx][n_kv][head_dim] at position *pos_dev. */
+ * [max_ctx][n_kv][head_dim] at position *pos_dev (ignored unless
+ * 0 <= *pos_dev < max_ctx). */
 int iam_rope_kv_append(iam_ctx* ctx, const float* q_dev, const float* k_dev, const float* v_dev,
                        const float* table_dev, const int* pos_dev, int n_heads, int n_kv,
-                       int head_dim, float* q_out_dev, uint16_t* kcache_dev,
+                       int head_dim, int max_ctx, float* q_out_dev, uint16_t* kcache_dev,
                        uint16_t* vcache_dev);
 /* Decode attention over positions 0..*pos_dev of an fp16 GQA cache
  * (dotSetScore2 aux.cl:497-540, sum_of_exps32_mx :204-210, softmax_add32_mx
@@ -173,9 +180,10 @@ int iam_rope_kv_append(iam_ctx* ctx, const float* q_dev, const float* k_dev, con
 int iam_attention_decode(iam_ctx* ctx, const float* q_dev, const uint16_t* kcache_dev,
                          const uint16_t* vcache_dev, const int* pos_dev, int n_heads, int n_kv,
                          int head_dim, int max_ctx, float* out_dev);
-/* fetchRow16to32 (aux.cl:442-452): out = (float) table[*token_dev][:] */
-int iam_embed_gather(iam_ctx* ctx, const uint16_t* table_dev, int cols, const int* token_dev,
-                     float* out_dev);
+/* fetchRow16to32 (aux.cl:442-452): out = (float) table[*token_dev][:]; a
+ * token outside [0, vocab) yields zeros. */
+int iam_embed_gather(iam_ctx* ctx, const uint16_t* table_dev, int cols, int vocab,
+                     const int* token_dev, float* out_dev);
 /* greedy pick (test_generation.cpp:235, :276): first index of the maximum */
 int iam_argmax(iam_ctx* ctx, const float* v_dev, int n, int* out_dev);
 
@@ -235,8 +243,16 @@ int iam_model_step_device(iam_model* m, float effort, const float* hidden_overri
  * out_tokens receives n_new ids. */
 int iam_model_generate(iam_model* m, const int* prompt, int n_prompt, int n_new, float effort,
                        int use_graph, int* out_tokens);
-/* MistralModel::reset_caches (model.hpp:233-237) */
+/* Continue greedy decoding from the current device state (the token picked
+ * by the previous step at the current position) for n_steps steps, replaying
+ * the captured step when use_graph is set.  Asynchronous. */
+int iam_model_decode(iam_model* m, int n_steps, float effort, int use_graph);
+/* MistralModel::reset_caches (model.hpp:233-237); also rewinds the position. */
 int iam_model_reset_caches(iam_model* m);
+/* Per-channel fp32 factors applied to the gathered embedding before the
+ * first layer (NULL restores plain fetchRow16to32).  Used for the skewed-
+ * channel decode workload, which scales 1% of hidden channels. */
+int iam_model_set_embed_scale(iam_model* m, const float* scale_host);
 /* Device pointer and size of a named model tensor, e.g. "layer3.w1.buckets",
  * "layer0.attn_gain", "embed", "final_gain", "lm_head.stats", "kcache",
  * "vcache", "rope", "logits", "token", "pos", "hidden". */

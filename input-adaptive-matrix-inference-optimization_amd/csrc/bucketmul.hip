@@ -120,8 +120,6 @@ struct DispatchDesc {
     uint2* list;
     uint32_t* counts;
     float* cutoff;
-    float* y;                 // zeroed if non-null
-    int m;
     int block_base;
 };
 
@@ -146,11 +144,6 @@ __global__ __launch_bounds__(kCutThreads) void k_dispatch(DispatchArgs a)
     const int lane = tid & 63;
     const int wave = tid >> 6;
 
-    // zero this chunk's share of y (the walk accumulates into it)
-    if (d.y) {
-        for (int i = g * kCutThreads + tid; i < d.m; i += d.G * kCutThreads) d.y[i] = 0.0f;
-    }
-
     const float cutoff = block_cutoff(d.x, d.probes, d.quantile, s_red, s_cnt);
     if (g == 0 && tid == 0) d.cutoff[0] = cutoff;
 
@@ -161,15 +154,40 @@ __global__ __launch_bounds__(kCutThreads) void k_dispatch(DispatchArgs a)
     float xi = 0.0f;
     if (i < d.in_size && r0 < d.rows) {
         xi = d.x[i];
-        const uint16_t* st = d.stats + (size_t)r0 * d.stats_stride + d.stats_channel;
+        // the 16 stats of this input, all loads issued before any use
+        uint32_t sv[16];
+        const uint16_t* st = d.stats + (size_t)r0 * d.stats_stride;
+        const bool whole = r0 + 16 <= d.rows;
+        if (whole && d.stats_stride == 1 && (((uintptr_t)st) & 15) == 0) {
+            const uint4* p4 = reinterpret_cast<const uint4*>(st);
+            const uint4 a0 = p4[0], a1 = p4[1];
+            const uint32_t w[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+            for (int kk = 0; kk < 16; kk++) sv[kk] = (w[kk >> 1] >> ((kk & 1) * 16)) & 0xffffu;
+        } else if (whole && d.stats_stride == 4 && d.stats_channel == 3 && (((uintptr_t)st) & 15) == 0) {
+            // reference layout: 4 equal channels per row, channel 3 read
+            const uint4* p4 = reinterpret_cast<const uint4*>(st);
+            uint4 a[8];
+#pragma unroll
+            for (int k8 = 0; k8 < 8; k8++) a[k8] = p4[k8];
+#pragma unroll
+            for (int k8 = 0; k8 < 8; k8++) {
+                sv[2 * k8] = a[k8].y >> 16;       // row 2*k8, channel 3
+                sv[2 * k8 + 1] = a[k8].w >> 16;   // row 2*k8+1, channel 3
+            }
+        } else {
+#pragma unroll
+            for (int kk = 0; kk < 16; kk++) {
+                const int rr = min(r0 + kk, d.rows - 1) - r0;
+                sv[kk] = st[(size_t)rr * d.stats_stride + d.stats_channel];
+            }
+        }
 #pragma unroll
         for (int kk = 0; kk < 16; kk++) {
-            if (r0 + kk < d.rows) {
-                float avg = h2f(st[(size_t)kk * d.stats_stride]);
-                float prod = __fmul_rn(xi, avg);
-                float imp = __fmul_rn(kScale, fabsf(prod));
-                if (imp >= cutoff) mask |= 1u << kk;   // bucketMul.cl:380
-            }
+            float avg = h2f(sv[kk]);
+            float prod = __fmul_rn(xi, avg);
+            float imp = __fmul_rn(kScale, fabsf(prod));
+            if (imp >= cutoff && r0 + kk < d.rows) mask |= 1u << kk;   // bucketMul.cl:380
         }
     }
     // ordered compaction: block exclusive scan of the per-thread counts
@@ -201,7 +219,8 @@ struct WalkDesc {
     const uint16_t* W;        // rows of the expert: W[row * C + col]
     const uint2* list;
     const uint32_t* counts;
-    float* y;
+    float* part;              // [P][16*C] partial sums, one row per row slice
+    unsigned long long* counters;   // walk bytes, rows, matrices (block 0 adds)
     int C;
     int G;
     int P;                    // row slices
@@ -250,7 +269,7 @@ struct VecLoad<1> {
 
 constexpr int kWalkThreads = 256;
 constexpr int kBatch = 256;           // list entries staged per round (bucketMul.cl:26 uses 256)
-constexpr int kUnroll = 4;
+constexpr int kUnroll = 8;           // row groups in flight per lane (a whole batch)
 
 // Lane layout: lane = q*8 + j.  q (0..7) picks one of 8 rows handled per wave
 // instruction, j (0..7) a vector of VEC columns, so a tile is 8*VEC columns
@@ -298,47 +317,55 @@ __global__ __launch_bounds__(kWalkThreads) void k_walk(WalkArgs a)
     if (tid == 0) s_pre[0] = 0;
     __syncthreads();
     const uint32_t S = s_pre[d.G];
+    if (w == 0 && tid == 0) {
+        atomicAdd(d.counters + 0, (unsigned long long)S * (unsigned long long)d.C * 2ull);
+        atomicAdd(d.counters + 1, (unsigned long long)S);
+        atomicAdd(d.counters + 2, 1ull);
+    }
     const uint32_t lo = (uint32_t)(((uint64_t)S * (uint32_t)p) / (uint32_t)d.P);
     const uint32_t hi = (uint32_t)(((uint64_t)S * (uint32_t)(p + 1)) / (uint32_t)d.P);
 
     const int q = lane >> 3;
     const int j = lane & 7;
     const int col0 = t * TW + j * VEC;
-    const bool colok = col0 < d.C;
+    // Lanes past the last column load column 0 and accumulate zeros, and the
+    // batch is padded with {row 0, x = 0}: every load is unconditional, so all
+    // kUnroll loads of a lane are in flight together.
+    const int colc = col0 < d.C ? col0 : 0;
+    const float xmask = col0 < d.C ? 1.0f : 0.0f;
     float* myacc = acc + q * QS + j;
     using LT = typename VecLoad<VEC>::T;
 
     for (uint32_t base = lo; base < hi; base += kBatch) {
         const int n = (hi - base) < (uint32_t)kBatch ? (int)(hi - base) : kBatch;
         __syncthreads();
-        if (tid < n) {
-            const uint32_t idx = base + (uint32_t)tid;
-            int lo_c = 0, hi_c = d.G;   // s_pre[lo_c] <= idx < s_pre[hi_c]
-            while (hi_c - lo_c > 1) {
-                int mid = (lo_c + hi_c) >> 1;
-                if (s_pre[mid] <= idx) lo_c = mid;
-                else hi_c = mid;
+        {
+            uint2 ent = make_uint2(0u, 0u);
+            if (tid < n) {
+                const uint32_t idx = base + (uint32_t)tid;
+                int lo_c = 0, hi_c = d.G;   // s_pre[lo_c] <= idx < s_pre[hi_c]
+                while (hi_c - lo_c > 1) {
+                    int mid = (lo_c + hi_c) >> 1;
+                    if (s_pre[mid] <= idx) lo_c = mid;
+                    else hi_c = mid;
+                }
+                ent = d.list[(size_t)lo_c * kChunkRows + (idx - s_pre[lo_c])];
             }
-            s_ent[tid] = d.list[(size_t)lo_c * kChunkRows + (idx - s_pre[lo_c])];
+            s_ent[tid] = ent;
         }
         __syncthreads();
-        for (int it = 0; it < kBatch / 32; it += kUnroll) {
+        const int groups = (n + 31) >> 5;        // rows are taken 32 at a time (4 waves x 8 slots)
+        for (int it = 0; it < groups; it += kUnroll) {
             LT v[kUnroll];
             float xv[kUnroll];
-            bool ok[kUnroll];
 #pragma unroll
             for (int u = 0; u < kUnroll; u++) {
-                const int rr = wave * 8 + q + 32 * (it + u);
-                ok[u] = colok && rr < n;
-                if (ok[u]) {
-                    const uint2 e = s_ent[rr];
-                    xv[u] = __uint_as_float(e.y);
-                    v[u] = *reinterpret_cast<const LT*>(d.W + (size_t)e.x * d.C + col0);
-                }
+                const uint2 e = s_ent[wave * 8 + q + 32 * (it + u)];
+                xv[u] = __uint_as_float(e.y) * xmask;
+                v[u] = *reinterpret_cast<const LT*>(d.W + (size_t)e.x * d.C + colc);
             }
 #pragma unroll
             for (int u = 0; u < kUnroll; u++) {
-                if (!ok[u]) continue;
                 uint32_t words[(VEC + 1) / 2];
                 VecLoad<VEC>::split(v[u], words);
 #pragma unroll
@@ -352,7 +379,10 @@ __global__ __launch_bounds__(kWalkThreads) void k_walk(WalkArgs a)
         }
     }
     __syncthreads();
-    // flush, y-linear so that atomics of a wave cover consecutive outputs
+    // flush this slice's partial sums for the tile's outputs: output
+    // col*16 + pos (bucketMul.cl:442-445), so the tile is one contiguous run
+    // of the slice's partial row and the stores coalesce.
+    float* prow = d.part + (size_t)p * d.C * 16;
     for (int idx = tid; idx < TW * 16; idx += kWalkThreads) {
         const int cl = idx >> 4;          // column within the tile
         const int pos = idx & 15;
@@ -363,7 +393,62 @@ __global__ __launch_bounds__(kWalkThreads) void k_walk(WalkArgs a)
         float s = 0.0f;
 #pragma unroll
         for (int qq = 0; qq < 8; qq++) s += acc[qq * QS + ai];
-        if (s != 0.0f) unsafeAtomicAdd(d.y + (size_t)col * 16 + pos, s);   // output col*16+pos, bucketMul.cl:442-445
+        prow[(size_t)col * 16 + pos] = s;
+    }
+}
+
+// y[o] = sum over row slices of part[p][o], in slice order 0..P-1 grouped by
+// p mod 16 then combined in group order: a fixed order, so y is the same on
+// every run (bucketIntegrate, bucketMul.cl:453-497, sums 64 fixed slices).
+struct ReduceDesc {
+    const float* part;
+    float* y;
+    int P;
+    int m;
+    int block_base;
+};
+
+struct ReduceArgs {
+    ReduceDesc d[kMaxMulti];
+    int n;
+};
+
+constexpr int kRedOut = 64;   // outputs per reduce block
+
+__global__ __launch_bounds__(256) void k_reduce(ReduceArgs a)
+{
+    __shared__ float4 red[16][kRedOut / 4];
+    const int b = (int)blockIdx.x;
+    int k = 0;
+    for (int i = 1; i < a.n; i++)
+        if (b >= a.d[i].block_base) k = i;
+    const ReduceDesc& d = a.d[k];
+    const int o0 = (b - d.block_base) * kRedOut;
+    const int tid = threadIdx.x;
+    const int ol = tid & 15, pg = tid >> 4;
+    const int o = o0 + ol * 4;
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (o < d.m) {
+        for (int p = pg; p < d.P; p += 16) {
+            const float4 v = *reinterpret_cast<const float4*>(d.part + (size_t)p * d.m + o);
+            s.x += v.x;
+            s.y += v.y;
+            s.z += v.z;
+            s.w += v.w;
+        }
+    }
+    red[pg][ol] = s;
+    __syncthreads();
+    if (pg == 0 && o < d.m) {
+        float4 t = red[0][ol];
+        for (int g = 1; g < 16; g++) {
+            const float4 v = red[g][ol];
+            t.x += v.x;
+            t.y += v.y;
+            t.z += v.z;
+            t.w += v.w;
+        }
+        *reinterpret_cast<float4*>(d.y + o) = t;
     }
 }
 
@@ -383,11 +468,24 @@ static double est_fraction(float effort)
     return 1.0;
 }
 
-int est_slices(int rows, float effort)
+double est_rows(int rows, float effort) { return std::max(1.0, rows * est_fraction(effort)); }
+
+// Row slices per matrix for one walk launch: about kWalkTarget workgroups in
+// total, shared by the matrices in proportion to their expected bytes, with
+// at least kMinSliceRows rows per slice.  Only the performance depends on it.
+constexpr int kWalkTarget = 512;
+constexpr int kMinSliceRows = 48;
+
+static void plan_slices(int n, const double* bytes, const double* rows, const int* T, int* P)
 {
-    double s = std::max(1.0, rows * est_fraction(effort));
-    int P = (int)std::ceil(s / 240.0);
-    return std::max(1, std::min(P, 4096));
+    double tot = 0;
+    for (int i = 0; i < n; i++) tot += bytes[i];
+    for (int i = 0; i < n; i++) {
+        double wgs = tot > 0 ? kWalkTarget * bytes[i] / tot : kWalkTarget / n;
+        int p = (int)std::lround(wgs / T[i]);
+        int pmax = std::max(1, (int)(rows[i] / kMinSliceRows));
+        P[i] = std::max(1, std::min(p, std::min(pmax, 4096)));
+    }
 }
 
 static int vec_of(int C)
@@ -398,7 +496,7 @@ static int vec_of(int C)
     return 1;
 }
 
-int bucketmul_dispatch(Ctx* c, int n, const MatOp* ops, int expert_no, float effort, bool zero_y)
+int bucketmul_dispatch(Ctx* c, int n, const MatOp* ops, int expert_no, float effort)
 {
     IAM_REQUIRE(n >= 1 && n <= kMaxMulti, "bucketmul: 1..3 matrices per launch");
     IAM_REQUIRE(!std::isnan(effort), "bucketmul: effort is NaN");
@@ -427,8 +525,7 @@ int bucketmul_dispatch(Ctx* c, int n, const MatOp* ops, int expert_no, float eff
         IAM_TRY(check_dev_range(c, M.probes, (size_t)(expert_no + 1) * kProbes * 2, "bucketmul probes"));
         IAM_TRY(check_dev_range(c, M.stats, (size_t)(expert_no + 1) * M.expert_rows * M.stats_stride * 2,
                                 "bucketmul stats"));
-        if (zero_y && ops[i].y)
-            IAM_TRY(check_dev_range(c, ops[i].y, (size_t)M.bucket_cols * 16 * sizeof(float), "bucketmul y"));
+
         IAM_TRY(ensure_slot(c, i, std::max(G, 1)));
         DispatchSlot& s = c->slots[i];
         DispatchDesc& d = args.d[i];
@@ -444,8 +541,6 @@ int bucketmul_dispatch(Ctx* c, int n, const MatOp* ops, int expert_no, float eff
         d.list = s.list;
         d.counts = s.counts;
         d.cutoff = s.cutoff;
-        d.y = zero_y ? ops[i].y : nullptr;
-        d.m = M.bucket_cols * 16;
         d.block_base = blocks;
         blocks += d.G;
         s.G = d.G;
@@ -458,45 +553,62 @@ int bucketmul_dispatch(Ctx* c, int n, const MatOp* ops, int expert_no, float eff
     return launch(c, "bucket_dispatch", k_dispatch, dim3(blocks), dim3(kCutThreads), 0, args);
 }
 
+void plan_walk(int n, const MatOp* ops, float effort, int* T, int* P, int* V)
+{
+    double bytes[kMaxMulti], rows[kMaxMulti];
+    for (int i = 0; i < n; i++) {
+        const iam_bucket_matrix& M = ops[i].mat;
+        V[i] = vec_of(M.bucket_cols);
+        T[i] = (M.bucket_cols + 8 * V[i] - 1) / (8 * V[i]);
+        rows[i] = est_rows(M.expert_rows, effort);
+        bytes[i] = rows[i] * M.bucket_cols;
+    }
+    plan_slices(n, bytes, rows, T, P);
+}
+
 int bucketmul_walk(Ctx* c, int n, const MatOp* ops)
 {
     IAM_REQUIRE(n >= 1 && n <= kMaxMulti, "bucketmul: 1..3 matrices per launch");
-    // group by vector width (the model's matrices all use 8)
-    int done = 0;
+    int T[kMaxMulti], P[kMaxMulti], V[kMaxMulti];
+    for (int i = 0; i < n; i++) {
+        const iam_bucket_matrix& M = ops[i].mat;
+        const DispatchSlot& s = c->slots[i];
+        IAM_REQUIRE(s.valid, "bucketmul: mul without a preceding calc_dispatch");
+        IAM_REQUIRE(M.buckets && ops[i].y, "bucketmul: null buckets/y");
+        IAM_REQUIRE(s.bucket_cols == M.bucket_cols && s.rows == M.expert_rows,
+                    "bucketmul: mul shape differs from calc_dispatch shape");
+        IAM_REQUIRE(((uintptr_t)M.buckets & 15) == 0, "bucketmul: buckets must be 16-byte aligned");
+        IAM_REQUIRE(((uintptr_t)ops[i].y & 15) == 0, "bucketmul: y must be 16-byte aligned");
+        IAM_TRY(check_dev_range(c, M.buckets, (size_t)(s.expert_no + 1) * M.expert_rows * M.bucket_cols * 2,
+                                "bucketmul buckets"));
+        IAM_TRY(check_dev_range(c, ops[i].y, (size_t)M.bucket_cols * 16 * sizeof(float), "bucketmul y"));
+        IAM_REQUIRE(s.effort == c->slots[0].effort, "bucketmul: slots dispatched at different efforts");
+    }
+    plan_walk(n, ops, c->slots[0].effort, T, P, V);
+    for (int i = 0; i < n; i++) IAM_TRY(ensure_partials(c, i, (size_t)P[i] * ops[i].mat.bucket_cols * 16));
+
+    // walk: one launch per vector width (the model's matrices all use 8)
     bool used[kMaxMulti] = {false, false, false};
-    while (done < n) {
-        int vec = 0;
+    for (int done = 0; done < n;) {
+        int vec = 0, blocks = 0, cnt = 0;
         WalkArgs args{};
-        int blocks = 0, cnt = 0;
         for (int i = 0; i < n; i++) {
-            if (used[i]) continue;
-            const iam_bucket_matrix& M = ops[i].mat;
-            int v = vec_of(M.bucket_cols);
-            if (vec == 0) vec = v;
-            if (v != vec) continue;
+            if (used[i] || (vec != 0 && V[i] != vec)) continue;
+            vec = V[i];
             const DispatchSlot& s = c->slots[i];
-            IAM_REQUIRE(s.valid, "bucketmul: mul without a preceding calc_dispatch");
-            IAM_REQUIRE(M.buckets && ops[i].y, "bucketmul: null buckets/y");
-            IAM_REQUIRE(s.bucket_cols == M.bucket_cols && s.rows == M.expert_rows,
-                        "bucketmul: mul shape differs from calc_dispatch shape");
-            IAM_REQUIRE(((uintptr_t)M.buckets & 15) == 0, "bucketmul: buckets must be 16-byte aligned");
-            IAM_TRY(check_dev_range(c, M.buckets,
-                                    (size_t)(s.expert_no + 1) * M.expert_rows * M.bucket_cols * 2,
-                                    "bucketmul buckets"));
-            IAM_TRY(check_dev_range(c, ops[i].y, (size_t)M.bucket_cols * 16 * sizeof(float), "bucketmul y"));
-            WalkDesc& d = args.d[cnt];
-            d.W = M.buckets + (size_t)s.expert_no * (size_t)M.expert_rows * M.bucket_cols;
+            WalkDesc& d = args.d[cnt++];
+            d.W = ops[i].mat.buckets + (size_t)s.expert_no * (size_t)ops[i].mat.expert_rows * ops[i].mat.bucket_cols;
             d.list = s.list;
             d.counts = s.counts;
-            d.y = ops[i].y;
-            d.C = M.bucket_cols;
+            d.part = s.part;
+            d.counters = c->counters;
+            d.C = ops[i].mat.bucket_cols;
             d.G = s.G;
-            d.P = est_slices(M.expert_rows, s.effort);
-            d.T = (M.bucket_cols + 8 * vec - 1) / (8 * vec);
+            d.P = P[i];
+            d.T = T[i];
             d.block_base = blocks;
-            blocks += d.P * d.T;
+            blocks += P[i] * T[i];
             used[i] = true;
-            cnt++;
             done++;
         }
         args.n = cnt;
@@ -509,7 +621,20 @@ int bucketmul_walk(Ctx* c, int n, const MatOp* ops)
         }
         IAM_TRY(rc);
     }
-    return IAM_OK;
+    // fixed-order sum of the slices into y
+    ReduceArgs ra{};
+    ra.n = n;
+    int rblocks = 0;
+    for (int i = 0; i < n; i++) {
+        ReduceDesc& d = ra.d[i];
+        d.part = c->slots[i].part;
+        d.y = ops[i].y;
+        d.P = P[i];
+        d.m = ops[i].mat.bucket_cols * 16;
+        d.block_base = rblocks;
+        rblocks += (d.m + kRedOut - 1) / kRedOut;
+    }
+    return launch(c, "bucket_reduce", k_reduce, dim3(rblocks), dim3(256), 0, ra);
 }
 
 __global__ void k_stats_compact(const uint16_t* __restrict__ s, size_t rows, int stride, int ch,
@@ -541,7 +666,7 @@ int iam_bucketmul_calc_dispatch(iam_ctx* c, const float* x, const uint16_t* stat
     op.mat.stats_channel = 3;
     op.x = x;
     op.in_size = in_size;
-    return bucketmul_dispatch(c, 1, &op, expert_no, effort, false);
+    return bucketmul_dispatch(c, 1, &op, expert_no, effort);
 }
 
 int iam_bucketmul_mul(iam_ctx* c, const uint16_t* buckets, int bucket_cols, float* y)
@@ -555,8 +680,6 @@ int iam_bucketmul_mul(iam_ctx* c, const uint16_t* buckets, int bucket_cols, floa
     op.mat.expert_rows = s.rows;
     op.mat.bucket_cols = bucket_cols;
     op.y = y;
-    IAM_TRY(check_dev_range(c, y, sizeof(float) * 16 * (size_t)bucket_cols, "mul y"));
-    IAM_TRY(zero_async(c, y, sizeof(float) * 16 * (size_t)bucket_cols));
     return bucketmul_walk(c, 1, &op);
 }
 
@@ -577,7 +700,7 @@ int iam_bucketmul_full(iam_ctx* c, const float* x, const uint16_t* stats, const 
     op.in_size = in_size;
     op.y = y;
     IAM_REQUIRE(y, "full: null y");
-    IAM_TRY(bucketmul_dispatch(c, 1, &op, expert_no, effort, true));
+    IAM_TRY(bucketmul_dispatch(c, 1, &op, expert_no, effort));
     return bucketmul_walk(c, 1, &op);
 }
 
@@ -594,7 +717,7 @@ int iam_bucketmul_multi(iam_ctx* c, int n, const iam_bucket_matrix* mats, const 
         ops[i].y = ys[i];
         IAM_REQUIRE(ys[i] && mats[i].buckets, "multi: null y/buckets");
     }
-    IAM_TRY(bucketmul_dispatch(c, n, ops, expert_no, effort, true));
+    IAM_TRY(bucketmul_dispatch(c, n, ops, expert_no, effort));
     return bucketmul_walk(c, n, ops);
 }
 

@@ -56,6 +56,8 @@ struct DispatchSlot {
     int expert_no = 0;
     float effort = 1.0f;
     bool valid = false;
+    float* part = nullptr;       // walk partial sums [P][m]
+    size_t part_cap = 0;         // floats
 };
 
 struct KernelStat {
@@ -82,7 +84,13 @@ struct Ctx {
     std::vector<hipEvent_t> event_pool;
     std::map<std::string, KernelStat> stats;
     DispatchSlot slots[kMaxMulti];
-    float* zero_scratch = nullptr;
+    float* attn_ws = nullptr;          // split-context attention partials
+    size_t attn_ws_floats = 0;
+    // bumped whenever a context-owned scratch buffer (dispatch lists, walk
+    // partials, attention workspace) is reallocated: captured graphs hold
+    // those addresses and must be re-captured when it changes
+    uint64_t scratch_gen = 0;
+    unsigned long long* counters = nullptr;   // device: walk bytes, rows, matrices
 };
 
 int ctx_alloc(Ctx* c, size_t bytes, void** out);
@@ -90,6 +98,7 @@ int ctx_alloc(Ctx* c, size_t bytes, void** out);
 int check_dev_range(Ctx* c, const void* p, size_t bytes, const char* what);
 int ctx_free(Ctx* c, void* p);
 int ensure_slot(Ctx* c, int slot, int chunks);
+int ensure_partials(Ctx* c, int slot, size_t floats);
 
 // Launch bookkeeping: with profiling on (and no graph capture in progress)
 // each launch is bracketed by a pair of pooled events.
@@ -123,13 +132,17 @@ struct MatOp {
     int in_size;
     float* y;        // may be null for dispatch-only
 };
-// cutoff + selection (+ zero y when zero_y) for n matrices into slots 0..n-1
-int bucketmul_dispatch(Ctx* c, int n, const MatOp* ops, int expert_no, float effort, bool zero_y);
-// walk for slots 0..n-1 (y must be zero, or zeroed by the dispatch)
+// cutoff + selection for n matrices into slots 0..n-1
+int bucketmul_dispatch(Ctx* c, int n, const MatOp* ops, int expert_no, float effort);
+// walk of slots 0..n-1 into per-slice partial sums, then the fixed-order
+// reduction into each y (overwritten)
 int bucketmul_walk(Ctx* c, int n, const MatOp* ops);
+// grid plan of one walk launch: column tiles T, row slices P and load width V
+void plan_walk(int n, const MatOp* ops, float effort, int* T, int* P, int* V);
+int ensure_attn_ws(Ctx* c, size_t floats);
 
 int quantile_of(float effort);
-int est_slices(int rows, float effort);
+double est_rows(int rows, float effort);
 
 }  // namespace iam
 

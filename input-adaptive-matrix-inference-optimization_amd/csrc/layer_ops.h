@@ -1,0 +1,27 @@
+// Host-side launchers of the layer kernels (no argument checks: the C ABI
+// entry points and the model check shapes and ranges before calling them).
+#pragma once
+
+#include "internal.h"
+
+namespace iam {
+
+int rmsnorm(Ctx* c, float* h, const float* delta, const uint16_t* gain, int n, float eps, float* out);
+int add(Ctx* c, const float* a, const float* b, int n, float* out);
+int silu_mul(Ctx* c, const float* g, const float* u, int n, float* out);
+int rope_kv(Ctx* c, const float* q, const float* k, const float* v, const float* table, const int* pos,
+            int n_heads, int n_kv, int hd, int max_ctx, float* q_out, uint16_t* kc, uint16_t* vc);
+int attention(Ctx* c, const float* q, const uint16_t* kc, const uint16_t* vc, const int* pos, int n_heads,
+              int n_kv, int max_ctx, float* ws, float* out);
+size_t attention_ws_floats(int n_heads, int max_ctx);
+int embed(Ctx* c, const uint16_t* table, int cols, int vocab, const int* tok, float* out);
+// first-max argmax into out[0]; if pos_inc is non-null, *pos_inc += 1
+int argmax(Ctx* c, const float* v, int n, int* out, int* pos_inc);
+
+// synthetic data and the GPU bucketizer
+int gen_f16(Ctx* c, uint64_t seed, uint64_t tid, size_t count, double mean, double sigma, uint16_t* out);
+int gen_f32(Ctx* c, uint64_t seed, uint64_t tid, size_t count, double mean, double sigma, float* out);
+int bucketize(Ctx* c, const uint16_t* w, int out_dim, int in_dim, uint16_t* buckets, uint16_t* stats,
+              uint16_t* probes);
+
+}  // namespace iam

@@ -1,0 +1,524 @@
+// Layer kernels around the sparse GEMV: RMSNorm + gain, residual add,
+// SiLU-gated activation, RoPE + KV append, decode attention, embedding
+// gather and greedy argmax (aux.cl, matrix.cl:27-32, bucketMul.cl:517-520).
+#include <hip/hip_fp16.h>
+
+#include <cmath>
+
+#include "internal.h"
+#include "layer_ops.h"
+
+namespace iam {
+
+__device__ __forceinline__ float h2f(uint16_t b) { return __half2float(__ushort_as_half(b)); }
+
+// ------------------------------------------------------------- RMSNorm ---
+// rmsNorm32fast (aux.cl:156-196): 256 threads, n/256 consecutive squares per
+// thread, a 256-way tree, scale = 1/sqrt(sum/n + eps) (rounded from double);
+// then the fp16 gain (mul16x32, aux.cl:434-440).  With `delta` the residual
+// add32 (bucketMul.cl:517-520) is applied to h first and written back.
+__global__ __launch_bounds__(256) void k_rmsnorm(float* __restrict__ h, const float* __restrict__ delta,
+                                                 const uint16_t* __restrict__ gain, int n, float eps,
+                                                 float* __restrict__ out)
+{
+#pragma clang fp contract(off)
+    __shared__ float part[256];
+    const int tid = threadIdx.x;
+    const int per = n / 256;
+    const int b0 = tid * per;
+    float s = 0.0f;
+    for (int i = b0; i < b0 + per; i++) {
+        float v = h[i];
+        if (delta) {
+            v = __fadd_rn(v, delta[i]);
+            h[i] = v;
+        }
+        s = __fadd_rn(s, __fmul_rn(v, v));
+    }
+    part[tid] = s;
+    __syncthreads();
+    for (int st = 128; st > 0; st >>= 1) {
+        if (tid < st) part[tid] = __fadd_rn(part[tid], part[tid + st]);
+        __syncthreads();
+    }
+    const float mean = __fdiv_rn(part[0], (float)n);
+    const float scale = (float)(1.0 / sqrt((double)__fadd_rn(mean, eps)));
+    for (int i = b0; i < b0 + per; i++) {
+        const float v = __fmul_rn(h[i], scale);
+        out[i] = __fmul_rn(h2f(gain[i]), v);
+    }
+}
+
+// ------------------------------------------------------------ residual ---
+__global__ void k_add(const float* __restrict__ a, const float* __restrict__ b, int n,
+                      float* __restrict__ out)
+{
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = __fadd_rn(a[i], b[i]);
+}
+
+// ---------------------------------------------------------------- SiLU ---
+// silu32 (matrix.cl:27-32): out = x3 * x1 / (1 + exp(-x1)), x1 = gate, x3 = up
+__global__ void k_silu_mul(const float* __restrict__ g, const float* __restrict__ u, int n,
+                           float* __restrict__ out)
+{
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        const float x1 = g[i];
+        out[i] = u[i] * x1 / (1.0f + expf(-x1));
+    }
+}
+
+// ---------------------------------------------------------------- RoPE ---
+// rope_mx (aux.cl:227-248): rotate-half pairs (d, d + hd/2) with the host
+// table row for the position; no contraction, so it matches the oracle.
+__device__ __forceinline__ float rope_one(const float* m, const float* row, int d, int half)
+{
+    const int fi = d < half ? d : d - half;
+    const float c = row[2 * fi], s = row[2 * fi + 1];
+    if (d < half) return __fsub_rn(__fmul_rn(m[d], c), __fmul_rn(m[d + half], s));
+    return __fadd_rn(__fmul_rn(m[d], c), __fmul_rn(m[d - half], s));
+}
+
+__global__ void k_rope(const float* __restrict__ in, const float* __restrict__ table,
+                       const int* __restrict__ pos_p, int n_heads, int hd, int max_pos,
+                       float* __restrict__ out)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int pos = *pos_p;
+    if (i >= n_heads * hd || pos < 0 || pos >= max_pos) return;
+    const int h = i / hd, d = i - h * hd;
+    out[i] = rope_one(in + h * hd, table + (size_t)pos * hd, d, hd / 2);
+}
+
+// RoPE of q and k, then store k (after RoPE) and v at the position as fp16
+// (attention.hpp:172-189 with the copies of :281-309; the reference applies
+// RoPE to the GQA-repeated k, which has the same values per repeated head).
+__global__ void k_rope_kv(const float* __restrict__ q, const float* __restrict__ k,
+                          const float* __restrict__ v, const float* __restrict__ table,
+                          const int* __restrict__ pos_p, int n_heads, int n_kv, int hd, int max_ctx,
+                          float* __restrict__ q_out, uint16_t* __restrict__ kc,
+                          uint16_t* __restrict__ vc)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int pos = *pos_p;
+    if (pos < 0 || pos >= max_ctx) return;
+    const int nq = n_heads * hd, nk = n_kv * hd;
+    const float* row = table + (size_t)pos * hd;
+    const int half = hd / 2;
+    if (i < nq) {
+        const int h = i / hd, d = i - h * hd;
+        q_out[i] = rope_one(q + h * hd, row, d, half);
+    } else if (i < nq + nk) {
+        const int j = i - nq;
+        const int h = j / hd, d = j - h * hd;
+        kc[(size_t)pos * nk + j] = __half_as_ushort(__float2half_rn(rope_one(k + h * hd, row, d, half)));
+    } else if (i < nq + 2 * nk) {
+        const int j = i - nq - nk;
+        vc[(size_t)pos * nk + j] = __half_as_ushort(__float2half_rn(v[j]));
+    }
+}
+
+// ------------------------------------------------------------ attention ---
+// Decode attention over an fp16 GQA cache, split over the context
+// ("flash-decoding"): workgroup (kv head, split) handles kAttnChunk
+// positions for the rep = n_heads/n_kv query heads that read this KV head.
+// It writes the partial max m, the partial sum l of exp(s - m) and the
+// unnormalised o; k_attn_combine merges the splits.  Scores follow
+// dotSetScore2 (aux.cl:497-540, s = q.k / sqrt(hd)); the softmax of
+// aux.cl:204-225 is exp(s)/sum exp(s), evaluated here with the running max
+// subtracted, which leaves p unchanged.
+constexpr int kAttnChunk = 256;
+constexpr int kAttnMaxRep = 8;
+
+__global__ __launch_bounds__(256) void k_attn_partial(const float* __restrict__ q,
+                                                      const uint16_t* __restrict__ kc,
+                                                      const uint16_t* __restrict__ vc,
+                                                      const int* __restrict__ pos_p, int n_heads,
+                                                      int n_kv, int max_ctx, float scale,
+                                                      float* __restrict__ ws, int n_split)
+{
+    constexpr int HD = 128;
+    __shared__ float sq[kAttnMaxRep * HD];
+    __shared__ float sp[kAttnMaxRep * kAttnChunk];
+    __shared__ float sred[kAttnMaxRep * 8];
+    __shared__ float so[kAttnMaxRep * HD];
+    const int kvh = blockIdx.x;
+    const int split = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int rep = n_heads / n_kv;
+    int n_tok = *pos_p + 1;
+    if (n_tok > max_ctx) n_tok = max_ctx;
+    const int t0 = split * kAttnChunk;
+    const int nt = min(kAttnChunk, max(0, n_tok - t0));
+    float* wbase = ws + ((size_t)(kvh * rep) * n_split + split) * (HD + 2);
+    // workspace row for query head h = kvh*rep + r, split s: ws[(h*n_split + s)*(HD+2)]
+    if (nt == 0) {
+        for (int i = tid; i < rep * (HD + 2); i += 256) {
+            const int r = i / (HD + 2), c = i - r * (HD + 2);
+            wbase[(size_t)r * n_split * (HD + 2) + c] = c == HD ? -INFINITY : 0.0f;
+        }
+        return;
+    }
+    for (int i = tid; i < rep * HD; i += 256) {
+        const int r = i / HD, d = i - r * HD;
+        sq[i] = q[(kvh * rep + r) * HD + d];
+    }
+    __syncthreads();
+    // scores: thread t -> position t0 + t
+    float sc[kAttnMaxRep];
+#pragma unroll
+    for (int r = 0; r < kAttnMaxRep; r++) sc[r] = -INFINITY;
+    if (tid < nt) {
+        const uint4* kr = reinterpret_cast<const uint4*>(kc + ((size_t)(t0 + tid) * n_kv + kvh) * HD);
+        float acc[kAttnMaxRep];
+#pragma unroll
+        for (int r = 0; r < kAttnMaxRep; r++) acc[r] = 0.0f;
+#pragma unroll 4
+        for (int v8 = 0; v8 < HD / 8; v8++) {
+            const uint4 w = kr[v8];
+            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float kv = h2f((uint16_t)(ww[e >> 1] >> ((e & 1) * 16)));
+                const int d = v8 * 8 + e;
+#pragma unroll
+                for (int r = 0; r < kAttnMaxRep; r++)
+                    if (r < rep) acc[r] += sq[r * HD + d] * kv;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < kAttnMaxRep; r++) sc[r] = acc[r] * scale;
+    }
+    // per-head max over the chunk
+    float mloc[kAttnMaxRep];
+#pragma unroll
+    for (int r = 0; r < kAttnMaxRep; r++) {
+        float m = sc[r];
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        if (lane == 0 && r < rep) sred[r * 8 + wave] = m;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kAttnMaxRep; r++)
+        mloc[r] = r < rep ? fmaxf(fmaxf(sred[r * 8 + 0], sred[r * 8 + 1]), fmaxf(sred[r * 8 + 2], sred[r * 8 + 3]))
+                          : 0.0f;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kAttnMaxRep; r++) {
+        if (r >= rep) break;
+        const float p = tid < nt ? expf(sc[r] - mloc[r]) : 0.0f;
+        sp[r * kAttnChunk + tid] = p;
+        float l = p;
+        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+        if (lane == 0) sred[r * 8 + 4 + wave] = l;
+    }
+    __syncthreads();
+    // weighted V: thread -> (dim d, half of the positions)
+    const int d = tid & (HD - 1);
+    const int hlf = tid >> 7;
+    float acc[kAttnMaxRep];
+#pragma unroll
+    for (int r = 0; r < kAttnMaxRep; r++) acc[r] = 0.0f;
+    for (int t = hlf; t < nt; t += 2) {
+        const float vv = h2f(vc[((size_t)(t0 + t) * n_kv + kvh) * HD + d]);
+#pragma unroll
+        for (int r = 0; r < kAttnMaxRep; r++)
+            if (r < rep) acc[r] += sp[r * kAttnChunk + t] * vv;
+    }
+    if (hlf == 1) {
+#pragma unroll
+        for (int r = 0; r < kAttnMaxRep; r++)
+            if (r < rep) so[r * HD + d] = acc[r];
+    }
+    __syncthreads();
+    if (hlf == 0) {
+        for (int r = 0; r < rep; r++) {
+            float* row = wbase + (size_t)r * n_split * (HD + 2);
+            row[d] = acc[r] + so[r * HD + d];
+            if (d == 0) {
+                row[HD] = mloc[r];
+                row[HD + 1] = sred[r * 8 + 4] + sred[r * 8 + 5] + sred[r * 8 + 6] + sred[r * 8 + 7];
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ ws, int n_split,
+                                                      float* __restrict__ out)
+{
+    constexpr int HD = 128;
+    const int h = blockIdx.x;
+    const int d = threadIdx.x;
+    const float* base = ws + (size_t)h * n_split * (HD + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < n_split; s++) M = fmaxf(M, base[(size_t)s * (HD + 2) + HD]);
+    float L = 0.0f, O = 0.0f;
+    for (int s = 0; s < n_split; s++) {
+        const float* row = base + (size_t)s * (HD + 2);
+        const float m = row[HD];
+        if (m == -INFINITY) continue;
+        const float w = expf(m - M);
+        L += row[HD + 1] * w;
+        O += row[d] * w;
+    }
+    out[h * HD + d] = O / L;
+}
+
+// ---------------------------------------------------------------- embed ---
+__global__ void k_embed(const uint16_t* __restrict__ table, int cols, int vocab,
+                        const int* __restrict__ tok_p, float* __restrict__ out)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int tok = *tok_p;
+    if (i >= cols) return;
+    out[i] = (tok >= 0 && tok < vocab) ? h2f(table[(size_t)tok * cols + i]) : 0.0f;
+}
+
+// --------------------------------------------------------------- argmax ---
+// first index of the maximum (std::max_element, test_generation.cpp:235)
+__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ v, int n,
+                                                 int* __restrict__ out, int* __restrict__ pos_inc)
+{
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    const int tid = threadIdx.x;
+    float bv = -INFINITY;
+    int bi = n;   // sentinel: larger than any index
+    for (int i = tid; i < n; i += 1024) {
+        const float x = v[i];
+        if (x > bv || (x == bv && i < bi)) {
+            bv = x;
+            bi = i;
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (ov > bv || (ov == bv && oi < bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if ((tid & 63) == 0) {
+        sv[tid >> 6] = bv;
+        si[tid >> 6] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 16; w++)
+            if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) {
+                bv = sv[w];
+                bi = si[w];
+            }
+        out[0] = bi < n ? bi : 0;
+        if (pos_inc) pos_inc[0] += 1;
+    }
+}
+
+// ------------------------------------------------------------------ host ---
+
+int rmsnorm(Ctx* c, float* h, const float* delta, const uint16_t* gain, int n, float eps, float* out)
+{
+    return launch(c, delta ? "add_rmsnorm" : "rmsnorm", k_rmsnorm, dim3(1), dim3(256), 0, h, delta, gain,
+                  n, eps, out);
+}
+
+int add(Ctx* c, const float* a, const float* b, int n, float* out)
+{
+    return launch(c, "add32", k_add, dim3((n + 255) / 256), dim3(256), 0, a, b, n, out);
+}
+
+int silu_mul(Ctx* c, const float* g, const float* u, int n, float* out)
+{
+    return launch(c, "silu_mul", k_silu_mul, dim3((n + 255) / 256), dim3(256), 0, g, u, n, out);
+}
+
+int rope_kv(Ctx* c, const float* q, const float* k, const float* v, const float* table, const int* pos,
+            int n_heads, int n_kv, int hd, int max_ctx, float* q_out, uint16_t* kc, uint16_t* vc)
+{
+    const int n = (n_heads + 2 * n_kv) * hd;
+    return launch(c, "rope_kv_append", k_rope_kv, dim3((n + 255) / 256), dim3(256), 0, q, k, v, table, pos,
+                  n_heads, n_kv, hd, max_ctx, q_out, kc, vc);
+}
+
+int attention(Ctx* c, const float* q, const uint16_t* kc, const uint16_t* vc, const int* pos, int n_heads,
+              int n_kv, int max_ctx, float* ws, float* out)
+{
+    const int n_split = (max_ctx + kAttnChunk - 1) / kAttnChunk;
+    const float scale = 1.0f / std::sqrt(128.0f);
+    IAM_TRY(launch(c, "attn_partial", k_attn_partial, dim3(n_kv, n_split), dim3(256), 0, q, kc, vc, pos,
+                   n_heads, n_kv, max_ctx, scale, ws, n_split));
+    return launch(c, "attn_combine", k_attn_combine, dim3(n_heads), dim3(128), 0, (const float*)ws, n_split,
+                  out);
+}
+
+size_t attention_ws_floats(int n_heads, int max_ctx)
+{
+    const int n_split = (max_ctx + kAttnChunk - 1) / kAttnChunk;
+    return (size_t)n_heads * n_split * (128 + 2);
+}
+
+int embed(Ctx* c, const uint16_t* table, int cols, int vocab, const int* tok, float* out)
+{
+    return launch(c, "embed_gather", k_embed, dim3((cols + 255) / 256), dim3(256), 0, table, cols, vocab, tok,
+                  out);
+}
+
+int argmax(Ctx* c, const float* v, int n, int* out, int* pos_inc)
+{
+    return launch(c, "argmax", k_argmax, dim3(1), dim3(1024), 0, v, n, out, pos_inc);
+}
+
+}  // namespace iam
+
+using namespace iam;
+
+static int attn_shape_ok(int n_heads, int n_kv, int head_dim, int max_ctx)
+{
+    IAM_REQUIRE(head_dim == 128, "attention: head_dim must be 128");
+    IAM_REQUIRE(n_kv >= 1 && n_heads >= n_kv && n_heads % n_kv == 0 && n_heads / n_kv <= kAttnMaxRep,
+                "attention: n_heads must be a multiple of n_kv with at most 8 query heads per KV head");
+    IAM_REQUIRE(max_ctx >= 1, "attention: max_ctx must be positive");
+    return IAM_OK;
+}
+
+extern "C" {
+
+int iam_rmsnorm_gain(iam_ctx* c, const float* in, const uint16_t* gain, int n, float eps, float* out)
+{
+    if (!c || !in || !gain || !out) return fail(IAM_E_INVALID, "rmsnorm: null argument");
+    IAM_REQUIRE(n > 0 && n % 256 == 0, "rmsnorm: n must be a positive multiple of 256");
+    IAM_TRY(check_dev_range(c, in, (size_t)n * 4, "rmsnorm in"));
+    IAM_TRY(check_dev_range(c, gain, (size_t)n * 2, "rmsnorm gain"));
+    IAM_TRY(check_dev_range(c, out, (size_t)n * 4, "rmsnorm out"));
+    return rmsnorm(c, const_cast<float*>(in), nullptr, gain, n, eps, out);
+}
+
+int iam_add_rmsnorm_gain(iam_ctx* c, float* h, const float* delta, const uint16_t* gain, int n, float eps,
+                         float* out)
+{
+    if (!c || !h || !delta || !gain || !out) return fail(IAM_E_INVALID, "add_rmsnorm: null argument");
+    IAM_REQUIRE(n > 0 && n % 256 == 0, "add_rmsnorm: n must be a positive multiple of 256");
+    IAM_TRY(check_dev_range(c, h, (size_t)n * 4, "add_rmsnorm h"));
+    IAM_TRY(check_dev_range(c, delta, (size_t)n * 4, "add_rmsnorm delta"));
+    IAM_TRY(check_dev_range(c, gain, (size_t)n * 2, "add_rmsnorm gain"));
+    IAM_TRY(check_dev_range(c, out, (size_t)n * 4, "add_rmsnorm out"));
+    return rmsnorm(c, h, delta, gain, n, eps, out);
+}
+
+int iam_add(iam_ctx* c, const float* a, const float* b, int n, float* out)
+{
+    if (!c || !a || !b || !out) return fail(IAM_E_INVALID, "add: null argument");
+    IAM_REQUIRE(n >= 0, "add: negative n");
+    IAM_TRY(check_dev_range(c, a, (size_t)n * 4, "add a"));
+    IAM_TRY(check_dev_range(c, b, (size_t)n * 4, "add b"));
+    IAM_TRY(check_dev_range(c, out, (size_t)n * 4, "add out"));
+    return add(c, a, b, n, out);
+}
+
+int iam_silu_mul(iam_ctx* c, const float* g, const float* u, int n, float* out)
+{
+    if (!c || !g || !u || !out) return fail(IAM_E_INVALID, "silu_mul: null argument");
+    IAM_REQUIRE(n >= 0, "silu_mul: negative n");
+    IAM_TRY(check_dev_range(c, g, (size_t)n * 4, "silu gate"));
+    IAM_TRY(check_dev_range(c, u, (size_t)n * 4, "silu up"));
+    IAM_TRY(check_dev_range(c, out, (size_t)n * 4, "silu out"));
+    return silu_mul(c, g, u, n, out);
+}
+
+int iam_rope_table(double theta, int head_dim, int max_pos, float* table)
+{
+    if (!table || head_dim <= 0 || head_dim % 2 || max_pos <= 0)
+        return fail(IAM_E_INVALID, "rope_table: bad argument");
+    // attention.hpp:213-219: freq in double then float; angle = pos * freq in
+    // float; cos/sin of the float angle
+    const int half = head_dim / 2;
+    for (int pos = 0; pos < max_pos; pos++) {
+        for (int i = 0; i < half; i++) {
+            double exponent = (2.0 * i) / head_dim;
+            float freq = (float)(1.0f / std::pow(theta, exponent));
+            float angle = (float)pos * freq;
+            table[((size_t)pos * half + i) * 2 + 0] = std::cos(angle);
+            table[((size_t)pos * half + i) * 2 + 1] = std::sin(angle);
+        }
+    }
+    return IAM_OK;
+}
+
+int iam_rope(iam_ctx* c, const float* in, const float* table, const int* pos, int n_heads, int head_dim,
+             float* out)
+{
+    if (!c || !in || !table || !pos || !out) return fail(IAM_E_INVALID, "rope: null argument");
+    IAM_REQUIRE(n_heads > 0 && head_dim > 0 && head_dim % 2 == 0, "rope: bad shape");
+    const size_t n = (size_t)n_heads * head_dim;
+    IAM_TRY(check_dev_range(c, in, n * 4, "rope in"));
+    IAM_TRY(check_dev_range(c, out, n * 4, "rope out"));
+    IAM_TRY(check_dev_range(c, pos, 4, "rope pos"));
+    // the table must hold whole rows; the kernel ignores positions past it
+    auto it = c->allocs.upper_bound((uintptr_t)table);
+    IAM_REQUIRE(it != c->allocs.begin(), "rope: table not allocated by this context");
+    --it;
+    const size_t avail = it->first + it->second - (uintptr_t)table;
+    const int max_pos = (int)(avail / ((size_t)head_dim * 4));
+    IAM_REQUIRE(max_pos >= 1, "rope: table too small");
+    return launch(c, "rope", k_rope, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, in, table, pos, n_heads,
+                  head_dim, max_pos, out);
+}
+
+int iam_rope_kv_append(iam_ctx* c, const float* q, const float* k, const float* v, const float* table,
+                       const int* pos, int n_heads, int n_kv, int head_dim, int max_ctx, float* q_out,
+                       uint16_t* kc, uint16_t* vc)
+{
+    if (!c || !q || !k || !v || !table || !pos || !q_out || !kc || !vc)
+        return fail(IAM_E_INVALID, "rope_kv_append: null argument");
+    IAM_REQUIRE(n_heads > 0 && n_kv > 0 && head_dim > 0 && head_dim % 2 == 0 && max_ctx > 0,
+                "rope_kv_append: bad shape");
+    const size_t nq = (size_t)n_heads * head_dim, nk = (size_t)n_kv * head_dim;
+    IAM_TRY(check_dev_range(c, q, nq * 4, "rope_kv q"));
+    IAM_TRY(check_dev_range(c, k, nk * 4, "rope_kv k"));
+    IAM_TRY(check_dev_range(c, v, nk * 4, "rope_kv v"));
+    IAM_TRY(check_dev_range(c, q_out, nq * 4, "rope_kv q_out"));
+    IAM_TRY(check_dev_range(c, table, (size_t)max_ctx * head_dim * 4, "rope_kv table"));
+    IAM_TRY(check_dev_range(c, kc, (size_t)max_ctx * nk * 2, "rope_kv kcache"));
+    IAM_TRY(check_dev_range(c, vc, (size_t)max_ctx * nk * 2, "rope_kv vcache"));
+    IAM_TRY(check_dev_range(c, pos, 4, "rope_kv pos"));
+    return rope_kv(c, q, k, v, table, pos, n_heads, n_kv, head_dim, max_ctx, q_out, kc, vc);
+}
+
+int iam_attention_decode(iam_ctx* c, const float* q, const uint16_t* kc, const uint16_t* vc, const int* pos,
+                         int n_heads, int n_kv, int head_dim, int max_ctx, float* out)
+{
+    if (!c || !q || !kc || !vc || !pos || !out) return fail(IAM_E_INVALID, "attention: null argument");
+    IAM_TRY(attn_shape_ok(n_heads, n_kv, head_dim, max_ctx));
+    const size_t nk = (size_t)n_kv * head_dim;
+    IAM_TRY(check_dev_range(c, q, (size_t)n_heads * head_dim * 4, "attention q"));
+    IAM_TRY(check_dev_range(c, kc, (size_t)max_ctx * nk * 2, "attention kcache"));
+    IAM_TRY(check_dev_range(c, vc, (size_t)max_ctx * nk * 2, "attention vcache"));
+    IAM_TRY(check_dev_range(c, out, (size_t)n_heads * head_dim * 4, "attention out"));
+    IAM_TRY(check_dev_range(c, pos, 4, "attention pos"));
+    IAM_TRY(ensure_attn_ws(c, attention_ws_floats(n_heads, max_ctx)));
+    return attention(c, q, kc, vc, pos, n_heads, n_kv, max_ctx, c->attn_ws, out);
+}
+
+int iam_embed_gather(iam_ctx* c, const uint16_t* table, int cols, int vocab, const int* tok, float* out)
+{
+    if (!c || !table || !tok || !out) return fail(IAM_E_INVALID, "embed: null argument");
+    IAM_REQUIRE(cols > 0 && vocab > 0, "embed: bad shape");
+    IAM_TRY(check_dev_range(c, table, (size_t)cols * vocab * 2, "embed table"));
+    IAM_TRY(check_dev_range(c, out, (size_t)cols * 4, "embed out"));
+    IAM_TRY(check_dev_range(c, tok, 4, "embed token"));
+    return embed(c, table, cols, vocab, tok, out);
+}
+
+int iam_argmax(iam_ctx* c, const float* v, int n, int* out)
+{
+    if (!c || !v || !out) return fail(IAM_E_INVALID, "argmax: null argument");
+    IAM_REQUIRE(n > 0, "argmax: n must be positive");
+    IAM_TRY(check_dev_range(c, v, (size_t)n * 4, "argmax v"));
+    IAM_TRY(check_dev_range(c, out, 4, "argmax out"));
+    return argmax(c, v, n, out, nullptr);
+}
+
+}  // extern "C"

@@ -79,7 +79,35 @@ int ensure_slot(Ctx* c, int slot, int chunks)
         s.list = nullptr;
         IAM_TRY(ctx_alloc(c, sizeof(uint2) * (size_t)chunks * kChunkRows, (void**)&s.list));
         s.cap_chunks = (size_t)chunks;
+        c->scratch_gen++;
     }
+    return IAM_OK;
+}
+
+int ensure_partials(Ctx* c, int slot, size_t floats)
+{
+    DispatchSlot& s = c->slots[slot];
+    if (floats <= s.part_cap) return IAM_OK;
+    if (c->capturing) return fail(IAM_E_STATE, "partial buffer growth during graph capture");
+    if (s.part) IAM_TRY(ctx_free(c, s.part));
+    s.part = nullptr;
+    s.part_cap = 0;
+    IAM_TRY(ctx_alloc(c, floats * sizeof(float), (void**)&s.part));
+    s.part_cap = floats;
+    c->scratch_gen++;
+    return IAM_OK;
+}
+
+int ensure_attn_ws(Ctx* c, size_t floats)
+{
+    if (floats <= c->attn_ws_floats) return IAM_OK;
+    if (c->capturing) return fail(IAM_E_STATE, "attention workspace growth during graph capture");
+    if (c->attn_ws) IAM_TRY(ctx_free(c, c->attn_ws));
+    c->attn_ws = nullptr;
+    c->attn_ws_floats = 0;
+    IAM_TRY(ctx_alloc(c, floats * sizeof(float), (void**)&c->attn_ws));
+    c->attn_ws_floats = floats;
+    c->scratch_gen++;
     return IAM_OK;
 }
 
@@ -184,6 +212,14 @@ int iam_ctx_create(int device, iam_ctx** out)
     c->total_mem = total_b;
     const size_t margin = 512ull << 20;   // gpu.hpp:28 safety margin
     c->usable = total_b > margin ? total_b - margin : total_b;
+    int rc = ctx_alloc(c, 4 * sizeof(unsigned long long), (void**)&c->counters);
+    if (rc == IAM_OK) rc = zero_async(c, c->counters, 4 * sizeof(unsigned long long));
+    if (rc == IAM_OK && hipStreamSynchronize(c->stream) != hipSuccess) rc = fail(IAM_E_HIP, "ctx_create: sync");
+    if (rc != IAM_OK) {
+        std::string err = g_last_error;
+        iam_ctx_destroy(c);
+        return fail(rc, err);
+    }
     *out = c;
     return IAM_OK;
 }
@@ -317,6 +353,22 @@ int iam_kernel_stats(iam_ctx* c, char* buf, size_t len)
        << total << "\n";
     std::string s = os.str();
     std::snprintf(buf, len, "%s", s.c_str());
+    return IAM_OK;
+}
+
+int iam_walk_counters(iam_ctx* c, uint64_t* bytes, uint64_t* rows, uint64_t* mats, int reset)
+{
+    if (!c) return fail(IAM_E_INVALID, "walk_counters: null context");
+    unsigned long long h[4] = {0, 0, 0, 0};
+    IAM_CHECK_HIP(hipMemcpyAsync(h, c->counters, sizeof(h), hipMemcpyDeviceToHost, c->stream));
+    IAM_CHECK_HIP(hipStreamSynchronize(c->stream));
+    if (bytes) *bytes = h[0];
+    if (rows) *rows = h[1];
+    if (mats) *mats = h[2];
+    if (reset) {
+        IAM_TRY(zero_async(c, c->counters, sizeof(h)));
+        IAM_CHECK_HIP(hipStreamSynchronize(c->stream));
+    }
     return IAM_OK;
 }
 

@@ -207,6 +207,11 @@ class Ctx:
                                                 C.c_size_t(n), C.byref(cnt)))
         return out[:n]
 
+    def walk_counters(self, reset=False):
+        b, r, m = C.c_uint64(), C.c_uint64(), C.c_uint64()
+        check(lib().iam_walk_counters(self.h, C.byref(b), C.byref(r), C.byref(m), 1 if reset else 0))
+        return b.value, r.value, m.value
+
     def stats_compact(self, stats, rows, stride=4, channel=3, out=None):
         if out is None:
             out = self.empty(rows, np.uint16)
@@ -229,16 +234,16 @@ class Ctx:
     def rope(self, x, table, pos_dev, n_heads, head_dim, out):
         check(lib().iam_rope(self.h, _vp(x), _vp(table), _vp(pos_dev), n_heads, head_dim, _vp(out)))
 
-    def rope_kv_append(self, q, k, v, table, pos_dev, n_heads, n_kv, head_dim, q_out, kc, vc):
+    def rope_kv_append(self, q, k, v, table, pos_dev, n_heads, n_kv, head_dim, max_ctx, q_out, kc, vc):
         check(lib().iam_rope_kv_append(self.h, _vp(q), _vp(k), _vp(v), _vp(table), _vp(pos_dev),
-                                       n_heads, n_kv, head_dim, _vp(q_out), _vp(kc), _vp(vc)))
+                                       n_heads, n_kv, head_dim, max_ctx, _vp(q_out), _vp(kc), _vp(vc)))
 
     def attention(self, q, kc, vc, pos_dev, n_heads, n_kv, head_dim, max_ctx, out):
         check(lib().iam_attention_decode(self.h, _vp(q), _vp(kc), _vp(vc), _vp(pos_dev), n_heads,
                                          n_kv, head_dim, max_ctx, _vp(out)))
 
-    def embed(self, table, cols, token_dev, out):
-        check(lib().iam_embed_gather(self.h, _vp(table), cols, _vp(token_dev), _vp(out)))
+    def embed(self, table, cols, vocab, token_dev, out):
+        check(lib().iam_embed_gather(self.h, _vp(table), cols, vocab, _vp(token_dev), _vp(out)))
 
     def argmax(self, v, n, out_dev):
         check(lib().iam_argmax(self.h, _vp(v), n, _vp(out_dev)))
@@ -298,6 +303,16 @@ class Model:
                                        C.c_float(effort), 1 if use_graph else 0,
                                        out.ctypes.data_as(C.c_void_p)))
         return out[:n_new]
+
+    def decode(self, n_steps, effort, use_graph=True):
+        check(lib().iam_model_decode(self.h, n_steps, C.c_float(effort), 1 if use_graph else 0))
+
+    def set_embed_scale(self, scale):
+        if scale is None:
+            check(lib().iam_model_set_embed_scale(self.h, None))
+        else:
+            a = np.ascontiguousarray(scale, np.float32)
+            check(lib().iam_model_set_embed_scale(self.h, a.ctypes.data_as(C.c_void_p)))
 
     def reset_caches(self):
         check(lib().iam_model_reset_caches(self.h))

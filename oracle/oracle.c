@@ -7,7 +7,8 @@
  * fp32 operation is a single IEEE-rounded operation.
  *
  * How each function is pinned (tests/test_oracle.py, tests/test_golden.py):
- *   orc_f32_to_f16 / orc_f16_to_f32 .... numpy astype(float16/float32) on 2^20
+ *   orc_f32_to_f16 / orc_f16_to_f32 /
+ *   orc_f64_to_f16 ..................... numpy astype(float16/float32) on 2^20
  *                                        values incl. subnormals, inf, ties
  *   orc_pack_fp16 / orc_unpack_fp16 .... the 5 verify_packing cases
  *                                        (preprocess_layer_fixed_gpu.py:340-346)
@@ -107,6 +108,41 @@ uint16_t orc_f32_to_f16(float f)
     }
 }
 
+uint16_t orc_f64_to_f16(double d)
+{
+    uint64_t x;
+    memcpy(&x, &d, 8);
+    uint16_t sign = (uint16_t)((x >> 48) & 0x8000u);
+    uint64_t ax = x & 0x7fffffffffffffffULL;
+    if (ax >= 0x7ff0000000000000ULL) {                 /* inf / nan */
+        if (ax == 0x7ff0000000000000ULL) return (uint16_t)(sign | 0x7c00u);
+        return (uint16_t)(sign | 0x7e00u | ((ax >> 42) & 0x3ffu));
+    }
+    int e = (int)(ax >> 52) - 1023;
+    uint64_t m = ax & 0xfffffffffffffULL;
+    if (e >= 16) return (uint16_t)(sign | 0x7c00u);
+    if (e >= -14) {                                    /* normal fp16 */
+        uint32_t h = ((uint32_t)(e + 15) << 10) | (uint32_t)(m >> 42);
+        uint64_t rem = m & ((1ULL << 42) - 1), half = 1ULL << 41;
+        if (rem > half || (rem == half && (h & 1u))) h++;  /* a carry may give inf */
+        return (uint16_t)(sign | h);
+    }
+    if (e < -25) return sign;                          /* below 2^-25: to zero */
+    {                                                  /* subnormal fp16 */
+        uint64_t mm = m | (1ULL << 52);                /* value = mm * 2^(e-52) */
+        int shift = 28 - e;                            /* n = value * 2^24 */
+        uint64_t n = mm >> shift;
+        uint64_t rem = mm & ((1ULL << shift) - 1), half = 1ULL << (shift - 1);
+        if (rem > half || (rem == half && (n & 1u))) n++;
+        return (uint16_t)(sign | n);
+    }
+}
+
+void orc_f64_to_f16_n(const double* in, uint16_t* out, size_t n)
+{
+    for (size_t i = 0; i < n; i++) out[i] = orc_f64_to_f16(in[i]);
+}
+
 void orc_f32_to_f16_n(const float* in, uint16_t* out, size_t n)
 {
     for (size_t i = 0; i < n; i++) out[i] = orc_f32_to_f16(in[i]);
@@ -172,7 +208,7 @@ void orc_gen_f16(uint64_t seed, uint64_t tensor_id, size_t count, double mean, d
 {
     for (size_t i = 0; i < count; i++) {
         double v = mean + sigma * orc_gen_normal(seed, tensor_id, i);
-        out[i] = orc_f32_to_f16((float)v);
+        out[i] = orc_f64_to_f16(v);
     }
 }
 

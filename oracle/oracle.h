@@ -28,6 +28,8 @@ extern "C" {
 /* ---- fp16 helpers -------------------------------------------------------- */
 float orc_f16_to_f32(uint16_t h);
 uint16_t orc_f32_to_f16(float f);                 /* round to nearest even */
+uint16_t orc_f64_to_f16(double d);                /* round to nearest even, one rounding */
+void orc_f64_to_f16_n(const double* in, uint16_t* out, size_t n);
 void orc_f32_to_f16_n(const float* in, uint16_t* out, size_t n);
 void orc_f16_to_f32_n(const uint16_t* in, float* out, size_t n);
 /* preprocess_layer_fixed_gpu.py:40-89 pack/unpack of a value with a 4-bit position */
@@ -36,7 +38,9 @@ void orc_unpack_fp16(uint16_t packed, float* value, int* position);
 
 /* ---- synthetic data (shared definition with the GPU generator) ---------- */
 /* Counter-based: element n of tensor `tensor_id` for seed `seed`.
- * normal = (sum of 12 uniform uint32 - 6*2^32) / 2^32 (Irwin-Hall, var 1). */
+ * normal = (sum of 12 uniform uint32 - 6*2^32) / 2^32 (Irwin-Hall, var 1).
+ * The f16 variant rounds mean + sigma*normal (double) once to fp16; the f32
+ * variant rounds it once to float. */
 double orc_gen_normal(uint64_t seed, uint64_t tensor_id, uint64_t n);
 uint32_t orc_gen_u32(uint64_t seed, uint64_t tensor_id, uint64_t n);
 void orc_gen_f16(uint64_t seed, uint64_t tensor_id, size_t count, double mean, double sigma, uint16_t* out);

@@ -65,6 +65,10 @@ def lib():
     L.orc_f32_to_f16.restype = C.c_uint16
     L.orc_f32_to_f16.argtypes = [C.c_float]
     L.orc_f32_to_f16_n.argtypes = [f32p, u16p, C.c_size_t]
+    L.orc_f64_to_f16.restype = C.c_uint16
+    L.orc_f64_to_f16.argtypes = [C.c_double]
+    L.orc_f64_to_f16_n.argtypes = [np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS"),
+                                   u16p, C.c_size_t]
     L.orc_f16_to_f32_n.argtypes = [u16p, f32p, C.c_size_t]
     L.orc_pack_fp16.restype = C.c_uint16
     L.orc_pack_fp16.argtypes = [C.c_float, C.c_int]
@@ -115,6 +119,13 @@ def f32_to_f16(a):
     a = np.ascontiguousarray(a, dtype=np.float32)
     out = np.empty(a.shape, dtype=np.uint16)
     lib().orc_f32_to_f16_n(a.ravel(), out.ravel(), a.size)
+    return out
+
+
+def f64_to_f16(a):
+    a = np.ascontiguousarray(a, dtype=np.float64)
+    out = np.empty(a.shape, dtype=np.uint16)
+    lib().orc_f64_to_f16_n(a.ravel(), out.ravel(), a.size)
     return out
 
 
@@ -253,3 +264,67 @@ def attention_f16kv(q, kcache, vcache, n_tok, n_heads, n_kv, head_dim):
 
 def argmax(v):
     return lib().orc_argmax(np.ascontiguousarray(v, np.float32), len(v))
+
+
+class OracleModel:
+    """An orc_model over host copies of a model's tensors.
+
+    read(name, dtype) returns the named tensor (e.g. "layer0.wq.buckets") as a
+    numpy array; cfg is a dict of ModelConfig fields.  The arrays are kept
+    alive by this object."""
+
+    MATS = ["wq", "wk", "wv", "wo", "w1", "w3", "w2"]
+
+    def __init__(self, cfg, read):
+        self.keep = []
+        self.cfg = dict(cfg)
+        c = self.cfg
+        layers = (Layer * c["n_layers"])()
+        for L in range(c["n_layers"]):
+            for w in self.MATS:
+                mat = getattr(layers[L], w)
+                b = read(f"layer{L}.{w}.buckets", np.uint16)
+                s = read(f"layer{L}.{w}.stats", np.uint16)
+                p = read(f"layer{L}.{w}.probes", np.uint16)
+                in_dim = s.size // 64
+                mat.buckets, mat.stats, mat.probes = self._p(b), self._p(s), self._p(p)
+                mat.in_dim, mat.out_dim = in_dim, b.size // in_dim
+            layers[L].attn_gain = self._p(read(f"layer{L}.attn_gain", np.uint16))
+            layers[L].ffn_gain = self._p(read(f"layer{L}.ffn_gain", np.uint16))
+        self.layers = layers
+        mod = Model()
+        mod.cfg = ModelConfig(**c)
+        mod.layers = C.cast(layers, C.c_void_p)
+        mod.embed = self._p(read("embed", np.uint16))
+        mod.final_gain = self._p(read("final_gain", np.uint16))
+        mod.lm_head.buckets = self._p(read("lm_head.buckets", np.uint16))
+        mod.lm_head.stats = self._p(read("lm_head.stats", np.uint16))
+        mod.lm_head.probes = self._p(read("lm_head.probes", np.uint16))
+        mod.lm_head.in_dim, mod.lm_head.out_dim = c["dim"], c["vocab"]
+        kv = c["n_layers"] * c["max_ctx"] * c["n_kv_heads"] * c["head_dim"]
+        self.kc = np.zeros(kv, np.uint16)
+        self.vc = np.zeros(kv, np.uint16)
+        mod.kcache, mod.vcache = self._p(self.kc), self._p(self.vc)
+        mod.rope = self._p(rope_table(c["rope_theta"], c["head_dim"], c["max_ctx"]))
+        self.mod = mod
+
+    def _p(self, a):
+        a = np.ascontiguousarray(a)
+        self.keep.append(a)
+        return a.ctypes.data
+
+    def forward(self, token, pos, effort, hidden_in=None):
+        logits = np.empty(self.cfg["vocab"], np.float32)
+        h = None
+        if hidden_in is not None:
+            hh = np.ascontiguousarray(hidden_in, np.float32)
+            self.keep.append(hh)
+            h = hh.ctypes.data
+        lib().orc_model_forward(C.byref(self.mod), token, pos, effort, h, logits)
+        return logits
+
+    def layer_forward(self, layer, pos, effort, h):
+        """orc_layer_forward on a copy of h; returns the layer output."""
+        out = np.ascontiguousarray(h, np.float32).copy()
+        lib().orc_layer_forward(C.byref(self.mod), layer, pos, effort, out)
+        return out

@@ -1,0 +1,155 @@
+"""Layer kernels, the synthetic generator and the GPU bucketizer against the
+oracle (through libiam.so)."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def rel(a, b):
+    b = np.asarray(b, np.float64)
+    return np.linalg.norm(np.asarray(a, np.float64) - b) / max(np.linalg.norm(b), 1e-30)
+
+
+def test_generator_bytes_match_oracle(O, ctx):
+    for tid, n, mean, sigma in [(1, 100003, 0.0, 0.02), (7, 4096, 1.0, 0.01), (3, 5000, 0.0, 1.0)]:
+        d16 = ctx.empty(n, np.uint16)
+        ctx.gen_f16(0, tid, n, mean, sigma, d16)
+        assert np.array_equal(d16.read(), O.gen_f16(0, tid, n, mean, sigma))
+        d32 = ctx.empty(n, np.float32)
+        ctx.gen_f32(5, tid, n, mean, sigma, d32)
+        assert np.array_equal(d32.read().view(np.uint32), O.gen_f32(5, tid, n, mean, sigma).view(np.uint32))
+        d16.free()
+        d32.free()
+
+
+def _gpu_bucketize(ctx, W):
+    out_dim, in_dim = W.shape
+    dw = ctx.upload(np.ascontiguousarray(W, np.uint16))
+    db = ctx.empty(out_dim * in_dim, np.uint16)
+    ds = ctx.empty(in_dim * 16 * 4, np.uint16)
+    dp = ctx.empty(in_dim, np.uint16)
+    ctx.bucketize(dw, out_dim, in_dim, db, ds, dp)
+    r = db.read(), ds.read(), dp.read()
+    for d in (dw, db, ds, dp):
+        d.free()
+    return r
+
+
+def test_gpu_bucketizer_matches_reference_fixtures(ctx):
+    d = np.load(os.path.join(HERE, "golden", "bucketize_fixtures.npz"))
+    meta = json.load(open(os.path.join(HERE, "golden", "bucketize_fixtures.json")))
+    for case in meta["cases"]:
+        name = case["name"]
+        b, s, p = _gpu_bucketize(ctx, d[f"{name}__W"])
+        assert np.array_equal(b, d[f"{name}__buckets"].ravel()), name
+        assert np.array_equal(s, d[f"{name}__stats"].ravel()), name
+        assert np.array_equal(p, d[f"{name}__probes"].ravel()), name
+
+
+@pytest.mark.parametrize("shape", [(4096, 4096), (1024, 4096), (32000, 512), (4096, 1536)])
+def test_gpu_bucketizer_matches_oracle(O, ctx, shape):
+    W = O.gen_f16(3, 77, shape[0] * shape[1], 0.0, 0.02).reshape(shape)
+    b, s, p = _gpu_bucketize(ctx, W)
+    ob, os_, op = O.bucketize(W)
+    assert np.array_equal(b, ob.ravel()) and np.array_equal(s, os_.ravel()) and np.array_equal(p, op)
+
+
+def test_rmsnorm_and_add(O, ctx):
+    x = O.gen_f32(0, 31, 4096, 0.0, 1.0)
+    dlt = O.gen_f32(0, 32, 4096, 0.0, 0.5)
+    g = O.gen_f16(0, 33, 4096, 1.0, 0.01)
+    dx, dd, dg, do = ctx.upload(x), ctx.upload(dlt), ctx.upload(g), ctx.empty(4096, np.float32)
+    ctx.rmsnorm_gain(dx, dg, 4096, 1e-5, do)
+    got = do.read()
+    want = O.rmsnorm_gain(x, g, 1e-5)
+    assert rel(got, want) < 1e-6
+    ctx.add_rmsnorm_gain(dx, dd, dg, 4096, 1e-5, do)
+    h = dx.read()
+    assert np.array_equal(h.view(np.uint32), (x + dlt).view(np.uint32))
+    assert rel(do.read(), O.rmsnorm_gain(x + dlt, g, 1e-5)) < 1e-6
+    ctx.add(dx, dd, 4096, do)
+    assert np.array_equal(do.read().view(np.uint32), (x + dlt + dlt).view(np.uint32))
+    for d_ in (dx, dd, dg, do):
+        d_.free()
+
+
+def test_silu_mul(O, ctx):
+    g = O.gen_f32(0, 34, 14336, 0.0, 2.0)
+    u = O.gen_f32(0, 35, 14336, 0.0, 1.0)
+    dg, du, do = ctx.upload(g), ctx.upload(u), ctx.empty(14336, np.float32)
+    ctx.silu_mul(dg, du, 14336, do)
+    assert rel(do.read(), O.silu_mul(g, u)) < 1e-6
+    for d_ in (dg, du, do):
+        d_.free()
+
+
+def test_rope_table_host_matches_oracle(iam, O):
+    t = iam.rope_table(10000.0, 128, 300)
+    assert np.array_equal(t.view(np.uint32), O.rope_table(10000.0, 128, 300).view(np.uint32))
+    t = iam.rope_table(1e6, 128, 64)
+    assert np.array_equal(t.view(np.uint32), O.rope_table(1e6, 128, 64).view(np.uint32))
+
+
+def test_rope_kv_append_and_attention(iam, O, ctx):
+    n_heads, n_kv, hd, max_ctx = 32, 8, 128, 640
+    table = iam.rope_table(10000.0, hd, max_ctx)
+    rng = np.random.default_rng(0)
+    kc = rng.normal(0, 1, (max_ctx, n_kv, hd)).astype(np.float16)
+    vc = rng.normal(0, 1, (max_ctx, n_kv, hd)).astype(np.float16)
+    q = O.gen_f32(0, 40, n_heads * hd, 0.0, 0.3)
+    k = O.gen_f32(0, 41, n_kv * hd, 0.0, 1.0)
+    v = O.gen_f32(0, 42, n_kv * hd, 0.0, 1.0)
+    dt = ctx.upload(table)
+    dkc, dvc = ctx.upload(kc.view(np.uint16)), ctx.upload(vc.view(np.uint16))
+    dq, dk, dv = ctx.upload(q), ctx.upload(k), ctx.upload(v)
+    dqr, dout = ctx.empty(n_heads * hd, np.float32), ctx.empty(n_heads * hd, np.float32)
+    for pos in (0, 1, 255, 256, 511, 600):
+        dpos = ctx.upload(np.array([pos], np.int32))
+        ctx.rope_kv_append(dq, dk, dv, dt, dpos, n_heads, n_kv, hd, max_ctx, dqr, dkc, dvc)
+        qr = dqr.read()
+        assert np.array_equal(qr.view(np.uint32), O.rope(q, table[pos], n_heads, hd).view(np.uint32))
+        kcache = dkc.read().reshape(max_ctx, n_kv, hd)
+        vcache = dvc.read().reshape(max_ctx, n_kv, hd)
+        assert np.array_equal(kcache[pos], O.f32_to_f16(O.rope(k, table[pos], n_kv, hd)).reshape(n_kv, hd))
+        assert np.array_equal(vcache[pos], O.f32_to_f16(v).reshape(n_kv, hd))
+        ctx.attention(dqr, dkc, dvc, dpos, n_heads, n_kv, hd, max_ctx, dout)
+        want = O.attention_f16kv(qr, kcache, vcache, pos + 1, n_heads, n_kv, hd)
+        assert rel(dout.read(), want) < 1e-5, pos
+        dpos.free()
+    # a position past the capacity writes nothing
+    before = dkc.read()
+    dpos = ctx.upload(np.array([max_ctx], np.int32))
+    ctx.rope_kv_append(dq, dk, dv, dt, dpos, n_heads, n_kv, hd, max_ctx, dqr, dkc, dvc)
+    assert np.array_equal(dkc.read(), before)
+    for d_ in (dt, dkc, dvc, dq, dk, dv, dqr, dout, dpos):
+        d_.free()
+
+
+def test_embed_and_argmax(O, ctx):
+    vocab, cols = 1000, 4096
+    tab = O.gen_f16(0, 50, vocab * cols, 0.0, 0.02)
+    dtab, dout = ctx.upload(tab), ctx.empty(cols, np.float32)
+    for tok in (0, 7, 999):
+        dt = ctx.upload(np.array([tok], np.int32))
+        ctx.embed(dtab, cols, vocab, dt, dout)
+        assert np.array_equal(dout.read(), O.f16_to_f32(tab[tok * cols:(tok + 1) * cols]))
+        dt.free()
+    dt = ctx.upload(np.array([vocab], np.int32))       # outside the vocabulary -> zeros
+    ctx.embed(dtab, cols, vocab, dt, dout)
+    assert not dout.read().any()
+    v = np.array([1, 5, 3, 5, 5, -1] + [0] * 40000, np.float32)
+    dv, di = ctx.upload(v), ctx.empty(1, np.int32)
+    ctx.argmax(dv, len(v), di)
+    assert di.read()[0] == 1
+    w = O.gen_f32(0, 51, 32000, 0.0, 1.0)
+    w[[100, 20000, 31999]] = w.max() + 1.0
+    dw = ctx.upload(w)
+    ctx.argmax(dw, 32000, di)
+    assert di.read()[0] == 100 == O.argmax(w)
+    for d_ in (dtab, dout, dt, dv, di, dw):
+        d_.free()

@@ -35,6 +35,26 @@ def test_f32_to_f16_matches_numpy(O):
     assert np.array_equal(got, want)
 
 
+def test_f64_to_f16_matches_numpy(O):
+    rng = np.random.default_rng(1)
+    bits = rng.integers(0, 2**63, size=1 << 20, dtype=np.uint64)
+    d = bits.view(np.float64)
+    d = d[np.isfinite(d)]
+    small = rng.normal(0, 0.02, 1 << 18)                      # the generator's range
+    sub = rng.uniform(-1, 1, 1 << 16) * 2.0**-14                # fp16 subnormals
+    # exact ties between fp16 neighbours and values one double ulp either side
+    h = rng.integers(0, 0x7bff, 4096, dtype=np.uint16).view(np.float16).astype(np.float64)
+    h2 = np.nextafter(h.astype(np.float16), np.float16(np.inf)).astype(np.float64)
+    mid = (h + h2) / 2
+    ties = np.concatenate([mid, np.nextafter(mid, np.inf), np.nextafter(mid, -np.inf), -mid])
+    special = np.array([0.0, -0.0, 65504.0, 65519.999, 65520.0, 1e300, -1e300, np.inf, -np.inf,
+                        2.0**-24, 2.0**-25, 2.0**-25 * (1 + 2.0**-52), 3 * 2.0**-26, 2.0**-14])
+    alld = np.concatenate([d, small, sub, ties, special])
+    with np.errstate(over="ignore"):
+        want = alld.astype(np.float16).view(np.uint16)
+    assert np.array_equal(O.f64_to_f16(alld), want)
+
+
 def test_f16_to_f32_all_codes(O):
     codes = np.arange(65536, dtype=np.uint32).astype(np.uint16)
     got = O.f16_to_f32(codes)
