@@ -139,6 +139,16 @@ int iam_effort_quantile(float effort);
  * the walk kernel, so graph replays count too.  Blocking. */
 int iam_walk_counters(iam_ctx* ctx, uint64_t* weight_bytes, uint64_t* rows, uint64_t* matrices,
                       int reset);
+/* Accumulation of the bucket walk (and of attention) for this context:
+ * IAM_ACC_FP64 (default) adds the exact fp64 products in fp64 and rounds each
+ * output once, so results do not depend on the order of the additions and
+ * equal the correctly rounded sums; IAM_ACC_FP32 accumulates in fp32 like
+ * the reference's bucketMul (bucketMul.cl:430-445).  Both are deterministic.
+ * No counterpart in the reference (its fp32 atomics are order dependent). */
+#define IAM_ACC_FP32 0
+#define IAM_ACC_FP64 1
+int iam_set_accumulation(iam_ctx* ctx, int mode);
+int iam_get_accumulation(iam_ctx* ctx, int* mode);
 /* Derive a compact copy stats3[r] = stats[r*4 + 3] (device), so the
  * selection reads 2 bytes per row instead of 8.  The file layout is unchanged. */
 int iam_stats_compact(iam_ctx* ctx, const uint16_t* stats_dev, size_t rows, int stride,
@@ -255,7 +265,8 @@ int iam_model_reset_caches(iam_model* m);
 int iam_model_set_embed_scale(iam_model* m, const float* scale_host);
 /* Device pointer and size of a named model tensor, e.g. "layer3.w1.buckets",
  * "layer0.attn_gain", "embed", "final_gain", "lm_head.stats", "kcache",
- * "vcache", "rope", "logits", "token", "pos", "hidden". */
+ * "vcache", "rope", "logits", "token", "pos", "hidden" (the residual stream
+ * after the last layer), "hidden_norm" (its final RMSNorm, the LM head input). */
 int iam_model_tensor(iam_model* m, const char* name, void** dev, size_t* bytes);
 /* The bucket-matrix descriptor of "layer{L}.{wq,wk,wv,wo,w1,w3,w2}" or "lm_head". */
 int iam_model_matrix(iam_model* m, const char* name, iam_bucket_matrix* out);

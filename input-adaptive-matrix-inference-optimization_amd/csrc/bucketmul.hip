@@ -8,13 +8,17 @@
 //               is a pure function of x[0:4096] and the probes), then selects
 //               the rows of its chunk of 256 inputs and compacts them in
 //               ascending order as {row, x[row/16]} (no global atomics, no
-//               float-encoded offsets); it also zeroes y.
+//               float-encoded offsets).
 //   k_walk      one launch: workgroup (slice p, column tile t) streams its
-//               share of the selected rows with 128-bit loads, scatter-adds
-//               x*w into per-row-slot LDS accumulators [pos][col] laid out
-//               bank-conflict-free, and flushes one fp32 atomic per output.
+//               share of the selected rows, scatter-adds x*w into lane-private
+//               LDS accumulators (no atomics) and writes one partial row per
+//               slice.
+//   k_reduce    one launch: sums the slice partials in a fixed order into y.
 // The cutoff and selection arithmetic is exact IEEE fp32 (no contraction), so
-// the cutoff bits and the selected set equal the oracle's.
+// the cutoff bits and the selected set equal the oracle's.  The walk
+// accumulates in fp32 or, by default, in fp64 (the product of an fp32 input
+// and an fp16 weight is exact in fp64), so y is the correctly rounded sum up
+// to fp64 rounding and does not depend on the order of the additions.
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
@@ -219,7 +223,7 @@ struct WalkDesc {
     const uint16_t* W;        // rows of the expert: W[row * C + col]
     const uint2* list;
     const uint32_t* counts;
-    float* part;              // [P][16*C] partial sums, one row per row slice
+    void* part;               // [P][16*C] partial sums (Acc), one row per row slice
     unsigned long long* counters;   // walk bytes, rows, matrices (block 0 adds)
     int C;
     int G;
@@ -247,11 +251,6 @@ __device__ __forceinline__ int xcd_remap(int b, int nblocks)
 template <int VEC>
 struct VecLoad;
 template <>
-struct VecLoad<8> {
-    using T = uint4;
-    __device__ static void split(const T& v, uint32_t* w) { w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w; }
-};
-template <>
 struct VecLoad<4> {
     using T = uint2;
     __device__ static void split(const T& v, uint32_t* w) { w[0] = v.x; w[1] = v.y; }
@@ -267,25 +266,46 @@ struct VecLoad<1> {
     __device__ static void split(const T& v, uint32_t* w) { w[0] = v; }
 };
 
-constexpr int kWalkThreads = 256;
-constexpr int kBatch = 256;           // list entries staged per round (bucketMul.cl:26 uses 256)
-constexpr int kUnroll = 8;           // row groups in flight per lane (a whole batch)
-
-// Lane layout: lane = q*8 + j.  q (0..7) picks one of 8 rows handled per wave
-// instruction, j (0..7) a vector of VEC columns, so a tile is 8*VEC columns
-// (64 columns = 128 bytes for VEC 8).  Accumulator copy q, entry
-// (pos, e, j) lives at q*QS + (pos*VEC + e)*8 + j with QS = 128*VEC + 8: for a
-// fixed e the 64 lanes of an instruction hit 64 distinct banks whatever the
-// positions (QS = 8 mod 64 and pos*8*VEC = 0 mod 64 for VEC 8).
-template <int VEC>
-__global__ __launch_bounds__(kWalkThreads) void k_walk(WalkArgs a)
+// x * w as the accumulator type: an fp32 product (bucketMul.cl:430-434), or
+// the exact product in fp64 (24 + 11 significant bits fit in 53).
+template <typename Acc>
+__device__ __forceinline__ Acc walk_prod(float x, uint32_t h);
+template <>
+__device__ __forceinline__ float walk_prod<float>(float x, uint32_t h) { return __fmul_rn(x, h2f(h)); }
+template <>
+__device__ __forceinline__ double walk_prod<double>(float x, uint32_t h)
 {
-    constexpr int TW = 8 * VEC;
-    constexpr int QS = 16 * VEC * 8 + 8;
-    __shared__ float acc[8 * QS];
+    return (double)x * (double)h2f(h);
+}
+
+// Walk of the selected rows.  Workgroup (row slice p, column tile t) takes
+// the slice's share of the selected-row list and the 64 columns of tile t.
+// Lane = q*NJ + j: j picks VEC consecutive columns (NJ = 64/VEC lanes cover
+// the 128-byte tile segment of one row), q picks one of NQ = VEC rows read
+// by the same instruction.  Every lane owns private accumulators for its VEC
+// columns x 16 output positions at acc[wave][(pos*VEC + e)*64 + lane]: the
+// scatter of a packed weight to its position (bucketMul.cl:430-445) is a
+// plain LDS read-add-write, with no atomics, and the 64 lanes of one access
+// always fall in 64 different banks.  Each lane adds in list order, and the
+// flush sums waves and row slots in a fixed order, so the result does not
+// depend on scheduling.  The VEC elements of one row go to distinct
+// addresses (different e), so their reads are issued together, then their
+// writes; the next row's reads follow the writes in the wave's LDS order.
+//
+// The list is the dispatch output: per chunk of 256 inputs, counts[g]
+// entries at list[g * kChunkRows].  All UNR list loads of a batch, then all
+// UNR weight loads, are unconditional (past the slice end a lane re-reads
+// the slice's last entry with x = 0) so they are in flight together.
+template <int VEC, typename Acc, int NW, int UNR>
+__global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
+{
+    constexpr int NJ = 64 / VEC, NQ = VEC, TW = 64;
+    constexpr int PER = 16 * VEC * 64;         // accumulators per wave
+    constexpr int NT = 64 * NW;
+    constexpr int STRIDE = NW * NQ;            // rows per workgroup instruction
+    __shared__ Acc acc[NW * PER];
     __shared__ uint32_t s_pre[kMaxChunks + 1];
-    __shared__ uint2 s_ent[kBatch];
-    __shared__ int s_wsum[4];
+    __shared__ uint32_t s_wsum[NW];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -299,22 +319,38 @@ __global__ __launch_bounds__(kWalkThreads) void k_walk(WalkArgs a)
     const int p = w / d.T;
     const int t = w - p * d.T;
 
-    for (int i = tid; i < 8 * QS; i += kWalkThreads) acc[i] = 0.0f;
+    Acc* my = acc + wave * PER + lane;
+#pragma unroll
+    for (int i = 0; i < 16 * VEC; i++) my[i * 64] = (Acc)0;
 
-    // prefix of the chunk counts (G <= 256: one value per thread)
-    uint32_t c = tid < d.G ? d.counts[tid] : 0u;
-    uint32_t incl = c;
+    // exclusive prefix of the chunk counts: thread tid owns chunks
+    // [tid*CPT, tid*CPT + CPT)
+    constexpr int CPT = (kMaxChunks + NT - 1) / NT;
+    uint32_t cl[CPT];
+    uint32_t mine = 0;
+#pragma unroll
+    for (int i = 0; i < CPT; i++) {
+        const int g = tid * CPT + i;
+        cl[i] = g < d.G ? d.counts[g] : 0u;
+        mine += cl[i];
+    }
+    uint32_t incl = mine;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-        uint32_t v = __shfl_up(incl, o, 64);
+        const uint32_t v = __shfl_up(incl, o, 64);
         if (lane >= o) incl += v;
     }
-    if (lane == 63) s_wsum[wave] = (int)incl;
+    if (lane == 63) s_wsum[wave] = incl;
     __syncthreads();
-    uint32_t woff = 0;
-    for (int i = 0; i < wave; i++) woff += (uint32_t)s_wsum[i];
-    if (tid < d.G) s_pre[tid + 1] = woff + incl;
-    if (tid == 0) s_pre[0] = 0;
+    uint32_t run = incl - mine;
+    for (int i = 0; i < wave; i++) run += s_wsum[i];
+#pragma unroll
+    for (int i = 0; i < CPT; i++) {
+        const int g = tid * CPT + i;
+        if (g < d.G) s_pre[g] = run;
+        run += cl[i];
+    }
+    if (tid == NT - 1) s_pre[d.G] = run;   // total (the last thread owns the last chunks)
     __syncthreads();
     const uint32_t S = s_pre[d.G];
     if (w == 0 && tid == 0) {
@@ -325,74 +361,89 @@ __global__ __launch_bounds__(kWalkThreads) void k_walk(WalkArgs a)
     const uint32_t lo = (uint32_t)(((uint64_t)S * (uint32_t)p) / (uint32_t)d.P);
     const uint32_t hi = (uint32_t)(((uint64_t)S * (uint32_t)(p + 1)) / (uint32_t)d.P);
 
-    const int q = lane >> 3;
-    const int j = lane & 7;
+    const int q = lane / NJ;
+    const int j = lane - q * NJ;
     const int col0 = t * TW + j * VEC;
-    // Lanes past the last column load column 0 and accumulate zeros, and the
-    // batch is padded with {row 0, x = 0}: every load is unconditional, so all
-    // kUnroll loads of a lane are in flight together.
+    // Lanes past the last column read column 0 and add zeros.
     const int colc = col0 < d.C ? col0 : 0;
     const float xmask = col0 < d.C ? 1.0f : 0.0f;
-    float* myacc = acc + q * QS + j;
     using LT = typename VecLoad<VEC>::T;
 
-    for (uint32_t base = lo; base < hi; base += kBatch) {
-        const int n = (hi - base) < (uint32_t)kBatch ? (int)(hi - base) : kBatch;
-        __syncthreads();
+    if (lo < hi) {
+        // chunk of the lane's current entry: s_pre[ch] <= idx < chend
+        int ch = 0;
         {
-            uint2 ent = make_uint2(0u, 0u);
-            if (tid < n) {
-                const uint32_t idx = base + (uint32_t)tid;
-                int lo_c = 0, hi_c = d.G;   // s_pre[lo_c] <= idx < s_pre[hi_c]
-                while (hi_c - lo_c > 1) {
-                    int mid = (lo_c + hi_c) >> 1;
-                    if (s_pre[mid] <= idx) lo_c = mid;
-                    else hi_c = mid;
-                }
-                ent = d.list[(size_t)lo_c * kChunkRows + (idx - s_pre[lo_c])];
+            const uint32_t first = lo;
+            int l = 0, h = d.G;
+            while (h - l > 1) {
+                const int m = (l + h) >> 1;
+                if (s_pre[m] <= first) l = m;
+                else h = m;
             }
-            s_ent[tid] = ent;
+            ch = l;
         }
-        __syncthreads();
-        const int groups = (n + 31) >> 5;        // rows are taken 32 at a time (4 waves x 8 slots)
-        for (int it = 0; it < groups; it += kUnroll) {
-            LT v[kUnroll];
-            float xv[kUnroll];
+        uint32_t chbeg = s_pre[ch], chend = s_pre[ch + 1];
+        for (uint32_t base = lo + (uint32_t)(wave * NQ); base < hi; base += (uint32_t)(STRIDE * UNR)) {
+            const uint2* ep[UNR];
+            bool ok[UNR];
 #pragma unroll
-            for (int u = 0; u < kUnroll; u++) {
-                const uint2 e = s_ent[wave * 8 + q + 32 * (it + u)];
-                xv[u] = __uint_as_float(e.y) * xmask;
-                v[u] = *reinterpret_cast<const LT*>(d.W + (size_t)e.x * d.C + colc);
+            for (int u = 0; u < UNR; u++) {
+                const uint32_t raw = base + (uint32_t)(q + u * STRIDE);
+                ok[u] = raw < hi;
+                const uint32_t idx = ok[u] ? raw : hi - 1;
+                while (idx >= chend) {
+                    ch++;
+                    chbeg = chend;
+                    chend = s_pre[ch + 1];
+                }
+                ep[u] = d.list + (size_t)ch * kChunkRows + (idx - chbeg);
             }
+            uint2 en[UNR];
 #pragma unroll
-            for (int u = 0; u < kUnroll; u++) {
+            for (int u = 0; u < UNR; u++) en[u] = *ep[u];
+            LT v[UNR];
+            float xv[UNR];
+#pragma unroll
+            for (int u = 0; u < UNR; u++) {
+                xv[u] = ok[u] ? __uint_as_float(en[u].y) * xmask : 0.0f;
+                v[u] = *reinterpret_cast<const LT*>(d.W + (size_t)en[u].x * d.C + colc);
+            }
+            // keep all UNR weight loads ahead of the accumulation
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int u = 0; u < UNR; u++) {
                 uint32_t words[(VEC + 1) / 2];
                 VecLoad<VEC>::split(v[u], words);
+                int ad[VEC];
+                Acc pr[VEC], old[VEC];
 #pragma unroll
                 for (int e = 0; e < VEC; e++) {
                     const uint32_t h = (words[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-                    const float prod = xv[u] * h2f(h);     // packed value, bucketMul.cl:430-434
-                    const int pos = (int)(h & 15u);
-                    atomicAdd(myacc + (pos * VEC + e) * 8, prod);
+                    ad[e] = ((int)(h & 15u) * VEC + e) * 64;
+                    pr[e] = walk_prod<Acc>(xv[u], h);
                 }
+#pragma unroll
+                for (int e = 0; e < VEC; e++) old[e] = my[ad[e]];
+#pragma unroll
+                for (int e = 0; e < VEC; e++) my[ad[e]] = old[e] + pr[e];
             }
         }
     }
     __syncthreads();
-    // flush this slice's partial sums for the tile's outputs: output
-    // col*16 + pos (bucketMul.cl:442-445), so the tile is one contiguous run
-    // of the slice's partial row and the stores coalesce.
-    float* prow = d.part + (size_t)p * d.C * 16;
-    for (int idx = tid; idx < TW * 16; idx += kWalkThreads) {
-        const int cl = idx >> 4;          // column within the tile
+    // flush: output col*16 + pos (bucketMul.cl:442-445) of this tile as one
+    // contiguous run of the slice's partial row
+    Acc* prow = reinterpret_cast<Acc*>(d.part) + (size_t)p * d.C * 16;
+    for (int idx = tid; idx < TW * 16; idx += NT) {
+        const int c = idx >> 4;          // column within the tile
         const int pos = idx & 15;
-        const int jj = cl / VEC, e = cl - jj * VEC;
-        const int col = t * TW + cl;
+        const int jj = c / VEC, e = c - jj * VEC;
+        const int col = t * TW + c;
         if (col >= d.C) continue;
-        const int ai = (pos * VEC + e) * 8 + jj;
-        float s = 0.0f;
+        const int ai = (pos * VEC + e) * 64 + jj;
+        Acc s = (Acc)0;
+        for (int ww = 0; ww < NW; ww++)
 #pragma unroll
-        for (int qq = 0; qq < 8; qq++) s += acc[qq * QS + ai];
+            for (int qq = 0; qq < NQ; qq++) s += acc[ww * PER + ai + qq * NJ];
         prow[(size_t)col * 16 + pos] = s;
     }
 }
@@ -401,7 +452,7 @@ __global__ __launch_bounds__(kWalkThreads) void k_walk(WalkArgs a)
 // p mod 16 then combined in group order: a fixed order, so y is the same on
 // every run (bucketIntegrate, bucketMul.cl:453-497, sums 64 fixed slices).
 struct ReduceDesc {
-    const float* part;
+    const void* part;
     float* y;
     int P;
     int m;
@@ -415,40 +466,35 @@ struct ReduceArgs {
 
 constexpr int kRedOut = 64;   // outputs per reduce block
 
+template <typename Acc>
 __global__ __launch_bounds__(256) void k_reduce(ReduceArgs a)
 {
-    __shared__ float4 red[16][kRedOut / 4];
+    __shared__ Acc red[16][kRedOut];
     const int b = (int)blockIdx.x;
     int k = 0;
     for (int i = 1; i < a.n; i++)
         if (b >= a.d[i].block_base) k = i;
     const ReduceDesc& d = a.d[k];
+    const Acc* part = reinterpret_cast<const Acc*>(d.part);
     const int o0 = (b - d.block_base) * kRedOut;
     const int tid = threadIdx.x;
     const int ol = tid & 15, pg = tid >> 4;
-    const int o = o0 + ol * 4;
-    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    const int o = o0 + ol * 4;   // m is a multiple of 16, so o..o+3 are in range together
+    Acc s[4] = {(Acc)0, (Acc)0, (Acc)0, (Acc)0};
     if (o < d.m) {
         for (int p = pg; p < d.P; p += 16) {
-            const float4 v = *reinterpret_cast<const float4*>(d.part + (size_t)p * d.m + o);
-            s.x += v.x;
-            s.y += v.y;
-            s.z += v.z;
-            s.w += v.w;
+            const Acc* r = part + (size_t)p * d.m + o;
+#pragma unroll
+            for (int i = 0; i < 4; i++) s[i] += r[i];
         }
     }
-    red[pg][ol] = s;
+#pragma unroll
+    for (int i = 0; i < 4; i++) red[pg][ol * 4 + i] = s[i];
     __syncthreads();
-    if (pg == 0 && o < d.m) {
-        float4 t = red[0][ol];
-        for (int g = 1; g < 16; g++) {
-            const float4 v = red[g][ol];
-            t.x += v.x;
-            t.y += v.y;
-            t.z += v.z;
-            t.w += v.w;
-        }
-        *reinterpret_cast<float4*>(d.y + o) = t;
+    if (tid < kRedOut && o0 + tid < d.m) {
+        Acc t = red[0][tid];
+        for (int g = 1; g < 16; g++) t += red[g][tid];
+        d.y[o0 + tid] = (float)t;
     }
 }
 
@@ -473,8 +519,8 @@ double est_rows(int rows, float effort) { return std::max(1.0, rows * est_fracti
 // Row slices per matrix for one walk launch: about kWalkTarget workgroups in
 // total, shared by the matrices in proportion to their expected bytes, with
 // at least kMinSliceRows rows per slice.  Only the performance depends on it.
-constexpr int kWalkTarget = 512;
-constexpr int kMinSliceRows = 48;
+constexpr int kWalkTarget = 1024;
+constexpr int kMinSliceRows = 64;
 
 static void plan_slices(int n, const double* bytes, const double* rows, const int* T, int* P)
 {
@@ -490,7 +536,6 @@ static void plan_slices(int n, const double* bytes, const double* rows, const in
 
 static int vec_of(int C)
 {
-    if (C % 8 == 0) return 8;
     if (C % 4 == 0) return 4;
     if (C % 2 == 0) return 2;
     return 1;
@@ -559,11 +604,27 @@ void plan_walk(int n, const MatOp* ops, float effort, int* T, int* P, int* V)
     for (int i = 0; i < n; i++) {
         const iam_bucket_matrix& M = ops[i].mat;
         V[i] = vec_of(M.bucket_cols);
-        T[i] = (M.bucket_cols + 8 * V[i] - 1) / (8 * V[i]);
+        T[i] = (M.bucket_cols + 63) / 64;   // 64-column tiles
         rows[i] = est_rows(M.expert_rows, effort);
         bytes[i] = rows[i] * M.bucket_cols;
     }
     plan_slices(n, bytes, rows, T, P);
+}
+
+// Launch shapes: fp32 accumulators with 4 columns per lane (16 KB of LDS per
+// wave), fp64 with 2 (also 16 KB per wave); two waves per workgroup and 16
+// rows in flight per lane.  Narrower tiles follow the column count.
+constexpr int kWalkWaves = 2;
+constexpr int kWalkUnroll = 16;
+
+template <typename Acc>
+static int launch_walk(Ctx* c, int vec, int blocks, const WalkArgs& args)
+{
+    const dim3 g(blocks), t(64 * kWalkWaves);
+    constexpr bool f64 = sizeof(Acc) == 8;
+    if (vec >= 4 && !f64) return launch(c, "bucket_walk", k_walk<4, Acc, kWalkWaves, kWalkUnroll>, g, t, 0, args);
+    if (vec >= 2) return launch(c, "bucket_walk", k_walk<2, Acc, kWalkWaves, kWalkUnroll>, g, t, 0, args);
+    return launch(c, "bucket_walk", k_walk<1, Acc, kWalkWaves, kWalkUnroll>, g, t, 0, args);
 }
 
 int bucketmul_walk(Ctx* c, int n, const MatOp* ops)
@@ -585,9 +646,11 @@ int bucketmul_walk(Ctx* c, int n, const MatOp* ops)
         IAM_REQUIRE(s.effort == c->slots[0].effort, "bucketmul: slots dispatched at different efforts");
     }
     plan_walk(n, ops, c->slots[0].effort, T, P, V);
-    for (int i = 0; i < n; i++) IAM_TRY(ensure_partials(c, i, (size_t)P[i] * ops[i].mat.bucket_cols * 16));
+    const size_t acc_bytes = c->acc64 ? 8 : 4;
+    for (int i = 0; i < n; i++)
+        IAM_TRY(ensure_partials(c, i, (size_t)P[i] * ops[i].mat.bucket_cols * 16 * acc_bytes));
 
-    // walk: one launch per vector width (the model's matrices all use 8)
+    // walk: one launch per load width (the model's matrices all share one)
     bool used[kMaxMulti] = {false, false, false};
     for (int done = 0; done < n;) {
         int vec = 0, blocks = 0, cnt = 0;
@@ -612,14 +675,7 @@ int bucketmul_walk(Ctx* c, int n, const MatOp* ops)
             done++;
         }
         args.n = cnt;
-        int rc = IAM_OK;
-        switch (vec) {
-            case 8: rc = launch(c, "bucket_walk", k_walk<8>, dim3(blocks), dim3(kWalkThreads), 0, args); break;
-            case 4: rc = launch(c, "bucket_walk4", k_walk<4>, dim3(blocks), dim3(kWalkThreads), 0, args); break;
-            case 2: rc = launch(c, "bucket_walk2", k_walk<2>, dim3(blocks), dim3(kWalkThreads), 0, args); break;
-            default: rc = launch(c, "bucket_walk1", k_walk<1>, dim3(blocks), dim3(kWalkThreads), 0, args); break;
-        }
-        IAM_TRY(rc);
+        IAM_TRY(c->acc64 ? launch_walk<double>(c, vec, blocks, args) : launch_walk<float>(c, vec, blocks, args));
     }
     // fixed-order sum of the slices into y
     ReduceArgs ra{};
@@ -634,7 +690,8 @@ int bucketmul_walk(Ctx* c, int n, const MatOp* ops)
         d.block_base = rblocks;
         rblocks += (d.m + kRedOut - 1) / kRedOut;
     }
-    return launch(c, "bucket_reduce", k_reduce, dim3(rblocks), dim3(256), 0, ra);
+    if (c->acc64) return launch(c, "bucket_reduce", k_reduce<double>, dim3(rblocks), dim3(256), 0, ra);
+    return launch(c, "bucket_reduce", k_reduce<float>, dim3(rblocks), dim3(256), 0, ra);
 }
 
 __global__ void k_stats_compact(const uint16_t* __restrict__ s, size_t rows, int stride, int ch,

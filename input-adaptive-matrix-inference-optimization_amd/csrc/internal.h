@@ -56,8 +56,8 @@ struct DispatchSlot {
     int expert_no = 0;
     float effort = 1.0f;
     bool valid = false;
-    float* part = nullptr;       // walk partial sums [P][m]
-    size_t part_cap = 0;         // floats
+    void* part = nullptr;        // walk partial sums [P][m] of the accumulator type
+    size_t part_cap = 0;         // bytes
 };
 
 struct KernelStat {
@@ -91,6 +91,8 @@ struct Ctx {
     // those addresses and must be re-captured when it changes
     uint64_t scratch_gen = 0;
     unsigned long long* counters = nullptr;   // device: walk bytes, rows, matrices
+    // accumulate the walk in fp64 (sums round once to fp32) instead of fp32
+    bool acc64 = true;
 };
 
 int ctx_alloc(Ctx* c, size_t bytes, void** out);
@@ -98,7 +100,7 @@ int ctx_alloc(Ctx* c, size_t bytes, void** out);
 int check_dev_range(Ctx* c, const void* p, size_t bytes, const char* what);
 int ctx_free(Ctx* c, void* p);
 int ensure_slot(Ctx* c, int slot, int chunks);
-int ensure_partials(Ctx* c, int slot, size_t floats);
+int ensure_partials(Ctx* c, int slot, size_t bytes);
 
 // Launch bookkeeping: with profiling on (and no graph capture in progress)
 // each launch is bracketed by a pair of pooled events.

@@ -58,14 +58,16 @@ __global__ void k_add(const float* __restrict__ a, const float* __restrict__ b, 
 }
 
 // ---------------------------------------------------------------- SiLU ---
-// silu32 (matrix.cl:27-32): out = x3 * x1 / (1 + exp(-x1)), x1 = gate, x3 = up
+// silu32 (matrix.cl:27-32): out = x3 * x1 / (1 + exp(-x1)), x1 = gate,
+// x3 = up, evaluated in fp64 and rounded once (the value the fp32 kernel
+// approximates)
 __global__ void k_silu_mul(const float* __restrict__ g, const float* __restrict__ u, int n,
                            float* __restrict__ out)
 {
     int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) {
-        const float x1 = g[i];
-        out[i] = u[i] * x1 / (1.0f + expf(-x1));
+        const double x1 = (double)g[i];
+        out[i] = (float)((double)u[i] * x1 / (1.0 + exp(-x1)));
     }
 }
 
@@ -121,28 +123,39 @@ __global__ void k_rope_kv(const float* __restrict__ q, const float* __restrict__
 
 // ------------------------------------------------------------ attention ---
 // Decode attention over an fp16 GQA cache, split over the context
-// ("flash-decoding"): workgroup (kv head, split) handles kAttnChunk
-// positions for the rep = n_heads/n_kv query heads that read this KV head.
-// It writes the partial max m, the partial sum l of exp(s - m) and the
-// unnormalised o; k_attn_combine merges the splits.  Scores follow
-// dotSetScore2 (aux.cl:497-540, s = q.k / sqrt(hd)); the softmax of
-// aux.cl:204-225 is exp(s)/sum exp(s), evaluated here with the running max
-// subtracted, which leaves p unchanged.
-constexpr int kAttnChunk = 256;
+// ("flash-decoding").  Workgroup (kv head, split) handles kAttnChunk
+// positions for the rep = n_heads/n_kv query heads that read this KV head
+// (repeat4x32, aux.cl:266-275, without materialising the repeat) and writes
+// the split's max m, sum l of exp(s - m) and unnormalised o; k_attn_combine
+// merges the splits.  Scores follow dotSetScore2 (aux.cl:497-540,
+// s = q.k / sqrt(hd)); the softmax of aux.cl:204-225 is exp(s)/sum exp(s),
+// evaluated with the running max subtracted, which leaves p unchanged.
+// Acc = double evaluates every dot product, exponential and sum in fp64
+// (products of fp32 and fp16 values are exact there) and rounds the output
+// once; Acc = float is the fp32 evaluation.
+constexpr int kAttnChunk = 64;
 constexpr int kAttnMaxRep = 8;
 
+template <typename Acc>
+__device__ __forceinline__ Acc acc_exp(Acc x);
+template <>
+__device__ __forceinline__ float acc_exp<float>(float x) { return expf(x); }
+template <>
+__device__ __forceinline__ double acc_exp<double>(double x) { return exp(x); }
+
+template <typename Acc>
 __global__ __launch_bounds__(256) void k_attn_partial(const float* __restrict__ q,
                                                       const uint16_t* __restrict__ kc,
                                                       const uint16_t* __restrict__ vc,
                                                       const int* __restrict__ pos_p, int n_heads,
-                                                      int n_kv, int max_ctx, float scale,
-                                                      float* __restrict__ ws, int n_split)
+                                                      int n_kv, int max_ctx, Acc scale,
+                                                      Acc* __restrict__ ws, int n_split)
 {
     constexpr int HD = 128;
-    __shared__ float sq[kAttnMaxRep * HD];
-    __shared__ float sp[kAttnMaxRep * kAttnChunk];
-    __shared__ float sred[kAttnMaxRep * 8];
-    __shared__ float so[kAttnMaxRep * HD];
+    __shared__ Acc sq[kAttnMaxRep * HD];
+    __shared__ Acc sp[kAttnMaxRep * kAttnChunk];
+    __shared__ Acc sml[kAttnMaxRep * 2];
+    __shared__ Acc so[4 * kAttnMaxRep * HD];
     const int kvh = blockIdx.x;
     const int split = blockIdx.y;
     const int tid = threadIdx.x;
@@ -152,118 +165,143 @@ __global__ __launch_bounds__(256) void k_attn_partial(const float* __restrict__ 
     if (n_tok > max_ctx) n_tok = max_ctx;
     const int t0 = split * kAttnChunk;
     const int nt = min(kAttnChunk, max(0, n_tok - t0));
-    float* wbase = ws + ((size_t)(kvh * rep) * n_split + split) * (HD + 2);
-    // workspace row for query head h = kvh*rep + r, split s: ws[(h*n_split + s)*(HD+2)]
+    // workspace row of query head h = kvh*rep + r, split s: ws[(h*n_split + s)*(HD+2)]
+    Acc* wbase = ws + ((size_t)(kvh * rep) * n_split + split) * (HD + 2);
     if (nt == 0) {
         for (int i = tid; i < rep * (HD + 2); i += 256) {
             const int r = i / (HD + 2), c = i - r * (HD + 2);
-            wbase[(size_t)r * n_split * (HD + 2) + c] = c == HD ? -INFINITY : 0.0f;
+            wbase[(size_t)r * n_split * (HD + 2) + c] = c == HD ? (Acc)-INFINITY : (Acc)0;
         }
         return;
     }
-    for (int i = tid; i < rep * HD; i += 256) {
-        const int r = i / HD, d = i - r * HD;
-        sq[i] = q[(kvh * rep + r) * HD + d];
-    }
+    for (int i = tid; i < rep * HD; i += 256) sq[i] = (Acc)q[(size_t)kvh * rep * HD + i];
     __syncthreads();
-    // scores: thread t -> position t0 + t
-    float sc[kAttnMaxRep];
+
+    // scores: thread = (position slot ps = tid/16, 8-dim chunk c = tid%16);
+    // positions t0 + ps + 16*i, i < 4, all K loads issued together
+    {
+        const int c = tid & 15, ps = tid >> 4;
+        uint4 kv4[4];
 #pragma unroll
-    for (int r = 0; r < kAttnMaxRep; r++) sc[r] = -INFINITY;
-    if (tid < nt) {
-        const uint4* kr = reinterpret_cast<const uint4*>(kc + ((size_t)(t0 + tid) * n_kv + kvh) * HD);
-        float acc[kAttnMaxRep];
-#pragma unroll
-        for (int r = 0; r < kAttnMaxRep; r++) acc[r] = 0.0f;
-#pragma unroll 4
-        for (int v8 = 0; v8 < HD / 8; v8++) {
-            const uint4 w = kr[v8];
-            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float kv = h2f((uint16_t)(ww[e >> 1] >> ((e & 1) * 16)));
-                const int d = v8 * 8 + e;
-#pragma unroll
-                for (int r = 0; r < kAttnMaxRep; r++)
-                    if (r < rep) acc[r] += sq[r * HD + d] * kv;
-            }
+        for (int i = 0; i < 4; i++) {
+            const int tt = min(t0 + ps + 16 * i, n_tok - 1);
+            kv4[i] = *reinterpret_cast<const uint4*>(kc + ((size_t)tt * n_kv + kvh) * HD + c * 8);
         }
 #pragma unroll
-        for (int r = 0; r < kAttnMaxRep; r++) sc[r] = acc[r] * scale;
-    }
-    // per-head max over the chunk
-    float mloc[kAttnMaxRep];
+        for (int i = 0; i < 4; i++) {
+            const uint32_t w[4] = {kv4[i].x, kv4[i].y, kv4[i].z, kv4[i].w};
+            Acc kf[8];
 #pragma unroll
-    for (int r = 0; r < kAttnMaxRep; r++) {
-        float m = sc[r];
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-        if (lane == 0 && r < rep) sred[r * 8 + wave] = m;
-    }
-    __syncthreads();
+            for (int e = 0; e < 8; e++) kf[e] = (Acc)h2f((uint16_t)(w[e >> 1] >> ((e & 1) * 16)));
+            for (int r = 0; r < rep; r++) {
+                Acc d = (Acc)0;
 #pragma unroll
-    for (int r = 0; r < kAttnMaxRep; r++)
-        mloc[r] = r < rep ? fmaxf(fmaxf(sred[r * 8 + 0], sred[r * 8 + 1]), fmaxf(sred[r * 8 + 2], sred[r * 8 + 3]))
-                          : 0.0f;
-    __syncthreads();
+                for (int e = 0; e < 8; e++) d = fma(sq[r * HD + c * 8 + e], kf[e], d);
+                // sum the 16 chunks of the position (16 consecutive lanes)
 #pragma unroll
-    for (int r = 0; r < kAttnMaxRep; r++) {
-        if (r >= rep) break;
-        const float p = tid < nt ? expf(sc[r] - mloc[r]) : 0.0f;
-        sp[r * kAttnChunk + tid] = p;
-        float l = p;
-        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
-        if (lane == 0) sred[r * 8 + 4 + wave] = l;
-    }
-    __syncthreads();
-    // weighted V: thread -> (dim d, half of the positions)
-    const int d = tid & (HD - 1);
-    const int hlf = tid >> 7;
-    float acc[kAttnMaxRep];
-#pragma unroll
-    for (int r = 0; r < kAttnMaxRep; r++) acc[r] = 0.0f;
-    for (int t = hlf; t < nt; t += 2) {
-        const float vv = h2f(vc[((size_t)(t0 + t) * n_kv + kvh) * HD + d]);
-#pragma unroll
-        for (int r = 0; r < kAttnMaxRep; r++)
-            if (r < rep) acc[r] += sp[r * kAttnChunk + t] * vv;
-    }
-    if (hlf == 1) {
-#pragma unroll
-        for (int r = 0; r < kAttnMaxRep; r++)
-            if (r < rep) so[r * HD + d] = acc[r];
-    }
-    __syncthreads();
-    if (hlf == 0) {
-        for (int r = 0; r < rep; r++) {
-            float* row = wbase + (size_t)r * n_split * (HD + 2);
-            row[d] = acc[r] + so[r * HD + d];
-            if (d == 0) {
-                row[HD] = mloc[r];
-                row[HD + 1] = sred[r * 8 + 4] + sred[r * 8 + 5] + sred[r * 8 + 6] + sred[r * 8 + 7];
+                for (int o = 8; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
+                const int tl = ps + 16 * i;
+                if (c == 0) sp[r * kAttnChunk + tl] = tl < nt ? d * scale : (Acc)-INFINITY;
             }
+        }
+    }
+    __syncthreads();
+    // softmax of the chunk per head: wave handles heads wave, wave+4
+    for (int r = wave; r < rep; r += 4) {
+        const Acc s = sp[r * kAttnChunk + lane];
+        Acc m = s;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = fmax(m, __shfl_xor(m, o, 64));
+        const Acc p = lane < nt ? acc_exp<Acc>(s - m) : (Acc)0;
+        Acc l = p;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+        sp[r * kAttnChunk + lane] = p;
+        if (lane == 0) {
+            sml[2 * r] = m;
+            sml[2 * r + 1] = l;
+        }
+    }
+    __syncthreads();
+    // weighted V: thread = (4-dim chunk dc = tid%32, position group g = tid/32);
+    // positions g + 8*i, i < 8, all V loads issued together
+    {
+        const int dc = tid & 31, g = tid >> 5;
+        uint2 v2[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int tt = min(t0 + g + 8 * i, n_tok - 1);
+            v2[i] = *reinterpret_cast<const uint2*>(vc + ((size_t)tt * n_kv + kvh) * HD + dc * 4);
+        }
+        Acc acc[kAttnMaxRep][4];
+#pragma unroll
+        for (int r = 0; r < kAttnMaxRep; r++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[r][e] = (Acc)0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int tl = g + 8 * i;
+            Acc vf[4];
+            vf[0] = (Acc)h2f((uint16_t)(v2[i].x & 0xffffu));
+            vf[1] = (Acc)h2f((uint16_t)(v2[i].x >> 16));
+            vf[2] = (Acc)h2f((uint16_t)(v2[i].y & 0xffffu));
+            vf[3] = (Acc)h2f((uint16_t)(v2[i].y >> 16));
+#pragma unroll
+            for (int r = 0; r < kAttnMaxRep; r++) {
+                if (r < rep) {
+                    const Acc p = sp[r * kAttnChunk + tl];   // 0 past the chunk end
+#pragma unroll
+                    for (int e = 0; e < 4; e++) acc[r][e] = fma(p, vf[e], acc[r][e]);
+                }
+            }
+        }
+        // the two position groups of a wave, then the 4 waves in order
+#pragma unroll
+        for (int r = 0; r < kAttnMaxRep; r++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[r][e] += __shfl_xor(acc[r][e], 32, 64);
+        if (lane < 32) {
+#pragma unroll
+            for (int r = 0; r < kAttnMaxRep; r++)
+                if (r < rep)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) so[(wave * kAttnMaxRep + r) * HD + dc * 4 + e] = acc[r][e];
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < rep * HD; i += 256) {
+        const int r = i / HD, d = i - r * HD;
+        const Acc o = so[(0 * kAttnMaxRep + r) * HD + d] + so[(1 * kAttnMaxRep + r) * HD + d] +
+                      so[(2 * kAttnMaxRep + r) * HD + d] + so[(3 * kAttnMaxRep + r) * HD + d];
+        Acc* row = wbase + (size_t)r * n_split * (HD + 2);
+        row[d] = o;
+        if (d == 0) {
+            row[HD] = sml[2 * r];
+            row[HD + 1] = sml[2 * r + 1];
         }
     }
 }
 
-__global__ __launch_bounds__(128) void k_attn_combine(const float* __restrict__ ws, int n_split,
+template <typename Acc>
+__global__ __launch_bounds__(128) void k_attn_combine(const Acc* __restrict__ ws, int n_split,
                                                       float* __restrict__ out)
 {
     constexpr int HD = 128;
     const int h = blockIdx.x;
     const int d = threadIdx.x;
-    const float* base = ws + (size_t)h * n_split * (HD + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < n_split; s++) M = fmaxf(M, base[(size_t)s * (HD + 2) + HD]);
-    float L = 0.0f, O = 0.0f;
+    const Acc* base = ws + (size_t)h * n_split * (HD + 2);
+    Acc M = (Acc)-INFINITY;
+    for (int s = 0; s < n_split; s++) M = fmax(M, base[(size_t)s * (HD + 2) + HD]);
+    Acc L = (Acc)0, O = (Acc)0;
     for (int s = 0; s < n_split; s++) {
-        const float* row = base + (size_t)s * (HD + 2);
-        const float m = row[HD];
-        if (m == -INFINITY) continue;
-        const float w = expf(m - M);
+        const Acc* row = base + (size_t)s * (HD + 2);
+        const Acc m = row[HD];
+        if (m == (Acc)-INFINITY) continue;
+        const Acc w = acc_exp<Acc>(m - M);
         L += row[HD + 1] * w;
         O += row[d] * w;
     }
-    out[h * HD + d] = O / L;
+    out[h * HD + d] = (float)(O / L);
 }
 
 // ---------------------------------------------------------------- embed ---
@@ -347,17 +385,25 @@ int attention(Ctx* c, const float* q, const uint16_t* kc, const uint16_t* vc, co
               int n_kv, int max_ctx, float* ws, float* out)
 {
     const int n_split = (max_ctx + kAttnChunk - 1) / kAttnChunk;
+    if (c->acc64) {
+        const double scale = 1.0 / std::sqrt(128.0);
+        IAM_TRY(launch(c, "attn_partial", k_attn_partial<double>, dim3(n_kv, n_split), dim3(256), 0, q, kc, vc,
+                       pos, n_heads, n_kv, max_ctx, scale, (double*)ws, n_split));
+        return launch(c, "attn_combine", k_attn_combine<double>, dim3(n_heads), dim3(128), 0,
+                      (const double*)ws, n_split, out);
+    }
     const float scale = 1.0f / std::sqrt(128.0f);
-    IAM_TRY(launch(c, "attn_partial", k_attn_partial, dim3(n_kv, n_split), dim3(256), 0, q, kc, vc, pos,
+    IAM_TRY(launch(c, "attn_partial", k_attn_partial<float>, dim3(n_kv, n_split), dim3(256), 0, q, kc, vc, pos,
                    n_heads, n_kv, max_ctx, scale, ws, n_split));
-    return launch(c, "attn_combine", k_attn_combine, dim3(n_heads), dim3(128), 0, (const float*)ws, n_split,
-                  out);
+    return launch(c, "attn_combine", k_attn_combine<float>, dim3(n_heads), dim3(128), 0, (const float*)ws,
+                  n_split, out);
 }
 
 size_t attention_ws_floats(int n_heads, int max_ctx)
 {
+    // room for fp64 partials: (o[128], m, l) per head and split
     const int n_split = (max_ctx + kAttnChunk - 1) / kAttnChunk;
-    return (size_t)n_heads * n_split * (128 + 2);
+    return (size_t)n_heads * n_split * (128 + 2) * 2;
 }
 
 int embed(Ctx* c, const uint16_t* table, int cols, int vocab, const int* tok, float* out)

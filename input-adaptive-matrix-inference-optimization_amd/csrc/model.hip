@@ -245,7 +245,7 @@ static int reserve(iam_model* m, float effort)
         int T[kMaxMulti], P[kMaxMulti], V[kMaxMulti];
         plan_walk(sizes[gi], ops, effort, T, P, V);
         for (int i = 0; i < sizes[gi]; i++)
-            IAM_TRY(ensure_partials(c, i, (size_t)P[i] * ops[i].mat.bucket_cols * 16));
+            IAM_TRY(ensure_partials(c, i, (size_t)P[i] * ops[i].mat.bucket_cols * 16 * (c->acc64 ? 8 : 4)));
     }
     return ensure_attn_ws(c, attention_ws_floats(C.n_heads, C.max_ctx));
 }
@@ -329,6 +329,7 @@ static bool lookup(iam_model* m, const std::string& name, TensorRef* out, const 
     else if (head == "pos") *out = {m->pos, 4};
     else if (head == "hidden") *out = {m->h, D * 4};
     else if (head == "hidden_in") *out = {m->s, D * 4};
+    else if (head == "hidden_norm") *out = {m->hn, D * 4};
     else if (head == "embed_scale") *out = {m->embed_scale, D * 4};
     else if (head == "history") *out = {m->hist, (size_t)(C.max_ctx + 1) * 4};
     else if (head.rfind("layer", 0) == 0) {

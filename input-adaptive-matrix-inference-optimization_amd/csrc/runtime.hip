@@ -84,16 +84,16 @@ int ensure_slot(Ctx* c, int slot, int chunks)
     return IAM_OK;
 }
 
-int ensure_partials(Ctx* c, int slot, size_t floats)
+int ensure_partials(Ctx* c, int slot, size_t bytes)
 {
     DispatchSlot& s = c->slots[slot];
-    if (floats <= s.part_cap) return IAM_OK;
+    if (bytes <= s.part_cap) return IAM_OK;
     if (c->capturing) return fail(IAM_E_STATE, "partial buffer growth during graph capture");
     if (s.part) IAM_TRY(ctx_free(c, s.part));
     s.part = nullptr;
     s.part_cap = 0;
-    IAM_TRY(ctx_alloc(c, floats * sizeof(float), (void**)&s.part));
-    s.part_cap = floats;
+    IAM_TRY(ctx_alloc(c, bytes, &s.part));
+    s.part_cap = bytes;
     c->scratch_gen++;
     return IAM_OK;
 }
@@ -376,6 +376,26 @@ int iam_kernel_stats_reset(iam_ctx* c)
 {
     if (!c) return fail(IAM_E_INVALID, "kernel_stats_reset: null context");
     c->stats.clear();
+    return IAM_OK;
+}
+
+int iam_set_accumulation(iam_ctx* c, int mode)
+{
+    if (!c) return fail(IAM_E_INVALID, "set_accumulation: null context");
+    IAM_REQUIRE(mode == IAM_ACC_FP32 || mode == IAM_ACC_FP64, "set_accumulation: mode must be IAM_ACC_FP32 or IAM_ACC_FP64");
+    IAM_REQUIRE(!c->capturing, "set_accumulation: not allowed during graph capture");
+    const bool f64 = mode == IAM_ACC_FP64;
+    if (f64 != c->acc64) {
+        c->acc64 = f64;
+        c->scratch_gen++;   // captured graphs hold kernels of the other mode
+    }
+    return IAM_OK;
+}
+
+int iam_get_accumulation(iam_ctx* c, int* mode)
+{
+    if (!c || !mode) return fail(IAM_E_INVALID, "get_accumulation: bad argument");
+    *mode = c->acc64 ? IAM_ACC_FP64 : IAM_ACC_FP32;
     return IAM_OK;
 }
 

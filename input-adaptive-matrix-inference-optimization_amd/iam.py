@@ -207,6 +207,15 @@ class Ctx:
                                                 C.c_size_t(n), C.byref(cnt)))
         return out[:n]
 
+    def set_accumulation(self, mode):
+        """"fp64" (default) or "fp32"."""
+        check(lib().iam_set_accumulation(self.h, {"fp32": 0, "fp64": 1}[mode]))
+
+    def get_accumulation(self):
+        m = C.c_int()
+        check(lib().iam_get_accumulation(self.h, C.byref(m)))
+        return "fp64" if m.value == 1 else "fp32"
+
     def walk_counters(self, reset=False):
         b, r, m = C.c_uint64(), C.c_uint64(), C.c_uint64()
         check(lib().iam_walk_counters(self.h, C.byref(b), C.byref(r), C.byref(m), 1 if reset else 0))
