@@ -125,12 +125,17 @@ int iam_bucketmul_multi(iam_ctx* ctx, int n, const iam_bucket_matrix* mats,
                         int expert_no, float effort);
 /* Parity outputs of the last calc_dispatch / multi call for matrix slot
  * `slot`: the cutoff (fp32, as written by findCutoffBinarySearch) and the
- * selected-row count S.  Blocking. */
+ * selected-row count S.  The selection is re-run by a separate list kernel
+ * that recomputes the cutoff on its own; the call fails with IAM_E_STATE if
+ * the two cutoffs differ.  Blocking. */
 int iam_bucketmul_dispatch_info(iam_ctx* ctx, int slot, float* cutoff, uint32_t* count);
 /* The selected rows (expert-local row ids, ascending) of slot `slot`; writes
  * min(S, cap) ids into rows_host.  Blocking. */
 int iam_bucketmul_dispatch_rows(iam_ctx* ctx, int slot, uint32_t* rows_host, size_t cap,
                                 uint32_t* count);
+/* Rows the last walk (mul / multi / full) of slot `slot` selected, counted
+ * inside the walk kernel.  Blocking.  No counterpart in the reference. */
+int iam_bucketmul_walk_count(iam_ctx* ctx, int slot, uint32_t* count);
 /* effort -> quantile exactly as bucket_mul.hpp:164 */
 int iam_effort_quantile(float effort);
 /* Device-side counters of the walk: the algorithmic weight bytes streamed
@@ -157,7 +162,8 @@ int iam_stats_compact(iam_ctx* ctx, const uint16_t* stats_dev, size_t rows, int 
 /* ------------------------------------------------------------ layer ops */
 
 /* rmsNorm32fast (aux.cl:156-196) then the fp16 gain mul16x32 (aux.cl:434-440) /
- * mulVec32by16 (aux.cl:301-306).  n must be a multiple of 256. */
+ * mulVec32by16 (aux.cl:301-306).  n must be a multiple of 1024, at most
+ * 16384; vectors 16-byte aligned, the gain 8-byte aligned. */
 int iam_rmsnorm_gain(iam_ctx* ctx, const float* in_dev, const uint16_t* gain_dev, int n,
                      float eps, float* out_dev);
 /* add32 (bucketMul.cl:517-520) into h, then rmsnorm_gain of the sum

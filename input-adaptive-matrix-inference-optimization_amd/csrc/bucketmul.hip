@@ -23,6 +23,8 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstring>
+#include <vector>
 
 #include "internal.h"
 
@@ -110,6 +112,34 @@ __device__ float block_cutoff(const float* __restrict__ x, const uint16_t* __res
     return bound;                                      // bucketMul.cl:211-213
 }
 
+// --------------------------------------------------------------- cutoff ---
+// One workgroup per matrix: the cutoff of findCutoffBinarySearch, and the
+// selected-row counter of the walk cleared (the walk adds to it).
+struct CutoffDesc {
+    const float* x;
+    const uint16_t* probes;   // already offset to the expert
+    int quantile;
+    float* cutoff;
+    uint32_t* count;
+};
+
+struct CutoffArgs {
+    CutoffDesc d[kMaxMulti];
+    int n;
+};
+
+__global__ __launch_bounds__(kCutThreads) void k_cutoff(CutoffArgs a)
+{
+    __shared__ float s_red[8];
+    __shared__ int s_cnt[8];
+    const CutoffDesc& d = a.d[blockIdx.x];
+    const float cut = block_cutoff(d.x, d.probes, d.quantile, s_red, s_cnt);
+    if (threadIdx.x == 0) {
+        d.cutoff[0] = cut;
+        d.count[0] = 0u;
+    }
+}
+
 // ------------------------------------------------------------- dispatch ---
 struct DispatchDesc {
     const float* x;
@@ -149,7 +179,7 @@ __global__ __launch_bounds__(kCutThreads) void k_dispatch(DispatchArgs a)
     const int wave = tid >> 6;
 
     const float cutoff = block_cutoff(d.x, d.probes, d.quantile, s_red, s_cnt);
-    if (g == 0 && tid == 0) d.cutoff[0] = cutoff;
+    if (g == 0 && tid == 0) d.cutoff[1] = cutoff;   // cross-checked against k_cutoff's cutoff[0]
 
     // prepareDispatch (bucketMul.cl:362-385) for the 16 rows of input i
     const int i = g * kChunkInputs + tid;
@@ -219,24 +249,6 @@ __global__ __launch_bounds__(kCutThreads) void k_dispatch(DispatchArgs a)
 }
 
 // ----------------------------------------------------------------- walk ---
-struct WalkDesc {
-    const uint16_t* W;        // rows of the expert: W[row * C + col]
-    const uint2* list;
-    const uint32_t* counts;
-    void* part;               // [P][16*C] partial sums (Acc), one row per row slice
-    unsigned long long* counters;   // walk bytes, rows, matrices (block 0 adds)
-    int C;
-    int G;
-    int P;                    // row slices
-    int T;                    // column tiles
-    int block_base;
-};
-
-struct WalkArgs {
-    WalkDesc d[kMaxMulti];
-    int n;
-};
-
 // Blocks are dealt to the 8 XCDs round robin (block b -> XCD b % 8).  Remap
 // so that consecutive work items (the column tiles of one row slice, which
 // share 128-byte lines at misaligned row starts) land on the same XCD and so
@@ -266,45 +278,79 @@ struct VecLoad<1> {
     __device__ static void split(const T& v, uint32_t* w) { w[0] = v; }
 };
 
-// x * w as the accumulator type: an fp32 product (bucketMul.cl:430-434), or
-// the exact product in fp64 (24 + 11 significant bits fit in 53).
+// acc + x * w in the accumulator type: an fp32 product added in fp32
+// (bucketMul.cl:430-434), or in fp64, where the product of an fp32 x and an
+// fp16 w is exact (24 + 11 significant bits fit in 53).
 template <typename Acc>
-__device__ __forceinline__ Acc walk_prod(float x, uint32_t h);
+__device__ __forceinline__ Acc walk_acc(Acc x, Acc w, Acc old);
 template <>
-__device__ __forceinline__ float walk_prod<float>(float x, uint32_t h) { return __fmul_rn(x, h2f(h)); }
-template <>
-__device__ __forceinline__ double walk_prod<double>(float x, uint32_t h)
+__device__ __forceinline__ float walk_acc<float>(float x, float w, float old)
 {
-    return (double)x * (double)h2f(h);
+    return __fadd_rn(old, __fmul_rn(x, w));   // bucketMul.cl:430-434: fp32 product, then the add
+}
+template <>
+__device__ __forceinline__ double walk_acc<double>(double x, double w, double old)
+{
+    return fma(x, w, old);   // the product is exact in fp64, so this is one rounded add
 }
 
-// Walk of the selected rows.  Workgroup (row slice p, column tile t) takes
-// the slice's share of the selected-row list and the 64 columns of tile t.
-// Lane = q*NJ + j: j picks VEC consecutive columns (NJ = 64/VEC lanes cover
-// the 128-byte tile segment of one row), q picks one of NQ = VEC rows read
+// Selection + walk.  Workgroup (input slice p, column tile t) owns the
+// inputs [p*IPS, (p+1)*IPS) and the 64 columns of tile t.
+//
+// Selection (prepareDispatch, bucketMul.cl:351-386): thread i takes input
+// p*IPS + i, loads its x and the stats of its 16 rows, and marks the rows
+// with 1e5 * |x * stat| >= cutoff -- the same fp32 operations as the
+// dispatch kernel, so the selected set is the same.  A block scan compacts
+// the selected rows in ascending order into LDS.
+//
+// Walk: lane = q*NJ + j: j picks VEC consecutive columns (NJ = 64/VEC lanes
+// cover the 128-byte tile segment of one row), q one of NQ = VEC rows read
 // by the same instruction.  Every lane owns private accumulators for its VEC
 // columns x 16 output positions at acc[wave][(pos*VEC + e)*64 + lane]: the
 // scatter of a packed weight to its position (bucketMul.cl:430-445) is a
 // plain LDS read-add-write, with no atomics, and the 64 lanes of one access
-// always fall in 64 different banks.  Each lane adds in list order, and the
+// fall in 64 different banks.  Each lane adds its rows in order and the
 // flush sums waves and row slots in a fixed order, so the result does not
 // depend on scheduling.  The VEC elements of one row go to distinct
 // addresses (different e), so their reads are issued together, then their
-// writes; the next row's reads follow the writes in the wave's LDS order.
-//
-// The list is the dispatch output: per chunk of 256 inputs, counts[g]
-// entries at list[g * kChunkRows].  All UNR list loads of a batch, then all
-// UNR weight loads, are unconditional (past the slice end a lane re-reads
-// the slice's last entry with x = 0) so they are in flight together.
+// writes; the next row's reads follow in the wave's LDS order.  All UNR
+// weight loads of a batch are unconditional (past the end a lane re-reads
+// the last selected row with x = 0), so they are in flight together.
+struct WalkDesc {
+    const uint16_t* W;        // rows of the expert: W[row * C + col]
+    const float* x;
+    const uint16_t* stats;    // row 0 of the expert
+    const float* cutoff;
+    uint32_t* count;          // selected rows, added by the tile-0 workgroups
+    void* part;               // [P][16*C] partial sums (Acc), one row per slice
+    unsigned long long* counters;   // walk bytes, rows, matrices
+    int stats_stride;
+    int stats_channel;
+    int rows;                 // R
+    int n_in;                 // inputs walked: min(ceil(R/16), in_size)
+    int C;
+    int IPS;                  // inputs per slice (<= threads per workgroup)
+    int P;                    // slices
+    int T;                    // column tiles
+    int block_base;
+};
+
+struct WalkArgs {
+    WalkDesc d[kMaxMulti];
+    int n;
+};
+
 template <int VEC, typename Acc, int NW, int UNR>
 __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
 {
+#pragma clang fp contract(off)
+    constexpr int NT = 64 * NW;
     constexpr int NJ = 64 / VEC, NQ = VEC, TW = 64;
     constexpr int PER = 16 * VEC * 64;         // accumulators per wave
-    constexpr int NT = 64 * NW;
     constexpr int STRIDE = NW * NQ;            // rows per workgroup instruction
     __shared__ Acc acc[NW * PER];
-    __shared__ uint32_t s_pre[kMaxChunks + 1];
+    __shared__ uint16_t s_row[NT * 16];        // selected rows, slice-local (input*16 + rank)
+    __shared__ float s_x[NT];
     __shared__ uint32_t s_wsum[NW];
 
     const int tid = threadIdx.x;
@@ -323,44 +369,80 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
 #pragma unroll
     for (int i = 0; i < 16 * VEC; i++) my[i * 64] = (Acc)0;
 
-    // exclusive prefix of the chunk counts: thread tid owns chunks
-    // [tid*CPT, tid*CPT + CPT)
-    constexpr int CPT = (kMaxChunks + NT - 1) / NT;
-    uint32_t cl[CPT];
-    uint32_t mine = 0;
+    // ---- selection of the slice's rows
+    const int i0 = p * d.IPS;
+    const int ni = min(d.IPS, d.n_in - i0);
+    const float cutoff = *d.cutoff;
+    uint32_t mask = 0;
+    float xi = 0.0f;
+    if (tid < ni) {
+        const int i = i0 + tid;
+        const int r0 = i * 16;
+        xi = d.x[i];
+        uint32_t sv[16];
+        const uint16_t* st = d.stats + (size_t)r0 * d.stats_stride;
+        const bool whole = r0 + 16 <= d.rows;
+        if (whole && d.stats_stride == 1 && (((uintptr_t)st) & 15) == 0) {
+            const uint4* p4 = reinterpret_cast<const uint4*>(st);
+            const uint4 a0 = p4[0], a1 = p4[1];
+            const uint32_t ww[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
 #pragma unroll
-    for (int i = 0; i < CPT; i++) {
-        const int g = tid * CPT + i;
-        cl[i] = g < d.G ? d.counts[g] : 0u;
-        mine += cl[i];
+            for (int kk = 0; kk < 16; kk++) sv[kk] = (ww[kk >> 1] >> ((kk & 1) * 16)) & 0xffffu;
+        } else if (whole && d.stats_stride == 4 && d.stats_channel == 3 && (((uintptr_t)st) & 15) == 0) {
+            const uint4* p4 = reinterpret_cast<const uint4*>(st);
+            uint4 q8[8];
+#pragma unroll
+            for (int k8 = 0; k8 < 8; k8++) q8[k8] = p4[k8];
+#pragma unroll
+            for (int k8 = 0; k8 < 8; k8++) {
+                sv[2 * k8] = q8[k8].y >> 16;       // row 2*k8, channel 3
+                sv[2 * k8 + 1] = q8[k8].w >> 16;   // row 2*k8+1, channel 3
+            }
+        } else {
+#pragma unroll
+            for (int kk = 0; kk < 16; kk++) {
+                const int rr = min(r0 + kk, d.rows - 1) - r0;
+                sv[kk] = st[(size_t)rr * d.stats_stride + d.stats_channel];
+            }
+        }
+#pragma unroll
+        for (int kk = 0; kk < 16; kk++) {
+            const float avg = h2f(sv[kk]);
+            const float prod = __fmul_rn(xi, avg);
+            const float imp = __fmul_rn(kScale, fabsf(prod));
+            if (imp >= cutoff && r0 + kk < d.rows) mask |= 1u << kk;   // bucketMul.cl:380
+        }
     }
-    uint32_t incl = mine;
+    const uint32_t cnt = (uint32_t)__popc(mask);
+    uint32_t incl = cnt;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
         const uint32_t v = __shfl_up(incl, o, 64);
         if (lane >= o) incl += v;
     }
     if (lane == 63) s_wsum[wave] = incl;
+    s_x[tid] = xi;
     __syncthreads();
-    uint32_t run = incl - mine;
-    for (int i = 0; i < wave; i++) run += s_wsum[i];
-#pragma unroll
-    for (int i = 0; i < CPT; i++) {
-        const int g = tid * CPT + i;
-        if (g < d.G) s_pre[g] = run;
-        run += cl[i];
+    uint32_t off = incl - cnt;
+    uint32_t n_sel = 0;
+    for (int i = 0; i < NW; i++) {
+        if (i < wave) off += s_wsum[i];
+        n_sel += s_wsum[i];
     }
-    if (tid == NT - 1) s_pre[d.G] = run;   // total (the last thread owns the last chunks)
+    while (mask) {
+        const int kk = __ffs(mask) - 1;
+        mask &= mask - 1;
+        s_row[off++] = (uint16_t)(tid * 16 + kk);
+    }
     __syncthreads();
-    const uint32_t S = s_pre[d.G];
-    if (w == 0 && tid == 0) {
-        atomicAdd(d.counters + 0, (unsigned long long)S * (unsigned long long)d.C * 2ull);
-        atomicAdd(d.counters + 1, (unsigned long long)S);
-        atomicAdd(d.counters + 2, 1ull);
+    if (t == 0 && tid == 0) {
+        atomicAdd(d.count, n_sel);
+        atomicAdd(d.counters + 0, (unsigned long long)n_sel * (unsigned long long)d.C * 2ull);
+        atomicAdd(d.counters + 1, (unsigned long long)n_sel);
+        if (p == 0) atomicAdd(d.counters + 2, 1ull);
     }
-    const uint32_t lo = (uint32_t)(((uint64_t)S * (uint32_t)p) / (uint32_t)d.P);
-    const uint32_t hi = (uint32_t)(((uint64_t)S * (uint32_t)(p + 1)) / (uint32_t)d.P);
 
+    // ---- walk of the selected rows
     const int q = lane / NJ;
     const int j = lane - q * NJ;
     const int col0 = t * TW + j * VEC;
@@ -368,84 +450,89 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     const int colc = col0 < d.C ? col0 : 0;
     const float xmask = col0 < d.C ? 1.0f : 0.0f;
     using LT = typename VecLoad<VEC>::T;
-
-    if (lo < hi) {
-        // chunk of the lane's current entry: s_pre[ch] <= idx < chend
-        int ch = 0;
-        {
-            const uint32_t first = lo;
-            int l = 0, h = d.G;
-            while (h - l > 1) {
-                const int m = (l + h) >> 1;
-                if (s_pre[m] <= first) l = m;
-                else h = m;
-            }
-            ch = l;
+    const uint16_t* wb = d.W + (size_t)i0 * 16 * d.C + colc;
+    const int ns = (int)n_sel;
+    // batch k: the wave's rows base_k + q + u*STRIDE, u < UNR; the loads of
+    // batch k+1 are issued before the accumulation of batch k
+    int rl[UNR];
+    float xl[UNR];
+    LT v[UNR];
+    auto issue = [&](int base) {
+#pragma unroll
+        for (int u = 0; u < UNR; u++) rl[u] = s_row[min(base + q + u * STRIDE, ns - 1)];
+#pragma unroll
+        for (int u = 0; u < UNR; u++) xl[u] = s_x[rl[u] >> 4];
+#pragma unroll
+        for (int u = 0; u < UNR; u++) v[u] = *reinterpret_cast<const LT*>(wb + (size_t)rl[u] * d.C);
+    };
+    const int first = wave * NQ;
+    if (first < ns) issue(first);
+    for (int base = first; base < ns; base += STRIDE * UNR) {
+        LT vc[UNR];
+        Acc xc[UNR];
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            vc[u] = v[u];
+            xc[u] = (Acc)(base + q + u * STRIDE < ns ? xl[u] * xmask : 0.0f);
         }
-        uint32_t chbeg = s_pre[ch], chend = s_pre[ch + 1];
-        for (uint32_t base = lo + (uint32_t)(wave * NQ); base < hi; base += (uint32_t)(STRIDE * UNR)) {
-            const uint2* ep[UNR];
-            bool ok[UNR];
+        if (base + STRIDE * UNR < ns) issue(base + STRIDE * UNR);
+        // keep the next batch's loads ahead of this batch's accumulation
+        asm volatile("" ::: "memory");
 #pragma unroll
-            for (int u = 0; u < UNR; u++) {
-                const uint32_t raw = base + (uint32_t)(q + u * STRIDE);
-                ok[u] = raw < hi;
-                const uint32_t idx = ok[u] ? raw : hi - 1;
-                while (idx >= chend) {
-                    ch++;
-                    chbeg = chend;
-                    chend = s_pre[ch + 1];
-                }
-                ep[u] = d.list + (size_t)ch * kChunkRows + (idx - chbeg);
+        for (int u = 0; u < UNR; u++) {
+            uint32_t words[(VEC + 1) / 2];
+            VecLoad<VEC>::split(vc[u], words);
+            int ad[VEC];
+            Acc wv[VEC], old[VEC];
+#pragma unroll
+            for (int e = 0; e < VEC; e++) {
+                const uint32_t h = (words[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+                ad[e] = ((int)(h & 15u) * VEC + e) * 64;
+                wv[e] = (Acc)h2f(h);
             }
-            uint2 en[UNR];
 #pragma unroll
-            for (int u = 0; u < UNR; u++) en[u] = *ep[u];
-            LT v[UNR];
-            float xv[UNR];
+            for (int e = 0; e < VEC; e++) old[e] = my[ad[e]];
 #pragma unroll
-            for (int u = 0; u < UNR; u++) {
-                xv[u] = ok[u] ? __uint_as_float(en[u].y) * xmask : 0.0f;
-                v[u] = *reinterpret_cast<const LT*>(d.W + (size_t)en[u].x * d.C + colc);
-            }
-            // keep all UNR weight loads ahead of the accumulation
-            asm volatile("" ::: "memory");
-#pragma unroll
-            for (int u = 0; u < UNR; u++) {
-                uint32_t words[(VEC + 1) / 2];
-                VecLoad<VEC>::split(v[u], words);
-                int ad[VEC];
-                Acc pr[VEC], old[VEC];
-#pragma unroll
-                for (int e = 0; e < VEC; e++) {
-                    const uint32_t h = (words[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-                    ad[e] = ((int)(h & 15u) * VEC + e) * 64;
-                    pr[e] = walk_prod<Acc>(xv[u], h);
-                }
-#pragma unroll
-                for (int e = 0; e < VEC; e++) old[e] = my[ad[e]];
-#pragma unroll
-                for (int e = 0; e < VEC; e++) my[ad[e]] = old[e] + pr[e];
-            }
+            for (int e = 0; e < VEC; e++) my[ad[e]] = walk_acc<Acc>(xc[u], wv[e], old[e]);
         }
     }
     __syncthreads();
-    // flush: output col*16 + pos (bucketMul.cl:442-445) of this tile as one
-    // contiguous run of the slice's partial row
-    Acc* prow = reinterpret_cast<Acc*>(d.part) + (size_t)p * d.C * 16;
-    for (int idx = tid; idx < TW * 16; idx += NT) {
-        const int c = idx >> 4;          // column within the tile
-        const int pos = idx & 15;
-        const int jj = c / VEC, e = c - jj * VEC;
-        const int col = t * TW + c;
-        if (col >= d.C) continue;
-        const int ai = (pos * VEC + e) * 64 + jj;
-        Acc s = (Acc)0;
+    // ---- flush.  Thread -> (pos, e, jj) with jj fastest, so the reads of the
+    // NW*NQ private copies are lane-contiguous; the sums go through a padded
+    // staging copy (one pad per 32 entries) into output order col*16 + pos
+    // (bucketMul.cl:442-445), written as one contiguous run of the slice's
+    // partial row.
+    constexpr int NOUT = TW * 16;
+    constexpr int OPT = NOUT / NT;             // outputs per thread
+    static_assert(NOUT % NT == 0 && NW * PER >= NOUT + NOUT / 32, "flush staging does not fit");
+    Acc sum[OPT];
+#pragma unroll
+    for (int k2 = 0; k2 < OPT; k2++) {
+        const int idx = tid + k2 * NT;
+        const int jj = idx % NJ;
+        const int pe = idx / NJ;               // pos*VEC + e
+        const int ai = pe * 64 + jj;
+        Acc s2 = (Acc)0;
         for (int ww = 0; ww < NW; ww++)
 #pragma unroll
-            for (int qq = 0; qq < NQ; qq++) s += acc[ww * PER + ai + qq * NJ];
-        prow[(size_t)col * 16 + pos] = s;
+            for (int qq = 0; qq < NQ; qq++) s2 += acc[ww * PER + ai + qq * NJ];
+        sum[k2] = s2;
     }
+    __syncthreads();
+    Acc* stage = acc;                          // NOUT + NOUT/32 entries, reused
+#pragma unroll
+    for (int k2 = 0; k2 < OPT; k2++) {
+        const int idx = tid + k2 * NT;
+        const int jj = idx % NJ;
+        const int pe = idx / NJ;
+        const int pos = pe / VEC, e = pe - pos * VEC;
+        const int o = (jj * VEC + e) * 16 + pos;
+        stage[o + (o >> 5)] = sum[k2];
+    }
+    __syncthreads();
+    Acc* prow = reinterpret_cast<Acc*>(d.part) + (size_t)p * d.C * 16 + (size_t)t * NOUT;
+    const int nout = min(NOUT, (d.C - t * TW) * 16);
+    for (int o = tid; o < nout; o += NT) prow[o] = stage[o + (o >> 5)];
 }
 
 // y[o] = sum over row slices of part[p][o], in slice order 0..P-1 grouped by
@@ -516,39 +603,63 @@ static double est_fraction(float effort)
 
 double est_rows(int rows, float effort) { return std::max(1.0, rows * est_fraction(effort)); }
 
-// Row slices per matrix for one walk launch: about kWalkTarget workgroups in
-// total, shared by the matrices in proportion to their expected bytes, with
-// at least kMinSliceRows rows per slice.  Only the performance depends on it.
-constexpr int kWalkTarget = 1024;
-constexpr int kMinSliceRows = 64;
+// Walk launch shape: NW waves per workgroup, each with 16 KB of private
+// accumulators (fp32: 4 columns per lane; fp64: 2), 16 rows in flight per
+// lane; a slice holds at most 64*NW inputs.
+// Walk launch shapes: a launch whose expected weight bytes are below
+// kWalkWideBytes uses 4 waves per workgroup and 16 rows in flight per lane
+// (more waves per slice: these launches are latency bound), a larger one 2
+// waves and 8 rows (more workgroups in flight).  Each wave holds 16 KB of
+// private accumulators (fp32: 4 columns per lane; fp64: 2); a slice holds at
+// most 64 inputs per wave.  A launch gets about one workgroup per
+// kWalkWgBytes of expected weight bytes, at least kWalkMinWgs.
+constexpr double kWalkWideBytes = 40e6;
+constexpr double kWalkWgBytes = 98304.0;
+constexpr double kWalkMinWgs = 256.0;
+constexpr double kWalkMaxWgs = 3072.0;
 
-static void plan_slices(int n, const double* bytes, const double* rows, const int* T, int* P)
+static int vec_of(int C, bool acc64)
 {
-    double tot = 0;
-    for (int i = 0; i < n; i++) tot += bytes[i];
-    for (int i = 0; i < n; i++) {
-        double wgs = tot > 0 ? kWalkTarget * bytes[i] / tot : kWalkTarget / n;
-        int p = (int)std::lround(wgs / T[i]);
-        int pmax = std::max(1, (int)(rows[i] / kMinSliceRows));
-        P[i] = std::max(1, std::min(p, std::min(pmax, 4096)));
-    }
-}
-
-static int vec_of(int C)
-{
-    if (C % 4 == 0) return 4;
+    if (C % 4 == 0 && !acc64) return 4;
     if (C % 2 == 0) return 2;
     return 1;
 }
 
+// Slices per matrix (only the performance depends on them): the launch's
+// workgroups are shared by the matrices in proportion to their bytes.
+void plan_walk(int n, const MatOp* ops, float effort, bool acc64, WalkPlan* plan)
+{
+    double bytes[kMaxMulti], tot = 0;
+    for (int i = 0; i < n; i++) {
+        const iam_bucket_matrix& M = ops[i].mat;
+        WalkPlan& pl = plan[i];
+        pl.V = vec_of(M.bucket_cols, acc64);
+        pl.T = (M.bucket_cols + 63) / 64;
+        pl.n_in = std::min((M.expert_rows + 15) / 16, ops[i].in_size);
+        bytes[i] = est_rows(pl.n_in * 16, effort) * M.bucket_cols * 2.0;
+        tot += bytes[i];
+    }
+    const int nw = tot < kWalkWideBytes ? 4 : 2;
+    const double target = std::min(kWalkMaxWgs, std::max(kWalkMinWgs, tot / kWalkWgBytes));
+    for (int i = 0; i < n; i++) {
+        WalkPlan& pl = plan[i];
+        pl.NW = nw;
+        const double wgs = tot > 0 ? target * bytes[i] / tot : target / n;
+        const int slices = std::max(1, (int)std::lround(wgs / pl.T));
+        pl.IPS = std::min(64 * nw, std::max(1, (pl.n_in + slices - 1) / slices));
+        pl.P = (pl.n_in + pl.IPS - 1) / pl.IPS;
+    }
+}
+
+// Record the selection problem of matrix op i in slot i and compute the
+// cutoffs (one workgroup per matrix).
 int bucketmul_dispatch(Ctx* c, int n, const MatOp* ops, int expert_no, float effort)
 {
     IAM_REQUIRE(n >= 1 && n <= kMaxMulti, "bucketmul: 1..3 matrices per launch");
     IAM_REQUIRE(!std::isnan(effort), "bucketmul: effort is NaN");
     IAM_REQUIRE(expert_no >= 0, "bucketmul: negative expert_no");
-    DispatchArgs args{};
+    CutoffArgs args{};
     args.n = n;
-    int blocks = 0;
     const int qv = quantile_of(effort);
     for (int i = 0; i < n; i++) {
         const iam_bucket_matrix& M = ops[i].mat;
@@ -561,8 +672,8 @@ int bucketmul_dispatch(Ctx* c, int n, const MatOp* ops, int expert_no, float eff
         const uint16_t* probes = M.probes + (size_t)expert_no * kProbes;
         IAM_REQUIRE(((uintptr_t)probes & 15) == 0, "bucketmul: probes must be 16-byte aligned");
         const int inputs = (M.expert_rows + 15) / 16;
-        const int G = (std::min(inputs, ops[i].in_size) + kChunkInputs - 1) / kChunkInputs;
-        IAM_REQUIRE(G <= kMaxChunks, "bucketmul: more than 65536 inputs per expert");
+        IAM_REQUIRE((std::min(inputs, ops[i].in_size) + kChunkInputs - 1) / kChunkInputs <= kMaxChunks,
+                    "bucketmul: more than 65536 inputs per expert");
         // every device range the kernels read or write must lie inside an
         // allocation of this context (the cutoff always reads x[0:4096])
         const size_t xn = std::max<size_t>(kProbes, std::min<size_t>((size_t)ops[i].in_size, (size_t)inputs));
@@ -570,67 +681,77 @@ int bucketmul_dispatch(Ctx* c, int n, const MatOp* ops, int expert_no, float eff
         IAM_TRY(check_dev_range(c, M.probes, (size_t)(expert_no + 1) * kProbes * 2, "bucketmul probes"));
         IAM_TRY(check_dev_range(c, M.stats, (size_t)(expert_no + 1) * M.expert_rows * M.stats_stride * 2,
                                 "bucketmul stats"));
-
-        IAM_TRY(ensure_slot(c, i, std::max(G, 1)));
+        IAM_TRY(ensure_slot(c, i));
         DispatchSlot& s = c->slots[i];
-        DispatchDesc& d = args.d[i];
-        d.x = ops[i].x;
-        d.probes = probes;
-        d.stats = M.stats + (size_t)expert_no * (size_t)M.expert_rows * M.stats_stride;
-        d.stats_stride = M.stats_stride;
-        d.stats_channel = M.stats_channel;
-        d.rows = M.expert_rows;
-        d.in_size = ops[i].in_size;
-        d.quantile = qv;
-        d.G = std::max(G, 1);
-        d.list = s.list;
-        d.counts = s.counts;
-        d.cutoff = s.cutoff;
-        d.block_base = blocks;
-        blocks += d.G;
-        s.G = d.G;
+        s.x = ops[i].x;
+        s.stats = M.stats + (size_t)expert_no * (size_t)M.expert_rows * M.stats_stride;
+        s.probes = probes;
+        s.stats_stride = M.stats_stride;
+        s.stats_channel = M.stats_channel;
         s.rows = M.expert_rows;
+        s.in_size = ops[i].in_size;
         s.bucket_cols = M.bucket_cols;
         s.expert_no = expert_no;
         s.effort = effort;
         s.valid = true;
+        CutoffDesc& d = args.d[i];
+        d.x = ops[i].x;
+        d.probes = probes;
+        d.quantile = qv;
+        d.cutoff = s.cutoff;
+        d.count = s.count;
     }
-    return launch(c, "bucket_dispatch", k_dispatch, dim3(blocks), dim3(kCutThreads), 0, args);
+    return launch(c, "bucket_cutoff", k_cutoff, dim3(n), dim3(kCutThreads), 0, args);
 }
 
-void plan_walk(int n, const MatOp* ops, float effort, int* T, int* P, int* V)
+// The selected-row list of slot i (k_dispatch), for the parity queries.
+static int bucketmul_list(Ctx* c, int i)
 {
-    double bytes[kMaxMulti], rows[kMaxMulti];
-    for (int i = 0; i < n; i++) {
-        const iam_bucket_matrix& M = ops[i].mat;
-        V[i] = vec_of(M.bucket_cols);
-        T[i] = (M.bucket_cols + 63) / 64;   // 64-column tiles
-        rows[i] = est_rows(M.expert_rows, effort);
-        bytes[i] = rows[i] * M.bucket_cols;
-    }
-    plan_slices(n, bytes, rows, T, P);
+    DispatchSlot& s = c->slots[i];
+    const int inputs = (s.rows + 15) / 16;
+    const int G = std::max(1, (std::min(inputs, s.in_size) + kChunkInputs - 1) / kChunkInputs);
+    IAM_TRY(ensure_list(c, i, G));
+    DispatchArgs args{};
+    args.n = 1;
+    DispatchDesc& d = args.d[0];
+    d.x = s.x;
+    d.probes = s.probes;
+    d.stats = s.stats;
+    d.stats_stride = s.stats_stride;
+    d.stats_channel = s.stats_channel;
+    d.rows = s.rows;
+    d.in_size = s.in_size;
+    d.quantile = quantile_of(s.effort);
+    d.G = G;
+    d.list = s.list;
+    d.counts = s.counts;
+    d.cutoff = s.cutoff;
+    d.block_base = 0;
+    s.G = G;
+    return launch(c, "bucket_list", k_dispatch, dim3(G), dim3(kCutThreads), 0, args);
 }
 
-// Launch shapes: fp32 accumulators with 4 columns per lane (16 KB of LDS per
-// wave), fp64 with 2 (also 16 KB per wave); two waves per workgroup and 16
-// rows in flight per lane.  Narrower tiles follow the column count.
-constexpr int kWalkWaves = 2;
-constexpr int kWalkUnroll = 16;
+template <typename Acc, int NW, int UNR>
+static int launch_walk_shape(Ctx* c, int vec, int blocks, const WalkArgs& args)
+{
+    const dim3 g(blocks), t(64 * NW);
+    if constexpr (sizeof(Acc) == 4) {
+        if (vec >= 4) return launch(c, "bucket_walk", k_walk<4, Acc, NW, UNR>, g, t, 0, args);
+    }
+    if (vec >= 2) return launch(c, "bucket_walk", k_walk<2, Acc, NW, UNR>, g, t, 0, args);
+    return launch(c, "bucket_walk", k_walk<1, Acc, NW, UNR>, g, t, 0, args);
+}
 
 template <typename Acc>
-static int launch_walk(Ctx* c, int vec, int blocks, const WalkArgs& args)
+static int launch_walk(Ctx* c, int nw, int vec, int blocks, const WalkArgs& args)
 {
-    const dim3 g(blocks), t(64 * kWalkWaves);
-    constexpr bool f64 = sizeof(Acc) == 8;
-    if (vec >= 4 && !f64) return launch(c, "bucket_walk", k_walk<4, Acc, kWalkWaves, kWalkUnroll>, g, t, 0, args);
-    if (vec >= 2) return launch(c, "bucket_walk", k_walk<2, Acc, kWalkWaves, kWalkUnroll>, g, t, 0, args);
-    return launch(c, "bucket_walk", k_walk<1, Acc, kWalkWaves, kWalkUnroll>, g, t, 0, args);
+    if (nw == 4) return launch_walk_shape<Acc, 4, 16>(c, vec, blocks, args);
+    return launch_walk_shape<Acc, 2, 8>(c, vec, blocks, args);
 }
 
 int bucketmul_walk(Ctx* c, int n, const MatOp* ops)
 {
     IAM_REQUIRE(n >= 1 && n <= kMaxMulti, "bucketmul: 1..3 matrices per launch");
-    int T[kMaxMulti], P[kMaxMulti], V[kMaxMulti];
     for (int i = 0; i < n; i++) {
         const iam_bucket_matrix& M = ops[i].mat;
         const DispatchSlot& s = c->slots[i];
@@ -645,10 +766,18 @@ int bucketmul_walk(Ctx* c, int n, const MatOp* ops)
         IAM_TRY(check_dev_range(c, ops[i].y, (size_t)M.bucket_cols * 16 * sizeof(float), "bucketmul y"));
         IAM_REQUIRE(s.effort == c->slots[0].effort, "bucketmul: slots dispatched at different efforts");
     }
-    plan_walk(n, ops, c->slots[0].effort, T, P, V);
+    // the walk reads x and in_size from the slots (the dispatch's inputs)
+    MatOp wops[kMaxMulti];
+    for (int i = 0; i < n; i++) {
+        wops[i] = ops[i];
+        wops[i].x = c->slots[i].x;
+        wops[i].in_size = c->slots[i].in_size;
+    }
+    WalkPlan plan[kMaxMulti];
+    plan_walk(n, wops, c->slots[0].effort, c->acc64, plan);
     const size_t acc_bytes = c->acc64 ? 8 : 4;
     for (int i = 0; i < n; i++)
-        IAM_TRY(ensure_partials(c, i, (size_t)P[i] * ops[i].mat.bucket_cols * 16 * acc_bytes));
+        IAM_TRY(ensure_partials(c, i, (size_t)plan[i].P * ops[i].mat.bucket_cols * 16 * acc_bytes));
 
     // walk: one launch per load width (the model's matrices all share one)
     bool used[kMaxMulti] = {false, false, false};
@@ -656,26 +785,33 @@ int bucketmul_walk(Ctx* c, int n, const MatOp* ops)
         int vec = 0, blocks = 0, cnt = 0;
         WalkArgs args{};
         for (int i = 0; i < n; i++) {
-            if (used[i] || (vec != 0 && V[i] != vec)) continue;
-            vec = V[i];
+            if (used[i] || (vec != 0 && plan[i].V != vec)) continue;
+            vec = plan[i].V;
             const DispatchSlot& s = c->slots[i];
             WalkDesc& d = args.d[cnt++];
             d.W = ops[i].mat.buckets + (size_t)s.expert_no * (size_t)ops[i].mat.expert_rows * ops[i].mat.bucket_cols;
-            d.list = s.list;
-            d.counts = s.counts;
+            d.x = s.x;
+            d.stats = s.stats;
+            d.cutoff = s.cutoff;
+            d.count = s.count;
             d.part = s.part;
             d.counters = c->counters;
+            d.stats_stride = s.stats_stride;
+            d.stats_channel = s.stats_channel;
+            d.rows = s.rows;
+            d.n_in = plan[i].n_in;
             d.C = ops[i].mat.bucket_cols;
-            d.G = s.G;
-            d.P = P[i];
-            d.T = T[i];
+            d.IPS = plan[i].IPS;
+            d.P = plan[i].P;
+            d.T = plan[i].T;
             d.block_base = blocks;
-            blocks += P[i] * T[i];
+            blocks += plan[i].P * plan[i].T;
             used[i] = true;
             done++;
         }
         args.n = cnt;
-        IAM_TRY(c->acc64 ? launch_walk<double>(c, vec, blocks, args) : launch_walk<float>(c, vec, blocks, args));
+        const int nw = plan[0].NW;
+        IAM_TRY(c->acc64 ? launch_walk<double>(c, nw, vec, blocks, args) : launch_walk<float>(c, nw, vec, blocks, args));
     }
     // fixed-order sum of the slices into y
     ReduceArgs ra{};
@@ -685,7 +821,7 @@ int bucketmul_walk(Ctx* c, int n, const MatOp* ops)
         ReduceDesc& d = ra.d[i];
         d.part = c->slots[i].part;
         d.y = ops[i].y;
-        d.P = P[i];
+        d.P = plan[i].P;
         d.m = ops[i].mat.bucket_cols * 16;
         d.block_base = rblocks;
         rblocks += (d.m + kRedOut - 1) / kRedOut;
@@ -778,45 +914,65 @@ int iam_bucketmul_multi(iam_ctx* c, int n, const iam_bucket_matrix* mats, const 
     return bucketmul_walk(c, n, ops);
 }
 
-int iam_bucketmul_dispatch_info(iam_ctx* c, int slot, float* cutoff, uint32_t* count)
+// The cutoff comes from k_cutoff; the selection is re-run by the list kernel
+// (which recomputes the cutoff on its own; the two must agree bit for bit).
+static int dispatch_query(Ctx* c, int slot, float* cutoff, std::vector<uint32_t>* rows, uint32_t* count)
 {
-    if (!c || slot < 0 || slot >= kMaxMulti) return fail(IAM_E_INVALID, "dispatch_info: bad argument");
-    const DispatchSlot& s = c->slots[slot];
-    if (!s.valid) return fail(IAM_E_STATE, "dispatch_info: no dispatch in this slot");
+    if (slot < 0 || slot >= kMaxMulti) return fail(IAM_E_INVALID, "dispatch query: bad slot");
+    DispatchSlot& s = c->slots[slot];
+    if (!s.valid) return fail(IAM_E_STATE, "dispatch query: no dispatch in this slot");
+    IAM_REQUIRE(!c->capturing, "dispatch query: not allowed during graph capture");
+    IAM_TRY(bucketmul_list(c, slot));
     IAM_CHECK_HIP(hipStreamSynchronize(c->stream));
-    float cut = 0;
+    float cut[2] = {0, 0};
     std::vector<uint32_t> counts(s.G);
-    IAM_CHECK_HIP(hipMemcpy(&cut, s.cutoff, sizeof(float), hipMemcpyDeviceToHost));
+    IAM_CHECK_HIP(hipMemcpy(cut, s.cutoff, sizeof(cut), hipMemcpyDeviceToHost));
     IAM_CHECK_HIP(hipMemcpy(counts.data(), s.counts, sizeof(uint32_t) * s.G, hipMemcpyDeviceToHost));
+    uint32_t b0, b1;
+    std::memcpy(&b0, &cut[0], 4);
+    std::memcpy(&b1, &cut[1], 4);
+    if (b0 != b1) return fail(IAM_E_STATE, "dispatch query: cutoff kernels disagree");
     uint64_t S = 0;
-    for (auto v : counts) S += v;
-    if (cutoff) *cutoff = cut;
+    std::vector<uint2> buf;
+    for (int g = 0; g < s.G; g++) {
+        if (counts[g] > (uint32_t)kChunkRows) return fail(IAM_E_STATE, "dispatch query: corrupt count");
+        if (rows && counts[g]) {
+            buf.resize(counts[g]);
+            IAM_CHECK_HIP(hipMemcpy(buf.data(), s.list + (size_t)g * kChunkRows, sizeof(uint2) * counts[g],
+                                    hipMemcpyDeviceToHost));
+            for (uint32_t i = 0; i < counts[g]; i++) rows->push_back(buf[i].x);
+        }
+        S += counts[g];
+    }
+    if (cutoff) *cutoff = cut[0];
     if (count) *count = (uint32_t)S;
     return IAM_OK;
 }
 
+int iam_bucketmul_dispatch_info(iam_ctx* c, int slot, float* cutoff, uint32_t* count)
+{
+    if (!c) return fail(IAM_E_INVALID, "dispatch_info: null context");
+    return dispatch_query(c, slot, cutoff, nullptr, count);
+}
+
 int iam_bucketmul_dispatch_rows(iam_ctx* c, int slot, uint32_t* rows, size_t cap, uint32_t* count)
 {
-    if (!c || slot < 0 || slot >= kMaxMulti) return fail(IAM_E_INVALID, "dispatch_rows: bad argument");
+    if (!c) return fail(IAM_E_INVALID, "dispatch_rows: null context");
+    std::vector<uint32_t> v;
+    uint32_t S = 0;
+    IAM_TRY(dispatch_query(c, slot, nullptr, &v, &S));
+    for (size_t i = 0; i < v.size() && i < cap && rows; i++) rows[i] = v[i];
+    if (count) *count = S;
+    return IAM_OK;
+}
+
+int iam_bucketmul_walk_count(iam_ctx* c, int slot, uint32_t* count)
+{
+    if (!c || !count || slot < 0 || slot >= kMaxMulti) return fail(IAM_E_INVALID, "walk_count: bad argument");
     const DispatchSlot& s = c->slots[slot];
-    if (!s.valid) return fail(IAM_E_STATE, "dispatch_rows: no dispatch in this slot");
+    if (!s.valid) return fail(IAM_E_STATE, "walk_count: no dispatch in this slot");
     IAM_CHECK_HIP(hipStreamSynchronize(c->stream));
-    std::vector<uint32_t> counts(s.G);
-    IAM_CHECK_HIP(hipMemcpy(counts.data(), s.counts, sizeof(uint32_t) * s.G, hipMemcpyDeviceToHost));
-    size_t out = 0;
-    std::vector<uint2> buf;
-    for (int g = 0; g < s.G; g++) {
-        if (counts[g] > (uint32_t)kChunkRows) return fail(IAM_E_STATE, "dispatch_rows: corrupt count");
-        buf.resize(counts[g]);
-        if (counts[g])
-            IAM_CHECK_HIP(hipMemcpy(buf.data(), s.list + (size_t)g * kChunkRows,
-                                    sizeof(uint2) * counts[g], hipMemcpyDeviceToHost));
-        for (uint32_t i = 0; i < counts[g]; i++) {
-            if (rows && out < cap) rows[out] = buf[i].x;
-            out++;
-        }
-    }
-    if (count) *count = (uint32_t)out;
+    IAM_CHECK_HIP(hipMemcpy(count, s.count, sizeof(uint32_t), hipMemcpyDeviceToHost));
     return IAM_OK;
 }
 

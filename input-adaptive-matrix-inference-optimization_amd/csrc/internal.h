@@ -43,19 +43,29 @@ constexpr int kMaxChunks = 256;             // in_dim up to 65536 per expert
 constexpr int kMaxMulti = 3;                // matrices per fused launch
 
 // ------------------------------------------------------- dispatch state ---
-// Selected rows of one matrix: per chunk of 4096 rows, the selected rows in
-// ascending order as {row id, bits of x[row/16]}, plus the chunk counts.
+// One matrix of the last cutoff launch: the selection problem (recorded by
+// bucketmul_dispatch, re-evaluated by the walk), the device cutoff and the
+// walk's selected-row counter, and the walk partials.  The selected-row
+// list (per chunk of 4096 rows, ascending {row id, bits of x[row/16]}) is
+// only built for the blocking parity queries.
 struct DispatchSlot {
-    uint2* list = nullptr;       // [G][kChunkRows]
-    uint32_t* counts = nullptr;  // [kMaxChunks]
-    float* cutoff = nullptr;     // [1]
-    size_t cap_chunks = 0;
-    int G = 0;                   // chunks in the last dispatch
+    const float* x = nullptr;
+    const uint16_t* stats = nullptr;   // row 0 of the expert
+    const uint16_t* probes = nullptr;  // probes of the expert
+    int stats_stride = 4;
+    int stats_channel = 3;
     int rows = 0;                // expert rows R
+    int in_size = 0;
     int bucket_cols = 0;
     int expert_no = 0;
     float effort = 1.0f;
     bool valid = false;
+    float* cutoff = nullptr;     // device [2]: k_cutoff's value, the list kernel's value
+    uint32_t* count = nullptr;   // device [1]: rows selected by the last walk
+    uint2* list = nullptr;       // [G][kChunkRows]
+    uint32_t* counts = nullptr;  // [kMaxChunks]
+    size_t cap_chunks = 0;
+    int G = 0;                   // chunks of the last list
     void* part = nullptr;        // walk partial sums [P][m] of the accumulator type
     size_t part_cap = 0;         // bytes
 };
@@ -99,7 +109,8 @@ int ctx_alloc(Ctx* c, size_t bytes, void** out);
 // IAM_OK if [p, p+bytes) lies inside one allocation of this context
 int check_dev_range(Ctx* c, const void* p, size_t bytes, const char* what);
 int ctx_free(Ctx* c, void* p);
-int ensure_slot(Ctx* c, int slot, int chunks);
+int ensure_slot(Ctx* c, int slot);
+int ensure_list(Ctx* c, int slot, int chunks);
 int ensure_partials(Ctx* c, int slot, size_t bytes);
 
 // Launch bookkeeping: with profiling on (and no graph capture in progress)
@@ -134,13 +145,22 @@ struct MatOp {
     int in_size;
     float* y;        // may be null for dispatch-only
 };
-// cutoff + selection for n matrices into slots 0..n-1
+// record the selection problems of n matrices in slots 0..n-1 and compute
+// their cutoffs
 int bucketmul_dispatch(Ctx* c, int n, const MatOp* ops, int expert_no, float effort);
-// walk of slots 0..n-1 into per-slice partial sums, then the fixed-order
-// reduction into each y (overwritten)
+// selection + walk of slots 0..n-1 into per-slice partial sums, then the
+// fixed-order reduction into each y (overwritten)
 int bucketmul_walk(Ctx* c, int n, const MatOp* ops);
-// grid plan of one walk launch: column tiles T, row slices P and load width V
-void plan_walk(int n, const MatOp* ops, float effort, int* T, int* P, int* V);
+// grid plan of one matrix in a walk launch
+struct WalkPlan {
+    int NW;     // waves per workgroup (the same for every matrix of a launch)
+    int V;      // columns per lane load
+    int T;      // 64-column tiles
+    int n_in;   // inputs walked
+    int IPS;    // inputs per slice
+    int P;      // slices
+};
+void plan_walk(int n, const MatOp* ops, float effort, bool acc64, WalkPlan* plan);
 int ensure_attn_ws(Ctx* c, size_t floats);
 
 int quantile_of(float effort);

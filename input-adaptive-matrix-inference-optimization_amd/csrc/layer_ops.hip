@@ -14,27 +14,54 @@ __device__ __forceinline__ float h2f(uint16_t b) { return __half2float(__ushort_
 
 // ------------------------------------------------------------- RMSNorm ---
 // rmsNorm32fast (aux.cl:156-196): 256 threads, n/256 consecutive squares per
-// thread, a 256-way tree, scale = 1/sqrt(sum/n + eps) (rounded from double);
-// then the fp16 gain (mul16x32, aux.cl:434-440).  With `delta` the residual
-// add32 (bucketMul.cl:517-520) is applied to h first and written back.
+// thread summed in order, a 256-way tree, scale = 1/sqrt(sum/n + eps)
+// (rounded from double); then the fp16 gain (mul16x32, aux.cl:434-440).
+// With `delta` the residual add32 (bucketMul.cl:517-520) is applied to h
+// first and written back.  Each thread's values, deltas and gains are loaded
+// with 16-byte loads issued together (n/256 must be a multiple of 4 and at
+// most kNormMaxPer) and kept in registers for the second pass.
+constexpr int kNormMaxPer = 64;
+
+template <int PER>
 __global__ __launch_bounds__(256) void k_rmsnorm(float* __restrict__ h, const float* __restrict__ delta,
-                                                 const uint16_t* __restrict__ gain, int n, float eps,
+                                                 const uint16_t* __restrict__ gain, float eps,
                                                  float* __restrict__ out)
 {
 #pragma clang fp contract(off)
     __shared__ float part[256];
     const int tid = threadIdx.x;
-    const int per = n / 256;
-    const int b0 = tid * per;
-    float s = 0.0f;
-    for (int i = b0; i < b0 + per; i++) {
-        float v = h[i];
-        if (delta) {
-            v = __fadd_rn(v, delta[i]);
-            h[i] = v;
-        }
-        s = __fadd_rn(s, __fmul_rn(v, v));
+    constexpr int n = PER * 256;
+    const int b0 = tid * PER;
+    float v[PER];
+    uint2 g4[PER / 4];
+#pragma unroll
+    for (int k = 0; k < PER / 4; k++) {
+        const float4 a = *reinterpret_cast<const float4*>(h + b0 + 4 * k);
+        v[4 * k] = a.x;
+        v[4 * k + 1] = a.y;
+        v[4 * k + 2] = a.z;
+        v[4 * k + 3] = a.w;
+        g4[k] = *reinterpret_cast<const uint2*>(gain + b0 + 4 * k);
     }
+    if (delta) {
+        float dv[PER];
+#pragma unroll
+        for (int k = 0; k < PER / 4; k++) {
+            const float4 a = *reinterpret_cast<const float4*>(delta + b0 + 4 * k);
+            dv[4 * k] = a.x;
+            dv[4 * k + 1] = a.y;
+            dv[4 * k + 2] = a.z;
+            dv[4 * k + 3] = a.w;
+        }
+#pragma unroll
+        for (int k = 0; k < PER; k++) v[k] = __fadd_rn(v[k], dv[k]);
+#pragma unroll
+        for (int k = 0; k < PER / 4; k++)
+            *reinterpret_cast<float4*>(h + b0 + 4 * k) = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < PER; k++) s = __fadd_rn(s, __fmul_rn(v[k], v[k]));
     part[tid] = s;
     __syncthreads();
     for (int st = 128; st > 0; st >>= 1) {
@@ -43,9 +70,14 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float* __restrict__ h, const fl
     }
     const float mean = __fdiv_rn(part[0], (float)n);
     const float scale = (float)(1.0 / sqrt((double)__fadd_rn(mean, eps)));
-    for (int i = b0; i < b0 + per; i++) {
-        const float v = __fmul_rn(h[i], scale);
-        out[i] = __fmul_rn(h2f(gain[i]), v);
+#pragma unroll
+    for (int k = 0; k < PER / 4; k++) {
+        float o[4];
+        const uint32_t gw[2] = {g4[k].x, g4[k].y};
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            o[e] = __fmul_rn(h2f((uint16_t)(gw[e >> 1] >> ((e & 1) * 16))), __fmul_rn(v[4 * k + e], scale));
+        *reinterpret_cast<float4*>(out + b0 + 4 * k) = make_float4(o[0], o[1], o[2], o[3]);
     }
 }
 
@@ -135,6 +167,7 @@ __global__ void k_rope_kv(const float* __restrict__ q, const float* __restrict__
 // once; Acc = float is the fp32 evaluation.
 constexpr int kAttnChunk = 64;
 constexpr int kAttnMaxRep = 8;
+constexpr int kMaxAttnSplits = 128;   // max_ctx up to 8192
 
 template <typename Acc>
 __device__ __forceinline__ Acc acc_exp(Acc x);
@@ -282,24 +315,50 @@ __global__ __launch_bounds__(256) void k_attn_partial(const float* __restrict__ 
     }
 }
 
+// Merge of the splits of one query head: only the splits that hold
+// positions (ceil(n_tok / kAttnChunk)) are read; their weights
+// exp(m_s - M) are computed once, then every dimension sums its split
+// values with the loads of 8 splits in flight.
 template <typename Acc>
-__global__ __launch_bounds__(128) void k_attn_combine(const Acc* __restrict__ ws, int n_split,
-                                                      float* __restrict__ out)
+__global__ __launch_bounds__(128) void k_attn_combine(const Acc* __restrict__ ws, const int* __restrict__ pos_p,
+                                                      int max_ctx, int n_split, float* __restrict__ out)
 {
     constexpr int HD = 128;
+    __shared__ Acc sw[kMaxAttnSplits];
+    __shared__ Acc sred[2];
     const int h = blockIdx.x;
     const int d = threadIdx.x;
+    int n_tok = *pos_p + 1;
+    if (n_tok > max_ctx) n_tok = max_ctx;
+    if (n_tok < 1) n_tok = 1;
+    const int na = min(n_split, (n_tok + kAttnChunk - 1) / kAttnChunk);
     const Acc* base = ws + (size_t)h * n_split * (HD + 2);
-    Acc M = (Acc)-INFINITY;
-    for (int s = 0; s < n_split; s++) M = fmax(M, base[(size_t)s * (HD + 2) + HD]);
+    // split maxima: thread s < na holds split s (na <= 128 is checked on the host)
+    const Acc ms = d < na ? base[(size_t)d * (HD + 2) + HD] : (Acc)-INFINITY;
+    Acc M = ms;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) M = fmax(M, __shfl_xor(M, o, 64));
+    if ((d & 63) == 0) sred[d >> 6] = M;
+    __syncthreads();
+    M = fmax(sred[0], sred[1]);
+    if (d < na) sw[d] = acc_exp<Acc>(ms - M);
+    __syncthreads();
     Acc L = (Acc)0, O = (Acc)0;
-    for (int s = 0; s < n_split; s++) {
-        const Acc* row = base + (size_t)s * (HD + 2);
-        const Acc m = row[HD];
-        if (m == (Acc)-INFINITY) continue;
-        const Acc w = acc_exp<Acc>(m - M);
-        L += row[HD + 1] * w;
-        O += row[d] * w;
+    for (int s0 = 0; s0 < na; s0 += 8) {
+        Acc ov[8], lv[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int s = min(s0 + i, na - 1);
+            ov[i] = base[(size_t)s * (HD + 2) + d];
+            lv[i] = base[(size_t)s * (HD + 2) + HD + 1];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            if (s0 + i < na) {
+                L += lv[i] * sw[s0 + i];
+                O += ov[i] * sw[s0 + i];
+            }
+        }
     }
     out[h * HD + d] = (float)(O / L);
 }
@@ -357,10 +416,38 @@ __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ v, in
 
 // ------------------------------------------------------------------ host ---
 
+template <int PER>
+static int rmsnorm_per(Ctx* c, float* h, const float* delta, const uint16_t* gain, float eps, float* out)
+{
+    return launch(c, delta ? "add_rmsnorm" : "rmsnorm", k_rmsnorm<PER>, dim3(1), dim3(256), 0, h, delta, gain, eps,
+                  out);
+}
+
 int rmsnorm(Ctx* c, float* h, const float* delta, const uint16_t* gain, int n, float eps, float* out)
 {
-    return launch(c, delta ? "add_rmsnorm" : "rmsnorm", k_rmsnorm, dim3(1), dim3(256), 0, h, delta, gain,
-                  n, eps, out);
+    IAM_REQUIRE(n % 1024 == 0 && n >= 1024 && n <= 256 * kNormMaxPer,
+                "rmsnorm: n must be a multiple of 1024 in [1024, 16384]");
+    IAM_REQUIRE(((uintptr_t)h & 15) == 0 && ((uintptr_t)out & 15) == 0 && ((uintptr_t)delta & 15) == 0 &&
+                    ((uintptr_t)gain & 7) == 0,
+                "rmsnorm: vectors must be 16-byte aligned and the gain 8-byte aligned");
+    switch (n / 256) {
+        case 4: return rmsnorm_per<4>(c, h, delta, gain, eps, out);
+        case 8: return rmsnorm_per<8>(c, h, delta, gain, eps, out);
+        case 12: return rmsnorm_per<12>(c, h, delta, gain, eps, out);
+        case 16: return rmsnorm_per<16>(c, h, delta, gain, eps, out);
+        case 20: return rmsnorm_per<20>(c, h, delta, gain, eps, out);
+        case 24: return rmsnorm_per<24>(c, h, delta, gain, eps, out);
+        case 28: return rmsnorm_per<28>(c, h, delta, gain, eps, out);
+        case 32: return rmsnorm_per<32>(c, h, delta, gain, eps, out);
+        case 36: return rmsnorm_per<36>(c, h, delta, gain, eps, out);
+        case 40: return rmsnorm_per<40>(c, h, delta, gain, eps, out);
+        case 44: return rmsnorm_per<44>(c, h, delta, gain, eps, out);
+        case 48: return rmsnorm_per<48>(c, h, delta, gain, eps, out);
+        case 52: return rmsnorm_per<52>(c, h, delta, gain, eps, out);
+        case 56: return rmsnorm_per<56>(c, h, delta, gain, eps, out);
+        case 60: return rmsnorm_per<60>(c, h, delta, gain, eps, out);
+        default: return rmsnorm_per<64>(c, h, delta, gain, eps, out);
+    }
 }
 
 int add(Ctx* c, const float* a, const float* b, int n, float* out)
@@ -385,18 +472,19 @@ int attention(Ctx* c, const float* q, const uint16_t* kc, const uint16_t* vc, co
               int n_kv, int max_ctx, float* ws, float* out)
 {
     const int n_split = (max_ctx + kAttnChunk - 1) / kAttnChunk;
+    IAM_REQUIRE(n_split <= kMaxAttnSplits, "attention: max_ctx above 8192");
     if (c->acc64) {
         const double scale = 1.0 / std::sqrt(128.0);
         IAM_TRY(launch(c, "attn_partial", k_attn_partial<double>, dim3(n_kv, n_split), dim3(256), 0, q, kc, vc,
                        pos, n_heads, n_kv, max_ctx, scale, (double*)ws, n_split));
         return launch(c, "attn_combine", k_attn_combine<double>, dim3(n_heads), dim3(128), 0,
-                      (const double*)ws, n_split, out);
+                      (const double*)ws, pos, max_ctx, n_split, out);
     }
     const float scale = 1.0f / std::sqrt(128.0f);
     IAM_TRY(launch(c, "attn_partial", k_attn_partial<float>, dim3(n_kv, n_split), dim3(256), 0, q, kc, vc, pos,
                    n_heads, n_kv, max_ctx, scale, ws, n_split));
-    return launch(c, "attn_combine", k_attn_combine<float>, dim3(n_heads), dim3(128), 0, (const float*)ws,
-                  n_split, out);
+    return launch(c, "attn_combine", k_attn_combine<float>, dim3(n_heads), dim3(128), 0, (const float*)ws, pos,
+                  max_ctx, n_split, out);
 }
 
 size_t attention_ws_floats(int n_heads, int max_ctx)
@@ -426,7 +514,7 @@ static int attn_shape_ok(int n_heads, int n_kv, int head_dim, int max_ctx)
     IAM_REQUIRE(head_dim == 128, "attention: head_dim must be 128");
     IAM_REQUIRE(n_kv >= 1 && n_heads >= n_kv && n_heads % n_kv == 0 && n_heads / n_kv <= kAttnMaxRep,
                 "attention: n_heads must be a multiple of n_kv with at most 8 query heads per KV head");
-    IAM_REQUIRE(max_ctx >= 1, "attention: max_ctx must be positive");
+    IAM_REQUIRE(max_ctx >= 1 && max_ctx <= kMaxAttnSplits * kAttnChunk, "attention: max_ctx must be in [1, 8192]");
     return IAM_OK;
 }
 
@@ -435,7 +523,7 @@ extern "C" {
 int iam_rmsnorm_gain(iam_ctx* c, const float* in, const uint16_t* gain, int n, float eps, float* out)
 {
     if (!c || !in || !gain || !out) return fail(IAM_E_INVALID, "rmsnorm: null argument");
-    IAM_REQUIRE(n > 0 && n % 256 == 0, "rmsnorm: n must be a positive multiple of 256");
+    IAM_REQUIRE(n > 0 && n % 1024 == 0, "rmsnorm: n must be a positive multiple of 1024");
     IAM_TRY(check_dev_range(c, in, (size_t)n * 4, "rmsnorm in"));
     IAM_TRY(check_dev_range(c, gain, (size_t)n * 2, "rmsnorm gain"));
     IAM_TRY(check_dev_range(c, out, (size_t)n * 4, "rmsnorm out"));
@@ -446,7 +534,7 @@ int iam_add_rmsnorm_gain(iam_ctx* c, float* h, const float* delta, const uint16_
                          float* out)
 {
     if (!c || !h || !delta || !gain || !out) return fail(IAM_E_INVALID, "add_rmsnorm: null argument");
-    IAM_REQUIRE(n > 0 && n % 256 == 0, "add_rmsnorm: n must be a positive multiple of 256");
+    IAM_REQUIRE(n > 0 && n % 1024 == 0, "add_rmsnorm: n must be a positive multiple of 1024");
     IAM_TRY(check_dev_range(c, h, (size_t)n * 4, "add_rmsnorm h"));
     IAM_TRY(check_dev_range(c, delta, (size_t)n * 4, "add_rmsnorm delta"));
     IAM_TRY(check_dev_range(c, gain, (size_t)n * 2, "add_rmsnorm gain"));

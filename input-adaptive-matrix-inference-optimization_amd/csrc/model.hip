@@ -234,18 +234,21 @@ static int reserve(iam_model* m, float effort)
 {
     Ctx* c = m->c;
     const iam_model_config& C = m->cfg;
-    const int gmax = (std::max(C.dim, C.ffn_dim) + kChunkInputs - 1) / kChunkInputs;
-    for (int s = 0; s < kMaxMulti; s++) IAM_TRY(ensure_slot(c, s, gmax));
+    for (int s = 0; s < kMaxMulti; s++) IAM_TRY(ensure_slot(c, s));
     const Layer& ly = m->layers[0];
     const Mat* groups[5][3] = {{&ly.wq, &ly.wk, &ly.wv}, {&ly.wo}, {&ly.w1, &ly.w3}, {&ly.w2}, {&m->lm}};
     const int sizes[5] = {3, 1, 2, 1, 1};
+    const int ins[5] = {C.dim, C.dim, C.dim, C.ffn_dim, C.dim};
     for (int gi = 0; gi < 5; gi++) {
         MatOp ops[kMaxMulti];
-        for (int i = 0; i < sizes[gi]; i++) ops[i].mat = groups[gi][i]->desc();
-        int T[kMaxMulti], P[kMaxMulti], V[kMaxMulti];
-        plan_walk(sizes[gi], ops, effort, T, P, V);
+        for (int i = 0; i < sizes[gi]; i++) {
+            ops[i].mat = groups[gi][i]->desc();
+            ops[i].in_size = ins[gi];
+        }
+        WalkPlan plan[kMaxMulti];
+        plan_walk(sizes[gi], ops, effort, c->acc64, plan);
         for (int i = 0; i < sizes[gi]; i++)
-            IAM_TRY(ensure_partials(c, i, (size_t)P[i] * ops[i].mat.bucket_cols * 16 * (c->acc64 ? 8 : 4)));
+            IAM_TRY(ensure_partials(c, i, (size_t)plan[i].P * ops[i].mat.bucket_cols * 16 * (c->acc64 ? 8 : 4)));
     }
     return ensure_attn_ws(c, attention_ws_floats(C.n_heads, C.max_ctx));
 }
@@ -387,11 +390,11 @@ int iam_model_create(iam_ctx* c, const iam_model_config* cfg, iam_model** out)
     IAM_REQUIRE(C.n_heads * C.head_dim == C.dim, "model: dim must equal n_heads * head_dim");
     IAM_REQUIRE(C.n_kv_heads >= 1 && C.n_heads % C.n_kv_heads == 0 && C.n_heads / C.n_kv_heads <= 8,
                 "model: n_heads must be a multiple of n_kv_heads (at most 8 per KV head)");
-    IAM_REQUIRE(C.dim >= kProbes && C.dim % 256 == 0,
-                "model: dim must be a multiple of 256 and at least 4096 (the cutoff reads 4096 inputs)");
+    IAM_REQUIRE(C.dim >= kProbes && C.dim % 1024 == 0 && C.dim <= 16384,
+                "model: dim must be a multiple of 1024 in [4096, 16384] (the cutoff reads 4096 inputs)");
     IAM_REQUIRE(C.ffn_dim >= kProbes && C.ffn_dim % 16 == 0, "model: ffn_dim must be >= 4096 and a multiple of 16");
     IAM_REQUIRE(C.vocab >= 16 && C.vocab % 16 == 0, "model: vocab must be a positive multiple of 16");
-    IAM_REQUIRE(C.max_ctx >= 1, "model: max_ctx must be positive");
+    IAM_REQUIRE(C.max_ctx >= 1 && C.max_ctx <= 8192, "model: max_ctx must be in [1, 8192]");
     IAM_REQUIRE(C.dim / 256 <= kMaxChunks && C.ffn_dim / 256 < kMaxChunks, "model: dims too large");
 
     iam_model* m = new iam_model();

@@ -66,20 +66,27 @@ int check_dev_range(Ctx* c, const void* p, size_t bytes, const char* what)
     return fail(IAM_E_INVALID, std::string(what) + ": range not inside an allocation of this context");
 }
 
-int ensure_slot(Ctx* c, int slot, int chunks)
+int ensure_slot(Ctx* c, int slot)
 {
     DispatchSlot& s = c->slots[slot];
-    if (!s.counts) {
-        IAM_TRY(ctx_alloc(c, sizeof(uint32_t) * kMaxChunks, (void**)&s.counts));
-        IAM_TRY(ctx_alloc(c, sizeof(float) * 4, (void**)&s.cutoff));
+    if (!s.cutoff) {
+        if (c->capturing) return fail(IAM_E_STATE, "dispatch buffer allocation during graph capture");
+        IAM_TRY(ctx_alloc(c, 16, (void**)&s.cutoff));
+        IAM_TRY(ctx_alloc(c, 16, (void**)&s.count));
+        c->scratch_gen++;
     }
+    return IAM_OK;
+}
+
+int ensure_list(Ctx* c, int slot, int chunks)
+{
+    DispatchSlot& s = c->slots[slot];
+    if (!s.counts) IAM_TRY(ctx_alloc(c, sizeof(uint32_t) * kMaxChunks, (void**)&s.counts));
     if ((size_t)chunks > s.cap_chunks) {
-        if (c->capturing) return fail(IAM_E_STATE, "dispatch buffer growth during graph capture");
         if (s.list) IAM_TRY(ctx_free(c, s.list));
         s.list = nullptr;
         IAM_TRY(ctx_alloc(c, sizeof(uint2) * (size_t)chunks * kChunkRows, (void**)&s.list));
         s.cap_chunks = (size_t)chunks;
-        c->scratch_gen++;
     }
     return IAM_OK;
 }

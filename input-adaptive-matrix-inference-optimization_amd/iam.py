@@ -10,6 +10,9 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "lib", "libiam.so")
+# a different build of the same library (e.g. another launch shape) may be
+# named with IAM_LIBRARY
+LIB_PATH = os.environ.get("IAM_LIBRARY", LIB_PATH)
 HEADER = os.path.join(os.path.dirname(HERE), "include", "iam.h")
 
 IAM_OK = 0
@@ -215,6 +218,12 @@ class Ctx:
         m = C.c_int()
         check(lib().iam_get_accumulation(self.h, C.byref(m)))
         return "fp64" if m.value == 1 else "fp32"
+
+    def walk_count(self, slot=0):
+        """Rows selected by the last walk of the slot (counted in the kernel)."""
+        n = C.c_uint32()
+        check(lib().iam_bucketmul_walk_count(self.h, slot, C.byref(n)))
+        return n.value
 
     def walk_counters(self, reset=False):
         b, r, m = C.c_uint64(), C.c_uint64(), C.c_uint64()

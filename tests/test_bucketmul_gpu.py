@@ -49,10 +49,13 @@ def run_gpu(ctx, b, s, p, x, effort, in_size=None, expert_no=0, expert_rows=None
     else:
         ctx.full_mul(dx, ds, dp, db, expert_no, in_size, C, R, effort, dy)
     y = dy.read()
+    walked = ctx.walk_count(0)
     cut, S = ctx.dispatch_info(0)
     rows = ctx.dispatch_rows(0)
     for d in (db, ds, dp, dx, dy):
         d.free()
+    # the walk selects its rows itself: it must have taken the listed set's size
+    assert walked == S, (walked, S)
     return y, cut, S, rows
 
 
@@ -193,7 +196,7 @@ def test_multi_matches_single(iam, O, ctx):
         oy, ocut, omask, oS = ref[k]
         cut, S = ctx.dispatch_info(k)
         assert np.float32(cut).view(np.uint32) == np.float32(ocut).view(np.uint32)
-        assert S == oS
+        assert S == oS and ctx.walk_count(k) == oS
         assert np.array_equal(ctx.dispatch_rows(k), np.nonzero(omask)[0].astype(np.uint32))
         assert rel_l2(y, oy) < 1e-5
     for d in bufs + outs + [dx]:
