@@ -6,7 +6,8 @@
  * links or calls it.  Built with -O2 -ffp-contract=off -fno-fast-math so every
  * fp32 operation is a single IEEE-rounded operation.
  *
- * How each function is pinned (tests/test_oracle.py, tests/test_golden.py):
+ * How each function is pinned (tests/test_oracle.py, against the fixtures in
+ * tests/golden/):
  *   orc_f32_to_f16 / orc_f16_to_f32 /
  *   orc_f64_to_f16 ..................... numpy astype(float16/float32) on 2^20
  *                                        values incl. subnormals, inf, ties
@@ -33,9 +34,12 @@
  *   orc_rope_table ..................... numpy float32 cos/sin of the same
  *                                        angles (within 1 ulp)
  *   orc_argmax ......................... numpy argmax (first maximum)
- *   orc_model_forward .................. composition of the above; checked by
- *                                        a numpy float64 re-composition on a
- *                                        tiny model
+ *   orc_layer_forward,
+ *   orc_model_forward .................. composition of the above; checked
+ *                                        step by step against a re-composition
+ *                                        from the separately pinned primitives
+ *                                        (op order, gains, residuals, KV slot)
+ *                                        on a 1-layer model over 3 positions
  */
 #include "oracle.h"
 

@@ -1,0 +1,106 @@
+"""The drop-in C++ headers (cpp/*.hpp through bin/iam_dropin) on a weights
+directory in the reference's file format: per-matrix _buckets.bin /
+_stats.bin / _probes.bin / _meta.txt (preprocess_layer_fixed_gpu.py:245-282,
+read by binary_loader.hpp) plus the .npy norms, embedding and dense LM head
+(transformer_layer.hpp:25-52, model.hpp:54-81).
+
+Checks: BucketMul::calcDispatch + mul on one weight file gives the oracle's
+cutoff bits, selected-row count and y (within 1 ulp); MistralModel greedy
+generation (graph replay and eager host argmax) gives the oracle model's
+tokens, with the dense LM head bucketized on load."""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+DROPIN = os.path.join(ROOT, "input-adaptive-matrix-inference-optimization_amd", "bin", "iam_dropin")
+CFG = dict(n_layers=1, dim=4096, ffn_dim=4096, n_heads=32, n_kv_heads=8, head_dim=128, vocab=256,
+           max_ctx=16, rope_theta=10000.0, norm_eps=1e-5)
+NAMES = {"wq": "q", "wk": "k", "wv": "v", "wo": "o", "w1": "gate", "w3": "up", "w2": "down"}
+SHAPES = {"wq": (4096, 4096), "wk": (1024, 4096), "wv": (1024, 4096), "wo": (4096, 4096),
+          "w1": (4096, 4096), "w3": (4096, 4096), "w2": (4096, 4096)}
+
+
+def write_matrix(d, name, b, s, p, out_dim, in_dim):
+    R, C = b.shape
+    b.astype("<u2").tofile(os.path.join(d, name + "_buckets.bin"))
+    s.astype("<u2").tofile(os.path.join(d, name + "_stats.bin"))
+    p.astype("<u2").tofile(os.path.join(d, name + "_probes.bin"))
+    with open(os.path.join(d, name + "_meta.txt"), "w") as f:
+        f.write(f"buckets_shape: 1 {R} {C}\nstats_shape: 1 {R} 4\nprobes_shape: 1 {in_dim}\n"
+                f"in_dim: {in_dim}\nout_dim: {out_dim}\nbsize: 16\n")
+
+
+@pytest.fixture(scope="module")
+def weights(O, tmp_path_factory):
+    d = str(tmp_path_factory.mktemp("weights"))
+    t = {}
+    for k, (w, shp) in enumerate(SHAPES.items()):
+        W = O.gen_f16(7, 600 + k, shp[0] * shp[1], 0.0, 0.02).reshape(shp)
+        b, s, p = O.bucketize(W)
+        write_matrix(d, f"layer0_{NAMES[w]}_proj_bucketmul_fp16", b, s, p, shp[0], shp[1])
+        t[f"layer0.{w}.buckets"], t[f"layer0.{w}.stats"], t[f"layer0.{w}.probes"] = b, s, p
+    V, D = CFG["vocab"], CFG["dim"]
+    t["layer0.attn_gain"] = O.gen_f16(7, 620, D, 1.0, 0.01)
+    t["layer0.ffn_gain"] = O.gen_f16(7, 621, D, 1.0, 0.01)
+    t["embed"] = O.gen_f16(7, 622, V * D, 0.0, 0.02)
+    t["final_gain"] = O.gen_f16(7, 623, D, 1.0, 0.01)
+    lm = O.gen_f16(7, 624, V * D, 0.0, 0.02).reshape(V, D)
+    np.save(os.path.join(d, "layer0_input_layernorm.npy"), t["layer0.attn_gain"].view(np.float16))
+    np.save(os.path.join(d, "layer0_post_attention_layernorm.npy"), t["layer0.ffn_gain"].view(np.float16))
+    np.save(os.path.join(d, "embed_tokens.npy"), t["embed"].view(np.float16).reshape(V, D))
+    np.save(os.path.join(d, "norm_weight.npy"), t["final_gain"].view(np.float16))
+    np.save(os.path.join(d, "lm_head.npy"), lm.view(np.float16))
+    lb, ls, lp = O.bucketize(lm)
+    t["lm_head.buckets"], t["lm_head.stats"], t["lm_head.probes"] = lb, ls, lp
+    return d, t
+
+
+def run(args):
+    assert os.path.exists(DROPIN), "bin/iam_dropin not built (run __graft_entry__.build())"
+    r = subprocess.run([DROPIN] + args, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    return r.stdout
+
+
+def test_bucketmul_from_reference_files(O, weights, tmp_path):
+    d, t = weights
+    x = O.gen_f32(7, 640, 4096, 0.0, 1.0)
+    xin, yout = str(tmp_path / "x.f32"), str(tmp_path / "y.f32")
+    x.tofile(xin)
+    out = run(["bucketmul", "-d", d, "-w", "layer0_q_proj_bucketmul_fp16", "-e", "0.25", "--in", xin, "--out", yout])
+    # "cutoff: <value> bits 0x<hex> selected: <S>"
+    fields = out.split()
+    bits = int(fields[fields.index("bits") + 1], 16)
+    S = int(fields[fields.index("selected:") + 1])
+    y = np.fromfile(yout, np.float32)
+    oy, ocut, omask, oS = O.bucketmul(x, t["layer0.wq.stats"], t["layer0.wq.probes"], t["layer0.wq.buckets"], 0.25)
+    assert bits == int(np.float32(ocut).view(np.uint32))
+    assert S == oS
+    iy = y.view(np.int32).astype(np.int64)
+    io = oy.view(np.int32).astype(np.int64)
+    assert np.abs(np.where(iy < 0, -(iy & 0x7FFFFFFF), iy) - np.where(io < 0, -(io & 0x7FFFFFFF), io)).max() <= 1
+
+
+@pytest.mark.parametrize("eager", [False, True])
+def test_generate_from_reference_files(O, weights, eager):
+    d, t = weights
+    prompt = [3, 141, 59, 26]
+    n_new = 6
+    args = ["generate", "-d", d, "-p", ",".join(map(str, prompt)), "-n", str(n_new), "-e", "0.25",
+            "--max-ctx", str(CFG["max_ctx"]), "--theta", "10000"]
+    if eager:
+        args.append("--eager")
+    out = run(args)
+    toks = [int(v) for v in out.split("tokens:")[1].split("\n")[0].split()]
+    orc = O.OracleModel(CFG, lambda name, dtype: np.ascontiguousarray(t[name]).view(dtype).ravel())
+    seq = list(prompt)
+    for pos in range(len(prompt) + n_new - 1):
+        lo = orc.forward(seq[pos], pos, 0.25)
+        if pos >= len(prompt) - 1:
+            seq.append(O.argmax(lo))
+    assert toks == seq[len(prompt):]

@@ -427,3 +427,51 @@ def test_generator_statistics_and_determinism(O):
     assert abs(hf.std() - 0.02) < 5e-4
     t = O.gen_tokens(0, 3, 100000, 32000)
     assert t.min() >= 0 and t.max() < 32000 and len(np.unique(t)) > 30000
+
+
+# ----------------------------------------------------------------- model ---
+
+def test_model_forward_is_the_layer_composition(O):
+    """orc_model_forward (transformer_layer.hpp:75-122, model.hpp:152-231)
+    equals the primitives chained in the reference order: RMSNorm(attn gain)
+    -> q,k,v -> RoPE of q and k at pos -> fp16 K/V rows at pos -> attention
+    over pos+1 tokens -> o -> +residual -> RMSNorm(ffn gain) -> w1, w3 ->
+    SiLU(w1)*w3 -> w2 -> +residual; final RMSNorm -> LM head."""
+    cfg = dict(n_layers=1, dim=4096, ffn_dim=4096, n_heads=32, n_kv_heads=8, head_dim=128, vocab=256,
+               max_ctx=4, rope_theta=10000.0, norm_eps=1e-5)
+    D, F, V, KVD = 4096, 4096, 256, 1024
+    shapes = {"wq": (D, D), "wk": (KVD, D), "wv": (KVD, D), "wo": (D, D), "w1": (F, D), "w3": (F, D), "w2": (D, F)}
+    mats = {}
+    for k, (name, shp) in enumerate(shapes.items()):
+        W = O.gen_f16(5, 500 + k, shp[0] * shp[1], 0.0, 0.02).reshape(shp)
+        mats[name] = O.bucketize(W)
+    lm = O.bucketize(O.gen_f16(5, 520, V * D, 0.0, 0.02).reshape(V, D))
+    t = {"layer0.attn_gain": O.gen_f16(5, 530, D, 1.0, 0.01), "layer0.ffn_gain": O.gen_f16(5, 531, D, 1.0, 0.01),
+         "embed": O.gen_f16(5, 532, V * D, 0.0, 0.02), "final_gain": O.gen_f16(5, 533, D, 1.0, 0.01),
+         "lm_head.buckets": lm[0], "lm_head.stats": lm[1], "lm_head.probes": lm[2]}
+    for name, (b, st, pr) in mats.items():
+        t[f"layer0.{name}.buckets"], t[f"layer0.{name}.stats"], t[f"layer0.{name}.probes"] = b, st, pr
+    orc = O.OracleModel(cfg, lambda name, dtype: np.ascontiguousarray(t[name]).view(dtype).ravel())
+    table = O.rope_table(10000.0, 128, 4)
+    kc = np.zeros((4, KVD), np.uint16)
+    vc = np.zeros((4, KVD), np.uint16)
+
+    def mm(name, x):
+        b, st, pr = mats[name]
+        return O.bucketmul(x, st, pr, b, 0.25)[0]
+
+    for pos, tok in enumerate([17, 200, 3]):
+        got = orc.forward(tok, pos, 0.25)
+        h = O.f16_to_f32(t["embed"].reshape(V, D)[tok])
+        hn = O.rmsnorm_gain(h, t["layer0.attn_gain"], 1e-5)
+        q, k, v = mm("wq", hn), mm("wk", hn), mm("wv", hn)
+        qr, kr = O.rope(q, table[pos], 32, 128), O.rope(k, table[pos], 8, 128)
+        kc[pos], vc[pos] = O.f32_to_f16(kr), O.f32_to_f16(v)
+        att = O.attention_f16kv(qr, kc, vc, pos + 1, 32, 8, 128)
+        h = h + mm("wo", att)
+        hn = O.rmsnorm_gain(h, t["layer0.ffn_gain"], 1e-5)
+        h = h + mm("w2", O.silu_mul(mm("w1", hn), mm("w3", hn)))
+        hn = O.rmsnorm_gain(h, t["final_gain"], 1e-5)
+        want = O.bucketmul(hn, lm[1], lm[2], lm[0], 0.25)[0]
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), pos
+        assert np.array_equal(orc.kc.reshape(4, KVD)[pos], kc[pos])
