@@ -340,38 +340,23 @@ struct WalkArgs {
     int n;
 };
 
-template <int VEC, typename Acc, int NW, int UNR>
-__global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
+// Selection of slice p (prepareDispatch, bucketMul.cl:351-386): thread i
+// takes input i0 + i, loads its x and the stats of its 16 rows, and marks the
+// rows with 1e5 * |x * stat| >= cutoff -- the same fp32 operations as the
+// dispatch kernel, so the selected set is the same.  A block scan compacts
+// the selected rows in ascending order into s_row (slice-local ids
+// input*16 + rank); s_x[i] = x[i0 + i].  Ends with a barrier; returns the
+// number of selected rows.  The tile-0 workgroup of the slice adds the count
+// to the matrix's counters.
+template <int NT>
+__device__ uint32_t select_slice(const WalkDesc& d, int p, int t, int i0, int ni, uint16_t* s_row, float* s_x,
+                                 uint32_t* s_wsum)
 {
 #pragma clang fp contract(off)
-    constexpr int NT = 64 * NW;
-    constexpr int NJ = 64 / VEC, NQ = VEC, TW = 64;
-    constexpr int PER = 16 * VEC * 64;         // accumulators per wave
-    constexpr int STRIDE = NW * NQ;            // rows per workgroup instruction
-    __shared__ Acc acc[NW * PER];
-    __shared__ uint16_t s_row[NT * 16];        // selected rows, slice-local (input*16 + rank)
-    __shared__ float s_x[NT];
-    __shared__ uint32_t s_wsum[NW];
-
+    constexpr int NW = NT / 64;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int b = xcd_remap((int)blockIdx.x, (int)gridDim.x);
-    int k = 0;
-    for (int i = 1; i < a.n; i++)
-        if (b >= a.d[i].block_base) k = i;
-    const WalkDesc& d = a.d[k];
-    const int w = b - d.block_base;
-    const int p = w / d.T;
-    const int t = w - p * d.T;
-
-    Acc* my = acc + wave * PER + lane;
-#pragma unroll
-    for (int i = 0; i < 16 * VEC; i++) my[i * 64] = (Acc)0;
-
-    // ---- selection of the slice's rows
-    const int i0 = p * d.IPS;
-    const int ni = min(d.IPS, d.n_in - i0);
     const float cutoff = *d.cutoff;
     uint32_t mask = 0;
     float xi = 0.0f;
@@ -441,6 +426,42 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
         atomicAdd(d.counters + 1, (unsigned long long)n_sel);
         if (p == 0) atomicAdd(d.counters + 2, 1ull);
     }
+    return n_sel;
+}
+
+template <int VEC, typename Acc, int NW, int UNR>
+__global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
+{
+#pragma clang fp contract(off)
+    constexpr int NT = 64 * NW;
+    constexpr int NJ = 64 / VEC, NQ = VEC, TW = 64;
+    constexpr int PER = 16 * VEC * 64;         // accumulators per wave
+    constexpr int STRIDE = NW * NQ;            // rows per workgroup instruction
+    __shared__ Acc acc[NW * PER];
+    __shared__ uint16_t s_row[NT * 16];        // selected rows, slice-local (input*16 + rank)
+    __shared__ float s_x[NT];
+    __shared__ uint32_t s_wsum[NW];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int b = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    int k = 0;
+    for (int i = 1; i < a.n; i++)
+        if (b >= a.d[i].block_base) k = i;
+    const WalkDesc& d = a.d[k];
+    const int w = b - d.block_base;
+    const int p = w / d.T;
+    const int t = w - p * d.T;
+
+    Acc* my = acc + wave * PER + lane;
+#pragma unroll
+    for (int i = 0; i < 16 * VEC; i++) my[i * 64] = (Acc)0;
+
+    // ---- selection of the slice's rows
+    const int i0 = p * d.IPS;
+    const int ni = min(d.IPS, d.n_in - i0);
+    const uint32_t n_sel = select_slice<NT>(d, p, t, i0, ni, s_row, s_x, s_wsum);
 
     // ---- walk of the selected rows
     const int q = lane / NJ;
@@ -535,6 +556,134 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     for (int o = tid; o < nout; o += NT) prow[o] = stage[o + (o >> 5)];
 }
 
+// Selection + walk with fp64 accumulation in wave-private LDS tiles.
+// Workgroup (input slice p, column tile t) owns the inputs [p*IPS,
+// (p+1)*IPS) and the 128 columns [128t, 128t + 128).
+//
+// Walk: lane = q*16 + j reads 16 bytes (8 columns 8j..8j+7) of row q of a
+// group of 4 selected rows, so one load instruction fetches the 256-byte tile
+// segments of 4 rows.  Wave w takes the groups w, w + NW, w + 2NW, ...  Each
+// packed weight is added, as the exact fp64 product x * w, to the wave's own
+// accumulator of its output (column c, position bits & 15) with a
+// non-returning LDS fp64 atomic add (bucketMul.cl:430-445 adds the fp32
+// product with a plain += per work-item).  Accumulator slot of (8j+e, pos) is
+// pos*128 + e*16 + j: for one element e the 16 lanes of a row hit 16
+// different bank pairs whatever their positions.  A wave's atomics are
+// applied in instruction order and, within an instruction, in lane order, so
+// the sums do not depend on scheduling; the flush adds the NW wave tiles in
+// wave order.  Rows past the end of the list re-read the last selected row
+// with x = 0, so every load of a batch is unconditional.
+template <int NW, int UNR>
+__global__ __launch_bounds__(64 * NW) void k_walk64(WalkArgs a)
+{
+#pragma clang fp contract(off)
+    constexpr int NT = 64 * NW;
+    constexpr int TW = 128;
+    constexpr int SLOTS = TW * 16;             // accumulators per wave
+    constexpr int GSTRIDE = NW * UNR;          // groups per workgroup batch
+    __shared__ double acc[NW * SLOTS];
+    __shared__ uint16_t s_row[NT * 16];
+    __shared__ float s_x[NT];
+    __shared__ uint32_t s_wsum[NW];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int b = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    int k = 0;
+    for (int i = 1; i < a.n; i++)
+        if (b >= a.d[i].block_base) k = i;
+    const WalkDesc& d = a.d[k];
+    const int w = b - d.block_base;
+    const int p = w / d.T;
+    const int t = w - p * d.T;
+
+    {
+        double2* z = reinterpret_cast<double2*>(acc + wave * SLOTS);
+#pragma unroll
+        for (int i = 0; i < SLOTS / 128; i++) z[i * 64 + lane] = make_double2(0.0, 0.0);
+    }
+
+    const int i0 = p * d.IPS;
+    const int ni = min(d.IPS, d.n_in - i0);
+    const int ns = (int)select_slice<NT>(d, p, t, i0, ni, s_row, s_x, s_wsum);
+
+    const int j = lane & 15;
+    const int q = lane >> 4;
+    const int col0 = t * TW + j * 8;
+    if (col0 < d.C) {   // C % 8 == 0: the lane's 8 columns are all in range
+        const uint16_t* wb = d.W + (size_t)i0 * 16 * d.C + col0;
+        double* accw = acc + wave * SLOTS + j;
+        const int ng = (ns + 3) >> 2;
+        int rl[UNR];
+        float xl[UNR];
+        uint4 v[UNR];
+        auto issue = [&](int g0) {
+#pragma unroll
+            for (int u = 0; u < UNR; u++) {
+                const int idx = (g0 + u * NW) * 4 + q;
+                rl[u] = s_row[min(idx, ns - 1)];
+                xl[u] = idx < ns ? 1.0f : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < UNR; u++) xl[u] *= s_x[rl[u] >> 4];
+#pragma unroll
+            for (int u = 0; u < UNR; u++)
+                v[u] = *reinterpret_cast<const uint4*>(wb + (size_t)rl[u] * d.C);
+        };
+        if (wave < ng) issue(wave);
+        for (int g0 = wave; g0 < ng; g0 += GSTRIDE) {
+            uint4 vc[UNR];
+            double xc[UNR];
+#pragma unroll
+            for (int u = 0; u < UNR; u++) {
+                vc[u] = v[u];
+                xc[u] = (double)xl[u];
+            }
+            if (g0 + GSTRIDE < ng) issue(g0 + GSTRIDE);
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int u = 0; u < UNR; u++) {
+                const uint32_t words[4] = {vc[u].x, vc[u].y, vc[u].z, vc[u].w};
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const uint32_t h = (words[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+                    const double wv = (double)h2f(h);
+                    atomicAdd(accw + (int)(h & 15u) * TW + e * 16, xc[u] * wv);
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // ---- flush: thread -> slots tid + k*NT (slot order, conflict-free), sum
+    // of the NW wave tiles in wave order, through a padded staging copy (one
+    // pad per 128 entries) into output order col*16 + pos (bucketMul.cl:
+    // 442-445), written as one contiguous run of the slice's partial row.
+    constexpr int OPT = SLOTS / NT;
+    static_assert(SLOTS % NT == 0 && NW * SLOTS >= SLOTS + SLOTS / 128, "flush staging does not fit");
+    double sum[OPT];
+#pragma unroll
+    for (int k2 = 0; k2 < OPT; k2++) {
+        const int sl = tid + k2 * NT;
+        double s2 = acc[sl];
+#pragma unroll
+        for (int ww = 1; ww < NW; ww++) s2 += acc[ww * SLOTS + sl];
+        sum[k2] = s2;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k2 = 0; k2 < OPT; k2++) {
+        const int sl = tid + k2 * NT;
+        const int pos = sl >> 7, e = (sl >> 4) & 7, jj = sl & 15;
+        const int o = (jj * 8 + e) * 16 + pos;
+        acc[o + (o >> 7)] = sum[k2];
+    }
+    __syncthreads();
+    double* prow = reinterpret_cast<double*>(d.part) + (size_t)p * d.C * 16 + (size_t)t * SLOTS;
+    const int nout = min(SLOTS, (d.C - t * TW) * 16);
+    for (int o = tid; o < nout; o += NT) prow[o] = acc[o + (o >> 7)];
+}
+
 // y[o] = sum over row slices of part[p][o], in slice order 0..P-1 grouped by
 // p mod 16 then combined in group order: a fixed order, so y is the same on
 // every run (bucketIntegrate, bucketMul.cl:453-497, sums 64 fixed slices).
@@ -613,13 +762,47 @@ double est_rows(int rows, float effort) { return std::max(1.0, rows * est_fracti
 // private accumulators (fp32: 4 columns per lane; fp64: 2); a slice holds at
 // most 64 inputs per wave.  A launch gets about one workgroup per
 // kWalkWgBytes of expected weight bytes, at least kWalkMinWgs.
-constexpr double kWalkWideBytes = 40e6;
-constexpr double kWalkWgBytes = 98304.0;
-constexpr double kWalkMinWgs = 256.0;
+#ifndef IAM_WALK_WIDE_BYTES
+#define IAM_WALK_WIDE_BYTES 40e6
+#endif
+#ifndef IAM_WALK_WG_BYTES
+#define IAM_WALK_WG_BYTES 98304.0
+#endif
+#ifndef IAM_WALK_MIN_WGS
+#define IAM_WALK_MIN_WGS 256.0
+#endif
+#ifndef IAM_WALK_SMALL_NW
+#define IAM_WALK_SMALL_NW 4
+#endif
+#ifndef IAM_WALK_SMALL_UNR
+#define IAM_WALK_SMALL_UNR 16
+#endif
+#ifndef IAM_WALK_BIG_NW
+#define IAM_WALK_BIG_NW 2
+#endif
+#ifndef IAM_WALK_BIG_UNR
+#define IAM_WALK_BIG_UNR 8
+#endif
+constexpr double kWalkWideBytes = IAM_WALK_WIDE_BYTES;
+constexpr double kWalkWgBytes = IAM_WALK_WG_BYTES;
+constexpr double kWalkMinWgs = IAM_WALK_MIN_WGS;
 constexpr double kWalkMaxWgs = 3072.0;
 
+#ifndef IAM_W64_NW
+#define IAM_W64_NW 4
+#endif
+#ifndef IAM_W64_UNR
+#define IAM_W64_UNR 4
+#endif
+#ifndef IAM_W64_WG_BYTES
+#define IAM_W64_WG_BYTES 131072.0
+#endif
+
+// 8: the fp64 walk with 16-byte loads and 128-column tiles (k_walk64);
+// otherwise the columns per lane load of k_walk.
 static int vec_of(int C, bool acc64)
 {
+    if (acc64 && C % 8 == 0) return 8;
     if (C % 4 == 0 && !acc64) return 4;
     if (C % 2 == 0) return 2;
     return 1;
@@ -630,23 +813,27 @@ static int vec_of(int C, bool acc64)
 void plan_walk(int n, const MatOp* ops, float effort, bool acc64, WalkPlan* plan)
 {
     double bytes[kMaxMulti], tot = 0;
+    bool all64 = true;
     for (int i = 0; i < n; i++) {
         const iam_bucket_matrix& M = ops[i].mat;
         WalkPlan& pl = plan[i];
         pl.V = vec_of(M.bucket_cols, acc64);
-        pl.T = (M.bucket_cols + 63) / 64;
+        all64 = all64 && pl.V == 8;
+        const int tw = pl.V == 8 ? 128 : 64;
+        pl.T = (M.bucket_cols + tw - 1) / tw;
         pl.n_in = std::min((M.expert_rows + 15) / 16, ops[i].in_size);
         bytes[i] = est_rows(pl.n_in * 16, effort) * M.bucket_cols * 2.0;
         tot += bytes[i];
     }
-    const int nw = tot < kWalkWideBytes ? 4 : 2;
-    const double target = std::min(kWalkMaxWgs, std::max(kWalkMinWgs, tot / kWalkWgBytes));
+    const int nw = all64 ? IAM_W64_NW : tot < kWalkWideBytes ? IAM_WALK_SMALL_NW : IAM_WALK_BIG_NW;
+    const double wg_bytes = all64 ? IAM_W64_WG_BYTES : kWalkWgBytes;
+    const double target = std::min(kWalkMaxWgs, std::max(kWalkMinWgs, tot / wg_bytes));
     for (int i = 0; i < n; i++) {
         WalkPlan& pl = plan[i];
-        pl.NW = nw;
+        pl.NW = pl.V == 8 ? IAM_W64_NW : nw;
         const double wgs = tot > 0 ? target * bytes[i] / tot : target / n;
         const int slices = std::max(1, (int)std::lround(wgs / pl.T));
-        pl.IPS = std::min(64 * nw, std::max(1, (pl.n_in + slices - 1) / slices));
+        pl.IPS = std::min(64 * pl.NW, std::max(1, (pl.n_in + slices - 1) / slices));
         pl.P = (pl.n_in + pl.IPS - 1) / pl.IPS;
     }
 }
@@ -745,8 +932,8 @@ static int launch_walk_shape(Ctx* c, int vec, int blocks, const WalkArgs& args)
 template <typename Acc>
 static int launch_walk(Ctx* c, int nw, int vec, int blocks, const WalkArgs& args)
 {
-    if (nw == 4) return launch_walk_shape<Acc, 4, 16>(c, vec, blocks, args);
-    return launch_walk_shape<Acc, 2, 8>(c, vec, blocks, args);
+    if (nw == IAM_WALK_SMALL_NW) return launch_walk_shape<Acc, IAM_WALK_SMALL_NW, IAM_WALK_SMALL_UNR>(c, vec, blocks, args);
+    return launch_walk_shape<Acc, IAM_WALK_BIG_NW, IAM_WALK_BIG_UNR>(c, vec, blocks, args);
 }
 
 int bucketmul_walk(Ctx* c, int n, const MatOp* ops)
@@ -782,11 +969,12 @@ int bucketmul_walk(Ctx* c, int n, const MatOp* ops)
     // walk: one launch per load width (the model's matrices all share one)
     bool used[kMaxMulti] = {false, false, false};
     for (int done = 0; done < n;) {
-        int vec = 0, blocks = 0, cnt = 0;
+        int vec = 0, blocks = 0, cnt = 0, nw = 0;
         WalkArgs args{};
         for (int i = 0; i < n; i++) {
             if (used[i] || (vec != 0 && plan[i].V != vec)) continue;
             vec = plan[i].V;
+            nw = plan[i].NW;
             const DispatchSlot& s = c->slots[i];
             WalkDesc& d = args.d[cnt++];
             d.W = ops[i].mat.buckets + (size_t)s.expert_no * (size_t)ops[i].mat.expert_rows * ops[i].mat.bucket_cols;
@@ -810,8 +998,12 @@ int bucketmul_walk(Ctx* c, int n, const MatOp* ops)
             done++;
         }
         args.n = cnt;
-        const int nw = plan[0].NW;
-        IAM_TRY(c->acc64 ? launch_walk<double>(c, nw, vec, blocks, args) : launch_walk<float>(c, nw, vec, blocks, args));
+        if (vec == 8)
+            IAM_TRY(launch(c, "bucket_walk", k_walk64<IAM_W64_NW, IAM_W64_UNR>, dim3(blocks), dim3(64 * IAM_W64_NW),
+                           0, args));
+        else
+            IAM_TRY(c->acc64 ? launch_walk<double>(c, nw, vec, blocks, args)
+                             : launch_walk<float>(c, nw, vec, blocks, args));
     }
     // fixed-order sum of the slices into y
     ReduceArgs ra{};
