@@ -27,6 +27,7 @@
 #include <vector>
 
 #include "internal.h"
+#include "layer_ops.h"
 
 namespace iam {
 
@@ -42,8 +43,34 @@ __device__ __forceinline__ float h2f(uint32_t bits16)
 // --------------------------------------------------------------- cutoff ---
 // findCutoffBinarySearch (bucketMul.cl:68-214) for one 256-thread workgroup.
 // Every thread ends with the same cutoff.  s_red needs 8 floats, s_cnt 8 ints.
-__device__ float block_cutoff(const float* __restrict__ x, const uint16_t* __restrict__ probes,
-                              int quantile, float* s_red, int* s_cnt)
+__device__ __forceinline__ float uniform_f(float v)
+{
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+
+// The search's bounds are midpoints inside the current bracket (minB,
+// maxB], so once the bracket holds few importances, count(imp > b) =
+// count(imp > maxB) + #(bracket values > b).  The rounds run on the whole
+// workgroup (one count exchange per round) until the bracket holds at most
+// kCandCap values by its counts (minCount - maxCount bounds them); those are
+// then compacted to wave 0, which finishes the rounds alone with no
+// barriers.  The tested bounds, counts and stop decisions are the
+// reference's exactly.
+constexpr int kCandCap = 256;   // 4 per lane of one wave
+
+// The 16 probes of thread tid (probes[16*tid ..]).
+__device__ __forceinline__ void load_probes(const uint16_t* __restrict__ probes, uint4 (&pr)[2])
+{
+    const uint4* pv = reinterpret_cast<const uint4*>(probes + threadIdx.x * kCutVPT);
+    pr[0] = pv[0];
+    pr[1] = pv[1];
+}
+
+// xs holds x[16*tid .. 16*tid + 16) and pr the thread's probes.  Scratch:
+// s_red >= 9 floats, s_cnt >= 16 ints, s_cand kCandCap floats.  Every
+// thread returns the cutoff; ends after a barrier.
+__device__ __forceinline__ float block_cutoff_x(const float (&xs)[kCutVPT], const uint4 (&pr)[2], int quantile, float* s_red,
+                                int* s_cnt, float* s_cand)
 {
 #pragma clang fp contract(off)
     const int tid = threadIdx.x;
@@ -51,12 +78,7 @@ __device__ float block_cutoff(const float* __restrict__ x, const uint16_t* __res
     const int wave = tid >> 6;
     float v[kCutVPT];
     {
-        const float4* xv = reinterpret_cast<const float4*>(x + tid * kCutVPT);
-        const uint4* pv = reinterpret_cast<const uint4*>(probes + tid * kCutVPT);
-        float4 xa = xv[0], xb = xv[1], xc = xv[2], xd = xv[3];
-        uint4 pa = pv[0], pb = pv[1];
-        float xs[16] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w,
-                        xc.x, xc.y, xc.z, xc.w, xd.x, xd.y, xd.z, xd.w};
+        const uint4 pa = pr[0], pb = pr[1];
         uint32_t ps[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
 #pragma unroll
         for (int k = 0; k < 16; k++) {
@@ -81,21 +103,16 @@ __device__ float block_cutoff(const float* __restrict__ x, const uint16_t* __res
         s_red[4 + wave] = mx;
     }
     __syncthreads();
-    const float gmin = fminf(fminf(s_red[0], s_red[1]), fminf(s_red[2], s_red[3]));
-    const float gmax = fmaxf(fmaxf(s_red[4], s_red[5]), fmaxf(s_red[6], s_red[7]));
+    // the search state is uniform: keep it in scalar registers
+    const float gmin = uniform_f(fminf(fminf(s_red[0], s_red[1]), fminf(s_red[2], s_red[3])));
+    const float gmax = uniform_f(fmaxf(fmaxf(s_red[4], s_red[5]), fmaxf(s_red[6], s_red[7])));
 
     const int target = kProbes - quantile;            // bucketMul.cl:81
     float minB = gmin, maxB = gmax;
-    float bound = __fmul_rn(__fadd_rn(gmin, gmax), 0.5f);
+    float bound = uniform_f(__fmul_rn(__fadd_rn(gmin, gmax), 0.5f));
     int minC = kProbes, maxC = 0;
-    for (int loop = 0; loop < 20; loop++) {
-        int c = 0;
-#pragma unroll
-        for (int k = 0; k < 16; k++) c += __popcll(__ballot(v[k] > bound));
-        if (lane == 0) s_cnt[(loop & 1) * 4 + wave] = c;
-        __syncthreads();
-        const int* sc = s_cnt + (loop & 1) * 4;
-        const int count = sc[0] + sc[1] + sc[2] + sc[3];
+    // one round of bucketMul.cl:178-200 given the count at bound; true = stop
+    auto round = [&](int count) -> bool {
         if (count < target) {                          // bucketMul.cl:178-186
             maxB = bound;
             maxC = count;
@@ -103,24 +120,132 @@ __device__ float block_cutoff(const float* __restrict__ x, const uint16_t* __res
             minB = bound;
             minC = count;
         }
-        const float next = __fmul_rn(__fadd_rn(minB, maxB), 0.5f);
+        const float next = uniform_f(__fmul_rn(__fadd_rn(minB, maxB), 0.5f));
         const int gap = maxC - minC;
         if (count == target || __fsub_rn(maxB, minB) < 0.00001f || (gap < 0 ? -gap : gap) < 3)
-            return bound;                              // bucketMul.cl:195-200
+            return true;                               // bucketMul.cl:195-200: the tested bound
         bound = next;
+        return false;
+    };
+    int loop = 0;
+    for (; loop < 20; loop++) {
+        if (minC - maxC <= kCandCap) break;
+        int c = 0;
+#pragma unroll
+        for (int k = 0; k < 16; k++) c += __popcll(__ballot(v[k] > bound));
+        if (lane == 0) s_cnt[(loop & 1) * 4 + wave] = c;
+        __syncthreads();
+        const int4 q4 = *reinterpret_cast<const int4*>(s_cnt + (loop & 1) * 4);
+        if (round(__builtin_amdgcn_readfirstlane(q4.x + q4.y + q4.z + q4.w))) return bound;
     }
-    return bound;                                      // bucketMul.cl:211-213
+    if (loop == 20) return bound;                      // bucketMul.cl:211-213: the untested midpoint
+
+    // compact the bracket values (minB, maxB] to s_cand (the count only
+    // needs the set, so the order is per wave, then by k, then by lane)
+    uint64_t bm[16];
+    int wtot = 0;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        bm[k] = __ballot(v[k] > minB && v[k] <= maxB);
+        wtot += __popcll(bm[k]);
+    }
+    if (lane == 0) s_cnt[8 + wave] = wtot;
+    __syncthreads();
+    int off = 0;
+    for (int w = 0; w < wave; w++) off += s_cnt[8 + w];
+    const int ncand = s_cnt[8] + s_cnt[9] + s_cnt[10] + s_cnt[11];   // <= minC - maxC <= kCandCap
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        if ((bm[k] >> lane) & 1ull) s_cand[off + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bm[k] >> 32),
+                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)bm[k], 0u))] = v[k];
+        off += __popcll(bm[k]);
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float cv[kCandCap / 64];
+#pragma unroll
+        for (int j = 0; j < kCandCap / 64; j++) cv[j] = lane + 64 * j < ncand ? s_cand[lane + 64 * j] : -INFINITY;
+        const int c0 = maxC;                           // count(imp > maxB) at the compaction
+        bool done = false;
+        for (; loop < 20 && !done; loop++) {
+            int c = c0;
+#pragma unroll
+            for (int j = 0; j < kCandCap / 64; j++) c += __popcll(__ballot(cv[j] > bound));
+            done = round(c);
+        }
+        if (lane == 0) s_red[8] = bound;
+    }
+    __syncthreads();
+    return s_red[8];
+}
+
+__device__ __forceinline__ void load16(const float* __restrict__ x, float (&xs)[kCutVPT])
+{
+    const float4* xv = reinterpret_cast<const float4*>(x + threadIdx.x * kCutVPT);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float4 a = xv[k];
+        xs[4 * k] = a.x;
+        xs[4 * k + 1] = a.y;
+        xs[4 * k + 2] = a.z;
+        xs[4 * k + 3] = a.w;
+    }
+}
+
+__device__ float block_cutoff(const float* __restrict__ x, const uint16_t* __restrict__ probes,
+                              int quantile, float* s_red, int* s_cnt, float* s_cand)
+{
+    float xs[kCutVPT];
+    uint4 pr[2];
+    load_probes(probes, pr);
+    load16(x, xs);
+    return block_cutoff_x(xs, pr, quantile, s_red, s_cnt, s_cand);
+}
+
+// rmsNorm32fast (aux.cl:156-196) of a 4096-vector by one 256-thread
+// workgroup, in the reference's fp32 order: 16 consecutive squares per
+// thread summed in order, then the 256-way tree (pairs tid, tid + st for st =
+// 128 .. 1: the first two levels through LDS, the rest as shuffles in wave
+// 0), scale = 1/sqrt(sum/4096 + eps) rounded from double, then the fp16 gain
+// (mul16x32, aux.cl:434-440).  v holds h[16*tid ..] on entry and the
+// normalized values on exit; gr the thread's 16 gains (gain[16*tid ..]).
+// s_red needs 257 floats; ends with a barrier.
+__device__ __forceinline__ void block_rmsnorm4096(float (&v)[kCutVPT], const uint4 (&gr)[2], float eps, float* s_red)
+{
+#pragma clang fp contract(off)
+    const int tid = threadIdx.x;
+    const uint4 g0 = gr[0], g1 = gr[1];
+    float sq = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kCutVPT; k++) sq = __fadd_rn(sq, __fmul_rn(v[k], v[k]));
+    s_red[tid] = sq;
+    __syncthreads();
+    if (tid < 64) {
+        // lane l: part[l] + part[l+128] and part[l+64] + part[l+192] (st = 128),
+        // their sum (st = 64), then st = 32 .. 1 as shuffles
+        const float a = __fadd_rn(s_red[tid], s_red[tid + 128]);
+        const float b = __fadd_rn(s_red[tid + 64], s_red[tid + 192]);
+        sq = __fadd_rn(a, b);
+#pragma unroll
+        for (int st = 32; st > 0; st >>= 1) sq = __fadd_rn(sq, __shfl_down(sq, st, 64));
+        if (tid == 0) s_red[256] = sq;
+    }
+    __syncthreads();
+    const float mean = __fdiv_rn(s_red[256], 4096.0f);
+    const float scale = (float)(1.0 / sqrt((double)__fadd_rn(mean, eps)));
+    const uint32_t gw[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+    for (int k = 0; k < kCutVPT; k++)
+        v[k] = __fmul_rn(h2f(gw[k >> 1] >> ((k & 1) * 16)), __fmul_rn(v[k], scale));
 }
 
 // --------------------------------------------------------------- cutoff ---
-// One workgroup per matrix: the cutoff of findCutoffBinarySearch, and the
-// selected-row counter of the walk cleared (the walk adds to it).
+// One workgroup per matrix: the cutoff of findCutoffBinarySearch.
 struct CutoffDesc {
     const float* x;
     const uint16_t* probes;   // already offset to the expert
     int quantile;
     float* cutoff;
-    uint32_t* count;
 };
 
 struct CutoffArgs {
@@ -130,14 +255,12 @@ struct CutoffArgs {
 
 __global__ __launch_bounds__(kCutThreads) void k_cutoff(CutoffArgs a)
 {
-    __shared__ float s_red[8];
-    __shared__ int s_cnt[8];
+    __shared__ float s_red[16];
+    __shared__ int s_cnt[16];
+    __shared__ float s_cand[kCandCap];
     const CutoffDesc& d = a.d[blockIdx.x];
-    const float cut = block_cutoff(d.x, d.probes, d.quantile, s_red, s_cnt);
-    if (threadIdx.x == 0) {
-        d.cutoff[0] = cut;
-        d.count[0] = 0u;
-    }
+    const float cut = block_cutoff(d.x, d.probes, d.quantile, s_red, s_cnt, s_cand);
+    if (threadIdx.x == 0) d.cutoff[0] = cut;
 }
 
 // ------------------------------------------------------------- dispatch ---
@@ -165,8 +288,9 @@ struct DispatchArgs {
 __global__ __launch_bounds__(kCutThreads) void k_dispatch(DispatchArgs a)
 {
 #pragma clang fp contract(off)
-    __shared__ float s_red[8];
-    __shared__ int s_cnt[8];
+    __shared__ float s_red[16];
+    __shared__ int s_cnt[16];
+    __shared__ float s_cand[kCandCap];
     __shared__ int s_wsum[4];
 
     int k = 0;
@@ -178,7 +302,7 @@ __global__ __launch_bounds__(kCutThreads) void k_dispatch(DispatchArgs a)
     const int lane = tid & 63;
     const int wave = tid >> 6;
 
-    const float cutoff = block_cutoff(d.x, d.probes, d.quantile, s_red, s_cnt);
+    const float cutoff = block_cutoff(d.x, d.probes, d.quantile, s_red, s_cnt, s_cand);
     if (g == 0 && tid == 0) d.cutoff[1] = cutoff;   // cross-checked against k_cutoff's cutoff[0]
 
     // prepareDispatch (bucketMul.cl:362-385) for the 16 rows of input i
@@ -318,12 +442,17 @@ __device__ __forceinline__ double walk_acc<double>(double x, double w, double ol
 // the last selected row with x = 0), so they are in flight together.
 struct WalkDesc {
     const uint16_t* W;        // rows of the expert: W[row * C + col]
-    const float* x;
+    float* x;
     const uint16_t* stats;    // row 0 of the expert
-    const float* cutoff;
-    uint32_t* count;          // selected rows, added by the tile-0 workgroups
+    float* cutoff;
+    uint32_t* slice_count;    // [P]: rows selected per slice (tile-0 workgroups)
     void* part;               // [P][16*C] partial sums (Acc), one row per slice
-    unsigned long long* counters;   // walk bytes, rows, matrices
+    const float* h;           // kInNorm: the vector to normalize
+    const uint16_t* gain;     // kInNorm: fp16 gain
+    const uint16_t* probes;   // kInX / kInNorm: probes of the expert
+    float eps;
+    int quantile;
+    int in_mode;              // WalkIn
     int stats_stride;
     int stats_channel;
     int rows;                 // R
@@ -348,48 +477,88 @@ struct WalkArgs {
 // input*16 + rank); s_x[i] = x[i0 + i].  Ends with a barrier; returns the
 // number of selected rows.  The tile-0 workgroup of the slice adds the count
 // to the matrix's counters.
+// Loads of the selection: the 16 stats (channel stats_channel) of input
+// i0 + tid's rows and, unless x_lds, its x.  Issued before the cutoff is
+// known so that their latency overlaps the search; the raw words are kept
+// (unpacked by select_finish) so that nothing waits for them here.  Layouts:
+// compact stats (stride 1, 2 x 16 bytes), the reference's [R][4] with channel
+// 3 (8 x 16 bytes), otherwise 16 scalar loads.
+struct SelLoads {
+    uint4 raw[8];
+    uint32_t sv[16];
+    float xi;
+    int kind;   // 0: stride 1, 1: stride 4 channel 3, 2: scalar
+};
+
+__device__ __forceinline__ void select_load(const WalkDesc& d, int i0, int ni, bool x_lds, SelLoads& L)
+{
+    const int tid = threadIdx.x;
+    L.xi = 0.0f;
+    const int i = i0 + min(tid, ni - 1);   // threads past the slice re-read its last input
+    const int r0 = i * 16;
+    const uint16_t* base = d.stats + (size_t)i0 * 16 * d.stats_stride;
+    const bool aligned = (((uintptr_t)base) & 15) == 0 && (d.rows & 15) == 0;
+    if (!x_lds) L.xi = d.x[i];
+    const uint16_t* st = d.stats + (size_t)r0 * d.stats_stride;
+    if (aligned && d.stats_stride == 1) {
+        L.kind = 0;
+        const uint4* p4 = reinterpret_cast<const uint4*>(st);
+        L.raw[0] = p4[0];
+        L.raw[1] = p4[1];
+    } else if (aligned && d.stats_stride == 4 && d.stats_channel == 3) {
+        L.kind = 1;
+        const uint4* p4 = reinterpret_cast<const uint4*>(st);
+#pragma unroll
+        for (int k8 = 0; k8 < 8; k8++) L.raw[k8] = p4[k8];
+    } else {
+        L.kind = 2;
+#pragma unroll
+        for (int kk = 0; kk < 16; kk++) {
+            const int rr = min(r0 + kk, d.rows - 1) - r0;
+            L.sv[kk] = st[(size_t)rr * d.stats_stride + d.stats_channel];
+        }
+    }
+}
+
+// The selection of slice p given its loads (prepareDispatch,
+// bucketMul.cl:351-386): a row is selected iff 1e5 * |x * stat| >= cutoff,
+// the same fp32 operations as the dispatch kernel, so the selected set is
+// the same.  A block scan compacts the selected rows in ascending order into
+// s_row (slice-local ids input*16 + rank); s_x[i] = x[i0 + i] (with x_lds it
+// already holds them, written before a barrier).  Ends with a barrier;
+// returns the number of selected rows, which the tile-0 workgroup of the
+// slice also stores in slice_count[p].
 template <int NT>
-__device__ uint32_t select_slice(const WalkDesc& d, int p, int t, int i0, int ni, uint16_t* s_row, float* s_x,
-                                 uint32_t* s_wsum)
+__device__ __forceinline__ uint32_t select_finish(const WalkDesc& d, float cutoff, int p, int t, int i0, int ni,
+                                                  const SelLoads& L, uint16_t* s_row, float* s_x, uint32_t* s_wsum,
+                                                  bool x_lds)
 {
 #pragma clang fp contract(off)
     constexpr int NW = NT / 64;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const float cutoff = *d.cutoff;
+    float xi = L.xi;
     uint32_t mask = 0;
-    float xi = 0.0f;
     if (tid < ni) {
-        const int i = i0 + tid;
-        const int r0 = i * 16;
-        xi = d.x[i];
+        if (x_lds) xi = s_x[tid];
         uint32_t sv[16];
-        const uint16_t* st = d.stats + (size_t)r0 * d.stats_stride;
-        const bool whole = r0 + 16 <= d.rows;
-        if (whole && d.stats_stride == 1 && (((uintptr_t)st) & 15) == 0) {
-            const uint4* p4 = reinterpret_cast<const uint4*>(st);
-            const uint4 a0 = p4[0], a1 = p4[1];
-            const uint32_t ww[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        if (L.kind == 0) {
+            const uint32_t ww[8] = {L.raw[0].x, L.raw[0].y, L.raw[0].z, L.raw[0].w,
+                                    L.raw[1].x, L.raw[1].y, L.raw[1].z, L.raw[1].w};
 #pragma unroll
             for (int kk = 0; kk < 16; kk++) sv[kk] = (ww[kk >> 1] >> ((kk & 1) * 16)) & 0xffffu;
-        } else if (whole && d.stats_stride == 4 && d.stats_channel == 3 && (((uintptr_t)st) & 15) == 0) {
-            const uint4* p4 = reinterpret_cast<const uint4*>(st);
-            uint4 q8[8];
-#pragma unroll
-            for (int k8 = 0; k8 < 8; k8++) q8[k8] = p4[k8];
+        } else if (L.kind == 1) {
 #pragma unroll
             for (int k8 = 0; k8 < 8; k8++) {
-                sv[2 * k8] = q8[k8].y >> 16;       // row 2*k8, channel 3
-                sv[2 * k8 + 1] = q8[k8].w >> 16;   // row 2*k8+1, channel 3
+                sv[2 * k8] = L.raw[k8].y >> 16;       // row 2*k8, channel 3
+                sv[2 * k8 + 1] = L.raw[k8].w >> 16;   // row 2*k8+1, channel 3
             }
         } else {
 #pragma unroll
-            for (int kk = 0; kk < 16; kk++) {
-                const int rr = min(r0 + kk, d.rows - 1) - r0;
-                sv[kk] = st[(size_t)rr * d.stats_stride + d.stats_channel];
-            }
+            for (int kk = 0; kk < 16; kk++) sv[kk] = L.sv[kk];
         }
+        const int r0 = (i0 + tid) * 16;
 #pragma unroll
         for (int kk = 0; kk < 16; kk++) {
             const float avg = h2f(sv[kk]);
@@ -406,7 +575,7 @@ __device__ uint32_t select_slice(const WalkDesc& d, int p, int t, int i0, int ni
         if (lane >= o) incl += v;
     }
     if (lane == 63) s_wsum[wave] = incl;
-    s_x[tid] = xi;
+    if (!x_lds) s_x[tid] = tid < ni ? xi : 0.0f;
     __syncthreads();
     uint32_t off = incl - cnt;
     uint32_t n_sel = 0;
@@ -420,13 +589,17 @@ __device__ uint32_t select_slice(const WalkDesc& d, int p, int t, int i0, int ni
         s_row[off++] = (uint16_t)(tid * 16 + kk);
     }
     __syncthreads();
-    if (t == 0 && tid == 0) {
-        atomicAdd(d.count, n_sel);
-        atomicAdd(d.counters + 0, (unsigned long long)n_sel * (unsigned long long)d.C * 2ull);
-        atomicAdd(d.counters + 1, (unsigned long long)n_sel);
-        if (p == 0) atomicAdd(d.counters + 2, 1ull);
-    }
+    if (t == 0 && tid == 0) d.slice_count[p] = n_sel;
     return n_sel;
+}
+
+template <int NT>
+__device__ uint32_t select_slice(const WalkDesc& d, float cutoff, int p, int t, int i0, int ni, uint16_t* s_row,
+                                 float* s_x, uint32_t* s_wsum)
+{
+    SelLoads L;
+    select_load(d, i0, ni, false, L);
+    return select_finish<NT>(d, cutoff, p, t, i0, ni, L, s_row, s_x, s_wsum, false);
 }
 
 template <int VEC, typename Acc, int NW, int UNR>
@@ -461,7 +634,7 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     // ---- selection of the slice's rows
     const int i0 = p * d.IPS;
     const int ni = min(d.IPS, d.n_in - i0);
-    const uint32_t n_sel = select_slice<NT>(d, p, t, i0, ni, s_row, s_x, s_wsum);
+    const uint32_t n_sel = select_slice<NT>(d, *d.cutoff, p, t, i0, ni, s_row, s_x, s_wsum);
 
     // ---- walk of the selected rows
     const int q = lane / NJ;
@@ -581,10 +754,13 @@ __global__ __launch_bounds__(64 * NW) void k_walk64(WalkArgs a)
     constexpr int TW = 128;
     constexpr int SLOTS = TW * 16;             // accumulators per wave
     constexpr int GSTRIDE = NW * UNR;          // groups per workgroup batch
+    static_assert(NT == kCutThreads, "the fused search and norm need 256 threads");
     __shared__ double acc[NW * SLOTS];
-    __shared__ uint16_t s_row[NT * 16];
+    __shared__ __align__(16) uint16_t s_row[NT * 16];
     __shared__ float s_x[NT];
     __shared__ uint32_t s_wsum[NW];
+    __shared__ float s_red[260];
+    __shared__ int s_cnt[16];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -598,15 +774,52 @@ __global__ __launch_bounds__(64 * NW) void k_walk64(WalkArgs a)
     const int p = w / d.T;
     const int t = w - p * d.T;
 
+    // every global load of the prologue is issued before any of it is used
+    const int i0 = p * d.IPS;
+    const int ni = min(d.IPS, d.n_in - i0);
+    const bool x_lds = d.in_mode == kInNorm;
+    float xs[kCutVPT];
+    uint4 pr[2], gr[2];
+    float cutoff = 0.0f;
+    if (d.in_mode == kInCutoff) {
+        cutoff = *d.cutoff;
+    } else {
+        load_probes(d.probes, pr);
+        load16(d.in_mode == kInNorm ? d.h : d.x, xs);
+        if (d.in_mode == kInNorm) {
+            gr[0] = reinterpret_cast<const uint4*>(d.gain + tid * kCutVPT)[0];
+            gr[1] = reinterpret_cast<const uint4*>(d.gain + tid * kCutVPT)[1];
+        }
+    }
+    SelLoads L;
+    select_load(d, i0, ni, x_lds, L);
     {
         double2* z = reinterpret_cast<double2*>(acc + wave * SLOTS);
 #pragma unroll
         for (int i = 0; i < SLOTS / 128; i++) z[i * 64 + lane] = make_double2(0.0, 0.0);
     }
-
-    const int i0 = p * d.IPS;
-    const int ni = min(d.IPS, d.n_in - i0);
-    const int ns = (int)select_slice<NT>(d, p, t, i0, ni, s_row, s_x, s_wsum);
+    if (d.in_mode != kInCutoff) {
+        if (d.in_mode == kInNorm) {
+            block_rmsnorm4096(xs, gr, d.eps, s_red);
+            if (w == 0 && k == 0) {
+                float4* xo = reinterpret_cast<float4*>(d.x + tid * kCutVPT);
+#pragma unroll
+                for (int k4 = 0; k4 < 4; k4++)
+                    xo[k4] = make_float4(xs[4 * k4], xs[4 * k4 + 1], xs[4 * k4 + 2], xs[4 * k4 + 3]);
+            }
+            // the slice's inputs for the selection (4096 inputs: all in xs)
+#pragma unroll
+            for (int k2 = 0; k2 < kCutVPT; k2++) {
+                const int i = tid * kCutVPT + k2 - i0;
+                if (i >= 0 && i < ni) s_x[i] = xs[k2];
+            }
+        }
+        // s_row is free until the selection: it holds the search's bracket values
+        static_assert(sizeof(uint16_t) * NT * 16 >= sizeof(float) * kCandCap, "s_row too small");
+        cutoff = block_cutoff_x(xs, pr, d.quantile, s_red, s_cnt, reinterpret_cast<float*>(s_row));
+        if (w == 0 && tid == 0) d.cutoff[0] = cutoff;
+    }
+    const int ns = (int)select_finish<NT>(d, cutoff, p, t, i0, ni, L, s_row, s_x, s_wsum, x_lds);
 
     const int j = lane & 15;
     const int q = lane >> 4;
@@ -684,53 +897,144 @@ __global__ __launch_bounds__(64 * NW) void k_walk64(WalkArgs a)
     for (int o = tid; o < nout; o += NT) prow[o] = acc[o + (o >> 7)];
 }
 
-// y[o] = sum over row slices of part[p][o], in slice order 0..P-1 grouped by
-// p mod 16 then combined in group order: a fixed order, so y is the same on
-// every run (bucketIntegrate, bucketMul.cl:453-497, sums 64 fixed slices).
+// y[o] = sum over the P row slices of part[p][o] (bucketIntegrate,
+// bucketMul.cl:453-497, sums 64 fixed slices), then the epilogue of the op
+// that consumes y.  Workgroup = 128 outputs; thread (ol, pg) sums outputs
+// 4ol..4ol+3 over slices pg, pg+8, ...; the 8 group sums are added in group
+// order.  The order is fixed, so y is the same on every run.  Block 0 of each
+// matrix adds up the per-slice selected-row counts.
 struct ReduceDesc {
-    const void* part;
+    const void* part;              // [P][m] of Acc
     float* y;
-    int P;
-    int m;
+    const uint32_t* slice_count;   // [P]
+    uint32_t* count;               // total selected rows
+    const void* part2;             // kEpSilu: the up projection's partials, counts and output
+    float* y2;
+    const uint32_t* slice_count2;
+    uint32_t* count2;
+    float* out;
+    const float* table;            // RoPE table [max_ctx][hd/2][2]
+    const int* pos;
+    uint16_t* cache;               // fp16 rows [max_ctx][m]
+    int P, P2, m, C;
+    int ep;
+    int max_ctx;
     int block_base;
 };
 
 struct ReduceArgs {
     ReduceDesc d[kMaxMulti];
     int n;
+    unsigned long long* counters;  // walk bytes, rows, matrices
 };
 
-constexpr int kRedOut = 64;   // outputs per reduce block
+constexpr int kRedOut = 128;   // outputs per reduce workgroup (one head of 128 for RoPE)
+
+template <typename Acc>
+__device__ __forceinline__ Acc group_sums(const Acc* __restrict__ part, int P, int m, int o, int pg, Acc (*red)[kRedOut],
+                                          int ol)
+{
+    Acc s[4] = {(Acc)0, (Acc)0, (Acc)0, (Acc)0};
+    if (o < m) {
+        // slices pg, pg + 8, ... added in order; the loads of 4 slices in flight
+        int p = pg;
+        for (; p + 24 < P; p += 32) {
+            Acc r[4][4];
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) r[u][i] = part[(size_t)(p + 8 * u) * m + o + i];
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) s[i] += r[u][i];
+        }
+        for (; p < P; p += 8)
+#pragma unroll
+            for (int i = 0; i < 4; i++) s[i] += part[(size_t)p * m + o + i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) red[pg][ol * 4 + i] = s[i];
+    __syncthreads();
+    const int tid = threadIdx.x;
+    Acc t = (Acc)0;
+    if (tid < kRedOut) {
+        t = red[0][tid];
+#pragma unroll
+        for (int g = 1; g < 8; g++) t += red[g][tid];
+    }
+    __syncthreads();
+    return t;
+}
+
+__device__ void sum_counts(const uint32_t* __restrict__ sc, int P, int C, uint32_t* count,
+                           unsigned long long* counters, unsigned long long* s_sum)
+{
+    const int tid = threadIdx.x;
+    unsigned long long v = 0;
+    for (int p = tid; p < P; p += 256) v += sc[p];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    if ((tid & 63) == 0) s_sum[tid >> 6] = v;
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned long long S = s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3];
+        count[0] = (uint32_t)S;
+        atomicAdd(counters + 0, S * (unsigned long long)C * 2ull);
+        atomicAdd(counters + 1, S);
+        atomicAdd(counters + 2, 1ull);
+    }
+    __syncthreads();
+}
 
 template <typename Acc>
 __global__ __launch_bounds__(256) void k_reduce(ReduceArgs a)
 {
-    __shared__ Acc red[16][kRedOut];
+#pragma clang fp contract(off)
+    __shared__ Acc red[8][kRedOut];
+    __shared__ float sy[kRedOut];
+    __shared__ unsigned long long s_sum[4];
     const int b = (int)blockIdx.x;
     int k = 0;
     for (int i = 1; i < a.n; i++)
         if (b >= a.d[i].block_base) k = i;
     const ReduceDesc& d = a.d[k];
-    const Acc* part = reinterpret_cast<const Acc*>(d.part);
-    const int o0 = (b - d.block_base) * kRedOut;
+    const int lb = b - d.block_base;
+    const int o0 = lb * kRedOut;
     const int tid = threadIdx.x;
-    const int ol = tid & 15, pg = tid >> 4;
-    const int o = o0 + ol * 4;   // m is a multiple of 16, so o..o+3 are in range together
-    Acc s[4] = {(Acc)0, (Acc)0, (Acc)0, (Acc)0};
-    if (o < d.m) {
-        for (int p = pg; p < d.P; p += 16) {
-            const Acc* r = part + (size_t)p * d.m + o;
-#pragma unroll
-            for (int i = 0; i < 4; i++) s[i] += r[i];
-        }
+    const int ol = tid & 31, pg = tid >> 5;
+    const int o = o0 + ol * 4;   // m is a multiple of 16: o..o+3 are in range together
+    if (lb == 0) {
+        sum_counts(d.slice_count, d.P, d.C, d.count, a.counters, s_sum);
+        if (d.ep == kEpSilu) sum_counts(d.slice_count2, d.P2, d.C, d.count2, a.counters, s_sum);
     }
-#pragma unroll
-    for (int i = 0; i < 4; i++) red[pg][ol * 4 + i] = s[i];
-    __syncthreads();
-    if (tid < kRedOut && o0 + tid < d.m) {
-        Acc t = red[0][tid];
-        for (int g = 1; g < 16; g++) t += red[g][tid];
-        d.y[o0 + tid] = (float)t;
+    const float yv = (float)group_sums<Acc>(reinterpret_cast<const Acc*>(d.part), d.P, d.m, o, pg, red, ol);
+    const int oo = o0 + tid;
+    const bool in = tid < kRedOut && oo < d.m;
+    if (in) d.y[oo] = yv;
+    if (d.ep == kEpSilu) {
+        const float uv = (float)group_sums<Acc>(reinterpret_cast<const Acc*>(d.part2), d.P2, d.m, o, pg, red, ol);
+        if (in) {
+            d.y2[oo] = uv;
+            const double x1 = (double)yv;
+            d.out[oo] = (float)((double)uv * x1 / (1.0 + exp(-x1)));
+        }
+    } else if (d.ep == kEpResid) {
+        if (in) d.out[oo] = __fadd_rn(d.out[oo], yv);
+    } else if (d.ep != kEpStore) {
+        const int pos = *d.pos;
+        const bool pos_ok = pos >= 0 && pos < d.max_ctx;
+        if (d.ep == kEpV) {
+            if (in && pos_ok) d.cache[(size_t)pos * d.m + oo] = __half_as_ushort(__float2half_rn(yv));
+        } else {
+            if (tid < kRedOut) sy[tid] = yv;
+            __syncthreads();
+            if (in && pos_ok) {
+                const float r = rope_one(sy, d.table + (size_t)pos * kRedOut, tid, kRedOut / 2);
+                if (d.ep == kEpRopeQ) d.out[oo] = r;
+                else d.cache[(size_t)pos * d.m + oo] = __half_as_ushort(__float2half_rn(r));
+            }
+        }
     }
 }
 
@@ -840,12 +1144,13 @@ void plan_walk(int n, const MatOp* ops, float effort, bool acc64, WalkPlan* plan
 
 // Record the selection problem of matrix op i in slot i and compute the
 // cutoffs (one workgroup per matrix).
-int bucketmul_dispatch(Ctx* c, int n, const MatOp* ops, int expert_no, float effort)
+// Validate the n matrix ops and record their selection problems in slots
+// 0..n-1; fills the cutoff launch arguments.
+static int record_slots(Ctx* c, int n, const MatOp* ops, int expert_no, float effort, CutoffArgs& args)
 {
     IAM_REQUIRE(n >= 1 && n <= kMaxMulti, "bucketmul: 1..3 matrices per launch");
     IAM_REQUIRE(!std::isnan(effort), "bucketmul: effort is NaN");
     IAM_REQUIRE(expert_no >= 0, "bucketmul: negative expert_no");
-    CutoffArgs args{};
     args.n = n;
     const int qv = quantile_of(effort);
     for (int i = 0; i < n; i++) {
@@ -886,8 +1191,14 @@ int bucketmul_dispatch(Ctx* c, int n, const MatOp* ops, int expert_no, float eff
         d.probes = probes;
         d.quantile = qv;
         d.cutoff = s.cutoff;
-        d.count = s.count;
     }
+    return IAM_OK;
+}
+
+int bucketmul_dispatch(Ctx* c, int n, const MatOp* ops, int expert_no, float effort)
+{
+    CutoffArgs args{};
+    IAM_TRY(record_slots(c, n, ops, expert_no, effort, args));
     return launch(c, "bucket_cutoff", k_cutoff, dim3(n), dim3(kCutThreads), 0, args);
 }
 
@@ -936,7 +1247,35 @@ static int launch_walk(Ctx* c, int nw, int vec, int blocks, const WalkArgs& args
     return launch_walk_shape<Acc, IAM_WALK_BIG_NW, IAM_WALK_BIG_UNR>(c, vec, blocks, args);
 }
 
-int bucketmul_walk(Ctx* c, int n, const MatOp* ops)
+// Partial sums [P][m] of the accumulator type, then the per-slice selected
+// row counts [P].
+static size_t partial_bytes(const WalkPlan& pl, int C, bool acc64)
+{
+    return (size_t)pl.P * C * 16 * (acc64 ? 8 : 4) + (size_t)pl.P * sizeof(uint32_t);
+}
+
+static uint32_t* slice_counts(const DispatchSlot& s, const WalkPlan& pl, bool acc64)
+{
+    return reinterpret_cast<uint32_t*>(static_cast<char*>(s.part) + (size_t)pl.P * s.bucket_cols * 16 * (acc64 ? 8 : 4));
+}
+
+int reserve_walk(Ctx* c, int n, const MatOp* ops, float effort)
+{
+    WalkPlan plan[kMaxMulti];
+    plan_walk(n, ops, effort, c->acc64, plan);
+    for (int i = 0; i < n; i++) {
+        IAM_TRY(ensure_slot(c, i));
+        IAM_TRY(ensure_partials(c, i, partial_bytes(plan[i], ops[i].mat.bucket_cols, c->acc64)));
+    }
+    return IAM_OK;
+}
+
+// Walk and reduce of slots 0..n-1 (recorded by record_slots).  in_mode is how
+// the k_walk64 launches get x and the cutoff (k_walk always reads the
+// cutoff of a preceding k_cutoff launch); ep (null: store y) the epilogue of
+// each op, kEpSilu pairing ops 0 (gate) and 1 (up).
+static int walk_and_reduce(Ctx* c, int n, const MatOp* ops, int in_mode, const float* h, const uint16_t* gain,
+                           float eps, const ReduceEp* ep)
 {
     IAM_REQUIRE(n >= 1 && n <= kMaxMulti, "bucketmul: 1..3 matrices per launch");
     for (int i = 0; i < n; i++) {
@@ -962,11 +1301,11 @@ int bucketmul_walk(Ctx* c, int n, const MatOp* ops)
     }
     WalkPlan plan[kMaxMulti];
     plan_walk(n, wops, c->slots[0].effort, c->acc64, plan);
-    const size_t acc_bytes = c->acc64 ? 8 : 4;
     for (int i = 0; i < n; i++)
-        IAM_TRY(ensure_partials(c, i, (size_t)plan[i].P * ops[i].mat.bucket_cols * 16 * acc_bytes));
+        IAM_TRY(ensure_partials(c, i, partial_bytes(plan[i], ops[i].mat.bucket_cols, c->acc64)));
+    const int qv = quantile_of(c->slots[0].effort);
 
-    // walk: one launch per load width (the model's matrices all share one)
+    // walk: one launch per kernel variant (the model's matrices all share one)
     bool used[kMaxMulti] = {false, false, false};
     for (int done = 0; done < n;) {
         int vec = 0, blocks = 0, cnt = 0, nw = 0;
@@ -978,12 +1317,17 @@ int bucketmul_walk(Ctx* c, int n, const MatOp* ops)
             const DispatchSlot& s = c->slots[i];
             WalkDesc& d = args.d[cnt++];
             d.W = ops[i].mat.buckets + (size_t)s.expert_no * (size_t)ops[i].mat.expert_rows * ops[i].mat.bucket_cols;
-            d.x = s.x;
+            d.x = const_cast<float*>(s.x);
             d.stats = s.stats;
             d.cutoff = s.cutoff;
-            d.count = s.count;
+            d.slice_count = slice_counts(s, plan[i], c->acc64);
             d.part = s.part;
-            d.counters = c->counters;
+            d.h = h;
+            d.gain = gain;
+            d.probes = s.probes;
+            d.eps = eps;
+            d.quantile = qv;
+            d.in_mode = vec == 8 ? in_mode : kInCutoff;
             d.stats_stride = s.stats_stride;
             d.stats_channel = s.stats_channel;
             d.rows = s.rows;
@@ -1005,21 +1349,74 @@ int bucketmul_walk(Ctx* c, int n, const MatOp* ops)
             IAM_TRY(c->acc64 ? launch_walk<double>(c, nw, vec, blocks, args)
                              : launch_walk<float>(c, nw, vec, blocks, args));
     }
-    // fixed-order sum of the slices into y
+    // fixed-order sum of the slices into y, with the epilogue
     ReduceArgs ra{};
-    ra.n = n;
-    int rblocks = 0;
+    ra.counters = c->counters;
+    int rblocks = 0, nd = 0;
     for (int i = 0; i < n; i++) {
-        ReduceDesc& d = ra.d[i];
-        d.part = c->slots[i].part;
+        const DispatchSlot& s = c->slots[i];
+        ReduceDesc& d = ra.d[nd++];
+        d.part = s.part;
         d.y = ops[i].y;
+        d.slice_count = slice_counts(s, plan[i], c->acc64);
+        d.count = s.count;
         d.P = plan[i].P;
         d.m = ops[i].mat.bucket_cols * 16;
+        d.C = ops[i].mat.bucket_cols;
+        d.ep = ep ? ep[i].ep : kEpStore;
+        if (ep) {
+            d.out = ep[i].out;
+            d.table = ep[i].table;
+            d.pos = ep[i].pos;
+            d.max_ctx = ep[i].max_ctx;
+            d.cache = ep[i].cache;
+        }
+        if (d.ep == kEpSilu) {
+            IAM_REQUIRE(i == 0 && n == 2 && ops[1].mat.bucket_cols == ops[0].mat.bucket_cols,
+                        "bucketmul: the SiLU epilogue pairs two matrices of one shape");
+            const DispatchSlot& s2 = c->slots[1];
+            d.part2 = s2.part;
+            d.y2 = ops[1].y;
+            d.slice_count2 = slice_counts(s2, plan[1], c->acc64);
+            d.count2 = s2.count;
+            d.P2 = plan[1].P;
+            i = n;   // the pair is one descriptor
+        }
         d.block_base = rblocks;
         rblocks += (d.m + kRedOut - 1) / kRedOut;
     }
+    ra.n = nd;
     if (c->acc64) return launch(c, "bucket_reduce", k_reduce<double>, dim3(rblocks), dim3(256), 0, ra);
     return launch(c, "bucket_reduce", k_reduce<float>, dim3(rblocks), dim3(256), 0, ra);
+}
+
+int bucketmul_walk(Ctx* c, int n, const MatOp* ops) { return walk_and_reduce(c, n, ops, kInCutoff, nullptr, nullptr, 0.0f, nullptr); }
+
+// One fused matrix group: record the slots, then either (all matrices on
+// k_walk64) a walk in which every workgroup computes its input (norm) and
+// cutoff itself, or the separate norm / cutoff launches before the walk;
+// then the reduce with its epilogue.  in_mode kInNorm: x = rmsnorm(h) *
+// gain is written to ops[0].x (every op must name the same x, 4096 inputs).
+int bucketmul_fused(Ctx* c, int n, const MatOp* ops, int expert_no, float effort, int in_mode, const float* h,
+                    const uint16_t* gain, float eps, const ReduceEp* ep)
+{
+    CutoffArgs args{};
+    IAM_TRY(record_slots(c, n, ops, expert_no, effort, args));
+    bool all64 = true;
+    for (int i = 0; i < n; i++) all64 = all64 && vec_of(ops[i].mat.bucket_cols, c->acc64) == 8;
+    if (in_mode == kInNorm) {
+        IAM_REQUIRE(h && gain, "bucketmul: norm input without h/gain");
+        for (int i = 0; i < n; i++)
+            IAM_REQUIRE(ops[i].in_size == kProbes && ops[i].x == ops[0].x,
+                        "bucketmul: the fused norm takes 4096 inputs shared by the group");
+        IAM_TRY(check_dev_range(c, h, kProbes * sizeof(float), "bucketmul h"));
+        IAM_TRY(check_dev_range(c, gain, kProbes * 2, "bucketmul gain"));
+        IAM_REQUIRE(((uintptr_t)h & 15) == 0 && ((uintptr_t)gain & 15) == 0, "bucketmul: h and gain must be 16-byte aligned");
+    }
+    if (all64) return walk_and_reduce(c, n, ops, in_mode, h, gain, eps, ep);
+    if (in_mode == kInNorm) IAM_TRY(rmsnorm(c, const_cast<float*>(h), nullptr, gain, kProbes, eps, const_cast<float*>(ops[0].x)));
+    IAM_TRY(launch(c, "bucket_cutoff", k_cutoff, dim3(n), dim3(kCutThreads), 0, args));
+    return walk_and_reduce(c, n, ops, kInCutoff, nullptr, nullptr, 0.0f, ep);
 }
 
 __global__ void k_stats_compact(const uint16_t* __restrict__ s, size_t rows, int stride, int ch,

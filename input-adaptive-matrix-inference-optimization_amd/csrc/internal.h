@@ -151,6 +151,40 @@ int bucketmul_dispatch(Ctx* c, int n, const MatOp* ops, int expert_no, float eff
 // selection + walk of slots 0..n-1 into per-slice partial sums, then the
 // fixed-order reduction into each y (overwritten)
 int bucketmul_walk(Ctx* c, int n, const MatOp* ops);
+
+// How a fused walk gets its input and cutoff.
+enum WalkIn : int {
+    kInCutoff = 0,   // x in memory, cutoff from a preceding cutoff launch
+    kInX = 1,        // x in memory; every walk workgroup runs the cutoff search itself
+    kInNorm = 2,     // x = rmsnorm(h) * gain (4096 inputs) computed by every
+                     // walk workgroup (the first one stores it to x), then the search
+};
+
+// What the reduce does with y after storing it.
+enum Epi : int {
+    kEpStore = 0,   // nothing more
+    kEpResid = 1,   // out += y (add32, bucketMul.cl:517-520)
+    kEpRopeQ = 2,   // out = rope(y) at *pos (rope_mx, aux.cl:227-248)
+    kEpRopeK = 3,   // cache row *pos = fp16(rope(y)) (attention.hpp:172-189, 281-309)
+    kEpV = 4,       // cache row *pos = fp16(y)
+    kEpSilu = 5,    // ops 0 (gate g) and 1 (up u): out = u * g / (1 + exp(-g)) (silu32, matrix.cl:27-32)
+};
+
+struct ReduceEp {
+    int ep = kEpStore;
+    float* out = nullptr;
+    const float* table = nullptr;   // RoPE table [max_ctx][64][2]
+    const int* pos = nullptr;       // device position
+    int max_ctx = 0;
+    uint16_t* cache = nullptr;      // fp16 rows [max_ctx][m]
+};
+
+// record + (norm, cutoff) + walk + reduce with epilogues of one matrix group;
+// ep may be null (store y)
+int bucketmul_fused(Ctx* c, int n, const MatOp* ops, int expert_no, float effort, int in_mode, const float* h,
+                    const uint16_t* gain, float eps, const ReduceEp* ep);
+// size the slots and partial buffers of a group so a later call allocates nothing
+int reserve_walk(Ctx* c, int n, const MatOp* ops, float effort);
 // grid plan of one matrix in a walk launch
 struct WalkPlan {
     int NW;     // waves per workgroup (the same for every matrix of a launch)

@@ -6,6 +6,17 @@
 
 namespace iam {
 
+// rope_mx (aux.cl:227-248): rotate-half pairs (d, d + hd/2) with the host
+// table row for the position ([hd/2] of {cos, sin}); no contraction, so it
+// matches the oracle.
+__device__ __forceinline__ float rope_one(const float* m, const float* row, int d, int half)
+{
+    const int fi = d < half ? d : d - half;
+    const float c = row[2 * fi], s = row[2 * fi + 1];
+    if (d < half) return __fsub_rn(__fmul_rn(m[d], c), __fmul_rn(m[d + half], s));
+    return __fadd_rn(__fmul_rn(m[d], c), __fmul_rn(m[d - half], s));
+}
+
 int rmsnorm(Ctx* c, float* h, const float* delta, const uint16_t* gain, int n, float eps, float* out);
 int add(Ctx* c, const float* a, const float* b, int n, float* out);
 int silu_mul(Ctx* c, const float* g, const float* u, int n, float* out);

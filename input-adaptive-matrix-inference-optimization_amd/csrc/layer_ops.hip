@@ -104,15 +104,6 @@ __global__ void k_silu_mul(const float* __restrict__ g, const float* __restrict_
 }
 
 // ---------------------------------------------------------------- RoPE ---
-// rope_mx (aux.cl:227-248): rotate-half pairs (d, d + hd/2) with the host
-// table row for the position; no contraction, so it matches the oracle.
-__device__ __forceinline__ float rope_one(const float* m, const float* row, int d, int half)
-{
-    const int fi = d < half ? d : d - half;
-    const float c = row[2 * fi], s = row[2 * fi + 1];
-    if (d < half) return __fsub_rn(__fmul_rn(m[d], c), __fmul_rn(m[d + half], s));
-    return __fadd_rn(__fmul_rn(m[d], c), __fmul_rn(m[d - half], s));
-}
 
 __global__ void k_rope(const float* __restrict__ in, const float* __restrict__ table,
                        const int* __restrict__ pos_p, int n_heads, int hd, int max_pos,

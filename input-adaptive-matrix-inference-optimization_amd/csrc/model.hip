@@ -153,8 +153,10 @@ __global__ __launch_bounds__(1024) void k_pick(const float* __restrict__ v, int 
     }
 }
 
-static int mat_op(iam_model* m, int n, const Mat* const* mats, const float* x, int in_size, float* const* ys,
-                  float effort)
+// One matrix group through bucketmul_fused: x (in memory, or the norm of h
+// written to x), cutoff, walk, reduce with the epilogues ep (null: store).
+static int mat_group(iam_model* m, int n, const Mat* const* mats, float* x, int in_size, float* const* ys,
+                     float effort, int in_mode, const float* h, const uint16_t* gain, const ReduceEp* ep)
 {
     MatOp ops[kMaxMulti];
     for (int i = 0; i < n; i++) {
@@ -163,12 +165,21 @@ static int mat_op(iam_model* m, int n, const Mat* const* mats, const float* x, i
         ops[i].in_size = in_size;
         ops[i].y = ys[i];
     }
-    IAM_TRY(bucketmul_dispatch(m->c, n, ops, 0, effort));
-    return bucketmul_walk(m->c, n, ops);
+    if (in_mode == kInNorm && in_size != kProbes) {
+        // the fused norm covers 4096 inputs; other widths normalize first
+        IAM_TRY(rmsnorm(m->c, const_cast<float*>(h), nullptr, gain, in_size, m->cfg.norm_eps, x));
+        in_mode = kInX;
+    }
+    return bucketmul_fused(m->c, n, ops, 0, effort, in_mode, h, gain, m->cfg.norm_eps, ep);
 }
 
 // One decode step reading token/pos from device memory.  logits_out may be
-// the model's own buffer or a caller buffer of vocab floats.
+// the model's own buffer or a caller buffer of vocab floats.  Per layer:
+//   q/k/v walk (attention norm of h fused in) -> reduce + RoPE + fp16 KV append
+//   -> attention -> o walk -> reduce + residual (h += o)
+//   -> w1/w3 walk (FFN norm of h fused in) -> reduce + SiLU gate
+//   -> w2 walk -> reduce + residual (h += d)
+// (transformer_layer.hpp:75-122, attention.hpp:135-202, feedforward.hpp:46-86).
 static int step(iam_model* m, float effort, const float* hidden_override, float* logits_out, bool pick)
 {
     Ctx* c = m->c;
@@ -185,41 +196,55 @@ static int step(iam_model* m, float effort, const float* hidden_override, float*
     const size_t kv_layer = (size_t)C.max_ctx * C.n_kv_heads * C.head_dim;
     for (int L = 0; L < C.n_layers; L++) {
         Layer& ly = m->layers[L];
-        // attention norm (with the previous layer's FFN residual folded in)
-        IAM_TRY(rmsnorm(c, m->h, L == 0 ? nullptr : m->d, ly.attn_gain, D, C.norm_eps, m->hn));
+        uint16_t* kc = m->kcache + (size_t)L * kv_layer;
+        uint16_t* vc = m->vcache + (size_t)L * kv_layer;
         {
             const Mat* mats[3] = {&ly.wq, &ly.wk, &ly.wv};
             float* ys[3] = {m->q, m->k, m->v};
-            IAM_TRY(mat_op(m, 3, mats, m->hn, D, ys, effort));
+            ReduceEp ep[3];
+            ep[0].ep = kEpRopeQ;
+            ep[0].out = m->qr;
+            ep[1].ep = kEpRopeK;
+            ep[1].cache = kc;
+            ep[2].ep = kEpV;
+            ep[2].cache = vc;
+            for (int i = 0; i < 3; i++) {
+                ep[i].table = m->rope;
+                ep[i].pos = m->pos;
+                ep[i].max_ctx = C.max_ctx;
+            }
+            IAM_TRY(mat_group(m, 3, mats, m->hn, D, ys, effort, kInNorm, m->h, ly.attn_gain, ep));
         }
-        uint16_t* kc = m->kcache + (size_t)L * kv_layer;
-        uint16_t* vc = m->vcache + (size_t)L * kv_layer;
-        IAM_TRY(rope_kv(c, m->q, m->k, m->v, m->rope, m->pos, C.n_heads, C.n_kv_heads, C.head_dim, C.max_ctx,
-                        m->qr, kc, vc));
         IAM_TRY(attention(c, m->qr, kc, vc, m->pos, C.n_heads, C.n_kv_heads, C.max_ctx, c->attn_ws, m->att));
         {
             const Mat* mats[1] = {&ly.wo};
             float* ys[1] = {m->o};
-            IAM_TRY(mat_op(m, 1, mats, m->att, D, ys, effort));
+            ReduceEp ep[1];
+            ep[0].ep = kEpResid;
+            ep[0].out = m->h;
+            IAM_TRY(mat_group(m, 1, mats, m->att, D, ys, effort, kInX, nullptr, nullptr, ep));
         }
-        IAM_TRY(rmsnorm(c, m->h, m->o, ly.ffn_gain, D, C.norm_eps, m->hn));
         {
             const Mat* mats[2] = {&ly.w1, &ly.w3};
             float* ys[2] = {m->g, m->u};
-            IAM_TRY(mat_op(m, 2, mats, m->hn, D, ys, effort));
+            ReduceEp ep[2];
+            ep[0].ep = kEpSilu;
+            ep[0].out = m->s;
+            IAM_TRY(mat_group(m, 2, mats, m->hn, D, ys, effort, kInNorm, m->h, ly.ffn_gain, ep));
         }
-        IAM_TRY(silu_mul(c, m->g, m->u, F, m->s));
         {
             const Mat* mats[1] = {&ly.w2};
             float* ys[1] = {m->d};
-            IAM_TRY(mat_op(m, 1, mats, m->s, F, ys, effort));
+            ReduceEp ep[1];
+            ep[0].ep = kEpResid;
+            ep[0].out = m->h;
+            IAM_TRY(mat_group(m, 1, mats, m->s, F, ys, effort, kInX, nullptr, nullptr, ep));
         }
     }
-    IAM_TRY(rmsnorm(c, m->h, m->d, m->final_gain, D, C.norm_eps, m->hn));
     {
         const Mat* mats[1] = {&m->lm};
         float* ys[1] = {logits_out};
-        IAM_TRY(mat_op(m, 1, mats, m->hn, D, ys, effort));
+        IAM_TRY(mat_group(m, 1, mats, m->hn, D, ys, effort, kInNorm, m->h, m->final_gain, nullptr));
     }
     if (pick)
         IAM_TRY(launch(c, "pick", k_pick, dim3(1), dim3(1024), 0, (const float*)logits_out, C.vocab, m->token,
@@ -245,10 +270,7 @@ static int reserve(iam_model* m, float effort)
             ops[i].mat = groups[gi][i]->desc();
             ops[i].in_size = ins[gi];
         }
-        WalkPlan plan[kMaxMulti];
-        plan_walk(sizes[gi], ops, effort, c->acc64, plan);
-        for (int i = 0; i < sizes[gi]; i++)
-            IAM_TRY(ensure_partials(c, i, (size_t)plan[i].P * ops[i].mat.bucket_cols * 16 * (c->acc64 ? 8 : 4)));
+        IAM_TRY(reserve_walk(c, sizes[gi], ops, effort));
     }
     return ensure_attn_ws(c, attention_ws_floats(C.n_heads, C.max_ctx));
 }
