@@ -40,9 +40,61 @@ __device__ __forceinline__ float h2f(uint32_t bits16)
     return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xffffu)));
 }
 
+// ------------------------------------------------------- wave reductions ---
+// DPP (gfx9 encodings): row_shr:n = 0x110 + n shifts within 16-lane rows,
+// row_bcast15 / row_bcast31 = 0x142 / 0x143 broadcast lane 15 / 31 of a row
+// group into the next rows (masked by row_mask).  Lanes with no source keep
+// `old`.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ int dpp_i(int old, int v)
+{
+    return __builtin_amdgcn_update_dpp(old, v, CTRL, ROW_MASK, 0xF, false);
+}
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_f(float old, float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK, 0xF,
+                                                      false));
+}
+
+// min / max over the 64 lanes, returned uniform
+__device__ __forceinline__ float wave_min(float v)
+{
+    v = fminf(v, dpp_f<0x111>(v, v));
+    v = fminf(v, dpp_f<0x112>(v, v));
+    v = fminf(v, dpp_f<0x114>(v, v));
+    v = fminf(v, dpp_f<0x118>(v, v));
+    v = fminf(v, dpp_f<0x142, 0xA>(v, v));
+    v = fminf(v, dpp_f<0x143, 0xC>(v, v));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+__device__ __forceinline__ float wave_max(float v)
+{
+    v = fmaxf(v, dpp_f<0x111>(v, v));
+    v = fmaxf(v, dpp_f<0x112>(v, v));
+    v = fmaxf(v, dpp_f<0x114>(v, v));
+    v = fmaxf(v, dpp_f<0x118>(v, v));
+    v = fmaxf(v, dpp_f<0x142, 0xA>(v, v));
+    v = fmaxf(v, dpp_f<0x143, 0xC>(v, v));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// inclusive prefix sum over the 64 lanes
+__device__ __forceinline__ int wave_incl_sum(int v)
+{
+    v += dpp_i<0x111>(0, v);
+    v += dpp_i<0x112>(0, v);
+    v += dpp_i<0x114>(0, v);
+    v += dpp_i<0x118>(0, v);
+    v += dpp_i<0x142, 0xA>(0, v);
+    v += dpp_i<0x143, 0xC>(0, v);
+    return v;
+}
+
 // --------------------------------------------------------------- cutoff ---
-// findCutoffBinarySearch (bucketMul.cl:68-214) for one 256-thread workgroup.
-// Every thread ends with the same cutoff.  s_red needs 8 floats, s_cnt 8 ints.
+// A wave-uniform float kept in a scalar register.
 __device__ __forceinline__ float uniform_f(float v)
 {
     return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
@@ -93,19 +145,18 @@ __device__ __forceinline__ float block_cutoff_x(const float (&xs)[kCutVPT], cons
         mn = fminf(mn, v[k]);
         mx = fmaxf(mx, v[k]);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        mn = fminf(mn, __shfl_xor(mn, o, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    }
+    mn = wave_min(mn);
+    mx = wave_max(mx);
     if (lane == 0) {
         s_red[wave] = mn;
         s_red[4 + wave] = mx;
     }
     __syncthreads();
     // the search state is uniform: keep it in scalar registers
-    const float gmin = uniform_f(fminf(fminf(s_red[0], s_red[1]), fminf(s_red[2], s_red[3])));
-    const float gmax = uniform_f(fmaxf(fmaxf(s_red[4], s_red[5]), fmaxf(s_red[6], s_red[7])));
+    const float4 mn4 = *reinterpret_cast<const float4*>(s_red);
+    const float4 mx4 = *reinterpret_cast<const float4*>(s_red + 4);
+    const float gmin = uniform_f(fminf(fminf(mn4.x, mn4.y), fminf(mn4.z, mn4.w)));
+    const float gmax = uniform_f(fmaxf(fmaxf(mx4.x, mx4.y), fmaxf(mx4.z, mx4.w)));
 
     const int target = kProbes - quantile;            // bucketMul.cl:81
     float minB = gmin, maxB = gmax;
@@ -151,9 +202,9 @@ __device__ __forceinline__ float block_cutoff_x(const float (&xs)[kCutVPT], cons
     }
     if (lane == 0) s_cnt[8 + wave] = wtot;
     __syncthreads();
-    int off = 0;
-    for (int w = 0; w < wave; w++) off += s_cnt[8 + w];
-    const int ncand = s_cnt[8] + s_cnt[9] + s_cnt[10] + s_cnt[11];   // <= minC - maxC <= kCandCap
+    const int4 wt = *reinterpret_cast<const int4*>(s_cnt + 8);
+    int off = (wave > 0 ? wt.x : 0) + (wave > 1 ? wt.y : 0) + (wave > 2 ? wt.z : 0);
+    const int ncand = wt.x + wt.y + wt.z + wt.w;   // <= minC - maxC <= kCandCap
 #pragma unroll
     for (int k = 0; k < 16; k++) {
         if ((bm[k] >> lane) & 1ull) s_cand[off + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bm[k] >> 32),
@@ -255,8 +306,8 @@ struct CutoffArgs {
 
 __global__ __launch_bounds__(kCutThreads) void k_cutoff(CutoffArgs a)
 {
-    __shared__ float s_red[16];
-    __shared__ int s_cnt[16];
+    __shared__ __align__(16) float s_red[16];
+    __shared__ __align__(16) int s_cnt[16];
     __shared__ float s_cand[kCandCap];
     const CutoffDesc& d = a.d[blockIdx.x];
     const float cut = block_cutoff(d.x, d.probes, d.quantile, s_red, s_cnt, s_cand);
@@ -288,8 +339,8 @@ struct DispatchArgs {
 __global__ __launch_bounds__(kCutThreads) void k_dispatch(DispatchArgs a)
 {
 #pragma clang fp contract(off)
-    __shared__ float s_red[16];
-    __shared__ int s_cnt[16];
+    __shared__ __align__(16) float s_red[16];
+    __shared__ __align__(16) int s_cnt[16];
     __shared__ float s_cand[kCandCap];
     __shared__ int s_wsum[4];
 
@@ -568,12 +619,7 @@ __device__ __forceinline__ uint32_t select_finish(const WalkDesc& d, float cutof
         }
     }
     const uint32_t cnt = (uint32_t)__popc(mask);
-    uint32_t incl = cnt;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t v = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += v;
-    }
+    const uint32_t incl = (uint32_t)wave_incl_sum((int)cnt);
     if (lane == 63) s_wsum[wave] = incl;
     if (!x_lds) s_x[tid] = tid < ni ? xi : 0.0f;
     __syncthreads();
@@ -759,8 +805,8 @@ __global__ __launch_bounds__(64 * NW) void k_walk64(WalkArgs a)
     __shared__ __align__(16) uint16_t s_row[NT * 16];
     __shared__ float s_x[NT];
     __shared__ uint32_t s_wsum[NW];
-    __shared__ float s_red[260];
-    __shared__ int s_cnt[16];
+    __shared__ __align__(16) float s_red[260];
+    __shared__ __align__(16) int s_cnt[16];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
