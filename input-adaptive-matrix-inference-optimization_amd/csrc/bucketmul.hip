@@ -28,6 +28,7 @@
 
 #include "internal.h"
 #include "layer_ops.h"
+#include "wave.h"
 
 namespace iam {
 
@@ -38,59 +39,6 @@ constexpr int kCutVPT = kProbes / kCutThreads;   // 16 importances per thread
 __device__ __forceinline__ float h2f(uint32_t bits16)
 {
     return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xffffu)));
-}
-
-// ------------------------------------------------------- wave reductions ---
-// DPP (gfx9 encodings): row_shr:n = 0x110 + n shifts within 16-lane rows,
-// row_bcast15 / row_bcast31 = 0x142 / 0x143 broadcast lane 15 / 31 of a row
-// group into the next rows (masked by row_mask).  Lanes with no source keep
-// `old`.
-template <int CTRL, int ROW_MASK = 0xF>
-__device__ __forceinline__ int dpp_i(int old, int v)
-{
-    return __builtin_amdgcn_update_dpp(old, v, CTRL, ROW_MASK, 0xF, false);
-}
-
-template <int CTRL, int ROW_MASK = 0xF>
-__device__ __forceinline__ float dpp_f(float old, float v)
-{
-    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK, 0xF,
-                                                      false));
-}
-
-// min / max over the 64 lanes, returned uniform
-__device__ __forceinline__ float wave_min(float v)
-{
-    v = fminf(v, dpp_f<0x111>(v, v));
-    v = fminf(v, dpp_f<0x112>(v, v));
-    v = fminf(v, dpp_f<0x114>(v, v));
-    v = fminf(v, dpp_f<0x118>(v, v));
-    v = fminf(v, dpp_f<0x142, 0xA>(v, v));
-    v = fminf(v, dpp_f<0x143, 0xC>(v, v));
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-
-__device__ __forceinline__ float wave_max(float v)
-{
-    v = fmaxf(v, dpp_f<0x111>(v, v));
-    v = fmaxf(v, dpp_f<0x112>(v, v));
-    v = fmaxf(v, dpp_f<0x114>(v, v));
-    v = fmaxf(v, dpp_f<0x118>(v, v));
-    v = fmaxf(v, dpp_f<0x142, 0xA>(v, v));
-    v = fmaxf(v, dpp_f<0x143, 0xC>(v, v));
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-
-// inclusive prefix sum over the 64 lanes
-__device__ __forceinline__ int wave_incl_sum(int v)
-{
-    v += dpp_i<0x111>(0, v);
-    v += dpp_i<0x112>(0, v);
-    v += dpp_i<0x114>(0, v);
-    v += dpp_i<0x118>(0, v);
-    v += dpp_i<0x142, 0xA>(0, v);
-    v += dpp_i<0x143, 0xC>(0, v);
-    return v;
 }
 
 // --------------------------------------------------------------- cutoff ---
@@ -974,30 +922,34 @@ struct ReduceArgs {
     unsigned long long* counters;  // walk bytes, rows, matrices
 };
 
-constexpr int kRedOut = 128;   // outputs per reduce workgroup (one head of 128 for RoPE)
+constexpr int kRedOut = 128;     // outputs per reduce workgroup (one head of 128 for RoPE)
+constexpr int kRedThreads = 256;
+constexpr int kRedGroups = kRedThreads / 32;   // slice groups: 32 threads x 4 outputs each
 
+// Thread (ol, pg) sums outputs 4ol..4ol+3 over the slices pg, pg + 32, ...
+// in slice order, with all of its loads issued together; the group sums are
+// then added in group order by threads 0..127 (which return the total).
 template <typename Acc>
-__device__ __forceinline__ Acc group_sums(const Acc* __restrict__ part, int P, int m, int o, int pg, Acc (*red)[kRedOut],
-                                          int ol)
+__device__ __forceinline__ Acc group_sums(const Acc* __restrict__ part, int P, int m, int o, int pg,
+                                          Acc (*red)[kRedOut], int ol)
 {
+    constexpr int U = 8;
     Acc s[4] = {(Acc)0, (Acc)0, (Acc)0, (Acc)0};
     if (o < m) {
-        // slices pg, pg + 8, ... added in order; the loads of 4 slices in flight
-        int p = pg;
-        for (; p + 24 < P; p += 32) {
-            Acc r[4][4];
+        for (int p0 = pg; p0 < P; p0 += U * kRedGroups) {
+            Acc r[U][4];
 #pragma unroll
-            for (int u = 0; u < 4; u++)
+            for (int u = 0; u < U; u++) {
+                const int p = min(p0 + u * kRedGroups, P - 1);
 #pragma unroll
-                for (int i = 0; i < 4; i++) r[u][i] = part[(size_t)(p + 8 * u) * m + o + i];
+                for (int i = 0; i < 4; i++) r[u][i] = part[(size_t)p * m + o + i];
+            }
 #pragma unroll
-            for (int u = 0; u < 4; u++)
+            for (int u = 0; u < U; u++)
+                if (p0 + u * kRedGroups < P)
 #pragma unroll
-                for (int i = 0; i < 4; i++) s[i] += r[u][i];
+                    for (int i = 0; i < 4; i++) s[i] += r[u][i];
         }
-        for (; p < P; p += 8)
-#pragma unroll
-            for (int i = 0; i < 4; i++) s[i] += part[(size_t)p * m + o + i];
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) red[pg][ol * 4 + i] = s[i];
@@ -1007,39 +959,36 @@ __device__ __forceinline__ Acc group_sums(const Acc* __restrict__ part, int P, i
     if (tid < kRedOut) {
         t = red[0][tid];
 #pragma unroll
-        for (int g = 1; g < 8; g++) t += red[g][tid];
+        for (int g = 1; g < kRedGroups; g++) t += red[g][tid];
     }
     __syncthreads();
     return t;
 }
 
+// total selected rows of a matrix (by one wave, no barrier) into count and
+// the context's counters
 __device__ void sum_counts(const uint32_t* __restrict__ sc, int P, int C, uint32_t* count,
-                           unsigned long long* counters, unsigned long long* s_sum)
+                           unsigned long long* counters)
 {
-    const int tid = threadIdx.x;
+    const int lane = threadIdx.x & 63;
     unsigned long long v = 0;
-    for (int p = tid; p < P; p += 256) v += sc[p];
+    for (int p = lane; p < P; p += 64) v += sc[p];
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    if ((tid & 63) == 0) s_sum[tid >> 6] = v;
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned long long S = s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3];
-        count[0] = (uint32_t)S;
-        atomicAdd(counters + 0, S * (unsigned long long)C * 2ull);
-        atomicAdd(counters + 1, S);
+    if (lane == 0) {
+        count[0] = (uint32_t)v;
+        atomicAdd(counters + 0, v * (unsigned long long)C * 2ull);
+        atomicAdd(counters + 1, v);
         atomicAdd(counters + 2, 1ull);
     }
-    __syncthreads();
 }
 
 template <typename Acc>
-__global__ __launch_bounds__(256) void k_reduce(ReduceArgs a)
+__global__ __launch_bounds__(kRedThreads) void k_reduce(ReduceArgs a)
 {
 #pragma clang fp contract(off)
-    __shared__ Acc red[8][kRedOut];
+    __shared__ Acc red[kRedGroups][kRedOut];
     __shared__ float sy[kRedOut];
-    __shared__ unsigned long long s_sum[4];
     const int b = (int)blockIdx.x;
     int k = 0;
     for (int i = 1; i < a.n; i++)
@@ -1050,10 +999,9 @@ __global__ __launch_bounds__(256) void k_reduce(ReduceArgs a)
     const int tid = threadIdx.x;
     const int ol = tid & 31, pg = tid >> 5;
     const int o = o0 + ol * 4;   // m is a multiple of 16: o..o+3 are in range together
-    if (lb == 0) {
-        sum_counts(d.slice_count, d.P, d.C, d.count, a.counters, s_sum);
-        if (d.ep == kEpSilu) sum_counts(d.slice_count2, d.P2, d.C, d.count2, a.counters, s_sum);
-    }
+    if (lb == 0 && tid >= kRedThreads - 64) sum_counts(d.slice_count, d.P, d.C, d.count, a.counters);
+    if (lb == 0 && d.ep == kEpSilu && tid >= kRedThreads - 128 && tid < kRedThreads - 64)
+        sum_counts(d.slice_count2, d.P2, d.C, d.count2, a.counters);
     const float yv = (float)group_sums<Acc>(reinterpret_cast<const Acc*>(d.part), d.P, d.m, o, pg, red, ol);
     const int oo = o0 + tid;
     const bool in = tid < kRedOut && oo < d.m;
@@ -1432,8 +1380,8 @@ static int walk_and_reduce(Ctx* c, int n, const MatOp* ops, int in_mode, const f
         rblocks += (d.m + kRedOut - 1) / kRedOut;
     }
     ra.n = nd;
-    if (c->acc64) return launch(c, "bucket_reduce", k_reduce<double>, dim3(rblocks), dim3(256), 0, ra);
-    return launch(c, "bucket_reduce", k_reduce<float>, dim3(rblocks), dim3(256), 0, ra);
+    if (c->acc64) return launch(c, "bucket_reduce", k_reduce<double>, dim3(rblocks), dim3(kRedThreads), 0, ra);
+    return launch(c, "bucket_reduce", k_reduce<float>, dim3(rblocks), dim3(kRedThreads), 0, ra);
 }
 
 int bucketmul_walk(Ctx* c, int n, const MatOp* ops) { return walk_and_reduce(c, n, ops, kInCutoff, nullptr, nullptr, 0.0f, nullptr); }

@@ -7,6 +7,7 @@
 
 #include "internal.h"
 #include "layer_ops.h"
+#include "wave.h"
 
 namespace iam {
 
@@ -146,16 +147,19 @@ __global__ void k_rope_kv(const float* __restrict__ q, const float* __restrict__
 
 // ------------------------------------------------------------ attention ---
 // Decode attention over an fp16 GQA cache, split over the context
-// ("flash-decoding").  Workgroup (kv head, split) handles kAttnChunk
+// ("flash-decoding").  Workgroup (kv head, split) handles kAttnChunk = 64
 // positions for the rep = n_heads/n_kv query heads that read this KV head
-// (repeat4x32, aux.cl:266-275, without materialising the repeat) and writes
-// the split's max m, sum l of exp(s - m) and unnormalised o; k_attn_combine
-// merges the splits.  Scores follow dotSetScore2 (aux.cl:497-540,
-// s = q.k / sqrt(hd)); the softmax of aux.cl:204-225 is exp(s)/sum exp(s),
-// evaluated with the running max subtracted, which leaves p unchanged.
-// Acc = double evaluates every dot product, exponential and sum in fp64
-// (products of fp32 and fp16 values are exact there) and rounds the output
-// once; Acc = float is the fp32 evaluation.
+// (repeat4x32, aux.cl:266-275, without materialising the repeat): wave r is
+// query head kvh*rep + r and lane i position t0 + i.  Each lane computes its
+// position's score over the 128 dimensions (dotSetScore2, aux.cl:497-540,
+// s = q.k / sqrt(hd)) with q broadcast from LDS; the softmax of
+// aux.cl:204-225 (exp(s)/sum exp(s)) is evaluated with the split's maximum
+// subtracted, which leaves p unchanged; then lane j accumulates dimensions
+// 2j, 2j+1 of sum p*V over the positions.  No value crosses waves, so there
+// is no barrier.  The split writes its max m, sum l of exp(s - m) and
+// unnormalised o; k_attn_combine merges the splits.  Acc = double evaluates
+// every product (exact: fp32 x fp16), exponential and sum in fp64 and the
+// output is rounded once; Acc = float is the fp32 evaluation.
 constexpr int kAttnChunk = 64;
 constexpr int kAttnMaxRep = 8;
 constexpr int kMaxAttnSplits = 128;   // max_ctx up to 8192
@@ -168,141 +172,74 @@ template <>
 __device__ __forceinline__ double acc_exp<double>(double x) { return exp(x); }
 
 template <typename Acc>
-__global__ __launch_bounds__(256) void k_attn_partial(const float* __restrict__ q,
-                                                      const uint16_t* __restrict__ kc,
-                                                      const uint16_t* __restrict__ vc,
-                                                      const int* __restrict__ pos_p, int n_heads,
-                                                      int n_kv, int max_ctx, Acc scale,
-                                                      Acc* __restrict__ ws, int n_split)
+__global__ __launch_bounds__(64 * kAttnMaxRep) void k_attn_partial(const float* __restrict__ q,
+                                                                   const uint16_t* __restrict__ kc,
+                                                                   const uint16_t* __restrict__ vc,
+                                                                   const int* __restrict__ pos_p, int n_heads,
+                                                                   int n_kv, int max_ctx, Acc scale,
+                                                                   Acc* __restrict__ ws, int n_split)
 {
     constexpr int HD = 128;
-    __shared__ Acc sq[kAttnMaxRep * HD];
-    __shared__ Acc sp[kAttnMaxRep * kAttnChunk];
-    __shared__ Acc sml[kAttnMaxRep * 2];
-    __shared__ Acc so[4 * kAttnMaxRep * HD];
+    __shared__ Acc sq[kAttnMaxRep][HD];
+    __shared__ Acc sp[kAttnMaxRep][kAttnChunk];
     const int kvh = blockIdx.x;
     const int split = blockIdx.y;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = threadIdx.x & 63;
+    const int r = threadIdx.x >> 6;
     const int rep = n_heads / n_kv;
     int n_tok = *pos_p + 1;
     if (n_tok > max_ctx) n_tok = max_ctx;
     const int t0 = split * kAttnChunk;
     const int nt = min(kAttnChunk, max(0, n_tok - t0));
     // workspace row of query head h = kvh*rep + r, split s: ws[(h*n_split + s)*(HD+2)]
-    Acc* wbase = ws + ((size_t)(kvh * rep) * n_split + split) * (HD + 2);
+    Acc* wrow = ws + ((size_t)(kvh * rep + r) * n_split + split) * (HD + 2);
+    if (r >= rep) return;
     if (nt == 0) {
-        for (int i = tid; i < rep * (HD + 2); i += 256) {
-            const int r = i / (HD + 2), c = i - r * (HD + 2);
-            wbase[(size_t)r * n_split * (HD + 2) + c] = c == HD ? (Acc)-INFINITY : (Acc)0;
-        }
+        for (int i = lane; i < HD + 2; i += 64) wrow[i] = i == HD ? (Acc)-INFINITY : (Acc)0;
         return;
     }
-    for (int i = tid; i < rep * HD; i += 256) sq[i] = (Acc)q[(size_t)kvh * rep * HD + i];
-    __syncthreads();
-
-    // scores: thread = (position slot ps = tid/16, 8-dim chunk c = tid%16);
-    // positions t0 + ps + 16*i, i < 4, all K loads issued together
-    {
-        const int c = tid & 15, ps = tid >> 4;
-        uint4 kv4[4];
+    // every load first: q of this head, the K row of position t0 + lane and
+    // dimensions 2*lane, 2*lane+1 of the V rows of the split's positions
+    const float* qh = q + (size_t)(kvh * rep + r) * HD;
+    const float q0 = qh[lane], q1 = qh[lane + 64];
+    const int tt = t0 + min(lane, nt - 1);
+    const uint4* kr = reinterpret_cast<const uint4*>(kc + ((size_t)tt * n_kv + kvh) * HD);
+    uint4 kv[HD / 8];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int tt = min(t0 + ps + 16 * i, n_tok - 1);
-            kv4[i] = *reinterpret_cast<const uint4*>(kc + ((size_t)tt * n_kv + kvh) * HD + c * 8);
-        }
+    for (int i = 0; i < HD / 8; i++) kv[i] = kr[i];
+    uint32_t vv[kAttnChunk];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t w[4] = {kv4[i].x, kv4[i].y, kv4[i].z, kv4[i].w};
-            Acc kf[8];
+    for (int i = 0; i < kAttnChunk; i++)
+        vv[i] = *reinterpret_cast<const uint32_t*>(vc + ((size_t)(t0 + min(i, nt - 1)) * n_kv + kvh) * HD + 2 * lane);
+    sq[r][lane] = (Acc)q0;
+    sq[r][lane + 64] = (Acc)q1;
+    // the wave's own LDS rows: its writes precede its reads, no barrier
+    Acc s = (Acc)0;
 #pragma unroll
-            for (int e = 0; e < 8; e++) kf[e] = (Acc)h2f((uint16_t)(w[e >> 1] >> ((e & 1) * 16)));
-            for (int r = 0; r < rep; r++) {
-                Acc d = (Acc)0;
+    for (int i = 0; i < HD / 8; i++) {
+        const uint32_t w[4] = {kv[i].x, kv[i].y, kv[i].z, kv[i].w};
 #pragma unroll
-                for (int e = 0; e < 8; e++) d = fma(sq[r * HD + c * 8 + e], kf[e], d);
-                // sum the 16 chunks of the position (16 consecutive lanes)
+        for (int e = 0; e < 8; e++) s = fma(sq[r][i * 8 + e], (Acc)h2f((uint16_t)(w[e >> 1] >> ((e & 1) * 16))), s);
+    }
+    s = lane < nt ? s * scale : (Acc)-INFINITY;
+    const Acc m = wave_max_t(s);
+    const Acc p = lane < nt ? acc_exp<Acc>(s - m) : (Acc)0;
+    const Acc l = wave_sum(p);
+    sp[r][lane] = p;
+    Acc o0 = (Acc)0, o1 = (Acc)0;
 #pragma unroll
-                for (int o = 8; o > 0; o >>= 1) d += __shfl_xor(d, o, 64);
-                const int tl = ps + 16 * i;
-                if (c == 0) sp[r * kAttnChunk + tl] = tl < nt ? d * scale : (Acc)-INFINITY;
-            }
+    for (int i = 0; i < kAttnChunk; i++) {
+        if (i < nt) {
+            const Acc pi = sp[r][i];
+            o0 = fma(pi, (Acc)h2f((uint16_t)(vv[i] & 0xffffu)), o0);
+            o1 = fma(pi, (Acc)h2f((uint16_t)(vv[i] >> 16)), o1);
         }
     }
-    __syncthreads();
-    // softmax of the chunk per head: wave handles heads wave, wave+4
-    for (int r = wave; r < rep; r += 4) {
-        const Acc s = sp[r * kAttnChunk + lane];
-        Acc m = s;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) m = fmax(m, __shfl_xor(m, o, 64));
-        const Acc p = lane < nt ? acc_exp<Acc>(s - m) : (Acc)0;
-        Acc l = p;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
-        sp[r * kAttnChunk + lane] = p;
-        if (lane == 0) {
-            sml[2 * r] = m;
-            sml[2 * r + 1] = l;
-        }
-    }
-    __syncthreads();
-    // weighted V: thread = (4-dim chunk dc = tid%32, position group g = tid/32);
-    // positions g + 8*i, i < 8, all V loads issued together
-    {
-        const int dc = tid & 31, g = tid >> 5;
-        uint2 v2[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int tt = min(t0 + g + 8 * i, n_tok - 1);
-            v2[i] = *reinterpret_cast<const uint2*>(vc + ((size_t)tt * n_kv + kvh) * HD + dc * 4);
-        }
-        Acc acc[kAttnMaxRep][4];
-#pragma unroll
-        for (int r = 0; r < kAttnMaxRep; r++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) acc[r][e] = (Acc)0;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int tl = g + 8 * i;
-            Acc vf[4];
-            vf[0] = (Acc)h2f((uint16_t)(v2[i].x & 0xffffu));
-            vf[1] = (Acc)h2f((uint16_t)(v2[i].x >> 16));
-            vf[2] = (Acc)h2f((uint16_t)(v2[i].y & 0xffffu));
-            vf[3] = (Acc)h2f((uint16_t)(v2[i].y >> 16));
-#pragma unroll
-            for (int r = 0; r < kAttnMaxRep; r++) {
-                if (r < rep) {
-                    const Acc p = sp[r * kAttnChunk + tl];   // 0 past the chunk end
-#pragma unroll
-                    for (int e = 0; e < 4; e++) acc[r][e] = fma(p, vf[e], acc[r][e]);
-                }
-            }
-        }
-        // the two position groups of a wave, then the 4 waves in order
-#pragma unroll
-        for (int r = 0; r < kAttnMaxRep; r++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) acc[r][e] += __shfl_xor(acc[r][e], 32, 64);
-        if (lane < 32) {
-#pragma unroll
-            for (int r = 0; r < kAttnMaxRep; r++)
-                if (r < rep)
-#pragma unroll
-                    for (int e = 0; e < 4; e++) so[(wave * kAttnMaxRep + r) * HD + dc * 4 + e] = acc[r][e];
-        }
-    }
-    __syncthreads();
-    for (int i = tid; i < rep * HD; i += 256) {
-        const int r = i / HD, d = i - r * HD;
-        const Acc o = so[(0 * kAttnMaxRep + r) * HD + d] + so[(1 * kAttnMaxRep + r) * HD + d] +
-                      so[(2 * kAttnMaxRep + r) * HD + d] + so[(3 * kAttnMaxRep + r) * HD + d];
-        Acc* row = wbase + (size_t)r * n_split * (HD + 2);
-        row[d] = o;
-        if (d == 0) {
-            row[HD] = sml[2 * r];
-            row[HD + 1] = sml[2 * r + 1];
-        }
+    wrow[2 * lane] = o0;
+    wrow[2 * lane + 1] = o1;
+    if (lane == 0) {
+        wrow[HD] = m;
+        wrow[HD + 1] = l;
     }
 }
 
@@ -466,14 +403,14 @@ int attention(Ctx* c, const float* q, const uint16_t* kc, const uint16_t* vc, co
     IAM_REQUIRE(n_split <= kMaxAttnSplits, "attention: max_ctx above 8192");
     if (c->acc64) {
         const double scale = 1.0 / std::sqrt(128.0);
-        IAM_TRY(launch(c, "attn_partial", k_attn_partial<double>, dim3(n_kv, n_split), dim3(256), 0, q, kc, vc,
-                       pos, n_heads, n_kv, max_ctx, scale, (double*)ws, n_split));
+        IAM_TRY(launch(c, "attn_partial", k_attn_partial<double>, dim3(n_kv, n_split), dim3(64 * (n_heads / n_kv)),
+                       0, q, kc, vc, pos, n_heads, n_kv, max_ctx, scale, (double*)ws, n_split));
         return launch(c, "attn_combine", k_attn_combine<double>, dim3(n_heads), dim3(128), 0,
                       (const double*)ws, pos, max_ctx, n_split, out);
     }
     const float scale = 1.0f / std::sqrt(128.0f);
-    IAM_TRY(launch(c, "attn_partial", k_attn_partial<float>, dim3(n_kv, n_split), dim3(256), 0, q, kc, vc, pos,
-                   n_heads, n_kv, max_ctx, scale, ws, n_split));
+    IAM_TRY(launch(c, "attn_partial", k_attn_partial<float>, dim3(n_kv, n_split), dim3(64 * (n_heads / n_kv)), 0, q,
+                   kc, vc, pos, n_heads, n_kv, max_ctx, scale, ws, n_split));
     return launch(c, "attn_combine", k_attn_combine<float>, dim3(n_heads), dim3(128), 0, (const float*)ws, pos,
                   max_ctx, n_split, out);
 }
