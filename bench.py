@@ -10,8 +10,11 @@ HIP graph and replayed).  `value` is decode tokens per second.
 
 roofline: the bucket walk kernel (the dominant one) -- the selected weight
 bytes it streams (2 * S * bucket_cols per matrix, counted on the device) per
-launch over its average launch time, timed with HIP events on the library's
-stream during eager steps, against the 8 TB/s HBM peak.
+launch over its average duration, timed with HIP events stamped by each
+walk's own dispatch on the library's stream during eager steps, against the
+8 TB/s HBM peak.  `traffic` is the walk's measured HBM bytes per launch
+(FETCH_SIZE + WRITE_SIZE, calibrated on a copy of known size) read from the
+committed counter summary profiles/walk_hbm_traffic_mistral7b_effort025.md.
 
 cpu_baseline: the C oracle on one host core, timed on a bounded sample
 (decoder layers and the LM head of the same model at the same effort and
@@ -58,6 +61,21 @@ def per_token_fixed_bytes(cfg, ctx_len):
     per_layer += 2 * 2 * KVD * ctx_len
     lm = 2 * 16 * D + 4 * D + 2 * 4096 + 4 * V
     return cfg["n_layers"] * per_layer + lm + 2 * D
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "walk_hbm_traffic_mistral7b_effort025.md")
+
+
+def walk_traffic():
+    """HBM bytes per walk launch from the committed counter summary, or None."""
+    try:
+        for line in open(TRAFFIC_PROFILE):
+            cells = [c.strip() for c in line.strip().strip("|").split("|")]
+            if len(cells) == 2 and cells[0] == "traffic_bytes_per_launch":
+                return float(cells[1])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(iam, model, cfg, pos, effort, budget_s=12.0):
@@ -156,8 +174,12 @@ def main():
     log(f"decode: {args.steps} tokens in {dt * 1e3:.1f} ms = {tok_s:.1f} tok/s; "
         f"{bytes_per_token / 1e9:.3f} GB/token -> {bytes_per_token * tok_s / 1e9:.0f} GB/s")
 
-    # per-kernel times from eager steps bracketed by HIP events
+    # per-kernel times: eager decode steps in which every kernel is launched
+    # with a pair of HIP events stamped by its own dispatch on the library's
+    # stream (hipExtLaunchKernelGGL), so each elapsed time is that kernel's
+    # duration
     ctx.kernel_stats_reset()
+    ctx.walk_counters(reset=True)
     ctx.profiling(True)
     model.decode(args.profile_steps, args.effort, use_graph=False)
     ctx.sync()
@@ -197,7 +219,7 @@ def main():
                    "global_batch": 1, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": "bucket_walk", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": walk_traffic(),
                      "bytes_per_launch": round(per_launch), "avg_launch_us": round(walk_avg_s * 1e6, 2)},
         "token_roofline": {"bytes_per_token": round(bytes_per_token), "achieved_GBs":
                            round(bytes_per_token * tok_s / 1e9, 1),

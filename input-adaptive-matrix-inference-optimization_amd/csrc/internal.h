@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 
 #include <cstdint>
 #include <map>
@@ -123,17 +124,22 @@ int launch(Ctx* c, const char* name, Kernel k, dim3 grid, dim3 block, size_t shm
            Args... args)
 {
     if (grid.x == 0 || grid.y == 0 || grid.z == 0) return IAM_OK;
-    PendingEvent ev{};
-    bool have = false;
     if (c->profiling && !c->capturing) {
+        // the events are stamped by the kernel's own dispatch, so the elapsed
+        // time is the kernel's duration, without host-side gaps
+        PendingEvent ev{};
         IAM_TRY(begin_launch(c, name, &ev));
-        have = true;
+        hipExtLaunchKernelGGL(k, grid, block, (uint32_t)shmem, c->stream, ev.start, ev.stop, 0, args...);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess)
+            return fail(IAM_E_HIP, std::string("launch ") + name + ": " + hipGetErrorString(e));
+        return end_launch(c, &ev, true);
     }
     hipLaunchKernelGGL(k, grid, block, shmem, c->stream, args...);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return fail(IAM_E_HIP, std::string("launch ") + name + ": " + hipGetErrorString(e));
-    return end_launch(c, &ev, have);
+    return IAM_OK;
 }
 
 int zero_async(Ctx* c, void* p, size_t bytes);

@@ -132,6 +132,11 @@ class Ctx:
         self.close()
 
     # ---- memory
+    def copy(self, dst, src, nbytes, dst_offset=0, src_offset=0):
+        """Device-to-device copy on the context's stream (asynchronous)."""
+        check(lib().iam_copy(self.h, _vp(dst), C.c_size_t(dst_offset), _vp(src), C.c_size_t(src_offset),
+                             C.c_size_t(nbytes)))
+
     def alloc(self, nbytes, dtype=np.uint8):
         return DevBuf(self, nbytes, dtype)
 
