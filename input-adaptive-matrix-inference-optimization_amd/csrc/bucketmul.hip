@@ -1120,7 +1120,9 @@ void plan_walk(int n, const MatOp* ops, float effort, bool acc64, WalkPlan* plan
         const int tw = pl.V == 8 ? 128 : 64;
         pl.T = (M.bucket_cols + tw - 1) / tw;
         pl.n_in = std::min((M.expert_rows + 15) / 16, ops[i].in_size);
-        bytes[i] = est_rows(pl.n_in * 16, effort) * M.bucket_cols * 2.0;
+        // the cost of a row is its tiles' width: a k_walk64 workgroup spends
+        // the same on a 64-column matrix's half-empty tile as on a full one
+        bytes[i] = est_rows(pl.n_in * 16, effort) * (pl.V == 8 ? pl.T * tw : M.bucket_cols) * 2.0;
         tot += bytes[i];
     }
     const int nw = all64 ? IAM_W64_NW : tot < kWalkWideBytes ? IAM_WALK_SMALL_NW : IAM_WALK_BIG_NW;
@@ -1136,8 +1138,6 @@ void plan_walk(int n, const MatOp* ops, float effort, bool acc64, WalkPlan* plan
     }
 }
 
-// Record the selection problem of matrix op i in slot i and compute the
-// cutoffs (one workgroup per matrix).
 // Validate the n matrix ops and record their selection problems in slots
 // 0..n-1; fills the cutoff launch arguments.
 static int record_slots(Ctx* c, int n, const MatOp* ops, int expert_no, float effort, CutoffArgs& args)

@@ -156,8 +156,10 @@ __global__ void k_rope_kv(const float* __restrict__ q, const float* __restrict__
 // aux.cl:204-225 (exp(s)/sum exp(s)) is evaluated with the split's maximum
 // subtracted, which leaves p unchanged; then lane j accumulates dimensions
 // 2j, 2j+1 of sum p*V over the positions.  No value crosses waves, so there
-// is no barrier.  The split writes its max m, sum l of exp(s - m) and
-// unnormalised o; k_attn_combine merges the splits.  Acc = double evaluates
+// is no barrier before the split writes its max m, sum l of exp(s - m) and
+// unnormalised o.  The splits of a KV head count themselves in on a counter
+// in the workspace; the last one to arrive merges them (combine_head) and
+// re-arms the counter, so one launch produces the attention output.  Acc = double evaluates
 // every product (exact: fp32 x fp16), exponential and sum in fp64 and the
 // output is rounded once; Acc = float is the fp32 evaluation.
 constexpr int kAttnChunk = 64;
@@ -171,17 +173,58 @@ __device__ __forceinline__ float acc_exp<float>(float x) { return expf(x); }
 template <>
 __device__ __forceinline__ double acc_exp<double>(double x) { return exp(x); }
 
+// Merge of the na splits of query head h by one wave: weights exp(m_s - M)
+// of the split maxima, L = sum of l_s * w_s and O = sum of o_s * w_s in split
+// order, out = O / L; lane j writes dimensions 2j, 2j+1.  sw: kMaxAttnSplits
+// entries of this wave.
+template <typename Acc>
+__device__ void combine_head(const Acc* __restrict__ ws, int h, int n_split, int na, Acc* sw, float* __restrict__ out)
+{
+    constexpr int HD = 128;
+    const int lane = threadIdx.x & 63;
+    const Acc* base = ws + (size_t)h * n_split * (HD + 2);
+    Acc M = (Acc)-INFINITY;
+    for (int s = lane; s < na; s += 64) M = fmax(M, base[(size_t)s * (HD + 2) + HD]);
+    M = wave_max_t(M);
+    for (int s = lane; s < na; s += 64) sw[s] = acc_exp<Acc>(base[(size_t)s * (HD + 2) + HD] - M);
+    Acc L = (Acc)0, O0 = (Acc)0, O1 = (Acc)0;
+    for (int s0 = 0; s0 < na; s0 += 8) {
+        Acc o0[8], o1[8], lv[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const Acc* row = base + (size_t)min(s0 + i, na - 1) * (HD + 2);
+            o0[i] = row[2 * lane];
+            o1[i] = row[2 * lane + 1];
+            lv[i] = row[HD + 1];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            if (s0 + i < na) {
+                const Acc w = sw[s0 + i];
+                L += lv[i] * w;
+                O0 += o0[i] * w;
+                O1 += o1[i] * w;
+            }
+        }
+    }
+    out[h * HD + 2 * lane] = (float)(O0 / L);
+    out[h * HD + 2 * lane + 1] = (float)(O1 / L);
+}
+
 template <typename Acc>
 __global__ __launch_bounds__(64 * kAttnMaxRep) void k_attn_partial(const float* __restrict__ q,
                                                                    const uint16_t* __restrict__ kc,
                                                                    const uint16_t* __restrict__ vc,
                                                                    const int* __restrict__ pos_p, int n_heads,
                                                                    int n_kv, int max_ctx, Acc scale,
-                                                                   Acc* __restrict__ ws, int n_split)
+                                                                   Acc* __restrict__ ws, int n_split,
+                                                                   unsigned int* __restrict__ done,
+                                                                   float* __restrict__ out)
 {
     constexpr int HD = 128;
     __shared__ Acc sq[kAttnMaxRep][HD];
-    __shared__ Acc sp[kAttnMaxRep][kAttnChunk];
+    __shared__ Acc sp[kAttnMaxRep][kMaxAttnSplits > kAttnChunk ? kMaxAttnSplits : kAttnChunk];
+    __shared__ int s_last;
     const int kvh = blockIdx.x;
     const int split = blockIdx.y;
     const int lane = threadIdx.x & 63;
@@ -194,10 +237,7 @@ __global__ __launch_bounds__(64 * kAttnMaxRep) void k_attn_partial(const float* 
     // workspace row of query head h = kvh*rep + r, split s: ws[(h*n_split + s)*(HD+2)]
     Acc* wrow = ws + ((size_t)(kvh * rep + r) * n_split + split) * (HD + 2);
     if (r >= rep) return;
-    if (nt == 0) {
-        for (int i = lane; i < HD + 2; i += 64) wrow[i] = i == HD ? (Acc)-INFINITY : (Acc)0;
-        return;
-    }
+    if (nt == 0) return;   // past the context: neither written nor counted
     // every load first: q of this head, the K row of position t0 + lane and
     // dimensions 2*lane, 2*lane+1 of the V rows of the split's positions
     const float* qh = q + (size_t)(kvh * rep + r) * HD;
@@ -241,54 +281,22 @@ __global__ __launch_bounds__(64 * kAttnMaxRep) void k_attn_partial(const float* 
         wrow[HD] = m;
         wrow[HD + 1] = l;
     }
-}
-
-// Merge of the splits of one query head: only the splits that hold
-// positions (ceil(n_tok / kAttnChunk)) are read; their weights
-// exp(m_s - M) are computed once, then every dimension sums its split
-// values with the loads of 8 splits in flight.
-template <typename Acc>
-__global__ __launch_bounds__(128) void k_attn_combine(const Acc* __restrict__ ws, const int* __restrict__ pos_p,
-                                                      int max_ctx, int n_split, float* __restrict__ out)
-{
-    constexpr int HD = 128;
-    __shared__ Acc sw[kMaxAttnSplits];
-    __shared__ Acc sred[2];
-    const int h = blockIdx.x;
-    const int d = threadIdx.x;
-    int n_tok = *pos_p + 1;
-    if (n_tok > max_ctx) n_tok = max_ctx;
-    if (n_tok < 1) n_tok = 1;
-    const int na = min(n_split, (n_tok + kAttnChunk - 1) / kAttnChunk);
-    const Acc* base = ws + (size_t)h * n_split * (HD + 2);
-    // split maxima: thread s < na holds split s (na <= 128 is checked on the host)
-    const Acc ms = d < na ? base[(size_t)d * (HD + 2) + HD] : (Acc)-INFINITY;
-    Acc M = ms;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) M = fmax(M, __shfl_xor(M, o, 64));
-    if ((d & 63) == 0) sred[d >> 6] = M;
+    // the last split of this KV head to finish merges the splits of its
+    // query heads (one wave per head) and re-arms the counter
+    // (one agent-scope fence per workgroup: the barrier orders the other
+    // waves' stores before thread 0's release)
+    const int na = (n_tok + kAttnChunk - 1) / kAttnChunk;
     __syncthreads();
-    M = fmax(sred[0], sred[1]);
-    if (d < na) sw[d] = acc_exp<Acc>(ms - M);
-    __syncthreads();
-    Acc L = (Acc)0, O = (Acc)0;
-    for (int s0 = 0; s0 < na; s0 += 8) {
-        Acc ov[8], lv[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int s = min(s0 + i, na - 1);
-            ov[i] = base[(size_t)s * (HD + 2) + d];
-            lv[i] = base[(size_t)s * (HD + 2) + HD + 1];
-        }
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            if (s0 + i < na) {
-                L += lv[i] * sw[s0 + i];
-                O += ov[i] * sw[s0 + i];
-            }
-        }
+    if (threadIdx.x == 0) {
+        __threadfence();
+        const bool last = atomicAdd(done + kvh, 1u) == (unsigned int)(na - 1);
+        if (last) __threadfence();
+        s_last = last;
     }
-    out[h * HD + d] = (float)(O / L);
+    __syncthreads();
+    if (!s_last) return;
+    combine_head<Acc>(ws, kvh * rep + r, n_split, na, sp[r], out);
+    if (threadIdx.x == 0) done[kvh] = 0u;
 }
 
 // ---------------------------------------------------------------- embed ---
@@ -396,30 +404,37 @@ int rope_kv(Ctx* c, const float* q, const float* k, const float* v, const float*
                   n_heads, n_kv, hd, max_ctx, q_out, kc, vc);
 }
 
+// The workspace holds one completion counter per KV head (zero between
+// launches) in its first kAttnCounters words, at the same place whatever
+// max_ctx a call names, then the partials (o[128], m, l) per head and split.
+constexpr int kAttnCounters = 64;
+static size_t attn_partial_floats(int n_heads, int max_ctx)
+{
+    const int n_split = (max_ctx + kAttnChunk - 1) / kAttnChunk;
+    return (size_t)n_heads * n_split * (128 + 2) * 2;
+}
+
 int attention(Ctx* c, const float* q, const uint16_t* kc, const uint16_t* vc, const int* pos, int n_heads,
               int n_kv, int max_ctx, float* ws, float* out)
 {
     const int n_split = (max_ctx + kAttnChunk - 1) / kAttnChunk;
     IAM_REQUIRE(n_split <= kMaxAttnSplits, "attention: max_ctx above 8192");
+    IAM_REQUIRE(n_kv <= kAttnCounters, "attention: more than 64 KV heads");
+    unsigned int* done = reinterpret_cast<unsigned int*>(ws);
+    ws += kAttnCounters;
     if (c->acc64) {
         const double scale = 1.0 / std::sqrt(128.0);
-        IAM_TRY(launch(c, "attn_partial", k_attn_partial<double>, dim3(n_kv, n_split), dim3(64 * (n_heads / n_kv)),
-                       0, q, kc, vc, pos, n_heads, n_kv, max_ctx, scale, (double*)ws, n_split));
-        return launch(c, "attn_combine", k_attn_combine<double>, dim3(n_heads), dim3(128), 0,
-                      (const double*)ws, pos, max_ctx, n_split, out);
+        return launch(c, "attention", k_attn_partial<double>, dim3(n_kv, n_split), dim3(64 * (n_heads / n_kv)), 0,
+                      q, kc, vc, pos, n_heads, n_kv, max_ctx, scale, (double*)ws, n_split, done, out);
     }
     const float scale = 1.0f / std::sqrt(128.0f);
-    IAM_TRY(launch(c, "attn_partial", k_attn_partial<float>, dim3(n_kv, n_split), dim3(64 * (n_heads / n_kv)), 0, q,
-                   kc, vc, pos, n_heads, n_kv, max_ctx, scale, ws, n_split));
-    return launch(c, "attn_combine", k_attn_combine<float>, dim3(n_heads), dim3(128), 0, (const float*)ws, pos,
-                  max_ctx, n_split, out);
+    return launch(c, "attention", k_attn_partial<float>, dim3(n_kv, n_split), dim3(64 * (n_heads / n_kv)), 0, q,
+                  kc, vc, pos, n_heads, n_kv, max_ctx, scale, ws, n_split, done, out);
 }
 
 size_t attention_ws_floats(int n_heads, int max_ctx)
 {
-    // room for fp64 partials: (o[128], m, l) per head and split
-    const int n_split = (max_ctx + kAttnChunk - 1) / kAttnChunk;
-    return (size_t)n_heads * n_split * (128 + 2) * 2;
+    return kAttnCounters + attn_partial_floats(n_heads, max_ctx);
 }
 
 int embed(Ctx* c, const uint16_t* table, int cols, int vocab, const int* tok, float* out)
