@@ -926,34 +926,45 @@ constexpr int kRedOut = 128;     // outputs per reduce workgroup (one head of 12
 constexpr int kRedThreads = 256;
 constexpr int kRedGroups = kRedThreads / 32;   // slice groups: 32 threads x 4 outputs each
 
-// Thread (ol, pg) sums outputs 4ol..4ol+3 over the slices pg, pg + 32, ...
-// in slice order, with all of its loads issued together; the group sums are
-// then added in group order by threads 0..127 (which return the total).
-template <typename Acc>
-__device__ __forceinline__ Acc group_sums(const Acc* __restrict__ part, int P, int m, int o, int pg,
-                                          Acc (*red)[kRedOut], int ol)
+// Thread (ol, pg) sums outputs 4ol..4ol+3 over the slices pg, pg + 8, ...
+// in slice order; the group sums are then added in group order by threads
+// 0..127.  The loads of U slices are issued together, so a matrix of up to
+// 8U slices costs one round trip.
+template <typename Acc, int U>
+__device__ __forceinline__ void slice_loads(const Acc* __restrict__ part, int P, int m, int o, int p0, Acc (&r)[U][4])
 {
-    constexpr int U = 8;
-    Acc s[4] = {(Acc)0, (Acc)0, (Acc)0, (Acc)0};
-    if (o < m) {
-        for (int p0 = pg; p0 < P; p0 += U * kRedGroups) {
-            Acc r[U][4];
 #pragma unroll
-            for (int u = 0; u < U; u++) {
-                const int p = min(p0 + u * kRedGroups, P - 1);
+    for (int u = 0; u < U; u++) {
+        const int p = min(p0 + u * kRedGroups, P - 1);
 #pragma unroll
-                for (int i = 0; i < 4; i++) r[u][i] = part[(size_t)p * m + o + i];
-            }
-#pragma unroll
-            for (int u = 0; u < U; u++)
-                if (p0 + u * kRedGroups < P)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) s[i] += r[u][i];
-        }
+        for (int i = 0; i < 4; i++) r[u][i] = part[(size_t)p * m + o + i];
     }
+}
+
+template <typename Acc, int U>
+__device__ __forceinline__ void slice_adds(int P, int p0, const Acc (&r)[U][4], Acc (&s)[4])
+{
 #pragma unroll
-    for (int i = 0; i < 4; i++) red[pg][ol * 4 + i] = s[i];
-    __syncthreads();
+    for (int u = 0; u < U; u++)
+        if (p0 + u * kRedGroups < P)
+#pragma unroll
+            for (int i = 0; i < 4; i++) s[i] += r[u][i];
+}
+
+template <typename Acc, int U>
+__device__ __forceinline__ void thread_sums(const Acc* __restrict__ part, int P, int m, int o, int pg, Acc (&s)[4])
+{
+    for (int p0 = pg; p0 < P; p0 += U * kRedGroups) {
+        Acc r[U][4];
+        slice_loads<Acc, U>(part, P, m, o, p0, r);
+        slice_adds<Acc, U>(P, p0, r, s);
+    }
+}
+
+// the 8 group sums of output tid (< kRedOut) in group order
+template <typename Acc>
+__device__ __forceinline__ Acc group_total(const Acc (*red)[kRedOut])
+{
     const int tid = threadIdx.x;
     Acc t = (Acc)0;
     if (tid < kRedOut) {
@@ -961,8 +972,52 @@ __device__ __forceinline__ Acc group_sums(const Acc* __restrict__ part, int P, i
 #pragma unroll
         for (int g = 1; g < kRedGroups; g++) t += red[g][tid];
     }
-    __syncthreads();
     return t;
+}
+
+template <typename Acc>
+__device__ __forceinline__ Acc group_sums(const Acc* __restrict__ part, int P, int m, int o, int pg,
+                                          Acc (*red)[kRedOut], int ol)
+{
+    Acc s[4] = {(Acc)0, (Acc)0, (Acc)0, (Acc)0};
+    if (o < m) thread_sums<Acc, 16>(part, P, m, o, pg, s);
+#pragma unroll
+    for (int i = 0; i < 4; i++) red[pg][ol * 4 + i] = s[i];
+    __syncthreads();
+    return group_total<Acc>(red);
+}
+
+// two matrices of the same output size at once (the gate and up
+// projections): with at most 64 slices each, all loads of both are issued
+// together
+template <typename Acc>
+__device__ __forceinline__ void group_sums2(const Acc* __restrict__ part, int P, const Acc* __restrict__ part2,
+                                            int P2, int m, int o, int pg, Acc (*red)[kRedOut],
+                                            Acc (*red2)[kRedOut], int ol, Acc& t1, Acc& t2)
+{
+    constexpr int U = 8;
+    Acc s[4] = {(Acc)0, (Acc)0, (Acc)0, (Acc)0};
+    Acc s2[4] = {(Acc)0, (Acc)0, (Acc)0, (Acc)0};
+    if (o < m) {
+        if (P <= U * kRedGroups && P2 <= U * kRedGroups) {
+            Acc r[U][4], r2[U][4];
+            slice_loads<Acc, U>(part, P, m, o, pg, r);
+            slice_loads<Acc, U>(part2, P2, m, o, pg, r2);
+            slice_adds<Acc, U>(P, pg, r, s);
+            slice_adds<Acc, U>(P2, pg, r2, s2);
+        } else {
+            thread_sums<Acc, U>(part, P, m, o, pg, s);
+            thread_sums<Acc, U>(part2, P2, m, o, pg, s2);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        red[pg][ol * 4 + i] = s[i];
+        red2[pg][ol * 4 + i] = s2[i];
+    }
+    __syncthreads();
+    t1 = group_total<Acc>(red);
+    t2 = group_total<Acc>(red2);
 }
 
 // total selected rows of a matrix (by one wave, no barrier) into count and
@@ -988,6 +1043,7 @@ __global__ __launch_bounds__(kRedThreads) void k_reduce(ReduceArgs a)
 {
 #pragma clang fp contract(off)
     __shared__ Acc red[kRedGroups][kRedOut];
+    __shared__ Acc red2[kRedGroups][kRedOut];
     __shared__ float sy[kRedOut];
     const int b = (int)blockIdx.x;
     int k = 0;
@@ -1002,29 +1058,44 @@ __global__ __launch_bounds__(kRedThreads) void k_reduce(ReduceArgs a)
     if (lb == 0 && tid >= kRedThreads - 64) sum_counts(d.slice_count, d.P, d.C, d.count, a.counters);
     if (lb == 0 && d.ep == kEpSilu && tid >= kRedThreads - 128 && tid < kRedThreads - 64)
         sum_counts(d.slice_count2, d.P2, d.C, d.count2, a.counters);
-    const float yv = (float)group_sums<Acc>(reinterpret_cast<const Acc*>(d.part), d.P, d.m, o, pg, red, ol);
     const int oo = o0 + tid;
     const bool in = tid < kRedOut && oo < d.m;
-    if (in) d.y[oo] = yv;
+    // the epilogue's own loads go out with the partial loads
+    const bool rope = d.ep == kEpRopeQ || d.ep == kEpRopeK;
+    const int pos = rope || d.ep == kEpV ? *d.pos : 0;
+    const bool pos_ok = pos >= 0 && pos < d.max_ctx;
+    float rc = 0.0f, rsn = 0.0f, resid = 0.0f;
+    if (rope && in && pos_ok) {
+        const int fi = tid < kRedOut / 2 ? tid : tid - kRedOut / 2;
+        rc = d.table[(size_t)pos * kRedOut + 2 * fi];
+        rsn = d.table[(size_t)pos * kRedOut + 2 * fi + 1];
+    }
+    if (d.ep == kEpResid && in) resid = d.out[oo];
     if (d.ep == kEpSilu) {
-        const float uv = (float)group_sums<Acc>(reinterpret_cast<const Acc*>(d.part2), d.P2, d.m, o, pg, red, ol);
+        Acc t1, t2;
+        group_sums2<Acc>(reinterpret_cast<const Acc*>(d.part), d.P, reinterpret_cast<const Acc*>(d.part2), d.P2,
+                         d.m, o, pg, red, red2, ol, t1, t2);
+        const float yv = (float)t1, uv = (float)t2;
         if (in) {
+            d.y[oo] = yv;
             d.y2[oo] = uv;
             const double x1 = (double)yv;
             d.out[oo] = (float)((double)uv * x1 / (1.0 + exp(-x1)));
         }
-    } else if (d.ep == kEpResid) {
-        if (in) d.out[oo] = __fadd_rn(d.out[oo], yv);
+        return;
+    }
+    const float yv = (float)group_sums<Acc>(reinterpret_cast<const Acc*>(d.part), d.P, d.m, o, pg, red, ol);
+    if (in) d.y[oo] = yv;
+    if (d.ep == kEpResid) {
+        if (in) d.out[oo] = __fadd_rn(resid, yv);
     } else if (d.ep != kEpStore) {
-        const int pos = *d.pos;
-        const bool pos_ok = pos >= 0 && pos < d.max_ctx;
         if (d.ep == kEpV) {
             if (in && pos_ok) d.cache[(size_t)pos * d.m + oo] = __half_as_ushort(__float2half_rn(yv));
         } else {
             if (tid < kRedOut) sy[tid] = yv;
             __syncthreads();
             if (in && pos_ok) {
-                const float r = rope_one(sy, d.table + (size_t)pos * kRedOut, tid, kRedOut / 2);
+                const float r = rope_cs(sy, tid, kRedOut / 2, rc, rsn);
                 if (d.ep == kEpRopeQ) d.out[oo] = r;
                 else d.cache[(size_t)pos * d.m + oo] = __half_as_ushort(__float2half_rn(r));
             }
@@ -1050,9 +1121,6 @@ static double est_fraction(float effort)
 
 double est_rows(int rows, float effort) { return std::max(1.0, rows * est_fraction(effort)); }
 
-// Walk launch shape: NW waves per workgroup, each with 16 KB of private
-// accumulators (fp32: 4 columns per lane; fp64: 2), 16 rows in flight per
-// lane; a slice holds at most 64*NW inputs.
 // Walk launch shapes: a launch whose expected weight bytes are below
 // kWalkWideBytes uses 4 waves per workgroup and 16 rows in flight per lane
 // (more waves per slice: these launches are latency bound), a larger one 2
@@ -1095,6 +1163,12 @@ constexpr double kWalkMaxWgs = 3072.0;
 #ifndef IAM_W64_WG_BYTES
 #define IAM_W64_WG_BYTES 131072.0
 #endif
+#ifndef IAM_W64_ROUND
+#define IAM_W64_ROUND 0
+#endif
+#ifndef IAM_W64_FIXED
+#define IAM_W64_FIXED 0
+#endif
 
 // 8: the fp64 walk with 16-byte loads and 128-column tiles (k_walk64);
 // otherwise the columns per lane load of k_walk.
@@ -1127,12 +1201,16 @@ void plan_walk(int n, const MatOp* ops, float effort, bool acc64, WalkPlan* plan
     }
     const int nw = all64 ? IAM_W64_NW : tot < kWalkWideBytes ? IAM_WALK_SMALL_NW : IAM_WALK_BIG_NW;
     const double wg_bytes = all64 ? IAM_W64_WG_BYTES : kWalkWgBytes;
-    const double target = std::min(kWalkMaxWgs, std::max(kWalkMinWgs, tot / wg_bytes));
+    double target = std::min(kWalkMaxWgs, std::max(kWalkMinWgs, tot / wg_bytes));
+    const bool fit = all64 && (IAM_W64_ROUND > 0 || IAM_W64_FIXED > 0);
+    if (all64 && IAM_W64_ROUND > 0)
+        target = std::max((double)IAM_W64_ROUND, std::round(target / IAM_W64_ROUND) * IAM_W64_ROUND);
+    if (all64 && IAM_W64_FIXED > 0) target = IAM_W64_FIXED;
     for (int i = 0; i < n; i++) {
         WalkPlan& pl = plan[i];
         pl.NW = pl.V == 8 ? IAM_W64_NW : nw;
         const double wgs = tot > 0 ? target * bytes[i] / tot : target / n;
-        const int slices = std::max(1, (int)std::lround(wgs / pl.T));
+        const int slices = std::max(1, fit ? (int)std::floor(wgs / pl.T + 1e-9) : (int)std::lround(wgs / pl.T));
         pl.IPS = std::min(64 * pl.NW, std::max(1, (pl.n_in + slices - 1) / slices));
         pl.P = (pl.n_in + pl.IPS - 1) / pl.IPS;
     }

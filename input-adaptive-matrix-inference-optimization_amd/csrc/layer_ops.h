@@ -9,12 +9,16 @@ namespace iam {
 // rope_mx (aux.cl:227-248): rotate-half pairs (d, d + hd/2) with the host
 // table row for the position ([hd/2] of {cos, sin}); no contraction, so it
 // matches the oracle.
+__device__ __forceinline__ float rope_cs(const float* m, int d, int half, float c, float s)
+{
+    if (d < half) return __fsub_rn(__fmul_rn(m[d], c), __fmul_rn(m[d + half], s));
+    return __fadd_rn(__fmul_rn(m[d], c), __fmul_rn(m[d - half], s));
+}
+
 __device__ __forceinline__ float rope_one(const float* m, const float* row, int d, int half)
 {
     const int fi = d < half ? d : d - half;
-    const float c = row[2 * fi], s = row[2 * fi + 1];
-    if (d < half) return __fsub_rn(__fmul_rn(m[d], c), __fmul_rn(m[d + half], s));
-    return __fadd_rn(__fmul_rn(m[d], c), __fmul_rn(m[d - half], s));
+    return rope_cs(m, d, half, row[2 * fi], row[2 * fi + 1]);
 }
 
 int rmsnorm(Ctx* c, float* h, const float* delta, const uint16_t* gain, int n, float eps, float* out);

@@ -154,10 +154,10 @@ __global__ void k_rope_kv(const float* __restrict__ q, const float* __restrict__
 // position's score over the 128 dimensions (dotSetScore2, aux.cl:497-540,
 // s = q.k / sqrt(hd)) with q broadcast from LDS; the softmax of
 // aux.cl:204-225 (exp(s)/sum exp(s)) is evaluated with the split's maximum
-// subtracted, which leaves p unchanged; then lane j accumulates dimensions
-// 2j, 2j+1 of sum p*V over the positions.  No value crosses waves, so there
-// is no barrier before the split writes its max m, sum l of exp(s - m) and
-// unnormalised o.  The splits of a KV head count themselves in on a counter
+// subtracted, which leaves p unchanged; then lane (g, j) accumulates
+// dimensions 8j..8j+7 of sum p*V over every fourth position.  The split's K
+// and V rows are loaded once per workgroup, 16 bytes per thread, into LDS;
+// the split writes its max m, sum l of exp(s - m) and unnormalised o.  The splits of a KV head count themselves in on a counter
 // in the workspace; the last one to arrive merges them (combine_head) and
 // re-arms the counter, so one launch produces the attention output.  Acc = double evaluates
 // every product (exact: fp32 x fp16), exponential and sum in fp64 and the
@@ -173,43 +173,83 @@ __device__ __forceinline__ float acc_exp<float>(float x) { return expf(x); }
 template <>
 __device__ __forceinline__ double acc_exp<double>(double x) { return exp(x); }
 
-// Merge of the na splits of query head h by one wave: weights exp(m_s - M)
-// of the split maxima, L = sum of l_s * w_s and O = sum of o_s * w_s in split
-// order, out = O / L; lane j writes dimensions 2j, 2j+1.  sw: kMaxAttnSplits
-// entries of this wave.
-template <typename Acc>
-__device__ void combine_head(const Acc* __restrict__ ws, int h, int n_split, int na, Acc* sw, float* __restrict__ out)
+template <typename T>
+__device__ __forceinline__ T readlane_t(T v, int l);
+template <>
+__device__ __forceinline__ float readlane_t<float>(float v, int l)
 {
-    constexpr int HD = 128;
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+template <>
+__device__ __forceinline__ double readlane_t<double>(double v, int l)
+{
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane((int)b, l);
+    const int hi = __builtin_amdgcn_readlane((int)(b >> 32), l);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+// Merge of the na <= kMaxAttnSplits splits of query head h by one wave:
+// lane s holds split s's (m_s, l_s) and computes w_s = exp(m_s - M) with M
+// the maximum of the m_s; L = sum of l_s * w_s and O = sum of o_s * w_s in
+// split order, out = O / L; lane j writes dimensions 2j, 2j+1.  The o loads
+// of a batch of 16 splits do not depend on M and are issued with the (m, l)
+// loads, so up to 16 splits (1024 positions) cost one round trip.
+template <typename Acc>
+__device__ void combine_head(const Acc* __restrict__ ws, int h, int n_split, int na, float* __restrict__ out)
+{
+    constexpr int HD = 128, B = 16;
+    static_assert(kMaxAttnSplits <= 128, "two splits per lane");
     const int lane = threadIdx.x & 63;
     const Acc* base = ws + (size_t)h * n_split * (HD + 2);
-    Acc M = (Acc)-INFINITY;
-    for (int s = lane; s < na; s += 64) M = fmax(M, base[(size_t)s * (HD + 2) + HD]);
-    M = wave_max_t(M);
-    for (int s = lane; s < na; s += 64) sw[s] = acc_exp<Acc>(base[(size_t)s * (HD + 2) + HD] - M);
-    Acc L = (Acc)0, O0 = (Acc)0, O1 = (Acc)0;
-    for (int s0 = 0; s0 < na; s0 += 8) {
-        Acc o0[8], o1[8], lv[8];
+    Acc mv[2], lv[2];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
+    for (int k = 0; k < 2; k++) {
+        const int s = lane + 64 * k;
+        mv[k] = s < na ? base[(size_t)s * (HD + 2) + HD] : (Acc)-INFINITY;
+        lv[k] = s < na ? base[(size_t)s * (HD + 2) + HD + 1] : (Acc)0;
+    }
+    Acc o0[B], o1[B];
+    auto load_batch = [&](int s0) {
+#pragma unroll
+        for (int i = 0; i < B; i++) {
             const Acc* row = base + (size_t)min(s0 + i, na - 1) * (HD + 2);
             o0[i] = row[2 * lane];
             o1[i] = row[2 * lane + 1];
-            lv[i] = row[HD + 1];
         }
+    };
+    load_batch(0);
+    const Acc M = wave_max_t(mv[0] > mv[1] ? mv[0] : mv[1]);
+    Acc wv[2];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            if (s0 + i < na) {
-                const Acc w = sw[s0 + i];
-                L += lv[i] * w;
-                O0 += o0[i] * w;
-                O1 += o1[i] * w;
+    for (int k = 0; k < 2; k++) wv[k] = lane + 64 * k < na ? acc_exp<Acc>(mv[k] - M) : (Acc)0;
+    Acc L = (Acc)0, O0 = (Acc)0, O1 = (Acc)0;
+    for (int s0 = 0; s0 < na; s0 += B) {
+        Acc c0[B], c1[B];
+#pragma unroll
+        for (int i = 0; i < B; i++) {
+            c0[i] = o0[i];
+            c1[i] = o1[i];
+        }
+        if (s0 + B < na) load_batch(s0 + B);
+#pragma unroll
+        for (int i = 0; i < B; i++) {
+            const int s = s0 + i;
+            if (s < na) {
+                const Acc w = readlane_t(s < 64 ? wv[0] : wv[1], s & 63);
+                L += readlane_t(s < 64 ? lv[0] : lv[1], s & 63) * w;
+                O0 += c0[i] * w;
+                O1 += c1[i] * w;
             }
         }
     }
     out[h * HD + 2 * lane] = (float)(O0 / L);
     out[h * HD + 2 * lane + 1] = (float)(O1 / L);
 }
+
+// LDS copies of the split's K and V rows: 128 fp16 + 8 fp16 of padding, so
+// that lanes reading 16 bytes of consecutive rows start on different banks.
+constexpr int kAttnRowStride = 128 + 8;
 
 template <typename Acc>
 __global__ __launch_bounds__(64 * kAttnMaxRep) void k_attn_partial(const float* __restrict__ q,
@@ -221,73 +261,108 @@ __global__ __launch_bounds__(64 * kAttnMaxRep) void k_attn_partial(const float* 
                                                                    unsigned int* __restrict__ done,
                                                                    float* __restrict__ out)
 {
-    constexpr int HD = 128;
+    constexpr int HD = 128, RS = kAttnRowStride;
+    __shared__ __align__(16) uint16_t sk[kAttnChunk * RS];
+    __shared__ __align__(16) uint16_t sv[kAttnChunk * RS];
     __shared__ Acc sq[kAttnMaxRep][HD];
-    __shared__ Acc sp[kAttnMaxRep][kMaxAttnSplits > kAttnChunk ? kMaxAttnSplits : kAttnChunk];
+    __shared__ Acc sp[kAttnMaxRep][kAttnChunk];
     __shared__ int s_last;
     const int kvh = blockIdx.x;
     const int split = blockIdx.y;
-    const int lane = threadIdx.x & 63;
-    const int r = threadIdx.x >> 6;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int r = tid >> 6;
     const int rep = n_heads / n_kv;
+    const int nthr = 64 * rep;
     int n_tok = *pos_p + 1;
     if (n_tok > max_ctx) n_tok = max_ctx;
     const int t0 = split * kAttnChunk;
     const int nt = min(kAttnChunk, max(0, n_tok - t0));
-    // workspace row of query head h = kvh*rep + r, split s: ws[(h*n_split + s)*(HD+2)]
-    Acc* wrow = ws + ((size_t)(kvh * rep + r) * n_split + split) * (HD + 2);
-    if (r >= rep) return;
     if (nt == 0) return;   // past the context: neither written nor counted
-    // every load first: q of this head, the K row of position t0 + lane and
-    // dimensions 2*lane, 2*lane+1 of the V rows of the split's positions
+    // the split's K and V rows, 16 bytes per thread and load, into LDS
     const float* qh = q + (size_t)(kvh * rep + r) * HD;
     const float q0 = qh[lane], q1 = qh[lane + 64];
-    const int tt = t0 + min(lane, nt - 1);
-    const uint4* kr = reinterpret_cast<const uint4*>(kc + ((size_t)tt * n_kv + kvh) * HD);
-    uint4 kv[HD / 8];
+    const int pieces = nt * (HD / 8);
+    for (int b0 = 0; b0 < pieces; b0 += 4 * nthr) {
+        uint4 kq[4], vq[4];
 #pragma unroll
-    for (int i = 0; i < HD / 8; i++) kv[i] = kr[i];
-    uint32_t vv[kAttnChunk];
+        for (int u = 0; u < 4; u++) {
+            const int idx = min(b0 + u * nthr + tid, pieces - 1);
+            const size_t g = ((size_t)(t0 + (idx >> 4)) * n_kv + kvh) * HD + (idx & 15) * 8;
+            kq[u] = *reinterpret_cast<const uint4*>(kc + g);
+            vq[u] = *reinterpret_cast<const uint4*>(vc + g);
+        }
 #pragma unroll
-    for (int i = 0; i < kAttnChunk; i++)
-        vv[i] = *reinterpret_cast<const uint32_t*>(vc + ((size_t)(t0 + min(i, nt - 1)) * n_kv + kvh) * HD + 2 * lane);
+        for (int u = 0; u < 4; u++) {
+            const int idx = b0 + u * nthr + tid;
+            if (idx < pieces) {
+                const int o = (idx >> 4) * RS + (idx & 15) * 8;
+                *reinterpret_cast<uint4*>(sk + o) = kq[u];
+                *reinterpret_cast<uint4*>(sv + o) = vq[u];
+            }
+        }
+    }
     sq[r][lane] = (Acc)q0;
     sq[r][lane + 64] = (Acc)q1;
-    // the wave's own LDS rows: its writes precede its reads, no barrier
+    __syncthreads();
+    // score of position t0 + lane for query head kvh*rep + r
     Acc s = (Acc)0;
+    {
+        const uint4* kr = reinterpret_cast<const uint4*>(sk + min(lane, nt - 1) * RS);
 #pragma unroll
-    for (int i = 0; i < HD / 8; i++) {
-        const uint32_t w[4] = {kv[i].x, kv[i].y, kv[i].z, kv[i].w};
+        for (int i = 0; i < HD / 8; i++) {
+            const uint4 kv = kr[i];
+            const uint32_t w[4] = {kv.x, kv.y, kv.z, kv.w};
 #pragma unroll
-        for (int e = 0; e < 8; e++) s = fma(sq[r][i * 8 + e], (Acc)h2f((uint16_t)(w[e >> 1] >> ((e & 1) * 16))), s);
+            for (int e = 0; e < 8; e++)
+                s = fma(sq[r][i * 8 + e], (Acc)h2f((uint16_t)(w[e >> 1] >> ((e & 1) * 16))), s);
+        }
     }
     s = lane < nt ? s * scale : (Acc)-INFINITY;
     const Acc m = wave_max_t(s);
     const Acc p = lane < nt ? acc_exp<Acc>(s - m) : (Acc)0;
     const Acc l = wave_sum(p);
-    sp[r][lane] = p;
-    Acc o0 = (Acc)0, o1 = (Acc)0;
+    sp[r][lane] = p;   // read back by this wave only: no barrier
+    // sum of p * V: lane (g, j) takes dimensions 8j..8j+7 of the positions
+    // g, g + 4, ...; the four g partials are added pairwise across lanes
+    const int g = lane >> 4, j = lane & 15;
+    Acc o[8];
 #pragma unroll
-    for (int i = 0; i < kAttnChunk; i++) {
+    for (int e = 0; e < 8; e++) o[e] = (Acc)0;
+#pragma unroll
+    for (int u = 0; u < kAttnChunk / 4; u++) {
+        const int i = g + 4 * u;
         if (i < nt) {
             const Acc pi = sp[r][i];
-            o0 = fma(pi, (Acc)h2f((uint16_t)(vv[i] & 0xffffu)), o0);
-            o1 = fma(pi, (Acc)h2f((uint16_t)(vv[i] >> 16)), o1);
+            const uint4 vv = *reinterpret_cast<const uint4*>(sv + i * RS + j * 8);
+            const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                o[e] = fma(pi, (Acc)h2f((uint16_t)(w[e >> 1] >> ((e & 1) * 16))), o[e]);
         }
     }
-    wrow[2 * lane] = o0;
-    wrow[2 * lane + 1] = o1;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        o[e] += __shfl_xor(o[e], 16, 64);
+        o[e] += __shfl_xor(o[e], 32, 64);
+    }
+    // workspace row of query head h = kvh*rep + r, split s: ws[(h*n_split + s)*(HD+2)]
+    Acc* wrow = ws + ((size_t)(kvh * rep + r) * n_split + split) * (HD + 2);
+    if (g == 0) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) wrow[j * 8 + e] = o[e];
+    }
     if (lane == 0) {
         wrow[HD] = m;
         wrow[HD + 1] = l;
     }
     // the last split of this KV head to finish merges the splits of its
-    // query heads (one wave per head) and re-arms the counter
-    // (one agent-scope fence per workgroup: the barrier orders the other
-    // waves' stores before thread 0's release)
+    // query heads (one wave per head) and re-arms the counter (one
+    // agent-scope fence per workgroup: the barrier orders the other waves'
+    // stores before thread 0's release)
     const int na = (n_tok + kAttnChunk - 1) / kAttnChunk;
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid == 0) {
         __threadfence();
         const bool last = atomicAdd(done + kvh, 1u) == (unsigned int)(na - 1);
         if (last) __threadfence();
@@ -295,8 +370,8 @@ __global__ __launch_bounds__(64 * kAttnMaxRep) void k_attn_partial(const float* 
     }
     __syncthreads();
     if (!s_last) return;
-    combine_head<Acc>(ws, kvh * rep + r, n_split, na, sp[r], out);
-    if (threadIdx.x == 0) done[kvh] = 0u;
+    combine_head<Acc>(ws, kvh * rep + r, n_split, na, out);
+    if (tid == 0) done[kvh] = 0u;
 }
 
 // ---------------------------------------------------------------- embed ---
