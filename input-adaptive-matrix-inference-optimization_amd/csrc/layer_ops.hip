@@ -150,18 +150,20 @@ __global__ void k_rope_kv(const float* __restrict__ q, const float* __restrict__
 // ("flash-decoding").  Workgroup (kv head, split) handles kAttnChunk = 64
 // positions for the rep = n_heads/n_kv query heads that read this KV head
 // (repeat4x32, aux.cl:266-275, without materialising the repeat): wave r is
-// query head kvh*rep + r and lane i position t0 + i.  Each lane computes its
-// position's score over the 128 dimensions (dotSetScore2, aux.cl:497-540,
-// s = q.k / sqrt(hd)) with q broadcast from LDS; the softmax of
-// aux.cl:204-225 (exp(s)/sum exp(s)) is evaluated with the split's maximum
-// subtracted, which leaves p unchanged; then lane (g, j) accumulates
-// dimensions 8j..8j+7 of sum p*V over every fourth position.  The split's K
-// and V rows are loaded once per workgroup, 16 bytes per thread, into LDS;
-// the split writes its max m, sum l of exp(s - m) and unnormalised o.  The splits of a KV head count themselves in on a counter
-// in the workspace; the last one to arrive merges them (combine_head) and
-// re-arms the counter, so one launch produces the attention output.  Acc = double evaluates
-// every product (exact: fp32 x fp16), exponential and sum in fp64 and the
-// output is rounded once; Acc = float is the fp32 evaluation.
+// query head kvh*rep + r % rep, half r / rep of the head dimension, and lane
+// i position t0 + i.  Each lane computes its position's half dot product
+// (dotSetScore2, aux.cl:497-540, s = q.k / sqrt(hd)) with q broadcast from
+// LDS, and the halves are added through LDS; the softmax of aux.cl:204-225
+// (exp(s)/sum exp(s)) is evaluated with the split's maximum subtracted, which
+// leaves p unchanged; then lane (g, j) accumulates 8 dimensions of the
+// wave's half of sum p*V over every eighth position.  The split's K and V
+// rows are loaded once per workgroup, 16 bytes per thread, into LDS; the
+// split writes its max m, sum l of exp(s - m) and unnormalised o.  The splits
+// of a KV head count themselves in on a counter in the workspace; the last
+// one to arrive merges them (combine_head) and re-arms the counter, so one
+// launch produces the attention output.  Acc = double evaluates every product
+// (exact: fp32 x fp16), exponential and sum in fp64 and the output is rounded
+// once; Acc = float is the fp32 evaluation.
 constexpr int kAttnChunk = 64;
 constexpr int kAttnMaxRep = 8;
 constexpr int kMaxAttnSplits = 128;   // max_ctx up to 8192
@@ -193,8 +195,7 @@ __device__ __forceinline__ double readlane_t<double>(double v, int l)
 // lane s holds split s's (m_s, l_s) and computes w_s = exp(m_s - M) with M
 // the maximum of the m_s; L = sum of l_s * w_s and O = sum of o_s * w_s in
 // split order, out = O / L; lane j writes dimensions 2j, 2j+1.  The o loads
-// of a batch of 16 splits do not depend on M and are issued with the (m, l)
-// loads, so up to 16 splits (1024 positions) cost one round trip.
+// go out in batches of 16 splits (1024 positions).
 template <typename Acc>
 __device__ void combine_head(const Acc* __restrict__ ws, int h, int n_split, int na, float* __restrict__ out)
 {
@@ -209,37 +210,27 @@ __device__ void combine_head(const Acc* __restrict__ ws, int h, int n_split, int
         mv[k] = s < na ? base[(size_t)s * (HD + 2) + HD] : (Acc)-INFINITY;
         lv[k] = s < na ? base[(size_t)s * (HD + 2) + HD + 1] : (Acc)0;
     }
-    Acc o0[B], o1[B];
-    auto load_batch = [&](int s0) {
-#pragma unroll
-        for (int i = 0; i < B; i++) {
-            const Acc* row = base + (size_t)min(s0 + i, na - 1) * (HD + 2);
-            o0[i] = row[2 * lane];
-            o1[i] = row[2 * lane + 1];
-        }
-    };
-    load_batch(0);
     const Acc M = wave_max_t(mv[0] > mv[1] ? mv[0] : mv[1]);
     Acc wv[2];
 #pragma unroll
     for (int k = 0; k < 2; k++) wv[k] = lane + 64 * k < na ? acc_exp<Acc>(mv[k] - M) : (Acc)0;
     Acc L = (Acc)0, O0 = (Acc)0, O1 = (Acc)0;
     for (int s0 = 0; s0 < na; s0 += B) {
-        Acc c0[B], c1[B];
+        Acc o0[B], o1[B];
 #pragma unroll
         for (int i = 0; i < B; i++) {
-            c0[i] = o0[i];
-            c1[i] = o1[i];
+            const Acc* row = base + (size_t)min(s0 + i, na - 1) * (HD + 2);
+            o0[i] = row[2 * lane];
+            o1[i] = row[2 * lane + 1];
         }
-        if (s0 + B < na) load_batch(s0 + B);
 #pragma unroll
         for (int i = 0; i < B; i++) {
             const int s = s0 + i;
             if (s < na) {
                 const Acc w = readlane_t(s < 64 ? wv[0] : wv[1], s & 63);
                 L += readlane_t(s < 64 ? lv[0] : lv[1], s & 63) * w;
-                O0 += c0[i] * w;
-                O1 += c1[i] * w;
+                O0 += o0[i] * w;
+                O1 += o1[i] * w;
             }
         }
     }
@@ -251,21 +242,25 @@ __device__ void combine_head(const Acc* __restrict__ ws, int h, int n_split, int
 // that lanes reading 16 bytes of consecutive rows start on different banks.
 constexpr int kAttnRowStride = 128 + 8;
 
+// Two waves per query head: wave r is head hr = r % rep, half hf = r / rep,
+// and takes dimensions [64 hf, 64 hf + 64) of the scores' dot products and
+// of sum p*V.
 template <typename Acc>
-__global__ __launch_bounds__(64 * kAttnMaxRep) void k_attn_partial(const float* __restrict__ q,
-                                                                   const uint16_t* __restrict__ kc,
-                                                                   const uint16_t* __restrict__ vc,
-                                                                   const int* __restrict__ pos_p, int n_heads,
-                                                                   int n_kv, int max_ctx, Acc scale,
-                                                                   Acc* __restrict__ ws, int n_split,
-                                                                   unsigned int* __restrict__ done,
-                                                                   float* __restrict__ out)
+__global__ __launch_bounds__(128 * kAttnMaxRep) void k_attn_partial(const float* __restrict__ q,
+                                                                    const uint16_t* __restrict__ kc,
+                                                                    const uint16_t* __restrict__ vc,
+                                                                    const int* __restrict__ pos_p, int n_heads,
+                                                                    int n_kv, int max_ctx, Acc scale,
+                                                                    Acc* __restrict__ ws, int n_split,
+                                                                    unsigned int* __restrict__ done,
+                                                                    float* __restrict__ out)
 {
-    constexpr int HD = 128, RS = kAttnRowStride;
+    constexpr int HD = 128, RS = kAttnRowStride, DH = HD / 2;
     __shared__ __align__(16) uint16_t sk[kAttnChunk * RS];
     __shared__ __align__(16) uint16_t sv[kAttnChunk * RS];
     __shared__ Acc sq[kAttnMaxRep][HD];
-    __shared__ Acc sp[kAttnMaxRep][kAttnChunk];
+    __shared__ Acc ss[2][kAttnMaxRep][kAttnChunk];          // half-dot products
+    __shared__ Acc sp[2 * kAttnMaxRep][kAttnChunk];         // p, one copy per wave
     __shared__ int s_last;
     const int kvh = blockIdx.x;
     const int split = blockIdx.y;
@@ -273,15 +268,15 @@ __global__ __launch_bounds__(64 * kAttnMaxRep) void k_attn_partial(const float* 
     const int lane = tid & 63;
     const int r = tid >> 6;
     const int rep = n_heads / n_kv;
-    const int nthr = 64 * rep;
+    const int hr = r % rep, hf = r / rep;
+    const int nthr = 128 * rep;
     int n_tok = *pos_p + 1;
     if (n_tok > max_ctx) n_tok = max_ctx;
     const int t0 = split * kAttnChunk;
     const int nt = min(kAttnChunk, max(0, n_tok - t0));
     if (nt == 0) return;   // past the context: neither written nor counted
     // the split's K and V rows, 16 bytes per thread and load, into LDS
-    const float* qh = q + (size_t)(kvh * rep + r) * HD;
-    const float q0 = qh[lane], q1 = qh[lane + 64];
+    const float qv = q[(size_t)(kvh * rep + hr) * HD + hf * DH + lane];
     const int pieces = nt * (HD / 8);
     for (int b0 = 0; b0 < pieces; b0 += 4 * nthr) {
         uint4 kq[4], vq[4];
@@ -302,39 +297,42 @@ __global__ __launch_bounds__(64 * kAttnMaxRep) void k_attn_partial(const float* 
             }
         }
     }
-    sq[r][lane] = (Acc)q0;
-    sq[r][lane + 64] = (Acc)q1;
+    sq[hr][hf * DH + lane] = (Acc)qv;
     __syncthreads();
-    // score of position t0 + lane for query head kvh*rep + r
-    Acc s = (Acc)0;
+    // half dot product of position t0 + lane, then the two halves in order
     {
-        const uint4* kr = reinterpret_cast<const uint4*>(sk + min(lane, nt - 1) * RS);
+        Acc sh = (Acc)0;
+        const uint4* kr = reinterpret_cast<const uint4*>(sk + min(lane, nt - 1) * RS + hf * DH);
 #pragma unroll
-        for (int i = 0; i < HD / 8; i++) {
+        for (int i = 0; i < DH / 8; i++) {
             const uint4 kv = kr[i];
             const uint32_t w[4] = {kv.x, kv.y, kv.z, kv.w};
 #pragma unroll
             for (int e = 0; e < 8; e++)
-                s = fma(sq[r][i * 8 + e], (Acc)h2f((uint16_t)(w[e >> 1] >> ((e & 1) * 16))), s);
+                sh = fma(sq[hr][hf * DH + i * 8 + e], (Acc)h2f((uint16_t)(w[e >> 1] >> ((e & 1) * 16))), sh);
         }
+        ss[hf][hr][lane] = sh;
     }
+    __syncthreads();
+    Acc s = ss[0][hr][lane] + ss[1][hr][lane];
     s = lane < nt ? s * scale : (Acc)-INFINITY;
     const Acc m = wave_max_t(s);
     const Acc p = lane < nt ? acc_exp<Acc>(s - m) : (Acc)0;
     const Acc l = wave_sum(p);
     sp[r][lane] = p;   // read back by this wave only: no barrier
-    // sum of p * V: lane (g, j) takes dimensions 8j..8j+7 of the positions
-    // g, g + 4, ...; the four g partials are added pairwise across lanes
-    const int g = lane >> 4, j = lane & 15;
+    // sum of p * V over this half's dimensions: lane (g, j) takes dimensions
+    // hf*64 + 8j..8j+7 of the positions g, g + 8, ...; the eight g partials
+    // are added pairwise across lanes
+    const int g = lane >> 3, j = lane & 7;
     Acc o[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) o[e] = (Acc)0;
 #pragma unroll
-    for (int u = 0; u < kAttnChunk / 4; u++) {
-        const int i = g + 4 * u;
+    for (int u = 0; u < kAttnChunk / 8; u++) {
+        const int i = g + 8 * u;
         if (i < nt) {
             const Acc pi = sp[r][i];
-            const uint4 vv = *reinterpret_cast<const uint4*>(sv + i * RS + j * 8);
+            const uint4 vv = *reinterpret_cast<const uint4*>(sv + i * RS + hf * DH + j * 8);
             const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
             for (int e = 0; e < 8; e++)
@@ -343,16 +341,17 @@ __global__ __launch_bounds__(64 * kAttnMaxRep) void k_attn_partial(const float* 
     }
 #pragma unroll
     for (int e = 0; e < 8; e++) {
+        o[e] += __shfl_xor(o[e], 8, 64);
         o[e] += __shfl_xor(o[e], 16, 64);
         o[e] += __shfl_xor(o[e], 32, 64);
     }
-    // workspace row of query head h = kvh*rep + r, split s: ws[(h*n_split + s)*(HD+2)]
-    Acc* wrow = ws + ((size_t)(kvh * rep + r) * n_split + split) * (HD + 2);
+    // workspace row of query head h = kvh*rep + hr, split s: ws[(h*n_split + s)*(HD+2)]
+    Acc* wrow = ws + ((size_t)(kvh * rep + hr) * n_split + split) * (HD + 2);
     if (g == 0) {
 #pragma unroll
-        for (int e = 0; e < 8; e++) wrow[j * 8 + e] = o[e];
+        for (int e = 0; e < 8; e++) wrow[hf * DH + j * 8 + e] = o[e];
     }
-    if (lane == 0) {
+    if (hf == 0 && lane == 0) {
         wrow[HD] = m;
         wrow[HD + 1] = l;
     }
@@ -370,7 +369,7 @@ __global__ __launch_bounds__(64 * kAttnMaxRep) void k_attn_partial(const float* 
     }
     __syncthreads();
     if (!s_last) return;
-    combine_head<Acc>(ws, kvh * rep + r, n_split, na, out);
+    if (hf == 0) combine_head<Acc>(ws, kvh * rep + hr, n_split, na, out);
     if (tid == 0) done[kvh] = 0u;
 }
 
@@ -499,11 +498,11 @@ int attention(Ctx* c, const float* q, const uint16_t* kc, const uint16_t* vc, co
     ws += kAttnCounters;
     if (c->acc64) {
         const double scale = 1.0 / std::sqrt(128.0);
-        return launch(c, "attention", k_attn_partial<double>, dim3(n_kv, n_split), dim3(64 * (n_heads / n_kv)), 0,
+        return launch(c, "attention", k_attn_partial<double>, dim3(n_kv, n_split), dim3(128 * (n_heads / n_kv)), 0,
                       q, kc, vc, pos, n_heads, n_kv, max_ctx, scale, (double*)ws, n_split, done, out);
     }
     const float scale = 1.0f / std::sqrt(128.0f);
-    return launch(c, "attention", k_attn_partial<float>, dim3(n_kv, n_split), dim3(64 * (n_heads / n_kv)), 0, q,
+    return launch(c, "attention", k_attn_partial<float>, dim3(n_kv, n_split), dim3(128 * (n_heads / n_kv)), 0, q,
                   kc, vc, pos, n_heads, n_kv, max_ctx, scale, ws, n_split, done, out);
 }
 

@@ -119,13 +119,33 @@ __global__ __launch_bounds__(1024) void k_pick(const float* __restrict__ v, int 
     const int tid = threadIdx.x;
     float bv = -INFINITY;
     int bi = n;
-    for (int i = tid; i < n; i += 1024) {
-        const float x = v[i];
+    auto take = [&](float x, int i) {
         if (x > bv || (x == bv && i < bi)) {
             bv = x;
             bi = i;
         }
+    };
+    // 16-byte loads, 8 per thread in flight (the order of the candidates a
+    // thread sees does not matter: ties go to the smaller index)
+    const int n4 = (reinterpret_cast<uintptr_t>(v) & 15) == 0 ? n >> 2 : 0;
+    const float4* v4 = reinterpret_cast<const float4*>(v);
+    constexpr int U = 8;
+    for (int b0 = 0; b0 < n4; b0 += U * 1024) {
+        float4 r[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) r[u] = v4[min(b0 + u * 1024 + tid, n4 - 1)];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int j = b0 + u * 1024 + tid;
+            if (j < n4) {
+                take(r[u].x, 4 * j);
+                take(r[u].y, 4 * j + 1);
+                take(r[u].z, 4 * j + 2);
+                take(r[u].w, 4 * j + 3);
+            }
+        }
     }
+    for (int i = 4 * n4 + tid; i < n; i += 1024) take(v[i], i);
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(bv, o, 64);
         const int oi = __shfl_xor(bi, o, 64);
