@@ -158,12 +158,11 @@ __global__ void k_rope_kv(const float* __restrict__ q, const float* __restrict__
 // leaves p unchanged; then lane (g, j) accumulates 8 dimensions of the
 // wave's half of sum p*V over every eighth position.  The split's K and V
 // rows are loaded once per workgroup, 16 bytes per thread, into LDS; the
-// split writes its max m, sum l of exp(s - m) and unnormalised o.  The splits
-// of a KV head count themselves in on a counter in the workspace; the last
-// one to arrive merges them (combine_head) and re-arms the counter, so one
-// launch produces the attention output.  Acc = double evaluates every product
-// (exact: fp32 x fp16), exponential and sum in fp64 and the output is rounded
-// once; Acc = float is the fp32 evaluation.
+// split writes its max m, sum l of exp(s - m) and unnormalised o, and
+// k_attn_combine merges the splits (a second launch costs less than a
+// release/acquire handoff between the splits' workgroups).  Acc = double
+// evaluates every product (exact: fp32 x fp16), exponential and sum in fp64
+// and the output is rounded once; Acc = float is the fp32 evaluation.
 constexpr int kAttnChunk = 64;
 constexpr int kAttnMaxRep = 8;
 constexpr int kMaxAttnSplits = 128;   // max_ctx up to 8192
@@ -251,9 +250,7 @@ __global__ __launch_bounds__(128 * kAttnMaxRep) void k_attn_partial(const float*
                                                                     const uint16_t* __restrict__ vc,
                                                                     const int* __restrict__ pos_p, int n_heads,
                                                                     int n_kv, int max_ctx, Acc scale,
-                                                                    Acc* __restrict__ ws, int n_split,
-                                                                    unsigned int* __restrict__ done,
-                                                                    float* __restrict__ out)
+                                                                    Acc* __restrict__ ws, int n_split)
 {
     constexpr int HD = 128, RS = kAttnRowStride, DH = HD / 2;
     __shared__ __align__(16) uint16_t sk[kAttnChunk * RS];
@@ -261,7 +258,6 @@ __global__ __launch_bounds__(128 * kAttnMaxRep) void k_attn_partial(const float*
     __shared__ Acc sq[kAttnMaxRep][HD];
     __shared__ Acc ss[2][kAttnMaxRep][kAttnChunk];          // half-dot products
     __shared__ Acc sp[2 * kAttnMaxRep][kAttnChunk];         // p, one copy per wave
-    __shared__ int s_last;
     const int kvh = blockIdx.x;
     const int split = blockIdx.y;
     const int tid = threadIdx.x;
@@ -355,22 +351,16 @@ __global__ __launch_bounds__(128 * kAttnMaxRep) void k_attn_partial(const float*
         wrow[HD] = m;
         wrow[HD + 1] = l;
     }
-    // the last split of this KV head to finish merges the splits of its
-    // query heads (one wave per head) and re-arms the counter (one
-    // agent-scope fence per workgroup: the barrier orders the other waves'
-    // stores before thread 0's release)
-    const int na = (n_tok + kAttnChunk - 1) / kAttnChunk;
-    __syncthreads();
-    if (tid == 0) {
-        __threadfence();
-        const bool last = atomicAdd(done + kvh, 1u) == (unsigned int)(na - 1);
-        if (last) __threadfence();
-        s_last = last;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    if (hf == 0) combine_head<Acc>(ws, kvh * rep + hr, n_split, na, out);
-    if (tid == 0) done[kvh] = 0u;
+}
+
+// Merge of the splits: one wave per query head.
+template <typename Acc>
+__global__ __launch_bounds__(64) void k_attn_combine(const Acc* __restrict__ ws, const int* __restrict__ pos_p,
+                                                    int max_ctx, int n_split, float* __restrict__ out)
+{
+    int n_tok = *pos_p + 1;
+    if (n_tok > max_ctx) n_tok = max_ctx;
+    combine_head<Acc>(ws, blockIdx.x, n_split, (n_tok + kAttnChunk - 1) / kAttnChunk, out);
 }
 
 // ---------------------------------------------------------------- embed ---
@@ -478,10 +468,7 @@ int rope_kv(Ctx* c, const float* q, const float* k, const float* v, const float*
                   n_heads, n_kv, hd, max_ctx, q_out, kc, vc);
 }
 
-// The workspace holds one completion counter per KV head (zero between
-// launches) in its first kAttnCounters words, at the same place whatever
-// max_ctx a call names, then the partials (o[128], m, l) per head and split.
-constexpr int kAttnCounters = 64;
+// The workspace holds the partials (o[128], m, l) per head and split.
 static size_t attn_partial_floats(int n_heads, int max_ctx)
 {
     const int n_split = (max_ctx + kAttnChunk - 1) / kAttnChunk;
@@ -493,22 +480,23 @@ int attention(Ctx* c, const float* q, const uint16_t* kc, const uint16_t* vc, co
 {
     const int n_split = (max_ctx + kAttnChunk - 1) / kAttnChunk;
     IAM_REQUIRE(n_split <= kMaxAttnSplits, "attention: max_ctx above 8192");
-    IAM_REQUIRE(n_kv <= kAttnCounters, "attention: more than 64 KV heads");
-    unsigned int* done = reinterpret_cast<unsigned int*>(ws);
-    ws += kAttnCounters;
     if (c->acc64) {
         const double scale = 1.0 / std::sqrt(128.0);
-        return launch(c, "attention", k_attn_partial<double>, dim3(n_kv, n_split), dim3(128 * (n_heads / n_kv)), 0,
-                      q, kc, vc, pos, n_heads, n_kv, max_ctx, scale, (double*)ws, n_split, done, out);
+        IAM_TRY(launch(c, "attn_partial", k_attn_partial<double>, dim3(n_kv, n_split), dim3(128 * (n_heads / n_kv)),
+                       0, q, kc, vc, pos, n_heads, n_kv, max_ctx, scale, (double*)ws, n_split));
+        return launch(c, "attn_combine", k_attn_combine<double>, dim3(n_heads), dim3(64), 0, (const double*)ws, pos,
+                      max_ctx, n_split, out);
     }
     const float scale = 1.0f / std::sqrt(128.0f);
-    return launch(c, "attention", k_attn_partial<float>, dim3(n_kv, n_split), dim3(128 * (n_heads / n_kv)), 0, q,
-                  kc, vc, pos, n_heads, n_kv, max_ctx, scale, ws, n_split, done, out);
+    IAM_TRY(launch(c, "attn_partial", k_attn_partial<float>, dim3(n_kv, n_split), dim3(128 * (n_heads / n_kv)), 0, q,
+                   kc, vc, pos, n_heads, n_kv, max_ctx, scale, ws, n_split));
+    return launch(c, "attn_combine", k_attn_combine<float>, dim3(n_heads), dim3(64), 0, (const float*)ws, pos,
+                  max_ctx, n_split, out);
 }
 
 size_t attention_ws_floats(int n_heads, int max_ctx)
 {
-    return kAttnCounters + attn_partial_floats(n_heads, max_ctx);
+    return attn_partial_floats(n_heads, max_ctx);
 }
 
 int embed(Ctx* c, const uint16_t* table, int cols, int vocab, const int* tok, float* out)

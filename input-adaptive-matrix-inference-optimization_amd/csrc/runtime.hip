@@ -114,9 +114,6 @@ int ensure_attn_ws(Ctx* c, size_t floats)
     c->attn_ws_floats = 0;
     IAM_TRY(ctx_alloc(c, floats * sizeof(float), (void**)&c->attn_ws));
     c->attn_ws_floats = floats;
-    // the attention kernel's per-KV-head counters start at zero and each
-    // launch leaves them at zero
-    IAM_CHECK_HIP(hipMemsetAsync(c->attn_ws, 0, floats * sizeof(float), c->stream));
     c->scratch_gen++;
     return IAM_OK;
 }
