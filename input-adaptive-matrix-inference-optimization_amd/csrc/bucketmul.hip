@@ -221,12 +221,17 @@ __device__ __forceinline__ void block_rmsnorm4096(float (&v)[kCutVPT], const uin
     __syncthreads();
     if (tid < 64) {
         // lane l: part[l] + part[l+128] and part[l+64] + part[l+192] (st = 128),
-        // their sum (st = 64), then st = 32 .. 1 as shuffles
+        // their sum (st = 64), then st = 32, 16 as shuffles and st = 8 .. 1
+        // within 16-lane rows by DPP row_shl (lane l takes lane l + st)
         const float a = __fadd_rn(s_red[tid], s_red[tid + 128]);
         const float b = __fadd_rn(s_red[tid + 64], s_red[tid + 192]);
         sq = __fadd_rn(a, b);
-#pragma unroll
-        for (int st = 32; st > 0; st >>= 1) sq = __fadd_rn(sq, __shfl_down(sq, st, 64));
+        sq = __fadd_rn(sq, __shfl_down(sq, 32, 64));
+        sq = __fadd_rn(sq, __shfl_down(sq, 16, 64));
+        sq = __fadd_rn(sq, dpp_f<0x108>(0.0f, sq));
+        sq = __fadd_rn(sq, dpp_f<0x104>(0.0f, sq));
+        sq = __fadd_rn(sq, dpp_f<0x102>(0.0f, sq));
+        sq = __fadd_rn(sq, dpp_f<0x101>(0.0f, sq));
         if (tid == 0) s_red[256] = sq;
     }
     __syncthreads();
@@ -468,14 +473,6 @@ struct WalkArgs {
     int n;
 };
 
-// Selection of slice p (prepareDispatch, bucketMul.cl:351-386): thread i
-// takes input i0 + i, loads its x and the stats of its 16 rows, and marks the
-// rows with 1e5 * |x * stat| >= cutoff -- the same fp32 operations as the
-// dispatch kernel, so the selected set is the same.  A block scan compacts
-// the selected rows in ascending order into s_row (slice-local ids
-// input*16 + rank); s_x[i] = x[i0 + i].  Ends with a barrier; returns the
-// number of selected rows.  The tile-0 workgroup of the slice adds the count
-// to the matrix's counters.
 // Loads of the selection: the 16 stats (channel stats_channel) of input
 // i0 + tid's rows and, unless x_lds, its x.  Issued before the cutoff is
 // known so that their latency overlaps the search; the raw words are kept
