@@ -16,6 +16,10 @@ walk's own dispatch on the library's stream during eager steps, against the
 (FETCH_SIZE + WRITE_SIZE, calibrated on a copy of known size) read from the
 committed counter summary profiles/walk_hbm_traffic_mistral7b_effort025.md.
 
+effort_sweep: the same decode continued at efforts 1.0, 0.5, 0.125 and
+0.05 (32 graph-replayed steps each): tok/s and the fraction of 8 TB/s for
+the bytes touched per token at that effort.
+
 cpu_baseline: the C oracle on one host core, timed on a bounded sample
 (decoder layers and the LM head of the same model at the same effort and
 context), scaled to tokens per second of the 32-layer model.
@@ -35,6 +39,8 @@ PKG = os.path.join(ROOT, "input-adaptive-matrix-inference-optimization_amd")
 MISTRAL = dict(n_layers=32, dim=4096, ffn_dim=14336, n_heads=32, n_kv_heads=8, head_dim=128,
                vocab=32000, max_ctx=4096, rope_theta=10000.0, norm_eps=1e-5)
 HBM_PEAK_GBS = 8000.0
+SWEEP_EFFORTS = [1.0, 0.5, 0.25, 0.125, 0.05]   # the configs' efforts
+SWEEP_WARMUP = 4
 
 
 def load_iam():
@@ -119,6 +125,69 @@ def cpu_baseline(iam, model, cfg, pos, effort, budget_s=12.0):
                       f"({t_lm * 1e3:.0f} ms), effort {effort}, scaled to {cfg['n_layers']} layers"}
 
 
+SKEW_EFFORTS = [0.05, 1.0]
+SKEW_SEQUENCES = 8
+
+
+def run_skew(args, iam, ctx):
+    """Skew stress on the same model (`--skew`): every layer's K and V filled
+    with N(0,1) fp16 values for all 4096 positions, then SKEW_SEQUENCES
+    sequences decoded back-to-back near the end of the context, each with its
+    own seeded 1% of hidden channels (41 of 4096) scaled 20x at the
+    embedding, at efforts 0.05 and 1.0 (graph-replayed steps)."""
+    cfg = dict(MISTRAL)
+    model = iam.Model(ctx, iam.ModelConfig(**cfg))
+    model.synthesize(0)
+    for name, tid in (("kcache", 9001), ("vcache", 9002)):
+        ptr, nbytes = model.tensor(name)
+        ctx.gen_f16(0, tid, nbytes // 2, 0.0, 1.0, ptr)
+    n = args.skew_steps
+    start = cfg["max_ctx"] - SWEEP_WARMUP - n - 1
+    if n < 1 or start < 1:
+        sys.exit(f"--skew-steps {n} must be in [1, {cfg['max_ctx'] - SWEEP_WARMUP - 2}]")
+    rng = np.random.default_rng(5)
+    res = {}
+    for e in SKEW_EFFORTS:
+        steps = 0
+        secs = 0.0
+        wbytes = 0
+        for sq in range(SKEW_SEQUENCES):
+            scale = np.ones(cfg["dim"], np.float32)
+            scale[rng.choice(cfg["dim"], cfg["dim"] // 100, replace=False)] = 20.0
+            model.set_embed_scale(scale)
+            model.write_tensor("pos", np.array([start], np.int32))
+            model.write_tensor("token", np.array([int(rng.integers(0, cfg["vocab"]))], np.int32))
+            model.decode(SWEEP_WARMUP, e)
+            ctx.sync()
+            ctx.walk_counters(reset=True)
+            t0 = time.perf_counter()
+            model.decode(n, e)
+            ctx.sync()
+            secs += time.perf_counter() - t0
+            b, _, _ = ctx.walk_counters(reset=True)
+            wbytes += b
+            steps += n
+        bpt = wbytes / steps + per_token_fixed_bytes(cfg, start + SWEEP_WARMUP + n // 2)
+        tps = steps / secs
+        res[str(e)] = {"tok_s": round(tps, 2), "ms_per_token": round(secs / steps * 1e3, 4),
+                       "bytes_per_token": round(bpt), "achieved_GBs": round(bpt * tps / 1e9, 1),
+                       "frac": round(bpt * tps / 1e9 / HBM_PEAK_GBS, 4)}
+        log(f"skew, effort {e}: {tps:.1f} tok/s over {steps} steps, {bpt / 1e9:.3f} GB/token")
+    out = {
+        "metric": "skew stress: decode tok/s at efforts 0.05 and 1.0, context 4096, 8 sequences",
+        "value": res[str(SKEW_EFFORTS[0])]["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": n,
+        "warmup": SWEEP_WARMUP, "higher_is_better": True, "vs_baseline": None,
+        "dtype": "fp16 weights, fp32 activations, %s accumulation" % args.acc,
+        "data": "synthetic (random-init weights, N(0,1) KV cache, random token ids)",
+        "config": {"workload": "Mistral-7B-shape decode, 1 percent of hidden channels x20 at the embedding, "
+                               f"positions {start}..{start + SWEEP_WARMUP + n - 1} of 4096",
+                   "sequences": SKEW_SEQUENCES, "efforts": SKEW_EFFORTS},
+        "efforts": res,
+    }
+    print(json.dumps(out), flush=True)
+    model.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -127,24 +196,35 @@ def main():
     ap.add_argument("--effort", type=float, default=0.25)
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--profile-steps", type=int, default=8)
+    ap.add_argument("--sweep-steps", type=int, default=32,
+                    help="timed decode steps per effort of the effort sweep (0: no sweep)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--acc", choices=["fp64", "fp32"], default="fp64",
                     help="walk/attention accumulation (fp64: results equal the correctly rounded sums)")
     ap.add_argument("--eager", action="store_true",
                     help="launch every kernel from the host instead of replaying a captured graph")
+    ap.add_argument("--skew", action="store_true",
+                    help="run the skew stress (efforts 0.05 and 1.0 at context 4096, 8 sequences) instead")
+    ap.add_argument("--skew-steps", type=int, default=32, help="timed decode steps per sequence and effort")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)
         sys.exit(2)
     cfg = dict(MISTRAL)
-    total = args.prompt + args.warmup + args.steps + args.profile_steps + 1
+    sweep_efforts = [e for e in SWEEP_EFFORTS if e != args.effort] if args.sweep_steps > 0 else []
+    total = (args.prompt + args.warmup + args.steps + args.profile_steps + 1
+             + len(sweep_efforts) * (SWEEP_WARMUP + args.sweep_steps))
     if total > cfg["max_ctx"]:
         sys.exit(f"prompt + warmup + steps + profile steps ({total}) exceed the KV capacity {cfg['max_ctx']}")
 
     iam = load_iam()
     ctx = iam.Ctx(0)
     ctx.set_accumulation(args.acc)
+    if args.skew:
+        run_skew(args, iam, ctx)
+        ctx.close()
+        return
     use_graph = not args.eager
     name, cus, mem = ctx.device_info()
     log(f"device {name}, {cus} CUs, {mem / 2**30:.0f} GiB")
@@ -191,7 +271,27 @@ def main():
     walk_avg_s = walk_ms / 1e3 / walk_calls
     achieved = per_launch / walk_avg_s / 1e9
 
+    # the same decode at the other efforts of the configs, continuing the
+    # sequence: tok/s and the roofline fraction of the bytes touched per token
+    sweep = {}
     pos_now = args.prompt + args.warmup + args.steps + args.profile_steps
+    for e in sweep_efforts:
+        model.decode(SWEEP_WARMUP, e, use_graph=use_graph)
+        ctx.sync()
+        ctx.walk_counters(reset=True)
+        t0 = time.perf_counter()
+        model.decode(args.sweep_steps, e, use_graph=use_graph)
+        ctx.sync()
+        dt_e = time.perf_counter() - t0
+        eb, _, _ = ctx.walk_counters(reset=True)
+        pos_e = pos_now + SWEEP_WARMUP + args.sweep_steps // 2
+        bpt = eb / args.sweep_steps + per_token_fixed_bytes(cfg, pos_e)
+        tps = args.sweep_steps / dt_e
+        sweep[str(e)] = {"tok_s": round(tps, 2), "ms_per_token": round(dt_e / args.sweep_steps * 1e3, 4),
+                         "bytes_per_token": round(bpt), "achieved_GBs": round(bpt * tps / 1e9, 1),
+                         "frac": round(bpt * tps / 1e9 / HBM_PEAK_GBS, 4)}
+        log(f"effort {e}: {tps:.1f} tok/s, {bpt / 1e9:.3f} GB/token -> {bpt * tps / 1e9:.0f} GB/s")
+        pos_now += SWEEP_WARMUP + args.sweep_steps
     cpu = None
     if not args.no_cpu_baseline:
         t = time.perf_counter()
@@ -224,6 +324,7 @@ def main():
         "token_roofline": {"bytes_per_token": round(bytes_per_token), "achieved_GBs":
                            round(bytes_per_token * tok_s / 1e9, 1),
                            "frac": round(bytes_per_token * tok_s / 1e9 / HBM_PEAK_GBS, 4)},
+        "effort_sweep": sweep,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
