@@ -66,13 +66,18 @@ __device__ __forceinline__ void load_probes(const uint16_t* __restrict__ probes,
     pr[1] = pv[1];
 }
 
-// xs holds x[16*tid .. 16*tid + 16) and pr the thread's probes.  Scratch:
-// s_red >= 9 floats, s_cnt >= 16 ints, s_cand kCandCap floats.  Every
-// thread returns the cutoff; ends after a barrier.
-__device__ __forceinline__ float block_cutoff_x(const float (&xs)[kCutVPT], const uint4 (&pr)[2], int quantile, float* s_red,
-                                int* s_cnt, float* s_cand)
+// xs holds x[16*tid .. 16*tid + 16) and pr the thread's probes for the
+// first kCutThreads threads; a block of NWV > 4 waves runs the same code and
+// its other threads hold no importances (NaN: never counted, ignored by the
+// min and max).  Scratch: s_red >= 2*NWV + 1 floats, s_cnt >= 3*NWV ints,
+// s_cand kCandCap floats.  Every thread returns the cutoff; ends after a
+// barrier.
+template <int NWV = 4>
+__device__ __forceinline__ float block_cutoff_x(const float (&xs)[kCutVPT], const uint4 (&pr)[2], int quantile,
+                                                float* s_red, int* s_cnt, float* s_cand)
 {
 #pragma clang fp contract(off)
+    static_assert(NWV % 4 == 0, "4 or 8 waves");
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -85,6 +90,7 @@ __device__ __forceinline__ float block_cutoff_x(const float (&xs)[kCutVPT], cons
             float p = h2f(ps[k >> 1] >> ((k & 1) * 16));
             float prod = __fmul_rn(xs[k], p);
             v[k] = __fmul_rn(kScale, fabsf(prod));   // bucketMul.cl:110
+            if (NWV > 4 && tid >= kCutThreads) v[k] = __int_as_float(0x7fc00000);
         }
     }
     float mn = 1e30f, mx = -1e30f;                    // bucketMul.cl:98-99
@@ -97,14 +103,20 @@ __device__ __forceinline__ float block_cutoff_x(const float (&xs)[kCutVPT], cons
     mx = wave_max(mx);
     if (lane == 0) {
         s_red[wave] = mn;
-        s_red[4 + wave] = mx;
+        s_red[NWV + wave] = mx;
     }
     __syncthreads();
     // the search state is uniform: keep it in scalar registers
-    const float4 mn4 = *reinterpret_cast<const float4*>(s_red);
-    const float4 mx4 = *reinterpret_cast<const float4*>(s_red + 4);
-    const float gmin = uniform_f(fminf(fminf(mn4.x, mn4.y), fminf(mn4.z, mn4.w)));
-    const float gmax = uniform_f(fmaxf(fmaxf(mx4.x, mx4.y), fmaxf(mx4.z, mx4.w)));
+    float gmin = 1e30f, gmax = -1e30f;
+#pragma unroll
+    for (int w4 = 0; w4 < NWV; w4 += 4) {
+        const float4 mn4 = *reinterpret_cast<const float4*>(s_red + w4);
+        const float4 mx4 = *reinterpret_cast<const float4*>(s_red + NWV + w4);
+        gmin = fminf(gmin, fminf(fminf(mn4.x, mn4.y), fminf(mn4.z, mn4.w)));
+        gmax = fmaxf(gmax, fmaxf(fmaxf(mx4.x, mx4.y), fmaxf(mx4.z, mx4.w)));
+    }
+    gmin = uniform_f(gmin);
+    gmax = uniform_f(gmax);
 
     const int target = kProbes - quantile;            // bucketMul.cl:81
     float minB = gmin, maxB = gmax;
@@ -132,10 +144,15 @@ __device__ __forceinline__ float block_cutoff_x(const float (&xs)[kCutVPT], cons
         int c = 0;
 #pragma unroll
         for (int k = 0; k < 16; k++) c += __popcll(__ballot(v[k] > bound));
-        if (lane == 0) s_cnt[(loop & 1) * 4 + wave] = c;
+        if (lane == 0) s_cnt[(loop & 1) * NWV + wave] = c;
         __syncthreads();
-        const int4 q4 = *reinterpret_cast<const int4*>(s_cnt + (loop & 1) * 4);
-        if (round(__builtin_amdgcn_readfirstlane(q4.x + q4.y + q4.z + q4.w))) return bound;
+        int tot = 0;
+#pragma unroll
+        for (int w4 = 0; w4 < NWV; w4 += 4) {
+            const int4 q4 = *reinterpret_cast<const int4*>(s_cnt + (loop & 1) * NWV + w4);
+            tot += q4.x + q4.y + q4.z + q4.w;
+        }
+        if (round(__builtin_amdgcn_readfirstlane(tot))) return bound;
     }
     if (loop == 20) return bound;                      // bucketMul.cl:211-213: the untested midpoint
 
@@ -148,11 +165,15 @@ __device__ __forceinline__ float block_cutoff_x(const float (&xs)[kCutVPT], cons
         bm[k] = __ballot(v[k] > minB && v[k] <= maxB);
         wtot += __popcll(bm[k]);
     }
-    if (lane == 0) s_cnt[8 + wave] = wtot;
+    if (lane == 0) s_cnt[2 * NWV + wave] = wtot;
     __syncthreads();
-    const int4 wt = *reinterpret_cast<const int4*>(s_cnt + 8);
-    int off = (wave > 0 ? wt.x : 0) + (wave > 1 ? wt.y : 0) + (wave > 2 ? wt.z : 0);
-    const int ncand = wt.x + wt.y + wt.z + wt.w;   // <= minC - maxC <= kCandCap
+    int off = 0, ncand = 0;   // ncand <= minC - maxC <= kCandCap
+#pragma unroll
+    for (int w2 = 0; w2 < NWV; w2++) {
+        const int c2 = s_cnt[2 * NWV + w2];
+        if (w2 < wave) off += c2;
+        ncand += c2;
+    }
 #pragma unroll
     for (int k = 0; k < 16; k++) {
         if ((bm[k] >> lane) & 1ull) s_cand[off + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bm[k] >> 32),
@@ -172,10 +193,10 @@ __device__ __forceinline__ float block_cutoff_x(const float (&xs)[kCutVPT], cons
             for (int j = 0; j < kCandCap / 64; j++) c += __popcll(__ballot(cv[j] > bound));
             done = round(c);
         }
-        if (lane == 0) s_red[8] = bound;
+        if (lane == 0) s_red[2 * NWV] = bound;
     }
     __syncthreads();
-    return s_red[8];
+    return s_red[2 * NWV];
 }
 
 __device__ __forceinline__ void load16(const float* __restrict__ x, float (&xs)[kCutVPT])
@@ -217,7 +238,7 @@ __device__ __forceinline__ void block_rmsnorm4096(float (&v)[kCutVPT], const uin
     float sq = 0.0f;
 #pragma unroll
     for (int k = 0; k < kCutVPT; k++) sq = __fadd_rn(sq, __fmul_rn(v[k], v[k]));
-    s_red[tid] = sq;
+    if (tid < kCutThreads) s_red[tid] = sq;
     __syncthreads();
     if (tid < 64) {
         // lane l: part[l] + part[l+128] and part[l+64] + part[l+192] (st = 128),
@@ -745,13 +766,14 @@ __global__ __launch_bounds__(64 * NW) void k_walk64(WalkArgs a)
     constexpr int TW = 128;
     constexpr int SLOTS = TW * 16;             // accumulators per wave
     constexpr int GSTRIDE = NW * UNR;          // groups per workgroup batch
-    static_assert(NT == kCutThreads, "the fused search and norm need 256 threads");
+    static_assert(NT == kCutThreads || NT == 2 * kCutThreads, "4 or 8 waves");
+    // the norm and the search hold x[16*tid ..] in the first kCutThreads threads
     __shared__ double acc[NW * SLOTS];
     __shared__ __align__(16) uint16_t s_row[NT * 16];
     __shared__ float s_x[NT];
     __shared__ uint32_t s_wsum[NW];
     __shared__ __align__(16) float s_red[260];
-    __shared__ __align__(16) int s_cnt[16];
+    __shared__ __align__(16) int s_cnt[32];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -769,12 +791,16 @@ __global__ __launch_bounds__(64 * NW) void k_walk64(WalkArgs a)
     const int i0 = p * d.IPS;
     const int ni = min(d.IPS, d.n_in - i0);
     const bool x_lds = d.in_mode == kInNorm;
+    const bool cut_thread = tid < kCutThreads;
     float xs[kCutVPT];
     uint4 pr[2], gr[2];
+#pragma unroll
+    for (int k2 = 0; k2 < kCutVPT; k2++) xs[k2] = 0.0f;
+    pr[0] = pr[1] = gr[0] = gr[1] = make_uint4(0u, 0u, 0u, 0u);
     float cutoff = 0.0f;
     if (d.in_mode == kInCutoff) {
         cutoff = *d.cutoff;
-    } else {
+    } else if (cut_thread) {
         load_probes(d.probes, pr);
         load16(d.in_mode == kInNorm ? d.h : d.x, xs);
         if (d.in_mode == kInNorm) {
@@ -792,7 +818,7 @@ __global__ __launch_bounds__(64 * NW) void k_walk64(WalkArgs a)
     if (d.in_mode != kInCutoff) {
         if (d.in_mode == kInNorm) {
             block_rmsnorm4096(xs, gr, d.eps, s_red);
-            if (w == 0 && k == 0) {
+            if (w == 0 && k == 0 && cut_thread) {
                 float4* xo = reinterpret_cast<float4*>(d.x + tid * kCutVPT);
 #pragma unroll
                 for (int k4 = 0; k4 < 4; k4++)
@@ -802,12 +828,12 @@ __global__ __launch_bounds__(64 * NW) void k_walk64(WalkArgs a)
 #pragma unroll
             for (int k2 = 0; k2 < kCutVPT; k2++) {
                 const int i = tid * kCutVPT + k2 - i0;
-                if (i >= 0 && i < ni) s_x[i] = xs[k2];
+                if (cut_thread && i >= 0 && i < ni) s_x[i] = xs[k2];
             }
         }
         // s_row is free until the selection: it holds the search's bracket values
         static_assert(sizeof(uint16_t) * NT * 16 >= sizeof(float) * kCandCap, "s_row too small");
-        cutoff = block_cutoff_x(xs, pr, d.quantile, s_red, s_cnt, reinterpret_cast<float*>(s_row));
+        cutoff = block_cutoff_x<NW>(xs, pr, d.quantile, s_red, s_cnt, reinterpret_cast<float*>(s_row));
         if (w == 0 && tid == 0) d.cutoff[0] = cutoff;
     }
     const int ns = (int)select_finish<NT>(d, cutoff, p, t, i0, ni, L, s_row, s_x, s_wsum, x_lds);
@@ -1151,20 +1177,21 @@ constexpr double kWalkWgBytes = IAM_WALK_WG_BYTES;
 constexpr double kWalkMinWgs = IAM_WALK_MIN_WGS;
 constexpr double kWalkMaxWgs = 3072.0;
 
-#ifndef IAM_W64_NW
-#define IAM_W64_NW 4
-#endif
+// k_walk64 launch shapes: below IAM_W64_WIDE_BYTES of expected weight bytes
+// 4 waves per workgroup and about one workgroup per IAM_W64_WG_BYTES (at
+// least 256; two fit a CU); above it 8 waves and one workgroup per CU
+// (IAM_W64_WIDE_WGS), so that no CU holds more work than another.
 #ifndef IAM_W64_UNR
 #define IAM_W64_UNR 4
 #endif
 #ifndef IAM_W64_WG_BYTES
 #define IAM_W64_WG_BYTES 131072.0
 #endif
-#ifndef IAM_W64_ROUND
-#define IAM_W64_ROUND 0
+#ifndef IAM_W64_WIDE_BYTES
+#define IAM_W64_WIDE_BYTES 40e6
 #endif
-#ifndef IAM_W64_FIXED
-#define IAM_W64_FIXED 0
+#ifndef IAM_W64_WIDE_WGS
+#define IAM_W64_WIDE_WGS 256
 #endif
 
 // 8: the fp64 walk with 16-byte loads and 128-column tiles (k_walk64);
@@ -1196,16 +1223,15 @@ void plan_walk(int n, const MatOp* ops, float effort, bool acc64, WalkPlan* plan
         bytes[i] = est_rows(pl.n_in * 16, effort) * (pl.V == 8 ? pl.T * tw : M.bucket_cols) * 2.0;
         tot += bytes[i];
     }
-    const int nw = all64 ? IAM_W64_NW : tot < kWalkWideBytes ? IAM_WALK_SMALL_NW : IAM_WALK_BIG_NW;
+    const bool wide64 = all64 && tot >= IAM_W64_WIDE_BYTES;
+    const int nw = all64 ? (wide64 ? 8 : 4) : tot < kWalkWideBytes ? IAM_WALK_SMALL_NW : IAM_WALK_BIG_NW;
     const double wg_bytes = all64 ? IAM_W64_WG_BYTES : kWalkWgBytes;
     double target = std::min(kWalkMaxWgs, std::max(kWalkMinWgs, tot / wg_bytes));
-    const bool fit = all64 && (IAM_W64_ROUND > 0 || IAM_W64_FIXED > 0);
-    if (all64 && IAM_W64_ROUND > 0)
-        target = std::max((double)IAM_W64_ROUND, std::round(target / IAM_W64_ROUND) * IAM_W64_ROUND);
-    if (all64 && IAM_W64_FIXED > 0) target = IAM_W64_FIXED;
+    const bool fit = wide64;   // at most target workgroups
+    if (wide64) target = IAM_W64_WIDE_WGS;
     for (int i = 0; i < n; i++) {
         WalkPlan& pl = plan[i];
-        pl.NW = pl.V == 8 ? IAM_W64_NW : nw;
+        pl.NW = nw;
         const double wgs = tot > 0 ? target * bytes[i] / tot : target / n;
         const int slices = std::max(1, fit ? (int)std::floor(wgs / pl.T + 1e-9) : (int)std::lround(wgs / pl.T));
         pl.IPS = std::min(64 * pl.NW, std::max(1, (pl.n_in + slices - 1) / slices));
@@ -1411,9 +1437,10 @@ static int walk_and_reduce(Ctx* c, int n, const MatOp* ops, int in_mode, const f
             done++;
         }
         args.n = cnt;
-        if (vec == 8)
-            IAM_TRY(launch(c, "bucket_walk", k_walk64<IAM_W64_NW, IAM_W64_UNR>, dim3(blocks), dim3(64 * IAM_W64_NW),
-                           0, args));
+        if (vec == 8 && nw == 8)
+            IAM_TRY(launch(c, "bucket_walk", k_walk64<8, IAM_W64_UNR>, dim3(blocks), dim3(512), 0, args));
+        else if (vec == 8)
+            IAM_TRY(launch(c, "bucket_walk", k_walk64<4, IAM_W64_UNR>, dim3(blocks), dim3(256), 0, args));
         else
             IAM_TRY(c->acc64 ? launch_walk<double>(c, nw, vec, blocks, args)
                              : launch_walk<float>(c, nw, vec, blocks, args));
