@@ -945,92 +945,100 @@ struct ReduceArgs {
     unsigned long long* counters;  // walk bytes, rows, matrices
 };
 
-constexpr int kRedOut = 128;     // outputs per reduce workgroup (one head of 128 for RoPE)
 constexpr int kRedThreads = 256;
-constexpr int kRedGroups = kRedThreads / 32;   // slice groups: 32 threads x 4 outputs each
+constexpr int kRedHead = 128;    // the RoPE epilogues need a head of 128 outputs in one workgroup
 
-// Thread (ol, pg) sums outputs 4ol..4ol+3 over the slices pg, pg + 8, ...
-// in slice order; the group sums are then added in group order by threads
-// 0..127.  The loads of U slices are issued together, so a matrix of up to
-// 8U slices costs one round trip.
-template <typename Acc, int U>
+// Workgroup of OUT outputs: thread (ol, pg) sums outputs 4ol..4ol+3 over the
+// slices pg, pg + G, ... (G = 256 / (OUT/4) slice groups) in slice order,
+// U loads at a time; the G group sums are then added in group order by
+// threads 0..OUT-1.
+template <typename Acc, int OUT>
+struct RedShape {
+    static constexpr int QUADS = OUT / 4;
+    static constexpr int G = kRedThreads / QUADS;
+    static constexpr int U = OUT == kRedHead ? 8 : 4;
+};
+
+template <typename Acc, int G, int U>
 __device__ __forceinline__ void slice_loads(const Acc* __restrict__ part, int P, int m, int o, int p0, Acc (&r)[U][4])
 {
 #pragma unroll
     for (int u = 0; u < U; u++) {
-        const int p = min(p0 + u * kRedGroups, P - 1);
+        const int p = min(p0 + u * G, P - 1);
 #pragma unroll
         for (int i = 0; i < 4; i++) r[u][i] = part[(size_t)p * m + o + i];
     }
 }
 
-template <typename Acc, int U>
+template <typename Acc, int G, int U>
 __device__ __forceinline__ void slice_adds(int P, int p0, const Acc (&r)[U][4], Acc (&s)[4])
 {
 #pragma unroll
     for (int u = 0; u < U; u++)
-        if (p0 + u * kRedGroups < P)
+        if (p0 + u * G < P)
 #pragma unroll
             for (int i = 0; i < 4; i++) s[i] += r[u][i];
 }
 
-template <typename Acc, int U>
+template <typename Acc, int G, int U>
 __device__ __forceinline__ void thread_sums(const Acc* __restrict__ part, int P, int m, int o, int pg, Acc (&s)[4])
 {
-    for (int p0 = pg; p0 < P; p0 += U * kRedGroups) {
+    for (int p0 = pg; p0 < P; p0 += U * G) {
         Acc r[U][4];
-        slice_loads<Acc, U>(part, P, m, o, p0, r);
-        slice_adds<Acc, U>(P, p0, r, s);
+        slice_loads<Acc, G, U>(part, P, m, o, p0, r);
+        slice_adds<Acc, G, U>(P, p0, r, s);
     }
 }
 
-// the 8 group sums of output tid (< kRedOut) in group order
-template <typename Acc>
-__device__ __forceinline__ Acc group_total(const Acc (*red)[kRedOut])
+// the G group sums of output tid (< OUT) in group order
+template <typename Acc, int OUT>
+__device__ __forceinline__ Acc group_total(const Acc (*red)[OUT])
 {
+    constexpr int G = RedShape<Acc, OUT>::G;
     const int tid = threadIdx.x;
     Acc t = (Acc)0;
-    if (tid < kRedOut) {
+    if (tid < OUT) {
         t = red[0][tid];
 #pragma unroll
-        for (int g = 1; g < kRedGroups; g++) t += red[g][tid];
+        for (int g = 1; g < G; g++) t += red[g][tid];
     }
     return t;
 }
 
-template <typename Acc>
+template <typename Acc, int OUT>
 __device__ __forceinline__ Acc group_sums(const Acc* __restrict__ part, int P, int m, int o, int pg,
-                                          Acc (*red)[kRedOut], int ol)
+                                          Acc (*red)[OUT], int ol)
 {
+    using S = RedShape<Acc, OUT>;
     Acc s[4] = {(Acc)0, (Acc)0, (Acc)0, (Acc)0};
-    if (o < m) thread_sums<Acc, 16>(part, P, m, o, pg, s);
+    if (o < m) thread_sums<Acc, S::G, S::U>(part, P, m, o, pg, s);
 #pragma unroll
     for (int i = 0; i < 4; i++) red[pg][ol * 4 + i] = s[i];
     __syncthreads();
-    return group_total<Acc>(red);
+    return group_total<Acc, OUT>(red);
 }
 
 // two matrices of the same output size at once (the gate and up
-// projections): with at most 64 slices each, all loads of both are issued
-// together
-template <typename Acc>
+// projections): when both fit one batch of loads, all loads of both are
+// issued together
+template <typename Acc, int OUT>
 __device__ __forceinline__ void group_sums2(const Acc* __restrict__ part, int P, const Acc* __restrict__ part2,
-                                            int P2, int m, int o, int pg, Acc (*red)[kRedOut],
-                                            Acc (*red2)[kRedOut], int ol, Acc& t1, Acc& t2)
+                                            int P2, int m, int o, int pg, Acc (*red)[OUT], Acc (*red2)[OUT],
+                                            int ol, Acc& t1, Acc& t2)
 {
-    constexpr int U = 8;
+    using S = RedShape<Acc, OUT>;
     Acc s[4] = {(Acc)0, (Acc)0, (Acc)0, (Acc)0};
     Acc s2[4] = {(Acc)0, (Acc)0, (Acc)0, (Acc)0};
     if (o < m) {
-        if (P <= U * kRedGroups && P2 <= U * kRedGroups) {
-            Acc r[U][4], r2[U][4];
-            slice_loads<Acc, U>(part, P, m, o, pg, r);
-            slice_loads<Acc, U>(part2, P2, m, o, pg, r2);
-            slice_adds<Acc, U>(P, pg, r, s);
-            slice_adds<Acc, U>(P2, pg, r2, s2);
+        if (P <= S::U * S::G && P2 <= S::U * S::G) {
+            Acc r[S::U][4], r2[S::U][4];
+            slice_loads<Acc, S::G, S::U>(part, P, m, o, pg, r);
+            slice_loads<Acc, S::G, S::U>(part2, P2, m, o, pg, r2);
+            slice_adds<Acc, S::G, S::U>(P, pg, r, s);
+            slice_adds<Acc, S::G, S::U>(P2, pg, r2, s2);
         } else {
-            thread_sums<Acc, U>(part, P, m, o, pg, s);
-            thread_sums<Acc, U>(part2, P2, m, o, pg, s2);
+            thread_sums<Acc, S::G, S::U>(part, P, m, o, pg, s);
+            thread_sums<Acc, S::G, S::U>(part2, P2, m, o, pg, s2);
         }
     }
 #pragma unroll
@@ -1039,8 +1047,8 @@ __device__ __forceinline__ void group_sums2(const Acc* __restrict__ part, int P,
         red2[pg][ol * 4 + i] = s2[i];
     }
     __syncthreads();
-    t1 = group_total<Acc>(red);
-    t2 = group_total<Acc>(red2);
+    t1 = group_total<Acc, OUT>(red);
+    t2 = group_total<Acc, OUT>(red2);
 }
 
 // total selected rows of a matrix (by one wave, no barrier) into count and
@@ -1061,43 +1069,45 @@ __device__ void sum_counts(const uint32_t* __restrict__ sc, int P, int C, uint32
     }
 }
 
-template <typename Acc>
+template <typename Acc, int OUT>
 __global__ __launch_bounds__(kRedThreads) void k_reduce(ReduceArgs a)
 {
 #pragma clang fp contract(off)
-    __shared__ Acc red[kRedGroups][kRedOut];
-    __shared__ Acc red2[kRedGroups][kRedOut];
-    __shared__ float sy[kRedOut];
+    using S = RedShape<Acc, OUT>;
+    __shared__ Acc red[S::G][OUT];
+    __shared__ Acc red2[S::G][OUT];
+    __shared__ float sy[OUT];
     const int b = (int)blockIdx.x;
     int k = 0;
     for (int i = 1; i < a.n; i++)
         if (b >= a.d[i].block_base) k = i;
     const ReduceDesc& d = a.d[k];
     const int lb = b - d.block_base;
-    const int o0 = lb * kRedOut;
+    const int o0 = lb * OUT;
     const int tid = threadIdx.x;
-    const int ol = tid & 31, pg = tid >> 5;
+    const int ol = tid % S::QUADS, pg = tid / S::QUADS;
     const int o = o0 + ol * 4;   // m is a multiple of 16: o..o+3 are in range together
     if (lb == 0 && tid >= kRedThreads - 64) sum_counts(d.slice_count, d.P, d.C, d.count, a.counters);
     if (lb == 0 && d.ep == kEpSilu && tid >= kRedThreads - 128 && tid < kRedThreads - 64)
         sum_counts(d.slice_count2, d.P2, d.C, d.count2, a.counters);
     const int oo = o0 + tid;
-    const bool in = tid < kRedOut && oo < d.m;
-    // the epilogue's own loads go out with the partial loads
-    const bool rope = d.ep == kEpRopeQ || d.ep == kEpRopeK;
+    const bool in = tid < OUT && oo < d.m;
+    // the epilogue's own loads go out with the partial loads (a RoPE
+    // epilogue comes with OUT = kRedHead)
+    const bool rope = OUT == kRedHead && (d.ep == kEpRopeQ || d.ep == kEpRopeK);
     const int pos = rope || d.ep == kEpV ? *d.pos : 0;
     const bool pos_ok = pos >= 0 && pos < d.max_ctx;
     float rc = 0.0f, rsn = 0.0f, resid = 0.0f;
     if (rope && in && pos_ok) {
-        const int fi = tid < kRedOut / 2 ? tid : tid - kRedOut / 2;
-        rc = d.table[(size_t)pos * kRedOut + 2 * fi];
-        rsn = d.table[(size_t)pos * kRedOut + 2 * fi + 1];
+        const int fi = tid < OUT / 2 ? tid : tid - OUT / 2;
+        rc = d.table[(size_t)pos * OUT + 2 * fi];
+        rsn = d.table[(size_t)pos * OUT + 2 * fi + 1];
     }
     if (d.ep == kEpResid && in) resid = d.out[oo];
     if (d.ep == kEpSilu) {
         Acc t1, t2;
-        group_sums2<Acc>(reinterpret_cast<const Acc*>(d.part), d.P, reinterpret_cast<const Acc*>(d.part2), d.P2,
-                         d.m, o, pg, red, red2, ol, t1, t2);
+        group_sums2<Acc, OUT>(reinterpret_cast<const Acc*>(d.part), d.P, reinterpret_cast<const Acc*>(d.part2),
+                              d.P2, d.m, o, pg, red, red2, ol, t1, t2);
         const float yv = (float)t1, uv = (float)t2;
         if (in) {
             d.y[oo] = yv;
@@ -1107,18 +1117,18 @@ __global__ __launch_bounds__(kRedThreads) void k_reduce(ReduceArgs a)
         }
         return;
     }
-    const float yv = (float)group_sums<Acc>(reinterpret_cast<const Acc*>(d.part), d.P, d.m, o, pg, red, ol);
+    const float yv = (float)group_sums<Acc, OUT>(reinterpret_cast<const Acc*>(d.part), d.P, d.m, o, pg, red, ol);
     if (in) d.y[oo] = yv;
     if (d.ep == kEpResid) {
         if (in) d.out[oo] = __fadd_rn(resid, yv);
     } else if (d.ep != kEpStore) {
         if (d.ep == kEpV) {
             if (in && pos_ok) d.cache[(size_t)pos * d.m + oo] = __half_as_ushort(__float2half_rn(yv));
-        } else {
-            if (tid < kRedOut) sy[tid] = yv;
+        } else if (rope) {
+            if (tid < OUT) sy[tid] = yv;
             __syncthreads();
             if (in && pos_ok) {
-                const float r = rope_cs(sy, tid, kRedOut / 2, rc, rsn);
+                const float r = rope_cs(sy, tid, OUT / 2, rc, rsn);
                 if (d.ep == kEpRopeQ) d.out[oo] = r;
                 else d.cache[(size_t)pos * d.m + oo] = __half_as_ushort(__float2half_rn(r));
             }
@@ -1449,6 +1459,9 @@ static int walk_and_reduce(Ctx* c, int n, const MatOp* ops, int in_mode, const f
     ReduceArgs ra{};
     ra.counters = c->counters;
     int rblocks = 0, nd = 0;
+    int rout = 32;
+    for (int i = 0; ep && i < n; i++)
+        if (ep[i].ep == kEpRopeQ || ep[i].ep == kEpRopeK) rout = kRedHead;
     for (int i = 0; i < n; i++) {
         const DispatchSlot& s = c->slots[i];
         ReduceDesc& d = ra.d[nd++];
@@ -1479,11 +1492,16 @@ static int walk_and_reduce(Ctx* c, int n, const MatOp* ops, int in_mode, const f
             i = n;   // the pair is one descriptor
         }
         d.block_base = rblocks;
-        rblocks += (d.m + kRedOut - 1) / kRedOut;
+        rblocks += (d.m + rout - 1) / rout;
     }
     ra.n = nd;
-    if (c->acc64) return launch(c, "bucket_reduce", k_reduce<double>, dim3(rblocks), dim3(kRedThreads), 0, ra);
-    return launch(c, "bucket_reduce", k_reduce<float>, dim3(rblocks), dim3(kRedThreads), 0, ra);
+    // a head of 128 outputs per workgroup for RoPE, else 32 outputs (more
+    // workgroups, fewer partials per thread)
+    if (rout == kRedHead)
+        return c->acc64 ? launch(c, "bucket_reduce", k_reduce<double, kRedHead>, dim3(rblocks), dim3(kRedThreads), 0, ra)
+                        : launch(c, "bucket_reduce", k_reduce<float, kRedHead>, dim3(rblocks), dim3(kRedThreads), 0, ra);
+    return c->acc64 ? launch(c, "bucket_reduce", k_reduce<double, 32>, dim3(rblocks), dim3(kRedThreads), 0, ra)
+                    : launch(c, "bucket_reduce", k_reduce<float, 32>, dim3(rblocks), dim3(kRedThreads), 0, ra);
 }
 
 int bucketmul_walk(Ctx* c, int n, const MatOp* ops) { return walk_and_reduce(c, n, ops, kInCutoff, nullptr, nullptr, 0.0f, nullptr); }
