@@ -145,6 +145,28 @@ def test_rope_kv_append_and_attention(iam, O, ctx):
         d_.free()
 
 
+def test_attention_long_context(iam, O, ctx):
+    """The split merge over every split a context of up to 8192 positions
+    has (128 splits of 64, two per lane of the merging wave), at positions
+    on and off split boundaries, with a 4-query-head GQA and a 1:1 layout."""
+    rng = np.random.default_rng(3)
+    for n_heads, n_kv, max_ctx, positions in ((32, 8, 8192, (4095, 4096, 8191)), (8, 8, 4160, (63, 4159))):
+        hd = 128
+        kc = rng.normal(0, 1, (max_ctx, n_kv, hd)).astype(np.float16)
+        vc = rng.normal(0, 1, (max_ctx, n_kv, hd)).astype(np.float16)
+        q = rng.normal(0, 0.3, n_heads * hd).astype(np.float32)
+        dkc, dvc = ctx.upload(kc.view(np.uint16)), ctx.upload(vc.view(np.uint16))
+        dq, dout = ctx.upload(q), ctx.empty(n_heads * hd, np.float32)
+        for pos in positions:
+            dpos = ctx.upload(np.array([pos], np.int32))
+            ctx.attention(dq, dkc, dvc, dpos, n_heads, n_kv, hd, max_ctx, dout)
+            want = O.attention_f16kv(q, kc.view(np.uint16), vc.view(np.uint16), pos + 1, n_heads, n_kv, hd)
+            assert ulps(dout.read(), want).max() <= 1, (n_heads, n_kv, pos)
+            dpos.free()
+        for d_ in (dkc, dvc, dq, dout):
+            d_.free()
+
+
 def test_embed_and_argmax(O, ctx):
     vocab, cols = 1000, 4096
     tab = O.gen_f16(0, 50, vocab * cols, 0.0, 0.02)
