@@ -225,12 +225,13 @@ __device__ float block_cutoff(const float* __restrict__ x, const uint16_t* __res
 // rmsNorm32fast (aux.cl:156-196) of a 4096-vector by one 256-thread
 // workgroup, in the reference's fp32 order: 16 consecutive squares per
 // thread summed in order, then the 256-way tree (pairs tid, tid + st for st =
-// 128 .. 1: the first two levels through LDS, the rest as shuffles in wave
-// 0), scale = 1/sqrt(sum/4096 + eps) rounded from double, then the fp16 gain
+// 128 .. 1: the thread sums through LDS, then the tree by every wave on its
+// own), scale = 1/sqrt(sum/4096 + eps) rounded from double, then the fp16 gain
 // (mul16x32, aux.cl:434-440).  v holds h[16*tid ..] on entry and the
 // normalized values on exit; gr the thread's 16 gains (gain[16*tid ..]).
-// s_red needs 257 floats; ends with a barrier.
-__device__ __forceinline__ void block_rmsnorm4096(float (&v)[kCutVPT], const uint4 (&gr)[2], float eps, float* s_red)
+// s_part: kCutThreads floats of scratch that nothing writes again before a
+// later barrier (each wave reads it after the one barrier here).
+__device__ __forceinline__ void block_rmsnorm4096(float (&v)[kCutVPT], const uint4 (&gr)[2], float eps, float* s_part)
 {
 #pragma clang fp contract(off)
     const int tid = threadIdx.x;
@@ -238,25 +239,25 @@ __device__ __forceinline__ void block_rmsnorm4096(float (&v)[kCutVPT], const uin
     float sq = 0.0f;
 #pragma unroll
     for (int k = 0; k < kCutVPT; k++) sq = __fadd_rn(sq, __fmul_rn(v[k], v[k]));
-    if (tid < kCutThreads) s_red[tid] = sq;
+    if (tid < kCutThreads) s_part[tid] = sq;
     __syncthreads();
-    if (tid < 64) {
-        // lane l: part[l] + part[l+128] and part[l+64] + part[l+192] (st = 128),
-        // their sum (st = 64), then st = 32, 16 as shuffles and st = 8 .. 1
-        // within 16-lane rows by DPP row_shl (lane l takes lane l + st)
-        const float a = __fadd_rn(s_red[tid], s_red[tid + 128]);
-        const float b = __fadd_rn(s_red[tid + 64], s_red[tid + 192]);
-        sq = __fadd_rn(a, b);
-        sq = __fadd_rn(sq, __shfl_down(sq, 32, 64));
-        sq = __fadd_rn(sq, __shfl_down(sq, 16, 64));
-        sq = __fadd_rn(sq, dpp_f<0x108>(0.0f, sq));
-        sq = __fadd_rn(sq, dpp_f<0x104>(0.0f, sq));
-        sq = __fadd_rn(sq, dpp_f<0x102>(0.0f, sq));
-        sq = __fadd_rn(sq, dpp_f<0x101>(0.0f, sq));
-        if (tid == 0) s_red[256] = sq;
-    }
-    __syncthreads();
-    const float mean = __fdiv_rn(s_red[256], 4096.0f);
+    // every wave runs the tree itself (no second barrier): lane l takes
+    // part[l] + part[l+128] and part[l+64] + part[l+192] (st = 128), their
+    // sum (st = 64), then st = 32, 16 as shuffles and st = 8 .. 1 within
+    // 16-lane rows by DPP row_shl (lane l takes lane l + st); lane 0 holds
+    // the total
+    const int lane = tid & 63;
+    const float a = __fadd_rn(s_part[lane], s_part[lane + 128]);
+    const float b = __fadd_rn(s_part[lane + 64], s_part[lane + 192]);
+    sq = __fadd_rn(a, b);
+    sq = __fadd_rn(sq, __shfl_down(sq, 32, 64));
+    sq = __fadd_rn(sq, __shfl_down(sq, 16, 64));
+    sq = __fadd_rn(sq, dpp_f<0x108>(0.0f, sq));
+    sq = __fadd_rn(sq, dpp_f<0x104>(0.0f, sq));
+    sq = __fadd_rn(sq, dpp_f<0x102>(0.0f, sq));
+    sq = __fadd_rn(sq, dpp_f<0x101>(0.0f, sq));
+    const float total = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sq)));
+    const float mean = __fdiv_rn(total, 4096.0f);
     const float scale = (float)(1.0 / sqrt((double)__fadd_rn(mean, eps)));
     const uint32_t gw[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
 #pragma unroll
@@ -817,7 +818,7 @@ __global__ __launch_bounds__(64 * NW) void k_walk64(WalkArgs a)
     }
     if (d.in_mode != kInCutoff) {
         if (d.in_mode == kInNorm) {
-            block_rmsnorm4096(xs, gr, d.eps, s_red);
+            block_rmsnorm4096(xs, gr, d.eps, reinterpret_cast<float*>(s_row));
             if (w == 0 && k == 0 && cut_thread) {
                 float4* xo = reinterpret_cast<float4*>(d.x + tid * kCutVPT);
 #pragma unroll
