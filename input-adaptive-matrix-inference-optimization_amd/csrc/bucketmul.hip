@@ -53,8 +53,8 @@ __device__ __forceinline__ float uniform_f(float v)
 // count(imp > maxB) + #(bracket values > b).  The rounds run on the whole
 // workgroup (one count exchange per round) until the bracket holds at most
 // kCandCap values by its counts (minCount - maxCount bounds them); those are
-// then compacted to wave 0, which finishes the rounds alone with no
-// barriers.  The tested bounds, counts and stop decisions are the
+// then compacted to LDS, and every wave finishes the rounds on them by itself
+// with no barriers.  The tested bounds, counts and stop decisions are the
 // reference's exactly.
 constexpr int kCandCap = 256;   // 4 per lane of one wave
 
@@ -69,9 +69,10 @@ __device__ __forceinline__ void load_probes(const uint16_t* __restrict__ probes,
 // xs holds x[16*tid .. 16*tid + 16) and pr the thread's probes for the
 // first kCutThreads threads; a block of NWV > 4 waves runs the same code and
 // its other threads hold no importances (NaN: never counted, ignored by the
-// min and max).  Scratch: s_red >= 2*NWV + 1 floats, s_cnt >= 3*NWV ints,
-// s_cand kCandCap floats.  Every thread returns the cutoff; ends after a
-// barrier.
+// min and max).  Scratch: s_red >= 2*NWV floats, s_cnt >= 3*NWV ints,
+// s_cand kCandCap floats.  Every thread returns the cutoff; a later writer of
+// the scratch must pass a barrier first (the waves read s_cand after the
+// last barrier here).
 template <int NWV = 4>
 __device__ __forceinline__ float block_cutoff_x(const float (&xs)[kCutVPT], const uint4 (&pr)[2], int quantile,
                                                 float* s_red, int* s_cnt, float* s_cand)
@@ -181,22 +182,19 @@ __device__ __forceinline__ float block_cutoff_x(const float (&xs)[kCutVPT], cons
         off += __popcll(bm[k]);
     }
     __syncthreads();
-    if (wave == 0) {
-        float cv[kCandCap / 64];
+    // every wave finishes the rounds on the compacted values by itself
+    float cv[kCandCap / 64];
 #pragma unroll
-        for (int j = 0; j < kCandCap / 64; j++) cv[j] = lane + 64 * j < ncand ? s_cand[lane + 64 * j] : -INFINITY;
-        const int c0 = maxC;                           // count(imp > maxB) at the compaction
-        bool done = false;
-        for (; loop < 20 && !done; loop++) {
-            int c = c0;
+    for (int j = 0; j < kCandCap / 64; j++) cv[j] = lane + 64 * j < ncand ? s_cand[lane + 64 * j] : -INFINITY;
+    const int c0 = maxC;                               // count(imp > maxB) at the compaction
+    bool done = false;
+    for (; loop < 20 && !done; loop++) {
+        int c = c0;
 #pragma unroll
-            for (int j = 0; j < kCandCap / 64; j++) c += __popcll(__ballot(cv[j] > bound));
-            done = round(c);
-        }
-        if (lane == 0) s_red[2 * NWV] = bound;
+        for (int j = 0; j < kCandCap / 64; j++) c += __popcll(__ballot(cv[j] > bound));
+        done = round(c);
     }
-    __syncthreads();
-    return s_red[2 * NWV];
+    return bound;
 }
 
 __device__ __forceinline__ void load16(const float* __restrict__ x, float (&xs)[kCutVPT])
