@@ -878,7 +878,11 @@ __global__ __launch_bounds__(64 * NW) void k_walk64(WalkArgs a)
                 for (int e = 0; e < 8; e++) {
                     const uint32_t h = (words[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
                     const double wv = (double)h2f(h);
-                    atomicAdd(accw + (int)(h & 15u) * TW + e * 16, xc[u] * wv);
+                    // position bits by one bit-field extract (kept as one
+                    // instruction), then one shift-add into the address
+                    uint32_t pos;
+                    asm("v_bfe_u32 %0, %1, %2, 4" : "=v"(pos) : "v"(words[e >> 1]), "i"((e & 1) * 16));
+                    atomicAdd(accw + pos * TW + e * 16, xc[u] * wv);
                 }
             }
         }
