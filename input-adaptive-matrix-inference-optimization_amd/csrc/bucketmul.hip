@@ -3,22 +3,25 @@
 // Reference pipeline (bucket_mul.hpp:147-267, bucketMul.cl):
 //   findCutoffBinarySearch -> prepareDispatch -> roundUp/zeroRange32 ->
 //   bucketMul -> bucketIntegrate                      (6 launches + 1 fill)
-// Here:
-//   k_dispatch  one launch: every workgroup recomputes the cutoff (the search
-//               is a pure function of x[0:4096] and the probes), then selects
-//               the rows of its chunk of 256 inputs and compacts them in
-//               ascending order as {row, x[row/16]} (no global atomics, no
-//               float-encoded offsets).
-//   k_walk      one launch: workgroup (slice p, column tile t) streams its
-//               share of the selected rows, scatter-adds x*w into lane-private
-//               LDS accumulators (no atomics) and writes one partial row per
-//               slice.
-//   k_reduce    one launch: sums the slice partials in a fixed order into y.
+// Here, per group of up to 3 matrices that share an input:
+//   k_walk64    one launch (fp64 accumulation): workgroup (input slice p,
+//               128-column tile t) computes the RMSNorm of h when the input
+//               is a norm, runs the cutoff search itself (a pure function of
+//               x[0:4096] and the probes), selects the rows of its slice and
+//               walks them, adding each exact product x*w to its wave's LDS
+//               tile with fp64 atomics in a fixed order, and writes one
+//               partial row per slice.
+//   k_reduce    one launch: sums the slice partials in a fixed order and
+//               applies the consumer's epilogue (residual add, RoPE and the
+//               fp16 KV append, the SiLU gate, or a store).
+// k_walk (fp32 accumulation, lane-private accumulators) follows k_cutoff;
+// k_cutoff and k_dispatch (one workgroup per matrix / per 256 inputs) serve
+// the standalone calls and the parity queries (cutoff, selected rows).
 // The cutoff and selection arithmetic is exact IEEE fp32 (no contraction), so
-// the cutoff bits and the selected set equal the oracle's.  The walk
-// accumulates in fp32 or, by default, in fp64 (the product of an fp32 input
-// and an fp16 weight is exact in fp64), so y is the correctly rounded sum up
-// to fp64 rounding and does not depend on the order of the additions.
+// the cutoff bits and the selected set equal the oracle's.  With fp64
+// accumulation (the product of an fp32 input and an fp16 weight is exact in
+// fp64) y is the correctly rounded sum up to fp64 rounding, and the fixed
+// order makes it the same on every run.
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
