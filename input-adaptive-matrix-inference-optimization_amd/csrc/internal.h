@@ -195,7 +195,7 @@ int reserve_walk(Ctx* c, int n, const MatOp* ops, float effort);
 struct WalkPlan {
     int NW;     // waves per workgroup (the same for every matrix of a launch)
     int V;      // columns per lane load
-    int T;      // 64-column tiles
+    int T;      // column tiles (128 columns for k_walk64, 64 for k_walk)
     int n_in;   // inputs walked
     int IPS;    // inputs per slice
     int P;      // slices

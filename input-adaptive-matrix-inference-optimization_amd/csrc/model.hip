@@ -4,11 +4,13 @@
 // TransformerLayer::forward (transformer_layer.hpp:75-122: norm -> attention
 // -> +res -> norm -> FFN -> +res), final norm, LM head, greedy argmax
 // (test_generation.cpp:235/276).  Differences that are the point of the
-// build: q/k/v and gate/up run as one cutoff launch and one walk launch per
-// group; the residual add is fused into the next RMSNorm; RoPE and the fp16
-// KV append are one kernel; attention is split over the context; the
-// position and token live in device memory so a whole step is captured once
-// as a HIP graph and replayed per token with no host round trip.
+// build: q/k/v and gate/up run as one walk launch and one reduce launch per
+// group; the walk computes the RMSNorm of its input and the cutoff itself;
+// the reduce applies the residual add, RoPE with the fp16 KV append, or the
+// SiLU gate to its sums; attention is split over the context (partials, then
+// their merge); the position and token live in device memory, so a whole
+// step is captured once as a HIP graph and replayed per token with no host
+// round trip.
 #include <hip/hip_fp16.h>
 
 #include <cstring>
