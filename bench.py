@@ -177,7 +177,8 @@ def run_skew(args, iam, ctx):
         "metric": "skew stress: decode tok/s at efforts 0.05 and 1.0, context 4096, 8 sequences",
         "value": res[str(SKEW_EFFORTS[0])]["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": n,
         "warmup": SWEEP_WARMUP, "higher_is_better": True, "vs_baseline": None,
-        "dtype": "fp16 weights, fp32 activations, %s accumulation" % args.acc,
+        "dtype": "f64" if args.acc == "fp64" else "f32",
+        "dtype_detail": "fp16 weights, fp32 activations, %s products and accumulation" % args.acc,
         "data": "synthetic (random-init weights, N(0,1) KV cache, random token ids)",
         "config": {"workload": "Mistral-7B-shape decode, 1 percent of hidden channels x20 at the embedding, "
                                f"positions {start}..{start + SWEEP_WARMUP + n - 1} of 4096",
@@ -309,7 +310,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16 weights, fp32 activations, %s accumulation" % args.acc,
+        "dtype": "f64" if args.acc == "fp64" else "f32",
+        "dtype_detail": "fp16 weights, fp32 activations, %s products and accumulation" % args.acc,
         "data": "synthetic (random-init weights, random prompt ids)",
         "config": {"workload": "Mistral-7B-shape greedy decode, effort 0.25, 512-token prompt, "
                                "bucket-layout LM head, fp16 GQA KV cache (4096 positions)",
