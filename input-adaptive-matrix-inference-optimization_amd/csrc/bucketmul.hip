@@ -1526,15 +1526,24 @@ int bucketmul_fused(Ctx* c, int n, const MatOp* ops, int expert_no, float effort
     for (int i = 0; i < n; i++) all64 = all64 && vec_of(ops[i].mat.bucket_cols, c->acc64) == 8;
     if (in_mode == kInNorm) {
         IAM_REQUIRE(h && gain, "bucketmul: norm input without h/gain");
+        const int ni = ops[0].in_size;
         for (int i = 0; i < n; i++)
-            IAM_REQUIRE(ops[i].in_size == kProbes && ops[i].x == ops[0].x,
-                        "bucketmul: the fused norm takes 4096 inputs shared by the group");
-        IAM_TRY(check_dev_range(c, h, kProbes * sizeof(float), "bucketmul h"));
-        IAM_TRY(check_dev_range(c, gain, kProbes * 2, "bucketmul gain"));
+            IAM_REQUIRE(ops[i].in_size == ni && ops[i].x == ops[0].x,
+                        "bucketmul: the norm input is shared by the group");
+        IAM_TRY(check_dev_range(c, h, (size_t)ni * sizeof(float), "bucketmul h"));
+        IAM_TRY(check_dev_range(c, gain, (size_t)ni * 2, "bucketmul gain"));
         IAM_REQUIRE(((uintptr_t)h & 15) == 0 && ((uintptr_t)gain & 15) == 0, "bucketmul: h and gain must be 16-byte aligned");
+        if (ni != kProbes) {
+            // the walk's own norm covers 4096 inputs: a wider vector is
+            // normalized by the RMSNorm kernel first (same order of sums)
+            IAM_REQUIRE(ni % 1024 == 0, "bucketmul: a norm input must be a multiple of 1024 long");
+            IAM_TRY(rmsnorm(c, const_cast<float*>(h), nullptr, gain, ni, eps, const_cast<float*>(ops[0].x)));
+            in_mode = kInX;
+        }
     }
     if (all64) return walk_and_reduce(c, n, ops, in_mode, h, gain, eps, ep);
-    if (in_mode == kInNorm) IAM_TRY(rmsnorm(c, const_cast<float*>(h), nullptr, gain, kProbes, eps, const_cast<float*>(ops[0].x)));
+    if (in_mode == kInNorm)
+        IAM_TRY(rmsnorm(c, const_cast<float*>(h), nullptr, gain, ops[0].in_size, eps, const_cast<float*>(ops[0].x)));
     IAM_TRY(launch(c, "bucket_cutoff", k_cutoff, dim3(n), dim3(kCutThreads), 0, args));
     return walk_and_reduce(c, n, ops, kInCutoff, nullptr, nullptr, 0.0f, ep);
 }

@@ -187,11 +187,6 @@ static int mat_group(iam_model* m, int n, const Mat* const* mats, float* x, int 
         ops[i].in_size = in_size;
         ops[i].y = ys[i];
     }
-    if (in_mode == kInNorm && in_size != kProbes) {
-        // the fused norm covers 4096 inputs; other widths normalize first
-        IAM_TRY(rmsnorm(m->c, const_cast<float*>(h), nullptr, gain, in_size, m->cfg.norm_eps, x));
-        in_mode = kInX;
-    }
     return bucketmul_fused(m->c, n, ops, 0, effort, in_mode, h, gain, m->cfg.norm_eps, ep);
 }
 
@@ -408,9 +403,10 @@ static bool lookup(iam_model* m, const std::string& name, TensorRef* out, const 
 static uint64_t tid_layer(int L, int k) { return 1000ull + 16ull * (uint64_t)L + (uint64_t)k; }
 constexpr uint64_t kTidEmbed = 10, kTidFinalGain = 11, kTidLm = 12;
 
-static int synth_mat(iam_model* m, Mat& w, uint64_t seed, uint64_t tid, uint16_t* scratch)
+static int synth_mat(iam_model* m, Mat& w, uint64_t seed, uint64_t tid, uint16_t* scratch, size_t scratch_elems)
 {
     Ctx* c = m->c;
+    IAM_REQUIRE((size_t)w.out_dim * w.in_dim <= scratch_elems, "synthesize: matrix larger than its staging buffer");
     IAM_TRY(gen_f16(c, seed, tid, (size_t)w.out_dim * w.in_dim, 0.0, 0.02, scratch));
     IAM_TRY(zero_async(c, w.probes, (size_t)std::max(w.in_dim, kProbes) * 2));
     IAM_TRY(bucketize(c, scratch, w.out_dim, w.in_dim, w.buckets, w.stats, w.probes));
@@ -508,19 +504,21 @@ int iam_model_synthesize(iam_model* m, uint64_t seed)
     if (!m) return fail(IAM_E_INVALID, "model_synthesize: null model");
     Ctx* c = m->c;
     const iam_model_config& C = m->cfg;
+    // the largest matrix: dim x dim (wq, wo), ffn x dim (w1, w3, w2) or vocab x dim
     size_t maxw = (size_t)C.vocab * C.dim;
     maxw = std::max(maxw, (size_t)C.ffn_dim * C.dim);
+    maxw = std::max(maxw, (size_t)C.dim * C.dim);
     uint16_t* scratch = nullptr;
     IAM_TRY(ctx_alloc(c, maxw * 2, (void**)&scratch));
     int rc = IAM_OK;
     for (int L = 0; L < C.n_layers && rc == IAM_OK; L++) {
         Layer& ly = m->layers[L];
         Mat* ws[7] = {&ly.wq, &ly.wk, &ly.wv, &ly.wo, &ly.w1, &ly.w3, &ly.w2};
-        for (int k = 0; k < 7 && rc == IAM_OK; k++) rc = synth_mat(m, *ws[k], seed, tid_layer(L, k), scratch);
+        for (int k = 0; k < 7 && rc == IAM_OK; k++) rc = synth_mat(m, *ws[k], seed, tid_layer(L, k), scratch, maxw);
         if (rc == IAM_OK) rc = gen_f16(c, seed, tid_layer(L, 7), C.dim, 1.0, 0.01, ly.attn_gain);
         if (rc == IAM_OK) rc = gen_f16(c, seed, tid_layer(L, 8), C.dim, 1.0, 0.01, ly.ffn_gain);
     }
-    if (rc == IAM_OK) rc = synth_mat(m, m->lm, seed, kTidLm, scratch);
+    if (rc == IAM_OK) rc = synth_mat(m, m->lm, seed, kTidLm, scratch, maxw);
     if (rc == IAM_OK) rc = gen_f16(c, seed, kTidEmbed, (size_t)C.vocab * C.dim, 0.0, 0.02, m->embed);
     if (rc == IAM_OK) rc = gen_f16(c, seed, kTidFinalGain, C.dim, 1.0, 0.01, m->final_gain);
     hipError_t e = hipStreamSynchronize(c->stream);

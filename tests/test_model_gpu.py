@@ -150,3 +150,31 @@ def test_model_rejects_bad_config(iam, ctx):
     bad["n_heads"] = 16
     with pytest.raises(iam.IamError):
         iam.Model(ctx, iam.ModelConfig(**bad))
+
+
+WIDE = dict(n_layers=1, dim=8192, ffn_dim=4096, n_heads=64, n_kv_heads=8, head_dim=128, vocab=256,
+            max_ctx=16, rope_theta=10000.0, norm_eps=1e-5)
+
+
+def test_wide_model_logits_and_tokens_match_oracle(O, iam, ctx):
+    """dim 8192 (64 query heads per 8 KV heads): the norms run as their own
+    kernel ahead of the walks and the cutoff reads the first 4096 inputs.
+    Logits within 1 ulp of the oracle's at every step (both running free) and
+    identical greedy tokens, at effort 0.25 and 1.0."""
+    m = iam.Model(ctx, iam.ModelConfig(**WIDE))
+    try:
+        m.synthesize(3)
+        dlog = ctx.empty(WIDE["vocab"], np.float32)
+        for effort in (0.25, 1.0):
+            orc = O.OracleModel(WIDE, m.read_tensor)
+            m.reset_caches()
+            toks = O.gen_tokens(3, 91, 6, WIDE["vocab"]).tolist()
+            for pos, tok in enumerate(toks):
+                m.forward(tok, pos, effort, dlog)
+                lg = dlog.read()
+                lo = orc.forward(tok, pos, effort)
+                assert ulps(lg, lo).max() <= 1, (effort, pos)
+                assert int(np.argmax(lg)) == O.argmax(lo), (effort, pos)
+        dlog.free()
+    finally:
+        m.close()
