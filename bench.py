@@ -6,7 +6,9 @@ vocabulary 32000 with a bucket-layout LM head, fp16 GQA KV cache of 4096
 positions, RoPE theta 10000; random-init synthetic weights N(0, 0.02^2)
 bucketized on the GPU; a 512-token random-id prompt fed token by token; then
 greedy decode at effort 0.25.  A step is one decode token (captured once as a
-HIP graph and replayed).  `value` is decode tokens per second.
+HIP graph and replayed).  `value` is decode tokens per second, timed with
+the library's walk counting switched off (the reduce then skips adding up
+the selected rows); the bytes per token come from steps run with it on.
 
 roofline: the bucket walk kernel (the dominant one) -- the selected weight
 bytes it streams (2 * S * bucket_cols per matrix, counted on the device) per
@@ -17,8 +19,9 @@ walk's own dispatch on the library's stream during eager steps, against the
 committed counter summary profiles/walk_hbm_traffic_mistral7b_effort025.md.
 
 effort_sweep: the same decode continued at efforts 1.0, 0.5, 0.125 and
-0.05 (32 graph-replayed steps each): tok/s and the fraction of 8 TB/s for
-the bytes touched per token at that effort.
+0.05 (32 graph-replayed steps each, counting off): tok/s and the fraction of
+8 TB/s for the bytes touched per token at that effort, the selected bytes
+counted over the next SWEEP_COUNT steps (counting on).
 
 cpu_baseline: the C oracle on one host core, timed on a bounded sample
 (decoder layers and the LM head of the same model at the same effort and
@@ -41,6 +44,7 @@ MISTRAL = dict(n_layers=32, dim=4096, ffn_dim=14336, n_heads=32, n_kv_heads=8, h
 HBM_PEAK_GBS = 8000.0
 SWEEP_EFFORTS = [1.0, 0.5, 0.25, 0.125, 0.05]   # the configs' efforts
 SWEEP_WARMUP = 4
+SWEEP_COUNT = 4   # steps with walk counting on after each timed run: bytes per token
 
 
 def load_iam():
@@ -142,13 +146,13 @@ def run_skew(args, iam, ctx):
         ptr, nbytes = model.tensor(name)
         ctx.gen_f16(0, tid, nbytes // 2, 0.0, 1.0, ptr)
     n = args.skew_steps
-    start = cfg["max_ctx"] - SWEEP_WARMUP - n - 1
+    start = cfg["max_ctx"] - SWEEP_WARMUP - n - SWEEP_COUNT - 1
     if n < 1 or start < 1:
-        sys.exit(f"--skew-steps {n} must be in [1, {cfg['max_ctx'] - SWEEP_WARMUP - 2}]")
+        sys.exit(f"--skew-steps {n} must be in [1, {cfg['max_ctx'] - SWEEP_WARMUP - SWEEP_COUNT - 2}]")
     rng = np.random.default_rng(5)
     res = {}
     for e in SKEW_EFFORTS:
-        steps = 0
+        steps = counted = 0
         secs = 0.0
         wbytes = 0
         for sq in range(SKEW_SEQUENCES):
@@ -157,17 +161,22 @@ def run_skew(args, iam, ctx):
             model.set_embed_scale(scale)
             model.write_tensor("pos", np.array([start], np.int32))
             model.write_tensor("token", np.array([int(rng.integers(0, cfg["vocab"]))], np.int32))
+            ctx.set_walk_counting(False)
             model.decode(SWEEP_WARMUP, e)
             ctx.sync()
-            ctx.walk_counters(reset=True)
             t0 = time.perf_counter()
             model.decode(n, e)
             ctx.sync()
             secs += time.perf_counter() - t0
+            steps += n
+            ctx.set_walk_counting(True)
+            ctx.walk_counters(reset=True)
+            model.decode(SWEEP_COUNT, e)
+            ctx.sync()
             b, _, _ = ctx.walk_counters(reset=True)
             wbytes += b
-            steps += n
-        bpt = wbytes / steps + per_token_fixed_bytes(cfg, start + SWEEP_WARMUP + n // 2)
+            counted += SWEEP_COUNT
+        bpt = wbytes / counted + per_token_fixed_bytes(cfg, start + SWEEP_WARMUP + n // 2)
         tps = steps / secs
         res[str(e)] = {"tok_s": round(tps, 2), "ms_per_token": round(secs / steps * 1e3, 4),
                        "bytes_per_token": round(bpt), "achieved_GBs": round(bpt * tps / 1e9, 1),
@@ -181,7 +190,7 @@ def run_skew(args, iam, ctx):
         "dtype_detail": "fp16 weights, fp32 activations, %s products and accumulation" % args.acc,
         "data": "synthetic (random-init weights, N(0,1) KV cache, random token ids)",
         "config": {"workload": "Mistral-7B-shape decode, 1 percent of hidden channels x20 at the embedding, "
-                               f"positions {start}..{start + SWEEP_WARMUP + n - 1} of 4096",
+                               f"positions {start}..{start + SWEEP_WARMUP + n + SWEEP_COUNT - 1} of 4096",
                    "sequences": SKEW_SEQUENCES, "efforts": SKEW_EFFORTS},
         "efforts": res,
     }
@@ -212,10 +221,12 @@ def main():
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)
         sys.exit(2)
+    if args.profile_steps < 1:
+        sys.exit("--profile-steps must be at least 1 (they give the walk's bytes and launch times)")
     cfg = dict(MISTRAL)
     sweep_efforts = [e for e in SWEEP_EFFORTS if e != args.effort] if args.sweep_steps > 0 else []
     total = (args.prompt + args.warmup + args.steps + args.profile_steps + 1
-             + len(sweep_efforts) * (SWEEP_WARMUP + args.sweep_steps))
+             + len(sweep_efforts) * (SWEEP_WARMUP + args.sweep_steps + SWEEP_COUNT))
     if total > cfg["max_ctx"]:
         sys.exit(f"prompt + warmup + steps + profile steps ({total}) exceed the KV capacity {cfg['max_ctx']}")
 
@@ -240,20 +251,18 @@ def main():
     ctx.sync()
     log(f"prefill of {args.prompt} tokens: {time.perf_counter() - t:.2f} s, first token {int(first[0])}")
 
+    # the timed decode runs with the walk counting off (a captured graph of
+    # that setting); the counted steps below give the bytes
+    ctx.set_walk_counting(False)
     model.decode(args.warmup, args.effort, use_graph=use_graph)
     ctx.sync()
-    ctx.walk_counters(reset=True)
     t0 = time.perf_counter()
     model.decode(args.steps, args.effort, use_graph=use_graph)
     ctx.sync()
     t1 = time.perf_counter()
-    wbytes, wrows, wmats = ctx.walk_counters(reset=True)
+    ctx.set_walk_counting(True)
     dt = t1 - t0
     tok_s = args.steps / dt
-    pos_mid = args.prompt + args.warmup + args.steps // 2
-    bytes_per_token = wbytes / args.steps + per_token_fixed_bytes(cfg, pos_mid)
-    log(f"decode: {args.steps} tokens in {dt * 1e3:.1f} ms = {tok_s:.1f} tok/s; "
-        f"{bytes_per_token / 1e9:.3f} GB/token -> {bytes_per_token * tok_s / 1e9:.0f} GB/s")
 
     # per-kernel times: eager decode steps in which every kernel is launched
     # with a pair of HIP events stamped by its own dispatch on the library's
@@ -271,28 +280,38 @@ def main():
     per_launch = pbytes / walk_calls
     walk_avg_s = walk_ms / 1e3 / walk_calls
     achieved = per_launch / walk_avg_s / 1e9
+    # bytes per token of the timed decode: the selected bytes of these
+    # counted steps (the next positions of the same sequence) + the fixed part
+    pos_mid = args.prompt + args.warmup + args.steps // 2
+    bytes_per_token = pbytes / args.profile_steps + per_token_fixed_bytes(cfg, pos_mid)
+    log(f"decode: {args.steps} tokens in {dt * 1e3:.1f} ms = {tok_s:.1f} tok/s; "
+        f"{bytes_per_token / 1e9:.3f} GB/token -> {bytes_per_token * tok_s / 1e9:.0f} GB/s")
 
     # the same decode at the other efforts of the configs, continuing the
     # sequence: tok/s and the roofline fraction of the bytes touched per token
     sweep = {}
     pos_now = args.prompt + args.warmup + args.steps + args.profile_steps
     for e in sweep_efforts:
+        ctx.set_walk_counting(False)
         model.decode(SWEEP_WARMUP, e, use_graph=use_graph)
         ctx.sync()
-        ctx.walk_counters(reset=True)
         t0 = time.perf_counter()
         model.decode(args.sweep_steps, e, use_graph=use_graph)
         ctx.sync()
         dt_e = time.perf_counter() - t0
+        ctx.set_walk_counting(True)
+        ctx.walk_counters(reset=True)
+        model.decode(SWEEP_COUNT, e, use_graph=use_graph)
+        ctx.sync()
         eb, _, _ = ctx.walk_counters(reset=True)
         pos_e = pos_now + SWEEP_WARMUP + args.sweep_steps // 2
-        bpt = eb / args.sweep_steps + per_token_fixed_bytes(cfg, pos_e)
+        bpt = eb / SWEEP_COUNT + per_token_fixed_bytes(cfg, pos_e)
         tps = args.sweep_steps / dt_e
         sweep[str(e)] = {"tok_s": round(tps, 2), "ms_per_token": round(dt_e / args.sweep_steps * 1e3, 4),
                          "bytes_per_token": round(bpt), "achieved_GBs": round(bpt * tps / 1e9, 1),
                          "frac": round(bpt * tps / 1e9 / HBM_PEAK_GBS, 4)}
         log(f"effort {e}: {tps:.1f} tok/s, {bpt / 1e9:.3f} GB/token -> {bpt * tps / 1e9:.0f} GB/s")
-        pos_now += SWEEP_WARMUP + args.sweep_steps
+        pos_now += SWEEP_WARMUP + args.sweep_steps + SWEEP_COUNT
     cpu = None
     if not args.no_cpu_baseline:
         t = time.perf_counter()

@@ -144,6 +144,14 @@ int iam_effort_quantile(float effort);
  * the walk kernel, so graph replays count too.  Blocking. */
 int iam_walk_counters(iam_ctx* ctx, uint64_t* weight_bytes, uint64_t* rows, uint64_t* matrices,
                       int reset);
+/* Counting of the walk's selected rows (default on): the reduce adds up the
+ * per-slice counts into the slot count (iam_bucketmul_walk_count) and the
+ * counters above.  Off, neither is updated (walk_count then fails with
+ * IAM_E_STATE for the slots walked) and each reduce launch is shorter: its
+ * first workgroup no longer waits for the counts and the counter atomics.
+ * Changing it re-captures the model's decode graph.  Not during capture.
+ * No counterpart in the reference. */
+int iam_set_walk_counting(iam_ctx* ctx, int on);
 /* Accumulation of the bucket walk (and of attention) for this context:
  * IAM_ACC_FP64 (default) adds the exact fp64 products in fp64 and rounds each
  * output once, so results do not depend on the order of the additions and

@@ -948,7 +948,7 @@ struct ReduceDesc {
 struct ReduceArgs {
     ReduceDesc d[kMaxMulti];
     int n;
-    unsigned long long* counters;  // walk bytes, rows, matrices
+    unsigned long long* counters;  // walk bytes, rows, matrices (null: no counting)
 };
 
 constexpr int kRedThreads = 256;
@@ -1093,8 +1093,8 @@ __global__ __launch_bounds__(kRedThreads) void k_reduce(ReduceArgs a)
     const int tid = threadIdx.x;
     const int ol = tid % S::QUADS, pg = tid / S::QUADS;
     const int o = o0 + ol * 4;   // m is a multiple of 16: o..o+3 are in range together
-    if (lb == 0 && tid >= kRedThreads - 64) sum_counts(d.slice_count, d.P, d.C, d.count, a.counters);
-    if (lb == 0 && d.ep == kEpSilu && tid >= kRedThreads - 128 && tid < kRedThreads - 64)
+    if (a.counters && lb == 0 && tid >= kRedThreads - 64) sum_counts(d.slice_count, d.P, d.C, d.count, a.counters);
+    if (a.counters && lb == 0 && d.ep == kEpSilu && tid >= kRedThreads - 128 && tid < kRedThreads - 64)
         sum_counts(d.slice_count2, d.P2, d.C, d.count2, a.counters);
     const int oo = o0 + tid;
     const bool in = tid < OUT && oo < d.m;
@@ -1463,7 +1463,8 @@ static int walk_and_reduce(Ctx* c, int n, const MatOp* ops, int in_mode, const f
     }
     // fixed-order sum of the slices into y, with the epilogue
     ReduceArgs ra{};
-    ra.counters = c->counters;
+    ra.counters = c->counting ? c->counters : nullptr;   // null: no counting
+    for (int i = 0; i < n; i++) c->slots[i].counted = c->counting;
     int rblocks = 0, nd = 0;
     int rout = 32;
     for (int i = 0; ep && i < n; i++)
@@ -1689,6 +1690,7 @@ int iam_bucketmul_walk_count(iam_ctx* c, int slot, uint32_t* count)
     if (!c || !count || slot < 0 || slot >= kMaxMulti) return fail(IAM_E_INVALID, "walk_count: bad argument");
     const DispatchSlot& s = c->slots[slot];
     if (!s.valid) return fail(IAM_E_STATE, "walk_count: no dispatch in this slot");
+    if (!s.counted) return fail(IAM_E_STATE, "walk_count: the last walk of this slot ran with counting off");
     IAM_CHECK_HIP(hipStreamSynchronize(c->stream));
     IAM_CHECK_HIP(hipMemcpy(count, s.count, sizeof(uint32_t), hipMemcpyDeviceToHost));
     return IAM_OK;

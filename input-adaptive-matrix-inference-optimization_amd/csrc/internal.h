@@ -63,6 +63,7 @@ struct DispatchSlot {
     bool valid = false;
     float* cutoff = nullptr;     // device [2]: k_cutoff's value, the list kernel's value
     uint32_t* count = nullptr;   // device [1]: rows selected by the last walk
+    bool counted = false;        // the last walk counted its rows (counting was on)
     uint2* list = nullptr;       // [G][kChunkRows]
     uint32_t* counts = nullptr;  // [kMaxChunks]
     size_t cap_chunks = 0;
@@ -102,6 +103,9 @@ struct Ctx {
     // those addresses and must be re-captured when it changes
     uint64_t scratch_gen = 0;
     unsigned long long* counters = nullptr;   // device: walk bytes, rows, matrices
+    // the reduce adds up the walk's selected rows into the slot counts and
+    // the counters (off: neither is updated, and the reduce is shorter)
+    bool counting = true;
     // accumulate the walk in fp64 (sums round once to fp32) instead of fp32
     bool acc64 = true;
 };

@@ -397,6 +397,17 @@ int iam_set_accumulation(iam_ctx* c, int mode)
     return IAM_OK;
 }
 
+int iam_set_walk_counting(iam_ctx* c, int on)
+{
+    if (!c) return fail(IAM_E_INVALID, "set_walk_counting: null context");
+    IAM_REQUIRE(!c->capturing, "set_walk_counting: not allowed during graph capture");
+    if ((on != 0) != c->counting) {
+        c->counting = on != 0;
+        c->scratch_gen++;   // captured graphs hold reduce launches of the other setting
+    }
+    return IAM_OK;
+}
+
 int iam_get_accumulation(iam_ctx* c, int* mode)
 {
     if (!c || !mode) return fail(IAM_E_INVALID, "get_accumulation: bad argument");

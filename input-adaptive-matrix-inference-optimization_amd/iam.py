@@ -219,6 +219,10 @@ class Ctx:
         """"fp64" (default) or "fp32"."""
         check(lib().iam_set_accumulation(self.h, {"fp32": 0, "fp64": 1}[mode]))
 
+    def set_walk_counting(self, on):
+        """Count the walk's selected rows (default on; off shortens each reduce)."""
+        check(lib().iam_set_walk_counting(self.h, 1 if on else 0))
+
     def get_accumulation(self):
         m = C.c_int()
         check(lib().iam_get_accumulation(self.h, C.byref(m)))

@@ -241,3 +241,29 @@ def test_accumulation_modes_deterministic(O, ctx, mode):
         assert ulps(runs[0], oy).max() <= 1
     else:
         assert rel_l2(runs[0], oy) < 1e-5
+
+
+def test_walk_counting_switch(O, iam, ctx):
+    """With counting off the outputs are bit-identical, the counters do not
+    move and walk_count reports that the slot was not counted; back on, the
+    count is the oracle's selected-row count again."""
+    b, s, p = make_matrix(O, 4096, 4096)
+    x = O.gen_f32(0, 77, 4096, 0.0, 1.0)
+    y_on, cut, S, rows = run_gpu(ctx, b, s, p, x, 0.25, split=False)
+    db, ds, dp, dx = ctx.upload(b), ctx.upload(s), ctx.upload(p), ctx.upload(x)
+    dy = ctx.empty(16 * b.shape[1], np.float32)
+    ctx.walk_counters(reset=True)
+    ctx.set_walk_counting(False)
+    try:
+        ctx.full_mul(dx, ds, dp, db, 0, 4096, b.shape[1], b.shape[0], 0.25, dy)
+        assert np.array_equal(dy.read().view(np.uint32), y_on.view(np.uint32))
+        assert ctx.walk_counters(reset=True) == (0, 0, 0)
+        with pytest.raises(iam.IamError):
+            ctx.walk_count(0)
+    finally:
+        ctx.set_walk_counting(True)
+    ctx.full_mul(dx, ds, dp, db, 0, 4096, b.shape[1], b.shape[0], 0.25, dy)
+    assert ctx.walk_count(0) == S
+    assert ctx.walk_counters(reset=True) == (2 * S * b.shape[1], S, 1)
+    for d in (db, ds, dp, dx, dy):
+        d.free()

@@ -128,6 +128,28 @@ def test_generate_graph_equals_eager_and_picks_argmax(O, ctx, model):
     dlog.free()
 
 
+def test_counting_off_gives_the_same_tokens(O, ctx, model):
+    """Graph-replayed greedy decode with the walk counting switched off (the
+    decode graph is re-captured) picks the same tokens, and the counters do
+    not move."""
+    prompt = O.gen_tokens(0, 96, 5, CFG["vocab"]).tolist()
+    model.reset_caches()
+    on = model.generate(prompt, 6, 0.25, use_graph=True).tolist()
+    ctx.walk_counters(reset=True)
+    ctx.set_walk_counting(False)
+    try:
+        model.reset_caches()
+        off = model.generate(prompt, 6, 0.25, use_graph=True).tolist()
+        assert ctx.walk_counters(reset=True) == (0, 0, 0)
+    finally:
+        ctx.set_walk_counting(True)
+    assert off == on
+    model.reset_caches()
+    again = model.generate(prompt, 6, 0.25, use_graph=True).tolist()
+    assert again == on
+    assert ctx.walk_counters(reset=True)[2] > 0
+
+
 def test_greedy_tokens_match_oracle(O, model):
     """Greedy decode from a 5-token prompt: the GPU's 16 new tokens (graph
     replay) are the oracle's."""
