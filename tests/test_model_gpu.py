@@ -150,6 +150,29 @@ def test_counting_off_gives_the_same_tokens(O, ctx, model):
     assert ctx.walk_counters(reset=True)[2] > 0
 
 
+@pytest.mark.parametrize("effort", [0.05, 1.0])
+def test_skewed_embedding_logits_match_oracle(O, ctx, model, effort):
+    """Skew stress: 1% of the hidden channels (41 of 4096) scaled 20x after
+    the embedding gather.  The oracle takes the same scaled embedding row as
+    its hidden input; logits within 1 ulp at every step, both running free."""
+    rng = np.random.default_rng(11)
+    scale = np.ones(CFG["dim"], np.float32)
+    scale[rng.choice(CFG["dim"], CFG["dim"] // 100, replace=False)] = 20.0
+    emb = O.f16_to_f32(model.read_tensor("embed", np.uint16)).reshape(CFG["vocab"], CFG["dim"])
+    orc = OracleModel(O, model)
+    model.reset_caches()
+    model.set_embed_scale(scale)
+    dlog = ctx.empty(CFG["vocab"], np.float32)
+    try:
+        for pos, tok in enumerate(O.gen_tokens(0, 93, 6, CFG["vocab"]).tolist()):
+            model.forward(tok, pos, effort, dlog)
+            lo = orc.forward(tok, pos, effort, hidden_in=emb[tok] * scale)
+            assert ulps(dlog.read(), lo).max() <= 1, pos
+    finally:
+        model.set_embed_scale(None)
+        dlog.free()
+
+
 def test_greedy_tokens_match_oracle(O, model):
     """Greedy decode from a 5-token prompt: the GPU's 16 new tokens (graph
     replay) are the oracle's."""
