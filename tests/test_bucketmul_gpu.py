@@ -133,6 +133,41 @@ def test_skewed_channels(O, ctx):
         check_against_oracle(O, ctx, b, s, p, x, effort)
 
 
+def _cutoff_patterns():
+    """x vectors that, with every probe 2^-6 (importance = fl(1e5 * |x| / 64),
+    the values of the oracle's known-answer cases), drive the bisection
+    through those paths while the walk still selects 11k-29k rows: name, x,
+    effort, (rounds, converged) of the oracle's trace."""
+    x = np.zeros(4096, np.float32)
+    x[:1025], x[1025:] = 64e-4, 64e-5                # 1025 at 10, the rest at 1: hit in round 1
+    yield "exact_hit_round1", x, 0.25, (1, 1)
+    yield "constant", np.full(4096, 0.64, np.float32), 0.5, (1, 1)   # min == max
+    yield "ramp_gap", np.arange(4096, dtype=np.float32) * np.float32(2.0 ** -14), 0.25, (11, 1)
+    x = np.zeros(4096, np.float32)
+    x[:1023], x[1023:1028] = 0.64, 0.32              # 1000 x1023, 500 x5: float midpoints stall
+    yield "round_limit_ties", x, 0.25, (20, 0)
+    x = np.zeros(4096, np.float32)
+    x[:3000] = -0.64                                 # 3000 ties: the bracket never gets below 256 values
+    yield "round_limit_wide_bracket", x, 0.25, (20, 0)
+
+
+@pytest.mark.parametrize("pattern", [p[0] for p in _cutoff_patterns()])
+def test_cutoff_edge_paths(O, ctx, pattern):
+    """The search's edge paths on the GPU, bit-exact against the oracle: the
+    standalone cutoff kernel (calc_dispatch), the walk's own search with
+    4-wave workgroups (full_mul, 256 outputs) and with 8-wave workgroups
+    (full_mul, the LM-head shape)."""
+    name, x, effort, (rounds, conv) = next(p for p in _cutoff_patterns() if p[0] == pattern)
+    probes = np.full(4096, 0x2400, np.uint16)
+    _, tr = O.find_cutoff(x, probes, O.effort_quantile(effort), trace=True)
+    assert (tr.rounds, tr.converged) == (rounds, conv)     # the pattern takes the intended path
+    b, s, _ = make_matrix(O, 256, 4096, tid=9)
+    check_against_oracle(O, ctx, b, s, probes, x, effort, split=True)
+    check_against_oracle(O, ctx, b, s, probes, x, effort, split=False)
+    b, s, _ = make_matrix(O, 32000, 4096, tid=5)
+    check_against_oracle(O, ctx, b, s, probes, x, effort, split=False)
+
+
 @pytest.mark.parametrize("out_dim", [16, 32, 48, 64, 80, 2048 + 16])
 def test_narrow_and_ragged_columns(O, ctx, out_dim):
     """bucket_cols 1..129: the 1/2/4/8-wide load paths and a partial last tile."""
