@@ -70,6 +70,13 @@ int iam_read(iam_ctx* ctx, void* dst_host, const void* src_dev, size_t src_offse
 int iam_copy(iam_ctx* ctx, void* dst_dev, size_t dst_offset, const void* src_dev,
              size_t src_offset, size_t bytes);
 
+/* Measured streaming-read bandwidth of the device (GB/s): reps timed passes
+ * of 16-byte loads over a zero-filled buffer of `bytes` (allocated and freed
+ * here; 2 GiB keeps it out of the 256 MB Infinity Cache).  Blocking.  No
+ * counterpart in the reference: the measured peak the walk's roofline is
+ * also reported against. */
+int iam_read_bandwidth(iam_ctx* ctx, size_t bytes, int reps, double* gb_per_s);
+
 /* Per-kernel profiling (gpu.hpp:104-106, :275-290, :411-432): when enabled each
  * launch is bracketed by HIP events and iam_sync folds the durations. */
 int iam_profiling(iam_ctx* ctx, int enable);

@@ -327,6 +327,75 @@ int iam_copy(iam_ctx* c, void* dst, size_t doff, const void* src, size_t soff, s
     return IAM_OK;
 }
 
+// Streaming read of n16 16-byte words: block b reads the b-th contiguous
+// chunk, 8 loads in flight per thread (of the shapes measured, the fastest:
+// 6.4-6.5 TB/s against 5.5 for a grid-stride loop with 4 loads 8 MB apart).
+// The xor of the words is stored only if it equals a value that a
+// zero-filled buffer cannot give, so the loads are kept and nothing is
+// written.
+__global__ __launch_bounds__(256) void k_read_stream(const uint4* __restrict__ p, size_t n16,
+                                                    uint32_t* __restrict__ sink)
+{
+    constexpr int U = 8;
+    const size_t chunk = (n16 + gridDim.x - 1) / gridDim.x;
+    const size_t b0 = (size_t)blockIdx.x * chunk;
+    const size_t b1 = b0 + chunk < n16 ? b0 + chunk : n16;
+    uint32_t acc = 0;
+    size_t i = b0 + threadIdx.x;
+    for (; i + (U - 1) * 256 < b1; i += U * 256) {
+        uint4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) v[u] = p[i + u * 256];
+#pragma unroll
+        for (int u = 0; u < U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; i < b1; i += 256) {
+        const uint4 a = p[i];
+        acc ^= a.x ^ a.y ^ a.z ^ a.w;
+    }
+    if (acc == 0x9e3779b9u) sink[blockIdx.x] = acc;
+}
+
+int iam_read_bandwidth(iam_ctx* c, size_t bytes, int reps, double* gb_per_s)
+{
+    if (!c || !gb_per_s) return fail(IAM_E_INVALID, "read_bandwidth: null argument");
+    IAM_REQUIRE(bytes >= (1u << 20) && bytes % 16 == 0, "read_bandwidth: bytes must be >= 1 MiB and a multiple of 16");
+    IAM_REQUIRE(reps >= 1 && reps <= 1000, "read_bandwidth: reps must be in [1, 1000]");
+    IAM_REQUIRE(!c->capturing, "read_bandwidth: not allowed during graph capture");
+    constexpr unsigned kBlocks = 8192;
+    void* buf = nullptr;
+    void* sink = nullptr;
+    IAM_TRY(ctx_alloc(c, bytes, &buf));
+    int rc = ctx_alloc(c, kBlocks * sizeof(uint32_t), &sink);
+    if (rc == IAM_OK) rc = zero_async(c, buf, bytes);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    float ms = 0.0f;
+    if (rc == IAM_OK && (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess))
+        rc = fail(IAM_E_HIP, "read_bandwidth: event creation failed");
+    const size_t n16 = bytes / 16;
+    // one untimed pass, then reps timed back to back
+    if (rc == IAM_OK) {
+        hipLaunchKernelGGL(k_read_stream, dim3(kBlocks), dim3(256), 0, c->stream, (const uint4*)buf, n16,
+                           (uint32_t*)sink);
+        (void)hipEventRecord(e0, c->stream);
+        for (int r = 0; r < reps; r++)
+            hipLaunchKernelGGL(k_read_stream, dim3(kBlocks), dim3(256), 0, c->stream, (const uint4*)buf, n16,
+                               (uint32_t*)sink);
+        (void)hipEventRecord(e1, c->stream);
+        hipError_t e = hipEventSynchronize(e1);
+        if (e == hipSuccess) e = hipGetLastError();
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+        if (e != hipSuccess) rc = fail(IAM_E_HIP, std::string("read_bandwidth: ") + hipGetErrorString(e));
+    }
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (sink) (void)ctx_free(c, sink);
+    (void)ctx_free(c, buf);
+    if (rc != IAM_OK) return rc;
+    *gb_per_s = ms > 0.0f ? (double)bytes * reps / (ms * 1e-3) / 1e9 : 0.0;
+    return IAM_OK;
+}
+
 int iam_profiling(iam_ctx* c, int enable)
 {
     if (!c) return fail(IAM_E_INVALID, "profiling: null context");

@@ -219,6 +219,12 @@ class Ctx:
         """"fp64" (default) or "fp32"."""
         check(lib().iam_set_accumulation(self.h, {"fp32": 0, "fp64": 1}[mode]))
 
+    def read_bandwidth(self, nbytes=2 << 30, reps=10):
+        """Measured streaming-read bandwidth in GB/s."""
+        g = C.c_double()
+        check(lib().iam_read_bandwidth(self.h, C.c_size_t(nbytes), reps, C.byref(g)))
+        return g.value
+
     def set_walk_counting(self, on):
         """Count the walk's selected rows (default on; off shortens each reduce)."""
         check(lib().iam_set_walk_counting(self.h, 1 if on else 0))

@@ -190,3 +190,15 @@ def test_embed_and_argmax(O, ctx):
     assert di.read()[0] == 100 == O.argmax(w)
     for d_ in (dtab, dout, dt, dv, di, dw):
         d_.free()
+
+
+def test_read_bandwidth(iam, ctx):
+    """The streaming-read measurement: a plausible figure over 1 GiB (past
+    the 256 MB Infinity Cache, so at most the 8 TB/s HBM peak), and bad
+    arguments are refused."""
+    g = ctx.read_bandwidth(1 << 30, 4)
+    assert 500.0 < g < 8400.0, g
+    with pytest.raises(iam.IamError):
+        ctx.read_bandwidth(1000, 4)
+    with pytest.raises(iam.IamError):
+        ctx.read_bandwidth(1 << 30, 0)
