@@ -2,6 +2,7 @@ import importlib.util
 import os
 import sys
 
+import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -36,3 +37,43 @@ def ctx(iam):
     c = iam.Ctx(0)
     yield c
     c.close()
+
+
+def load_converter():
+    spec = importlib.util.spec_from_file_location("convert_checkpoint", os.path.join(PKG, "convert_checkpoint.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+@pytest.fixture(scope="session")
+def conv():
+    return load_converter()
+
+
+def write_safetensors(path, tensors):
+    """A safetensors file: 8-byte little-endian header length, the JSON
+    header (dtype, shape, data_offsets per tensor), the raw tensors.
+    tensors: name -> (dtype string, shape, numpy array of the raw elements)."""
+    import json
+    import struct
+    header, blobs, off = {}, [], 0
+    for name, (dt, shape, raw) in tensors.items():
+        b = np.ascontiguousarray(raw).tobytes()
+        header[name] = {"dtype": dt, "shape": list(shape), "data_offsets": [off, off + len(b)]}
+        blobs.append(b)
+        off += len(b)
+    header["__metadata__"] = {"format": "pt"}
+    h = json.dumps(header).encode()
+    h += b" " * ((8 - len(h) % 8) % 8)
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(h)))
+        f.write(h)
+        for b in blobs:
+            f.write(b)
+
+
+def f32_to_bf16_bits(a):
+    """Round finite fp32 values to bf16 (nearest, ties to even): the raw bits."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
