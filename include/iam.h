@@ -130,7 +130,20 @@ int iam_bucketmul_full(iam_ctx* ctx, const float* x_dev, const uint16_t* stats_d
 int iam_bucketmul_multi(iam_ctx* ctx, int n, const iam_bucket_matrix* mats,
                         const float* const* xs_dev, const int* in_sizes, float* const* ys_dev,
                         int expert_no, float effort);
-/* Parity outputs of the last calc_dispatch / multi call for matrix slot
+/* One matrix group (1..3 matrices sharing one input) in two launches, as
+ * the model's decode step runs it: every walk workgroup computes the input
+ * itself -- x_dev as given, or, when h_dev is not null, x = RMSNorm(h) * gain
+ * (rmsNorm32fast + mul16x32, aux.cl:156-196, :434-440; written to x_dev) --
+ * then the cutoff (the same bisection as calc_dispatch, in every workgroup),
+ * selects and walks its input slice; the second launch sums the slices into
+ * ys_dev[i].  Results equal calc_dispatch + mul.  A norm input of other than
+ * 4096 values is normalized by a separate RMSNorm launch first.  No
+ * counterpart in the reference, which runs the cutoff as a launch of its
+ * own (bucket_mul.hpp:147-176). */
+int iam_bucketmul_fused(iam_ctx* ctx, int n, const iam_bucket_matrix* mats, float* x_dev, int in_size,
+                        float* const* ys_dev, int expert_no, float effort, const float* h_dev,
+                        const uint16_t* gain_dev, float eps);
+/* Parity outputs of the last calc_dispatch / multi / fused call for matrix slot
  * `slot`: the cutoff (fp32, as written by findCutoffBinarySearch) and the
  * selected-row count S.  The selection is re-run by a separate list kernel
  * that recomputes the cutoff on its own; the call fails with IAM_E_STATE if

@@ -1633,6 +1633,25 @@ int iam_bucketmul_multi(iam_ctx* c, int n, const iam_bucket_matrix* mats, const 
     return bucketmul_walk(c, n, ops);
 }
 
+int iam_bucketmul_fused(iam_ctx* c, int n, const iam_bucket_matrix* mats, float* x, int in_size,
+                        float* const* ys, int expert_no, float effort, const float* h, const uint16_t* gain,
+                        float eps)
+{
+    if (!c || !mats || !x || !ys) return fail(IAM_E_INVALID, "fused: null argument");
+    if (n < 1 || n > kMaxMulti) return fail(IAM_E_INVALID, "fused: n must be 1..3");
+    IAM_REQUIRE((h == nullptr) == (gain == nullptr), "fused: h and gain go together");
+    IAM_REQUIRE(!h || (std::isfinite(eps) && eps >= 0.0f), "fused: eps must be finite and >= 0");
+    MatOp ops[kMaxMulti];
+    for (int i = 0; i < n; i++) {
+        ops[i].mat = mats[i];
+        ops[i].x = x;
+        ops[i].in_size = in_size;
+        ops[i].y = ys[i];
+        IAM_REQUIRE(ys[i] && mats[i].buckets, "fused: null y/buckets");
+    }
+    return bucketmul_fused(c, n, ops, expert_no, effort, h ? kInNorm : kInX, h, gain, eps, nullptr);
+}
+
 // The cutoff comes from k_cutoff; the selection is re-run by the list kernel
 // (which recomputes the cutoff on its own; the two must agree bit for bit).
 static int dispatch_query(Ctx* c, int slot, float* cutoff, std::vector<uint32_t>* rows, uint32_t* count)

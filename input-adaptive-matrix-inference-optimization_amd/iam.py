@@ -200,6 +200,16 @@ class Ctx:
         Y = (C.c_void_p * n)(*[y.ptr if not isinstance(y, int) else y for y in ys])
         check(lib().iam_bucketmul_multi(self.h, n, M, X, I, Y, expert_no, C.c_float(effort)))
 
+    def fused(self, mats, x, in_size, ys, effort, h=None, gain=None, eps=1e-5, expert_no=0):
+        """One matrix group with the input (or RMSNorm(h) * gain, written to x)
+        and the cutoff computed inside the walk."""
+        n = len(mats)
+        M = (BucketMatrix * n)(*mats)
+        Y = (C.c_void_p * n)(*[y.ptr if not isinstance(y, int) else y for y in ys])
+        check(lib().iam_bucketmul_fused(self.h, n, M, _vp(x), in_size, Y, expert_no, C.c_float(effort),
+                                        _vp(h) if h is not None else None,
+                                        _vp(gain) if gain is not None else None, C.c_float(eps)))
+
     def dispatch_info(self, slot=0):
         cut = C.c_float()
         cnt = C.c_uint32()

@@ -37,13 +37,19 @@ def rel_l2(a, b):
     return np.linalg.norm(a.astype(np.float64) - b) / (nb if nb > 0 else 1.0)
 
 
-def run_gpu(ctx, b, s, p, x, effort, in_size=None, expert_no=0, expert_rows=None, split=True):
+def run_gpu(ctx, b, s, p, x, effort, in_size=None, expert_no=0, expert_rows=None, split=True, fused=None):
+    """split: calc_dispatch + mul; else full_mul (both with the cutoff
+    launch); fused (the iam module): the walk computes the cutoff itself
+    (iam_bucketmul_fused)."""
     R = expert_rows if expert_rows is not None else b.shape[0]
     C = b.shape[1]
     in_size = in_size if in_size is not None else R // 16
     db, ds, dp, dx = ctx.upload(b), ctx.upload(s), ctx.upload(p), ctx.upload(x)
     dy = ctx.empty(16 * C, np.float32)
-    if split:
+    if fused is not None:
+        mat = fused.BucketMatrix(db.ptr, ds.ptr, dp.ptr, R, C, 4, 3)
+        ctx.fused([mat], dx, in_size, [dy], effort, expert_no=expert_no)
+    elif split:
         ctx.calc_dispatch(dx, ds, dp, expert_no, in_size, C, R, effort)
         ctx.mul(db, C, dy)
     else:
@@ -152,20 +158,52 @@ def _cutoff_patterns():
 
 
 @pytest.mark.parametrize("pattern", [p[0] for p in _cutoff_patterns()])
-def test_cutoff_edge_paths(O, ctx, pattern):
+def test_cutoff_edge_paths(O, iam, ctx, pattern):
     """The search's edge paths on the GPU, bit-exact against the oracle: the
-    standalone cutoff kernel (calc_dispatch), the walk's own search with
-    4-wave workgroups (full_mul, 256 outputs) and with 8-wave workgroups
-    (full_mul, the LM-head shape)."""
+    standalone cutoff kernel (calc_dispatch + mul), and the walk's own search
+    (iam_bucketmul_fused) with 4-wave workgroups (256 outputs) and with
+    8-wave workgroups (the LM-head shape)."""
     name, x, effort, (rounds, conv) = next(p for p in _cutoff_patterns() if p[0] == pattern)
     probes = np.full(4096, 0x2400, np.uint16)
     _, tr = O.find_cutoff(x, probes, O.effort_quantile(effort), trace=True)
     assert (tr.rounds, tr.converged) == (rounds, conv)     # the pattern takes the intended path
     b, s, _ = make_matrix(O, 256, 4096, tid=9)
     check_against_oracle(O, ctx, b, s, probes, x, effort, split=True)
-    check_against_oracle(O, ctx, b, s, probes, x, effort, split=False)
+    check_against_oracle(O, ctx, b, s, probes, x, effort, fused=iam)
     b, s, _ = make_matrix(O, 32000, 4096, tid=5)
-    check_against_oracle(O, ctx, b, s, probes, x, effort, split=False)
+    check_against_oracle(O, ctx, b, s, probes, x, effort, fused=iam)
+
+
+@pytest.mark.parametrize("in_dim", [4096, 8192])
+def test_fused_norm_input(O, iam, ctx, in_dim):
+    """iam_bucketmul_fused with a norm input: x = RMSNorm(h) * gain is the
+    oracle's bit for bit (inside the walk for 4096 inputs, a separate RMSNorm
+    launch for 8192); cutoff, rows and y match the oracle on that x; two
+    matrices share the input."""
+    rng = np.random.default_rng(in_dim)
+    h = rng.normal(0, 1.5, in_dim).astype(np.float32)
+    gain = O.gen_f16(3, 50, in_dim, 1.0, 0.01)
+    mats = [make_matrix(O, 256, in_dim, tid=60), make_matrix(O, 512, in_dim, tid=61)]
+    want_x = O.rmsnorm_gain(h, gain, 1e-5)
+    dh, dg, dx = ctx.upload(h), ctx.upload(gain), ctx.empty(max(in_dim, 4096), np.float32)
+    bufs, descs, ys = [], [], []
+    for b, s, p in mats:
+        db, ds, dp = ctx.upload(b), ctx.upload(s), ctx.upload(p)
+        bufs += [db, ds, dp]
+        descs.append(iam.BucketMatrix(db.ptr, ds.ptr, dp.ptr, b.shape[0], b.shape[1], 4, 3))
+        ys.append(ctx.empty(16 * b.shape[1], np.float32))
+    ctx.fused(descs, dx, in_dim, ys, 0.25, h=dh, gain=dg, eps=1e-5)
+    x = dx.read()[:in_dim]
+    assert np.array_equal(x.view(np.uint32), want_x.view(np.uint32))
+    for k, (b, s, p) in enumerate(mats):
+        cut, S = ctx.dispatch_info(k)
+        oy, ocut, omask, oS = O.bucketmul(x, s, p, b, 0.25, in_size=in_dim)
+        assert np.float32(cut).view(np.uint32) == np.float32(ocut).view(np.uint32)
+        assert S == oS and ctx.walk_count(k) == oS
+        d = ulps(ys[k].read(), oy)
+        assert d.max() <= 1 and np.count_nonzero(d) <= 2
+    for d in bufs + ys + [dh, dg, dx]:
+        d.free()
 
 
 @pytest.mark.parametrize("out_dim", [16, 32, 48, 64, 80, 2048 + 16])
