@@ -133,6 +133,89 @@ def cpu_baseline(iam, model, cfg, pos, effort, budget_s=12.0):
                       f"({t_lm * 1e3:.0f} ms), effort {effort}, scaled to {cfg['n_layers']} layers"}
 
 
+CONFIG1_COPIES = 40   # 40 x 32 MB of buckets: past the 256 MB Infinity Cache
+
+
+def run_config1(args, iam, ctx):
+    """Config 1 of the workload set (`--config1`): one 4096x4096 bucketMul at
+    effort 0.25, W ~ N(0, 0.02^2) bucketized on the GPU, x ~ N(0, 1), seed 0.
+    Timed as the decode step runs a matrix group (iam_bucketmul_fused: input,
+    cutoff, selection and walk in one launch, the reduce in a second) and as
+    the reference's calcDispatch + mul (multi: a cutoff launch, the walk, the
+    reduce).  CONFIG1_COPIES copies of the bucketized matrix are used in
+    turn, so none is in the Infinity Cache when it is read again; kernel
+    durations come from per-dispatch events.  Bytes per call:
+    2*S*C + 2*R + 4*in + 2*4096 + 4*m (selected rows, one stats value per row,
+    x, probes, y)."""
+    n = out_dim = in_dim = 4096
+    R, C = in_dim * 16, out_dim // 16
+    u16 = np.uint16
+    W = ctx.empty(n * n, u16)
+    ctx.gen_f16(0, 1, n * n, 0.0, 0.02, W)
+    x = ctx.empty(in_dim, np.float32)
+    ctx.gen_f32(0, 2, in_dim, 0.0, 1.0, x)
+    b0, s0, p0 = ctx.empty(R * C, u16), ctx.empty(R * 4, u16), ctx.empty(in_dim, u16)
+    ctx.bucketize(W, out_dim, in_dim, b0, s0, p0)
+    s3 = ctx.stats_compact(s0, R)
+    mats, bufs = [], [W, b0, s0, p0, s3]
+    for k in range(CONFIG1_COPIES):
+        b, st, pr = ctx.empty(R * C, u16), ctx.empty(R, u16), ctx.empty(in_dim, u16)
+        ctx.copy(b, b0, R * C * 2)
+        ctx.copy(st, s3, R * 2)
+        ctx.copy(pr, p0, in_dim * 2)
+        bufs += [b, st, pr]
+        mats.append(iam.BucketMatrix(b.ptr, st.ptr, pr.ptr, R, C, 1, 0))
+    y = ctx.empty(out_dim, np.float32)
+    reps = args.config1_reps
+    res = {}
+    for mode in ("fused", "multi"):
+        def call(m):
+            if mode == "fused":
+                ctx.fused([m], x, in_dim, [y], args.effort)
+            else:
+                ctx.multi([m], [x], [in_dim], [y], args.effort)
+        for m in mats:
+            call(m)
+        ctx.sync()
+        ctx.walk_counters(reset=True)
+        ctx.kernel_stats_reset()
+        ctx.profiling(True)
+        for r in range(reps):
+            call(mats[r % CONFIG1_COPIES])
+        ctx.sync()
+        ctx.profiling(False)
+        _, rows, _ = ctx.walk_counters(reset=True)
+        t_ms = 0.0
+        parts = {}
+        for name in ("bucket_cutoff", "bucket_walk", "bucket_reduce"):
+            ms, calls = ctx.kernel_stat(name)
+            if calls:
+                parts[name.split("_")[1] + "_us"] = round(ms / calls * 1e3, 2)
+                t_ms += ms / reps
+        S = rows / reps
+        B = 2 * S * C + 2 * R + 4 * in_dim + 2 * 4096 + 4 * out_dim
+        res[mode] = dict(time_us=round(t_ms * 1e3, 2), **parts, selected_rows=round(S),
+                         bytes_per_call=round(B), achieved_GBs=round(B / (t_ms * 1e-3) / 1e9, 1))
+        log(f"config 1, {mode}: {t_ms * 1e3:.2f} us per call ({parts}), S = {S:.0f}, "
+            f"{B / 1e6:.2f} MB -> {B / (t_ms * 1e-3) / 1e9:.0f} GB/s")
+    stream_gbs = ctx.read_bandwidth(2 << 30, 10)
+    for d in bufs + [x, y]:
+        d.free()
+    f = res["fused"]
+    out = {
+        "metric": "config 1: one 4096x4096 bucketMul at effort 0.25 (cutoff, selection, walk, reduce), "
+                  "achieved GB/s of the selected rows + stats + x + probes + y",
+        "value": f["achieved_GBs"], "unit": "GB/s", "n_gpus": 1, "steps": reps, "higher_is_better": True,
+        "dtype": "f64" if args.acc == "fp64" else "f32", "data": "synthetic (seed 0)",
+        "config": {"workload": "W 4096x4096 fp16 N(0, 0.02^2) in bucket layout, x 4096 fp32 N(0,1), "
+                               f"effort {args.effort}, {CONFIG1_COPIES} rotating copies of W"},
+        "frac": round(f["achieved_GBs"] / HBM_PEAK_GBS, 4),
+        "frac_of_stream": round(f["achieved_GBs"] / stream_gbs, 4), "stream_read_GBs": round(stream_gbs, 1),
+        "fused": res["fused"], "cutoff_launch": res["multi"],
+    }
+    print(json.dumps(out), flush=True)
+
+
 SKEW_EFFORTS = [0.05, 1.0]
 SKEW_SEQUENCES = 8
 
@@ -220,6 +303,9 @@ def main():
     ap.add_argument("--skew", action="store_true",
                     help="run the skew stress (efforts 0.05 and 1.0 at context 4096, 8 sequences) instead")
     ap.add_argument("--skew-steps", type=int, default=32, help="timed decode steps per sequence and effort")
+    ap.add_argument("--config1", action="store_true",
+                    help="time config 1 instead (one 4096x4096 bucketMul, rotating copies of W)")
+    ap.add_argument("--config1-reps", type=int, default=400, help="timed calls per mode of --config1")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
@@ -239,6 +325,10 @@ def main():
     ctx.set_accumulation(args.acc)
     if args.skew:
         run_skew(args, iam, ctx)
+        ctx.close()
+        return
+    if args.config1:
+        run_config1(args, iam, ctx)
         ctx.close()
         return
     use_graph = not args.eager
