@@ -6,14 +6,16 @@
 // Here, per group of up to 3 matrices that share an input:
 //   k_walk64    one launch (fp64 accumulation): workgroup (input slice p,
 //               128-column tile t) computes the RMSNorm of h when the input
-//               is a norm, runs the cutoff search itself (a pure function of
+//               is a norm of 4096 values (a wider one goes through the
+//               RMSNorm kernel first), runs the cutoff search itself (a pure function of
 //               x[0:4096] and the probes), selects the rows of its slice and
 //               walks them, adding each exact product x*w to its wave's LDS
 //               tile with fp64 atomics in a fixed order, and writes one
 //               partial row per slice.
 //   k_reduce    one launch: sums the slice partials in a fixed order and
 //               applies the consumer's epilogue (residual add, RoPE and the
-//               fp16 KV append, the SiLU gate, or a store).
+//               fp16 KV append, the SiLU gate, or a store); with walk
+//               counting on it also adds up the selected rows.
 // k_walk (fp32 accumulation, lane-private accumulators) follows k_cutoff;
 // k_cutoff and k_dispatch (one workgroup per matrix / per 256 inputs) serve
 // the standalone calls and the parity queries (cutoff, selected rows).
