@@ -190,17 +190,58 @@ __device__ __forceinline__ double readlane_t<double>(double v, int l)
     return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
 }
 
-// Merge of the na <= kMaxAttnSplits splits of query head h by one wave:
-// lane s holds split s's (m_s, l_s) and computes w_s = exp(m_s - M) with M
-// the maximum of the m_s; L = sum of l_s * w_s and O = sum of o_s * w_s in
-// split order, out = O / L; lane j writes dimensions 2j, 2j+1.  The o loads
-// go out in batches of 16 splits (1024 positions).
+// Merge of the na <= kMaxAttnSplits splits of query head h.  Every wave
+// that takes part loads all (m_s, l_s) (lane s holds splits s and s + 64)
+// and computes M, the maximum of the m_s, and w_s = exp(m_s - M); a wave
+// sums l_s * w_s and o_s * w_s over a contiguous range of splits in split
+// order, 16 o loads in flight at a time; out = O / L, lane j writing
+// dimensions 2j, 2j+1.  Up to 16 splits (1024 positions) wave 0 takes them
+// all in one batch and the other waves return; beyond that each of the
+// kCombWaves waves takes a contiguous share and the shares are added in wave
+// order, so the o loads of a long context go out at once instead of in
+// sequential batches.
+constexpr int kCombWaves = 4;
+constexpr int kCombBatch = 16;
+
+template <typename Acc>
+__device__ __forceinline__ void combine_range(const Acc* __restrict__ base, int sb, int se, const Acc (&wv)[2],
+                                              const Acc (&lv)[2], Acc& L, Acc& O0, Acc& O1)
+{
+    constexpr int HD = 128, B = kCombBatch;
+    const int lane = threadIdx.x & 63;
+    L = O0 = O1 = (Acc)0;
+    for (int s0 = sb; s0 < se; s0 += B) {
+        Acc o0[B], o1[B];
+#pragma unroll
+        for (int i = 0; i < B; i++) {
+            const Acc* row = base + (size_t)min(s0 + i, se - 1) * (HD + 2);
+            o0[i] = row[2 * lane];
+            o1[i] = row[2 * lane + 1];
+        }
+#pragma unroll
+        for (int i = 0; i < B; i++) {
+            const int s = s0 + i;
+            if (s < se) {
+                const Acc w = readlane_t(s < 64 ? wv[0] : wv[1], s & 63);
+                L += readlane_t(s < 64 ? lv[0] : lv[1], s & 63) * w;
+                O0 += o0[i] * w;
+                O1 += o1[i] * w;
+            }
+        }
+    }
+}
+
 template <typename Acc>
 __device__ void combine_head(const Acc* __restrict__ ws, int h, int n_split, int na, float* __restrict__ out)
 {
-    constexpr int HD = 128, B = 16;
+    constexpr int HD = 128;
     static_assert(kMaxAttnSplits <= 128, "two splits per lane");
+    __shared__ Acc sO[kCombWaves][HD];
+    __shared__ Acc sL[kCombWaves];
     const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const bool one = na <= kCombBatch;   // uniform over the workgroup
+    if (one && wave != 0) return;
     const Acc* base = ws + (size_t)h * n_split * (HD + 2);
     Acc mv[2], lv[2];
 #pragma unroll
@@ -213,28 +254,31 @@ __device__ void combine_head(const Acc* __restrict__ ws, int h, int n_split, int
     Acc wv[2];
 #pragma unroll
     for (int k = 0; k < 2; k++) wv[k] = lane + 64 * k < na ? acc_exp<Acc>(mv[k] - M) : (Acc)0;
-    Acc L = (Acc)0, O0 = (Acc)0, O1 = (Acc)0;
-    for (int s0 = 0; s0 < na; s0 += B) {
-        Acc o0[B], o1[B];
-#pragma unroll
-        for (int i = 0; i < B; i++) {
-            const Acc* row = base + (size_t)min(s0 + i, na - 1) * (HD + 2);
-            o0[i] = row[2 * lane];
-            o1[i] = row[2 * lane + 1];
-        }
-#pragma unroll
-        for (int i = 0; i < B; i++) {
-            const int s = s0 + i;
-            if (s < na) {
-                const Acc w = readlane_t(s < 64 ? wv[0] : wv[1], s & 63);
-                L += readlane_t(s < 64 ? lv[0] : lv[1], s & 63) * w;
-                O0 += o0[i] * w;
-                O1 += o1[i] * w;
-            }
-        }
+    Acc L, O0, O1;
+    if (one) {
+        combine_range<Acc>(base, 0, na, wv, lv, L, O0, O1);
+        out[h * HD + 2 * lane] = (float)(O0 / L);
+        out[h * HD + 2 * lane + 1] = (float)(O1 / L);
+        return;
     }
-    out[h * HD + 2 * lane] = (float)(O0 / L);
-    out[h * HD + 2 * lane + 1] = (float)(O1 / L);
+    const int per = (na + kCombWaves - 1) / kCombWaves;
+    const int sb = wave * per;
+    combine_range<Acc>(base, sb, min(na, sb + per), wv, lv, L, O0, O1);
+    sO[wave][2 * lane] = O0;
+    sO[wave][2 * lane + 1] = O1;
+    if (lane == 0) sL[wave] = L;
+    __syncthreads();
+    if (wave == 0) {
+        Acc Lt = sL[0], Ot0 = sO[0][2 * lane], Ot1 = sO[0][2 * lane + 1];
+#pragma unroll
+        for (int w = 1; w < kCombWaves; w++) {
+            Lt += sL[w];
+            Ot0 += sO[w][2 * lane];
+            Ot1 += sO[w][2 * lane + 1];
+        }
+        out[h * HD + 2 * lane] = (float)(Ot0 / Lt);
+        out[h * HD + 2 * lane + 1] = (float)(Ot1 / Lt);
+    }
 }
 
 // LDS copies of the split's K and V rows: 128 fp16 + 8 fp16 of padding, so
@@ -355,7 +399,7 @@ __global__ __launch_bounds__(128 * kAttnMaxRep) void k_attn_partial(const float*
 
 // Merge of the splits: one wave per query head.
 template <typename Acc>
-__global__ __launch_bounds__(64) void k_attn_combine(const Acc* __restrict__ ws, const int* __restrict__ pos_p,
+__global__ __launch_bounds__(64 * kCombWaves) void k_attn_combine(const Acc* __restrict__ ws, const int* __restrict__ pos_p,
                                                     int max_ctx, int n_split, float* __restrict__ out)
 {
     int n_tok = *pos_p + 1;
@@ -484,13 +528,13 @@ int attention(Ctx* c, const float* q, const uint16_t* kc, const uint16_t* vc, co
         const double scale = 1.0 / std::sqrt(128.0);
         IAM_TRY(launch(c, "attn_partial", k_attn_partial<double>, dim3(n_kv, n_split), dim3(128 * (n_heads / n_kv)),
                        0, q, kc, vc, pos, n_heads, n_kv, max_ctx, scale, (double*)ws, n_split));
-        return launch(c, "attn_combine", k_attn_combine<double>, dim3(n_heads), dim3(64), 0, (const double*)ws, pos,
+        return launch(c, "attn_combine", k_attn_combine<double>, dim3(n_heads), dim3(64 * kCombWaves), 0, (const double*)ws, pos,
                       max_ctx, n_split, out);
     }
     const float scale = 1.0f / std::sqrt(128.0f);
     IAM_TRY(launch(c, "attn_partial", k_attn_partial<float>, dim3(n_kv, n_split), dim3(128 * (n_heads / n_kv)), 0, q,
                    kc, vc, pos, n_heads, n_kv, max_ctx, scale, ws, n_split));
-    return launch(c, "attn_combine", k_attn_combine<float>, dim3(n_heads), dim3(64), 0, (const float*)ws, pos,
+    return launch(c, "attn_combine", k_attn_combine<float>, dim3(n_heads), dim3(64 * kCombWaves), 0, (const float*)ws, pos,
                   max_ctx, n_split, out);
 }
 
