@@ -246,7 +246,7 @@ def run_skew(args, iam, ctx):
             scale = np.ones(cfg["dim"], np.float32)
             scale[rng.choice(cfg["dim"], cfg["dim"] // 100, replace=False)] = 20.0
             model.set_embed_scale(scale)
-            model.write_tensor("pos", np.array([start], np.int32))
+            model.set_position(start)
             model.write_tensor("token", np.array([int(rng.integers(0, cfg["vocab"]))], np.int32))
             ctx.set_walk_counting(False)
             model.decode(SWEEP_WARMUP, e)

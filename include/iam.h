@@ -291,6 +291,10 @@ int iam_model_generate(iam_model* m, const int* prompt, int n_prompt, int n_new,
  * by the previous step at the current position) for n_steps steps, replaying
  * the captured step when use_graph is set.  Asynchronous. */
 int iam_model_decode(iam_model* m, int n_steps, float effort, int use_graph);
+/* Set the device position the next step computes (0 <= pos <= max_ctx).
+ * decode and step_device refuse steps past the KV capacity, counted from
+ * this position (or from forward / generate / reset_caches). */
+int iam_model_set_position(iam_model* m, int pos);
 /* MistralModel::reset_caches (model.hpp:233-237); also rewinds the position. */
 int iam_model_reset_caches(iam_model* m);
 /* Per-channel fp32 factors applied to the gathered embedding before the

@@ -3,27 +3,27 @@
 // Reference pipeline (bucket_mul.hpp:147-267, bucketMul.cl):
 //   findCutoffBinarySearch -> prepareDispatch -> roundUp/zeroRange32 ->
 //   bucketMul -> bucketIntegrate                      (6 launches + 1 fill)
-// Here, per group of up to 3 matrices that share an input:
-//   k_walk64    one launch (fp64 accumulation): workgroup (input slice p,
-//               128-column tile t) computes the RMSNorm of h when the input
-//               is a norm of 4096 values (a wider one goes through the
-//               RMSNorm kernel first), runs the cutoff search itself (a pure function of
-//               x[0:4096] and the probes), selects the rows of its slice and
-//               walks them, adding each exact product x*w to its wave's LDS
-//               tile with fp64 atomics in a fixed order, and writes one
-//               partial row per slice.
-//   k_reduce    one launch: sums the slice partials in a fixed order and
-//               applies the consumer's epilogue (residual add, RoPE and the
-//               fp16 KV append, the SiLU gate, or a store); with walk
-//               counting on it also adds up the selected rows.
-// k_walk (fp32 accumulation, lane-private accumulators) follows k_cutoff;
-// k_cutoff and k_dispatch (one workgroup per matrix / per 256 inputs) serve
-// the standalone calls and the parity queries (cutoff, selected rows).
-// The cutoff and selection arithmetic is exact IEEE fp32 (no contraction), so
-// the cutoff bits and the selected set equal the oracle's.  With fp64
-// accumulation (the product of an fp32 input and an fp16 weight is exact in
-// fp64) y is the correctly rounded sum up to fp64 rounding, and the fixed
-// order makes it the same on every run.
+// Here one launch per group of up to 3 matrices that share an input
+// (k_walk): workgroup (input slice p, 64-column tile t) computes the input
+// itself when it is a norm, a residual sum, an embedding row or an attention
+// output, runs the cutoff search (a pure function of x[0:4096] and the
+// probes, search.h), selects the rows of its slice and walks them, adding
+// each product x*w to its wave's LDS tile; the tiles are then added in wave
+// order and flushed with one global atomic add per output into an
+// accumulator that starts at zero.  The accumulator is read either by the
+// next launch of the decode step (which applies the residual add, RoPE or
+// the attention normalisation itself) or, in the finalize modes, by the
+// last workgroup to flush each column tile: it takes the sums (clearing the
+// accumulator for the next call) and stores fp32 outputs, the SiLU gate, or
+// the logits and the greedy pick.  k_cutoff serves the split calcDispatch /
+// mul calls and k_dispatch the parity queries (cutoff, selected rows).
+//
+// The cutoff and selection arithmetic is exact IEEE fp32 (no contraction),
+// so the cutoff bits and the selected set equal the oracle's.  With fp64
+// accumulation the product of an fp32 input and an fp16 weight is exact, so
+// each output is the sum of exact products rounded once at the end; only the
+// order of the fp64 additions (atomics from the workgroups) varies, far
+// below an fp32 ulp.
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
@@ -31,37 +31,20 @@
 #include <cstring>
 #include <vector>
 
+#include "accum.h"
 #include "internal.h"
 #include "layer_ops.h"
+#include "search.h"
 #include "wave.h"
 
 namespace iam {
 
 constexpr float kScale = 100000.0f;   // bucketMul.cl:17
-constexpr int kCutThreads = 256;
-constexpr int kCutVPT = kProbes / kCutThreads;   // 16 importances per thread
 
 __device__ __forceinline__ float h2f(uint32_t bits16)
 {
     return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xffffu)));
 }
-
-// --------------------------------------------------------------- cutoff ---
-// A wave-uniform float kept in a scalar register.
-__device__ __forceinline__ float uniform_f(float v)
-{
-    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
-}
-
-// The search's bounds are midpoints inside the current bracket (minB,
-// maxB], so once the bracket holds few importances, count(imp > b) =
-// count(imp > maxB) + #(bracket values > b).  The rounds run on the whole
-// workgroup (one count exchange per round) until the bracket holds at most
-// kCandCap values by its counts (minCount - maxCount bounds them); those are
-// then compacted to LDS, and every wave finishes the rounds on them by itself
-// with no barriers.  The tested bounds, counts and stop decisions are the
-// reference's exactly.
-constexpr int kCandCap = 256;   // 4 per lane of one wave
 
 // The 16 probes of thread tid (probes[16*tid ..]).
 __device__ __forceinline__ void load_probes(const uint16_t* __restrict__ probes, uint4 (&pr)[2])
@@ -69,137 +52,6 @@ __device__ __forceinline__ void load_probes(const uint16_t* __restrict__ probes,
     const uint4* pv = reinterpret_cast<const uint4*>(probes + threadIdx.x * kCutVPT);
     pr[0] = pv[0];
     pr[1] = pv[1];
-}
-
-// xs holds x[16*tid .. 16*tid + 16) and pr the thread's probes for the
-// first kCutThreads threads; a block of NWV > 4 waves runs the same code and
-// its other threads hold no importances (NaN: never counted, ignored by the
-// min and max).  Scratch: s_red >= 2*NWV floats, s_cnt >= 3*NWV ints,
-// s_cand kCandCap floats.  Every thread returns the cutoff; a later writer of
-// the scratch must pass a barrier first (the waves read s_cand after the
-// last barrier here).
-template <int NWV = 4>
-__device__ __forceinline__ float block_cutoff_x(const float (&xs)[kCutVPT], const uint4 (&pr)[2], int quantile,
-                                                float* s_red, int* s_cnt, float* s_cand)
-{
-#pragma clang fp contract(off)
-    static_assert(NWV % 4 == 0, "4 or 8 waves");
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    float v[kCutVPT];
-    {
-        const uint4 pa = pr[0], pb = pr[1];
-        uint32_t ps[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
-#pragma unroll
-        for (int k = 0; k < 16; k++) {
-            float p = h2f(ps[k >> 1] >> ((k & 1) * 16));
-            float prod = __fmul_rn(xs[k], p);
-            v[k] = __fmul_rn(kScale, fabsf(prod));   // bucketMul.cl:110
-            if (NWV > 4 && tid >= kCutThreads) v[k] = __int_as_float(0x7fc00000);
-        }
-    }
-    float mn = 1e30f, mx = -1e30f;                    // bucketMul.cl:98-99
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
-        mn = fminf(mn, v[k]);
-        mx = fmaxf(mx, v[k]);
-    }
-    mn = wave_min(mn);
-    mx = wave_max(mx);
-    if (lane == 0) {
-        s_red[wave] = mn;
-        s_red[NWV + wave] = mx;
-    }
-    __syncthreads();
-    // the search state is uniform: keep it in scalar registers
-    float gmin = 1e30f, gmax = -1e30f;
-#pragma unroll
-    for (int w4 = 0; w4 < NWV; w4 += 4) {
-        const float4 mn4 = *reinterpret_cast<const float4*>(s_red + w4);
-        const float4 mx4 = *reinterpret_cast<const float4*>(s_red + NWV + w4);
-        gmin = fminf(gmin, fminf(fminf(mn4.x, mn4.y), fminf(mn4.z, mn4.w)));
-        gmax = fmaxf(gmax, fmaxf(fmaxf(mx4.x, mx4.y), fmaxf(mx4.z, mx4.w)));
-    }
-    gmin = uniform_f(gmin);
-    gmax = uniform_f(gmax);
-
-    const int target = kProbes - quantile;            // bucketMul.cl:81
-    float minB = gmin, maxB = gmax;
-    float bound = uniform_f(__fmul_rn(__fadd_rn(gmin, gmax), 0.5f));
-    int minC = kProbes, maxC = 0;
-    // one round of bucketMul.cl:178-200 given the count at bound; true = stop
-    auto round = [&](int count) -> bool {
-        if (count < target) {                          // bucketMul.cl:178-186
-            maxB = bound;
-            maxC = count;
-        } else {
-            minB = bound;
-            minC = count;
-        }
-        const float next = uniform_f(__fmul_rn(__fadd_rn(minB, maxB), 0.5f));
-        const int gap = maxC - minC;
-        if (count == target || __fsub_rn(maxB, minB) < 0.00001f || (gap < 0 ? -gap : gap) < 3)
-            return true;                               // bucketMul.cl:195-200: the tested bound
-        bound = next;
-        return false;
-    };
-    int loop = 0;
-    for (; loop < 20; loop++) {
-        if (minC - maxC <= kCandCap) break;
-        int c = 0;
-#pragma unroll
-        for (int k = 0; k < 16; k++) c += __popcll(__ballot(v[k] > bound));
-        if (lane == 0) s_cnt[(loop & 1) * NWV + wave] = c;
-        __syncthreads();
-        int tot = 0;
-#pragma unroll
-        for (int w4 = 0; w4 < NWV; w4 += 4) {
-            const int4 q4 = *reinterpret_cast<const int4*>(s_cnt + (loop & 1) * NWV + w4);
-            tot += q4.x + q4.y + q4.z + q4.w;
-        }
-        if (round(__builtin_amdgcn_readfirstlane(tot))) return bound;
-    }
-    if (loop == 20) return bound;                      // bucketMul.cl:211-213: the untested midpoint
-
-    // compact the bracket values (minB, maxB] to s_cand (the count only
-    // needs the set, so the order is per wave, then by k, then by lane)
-    uint64_t bm[16];
-    int wtot = 0;
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
-        bm[k] = __ballot(v[k] > minB && v[k] <= maxB);
-        wtot += __popcll(bm[k]);
-    }
-    if (lane == 0) s_cnt[2 * NWV + wave] = wtot;
-    __syncthreads();
-    int off = 0, ncand = 0;   // ncand <= minC - maxC <= kCandCap
-#pragma unroll
-    for (int w2 = 0; w2 < NWV; w2++) {
-        const int c2 = s_cnt[2 * NWV + w2];
-        if (w2 < wave) off += c2;
-        ncand += c2;
-    }
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
-        if ((bm[k] >> lane) & 1ull) s_cand[off + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bm[k] >> 32),
-                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)bm[k], 0u))] = v[k];
-        off += __popcll(bm[k]);
-    }
-    __syncthreads();
-    // every wave finishes the rounds on the compacted values by itself
-    float cv[kCandCap / 64];
-#pragma unroll
-    for (int j = 0; j < kCandCap / 64; j++) cv[j] = lane + 64 * j < ncand ? s_cand[lane + 64 * j] : -INFINITY;
-    const int c0 = maxC;                               // count(imp > maxB) at the compaction
-    bool done = false;
-    for (; loop < 20 && !done; loop++) {
-        int c = c0;
-#pragma unroll
-        for (int j = 0; j < kCandCap / 64; j++) c += __popcll(__ballot(cv[j] > bound));
-        done = round(c);
-    }
-    return bound;
 }
 
 __device__ __forceinline__ void load16(const float* __restrict__ x, float (&xs)[kCutVPT])
@@ -215,40 +67,49 @@ __device__ __forceinline__ void load16(const float* __restrict__ x, float (&xs)[
     }
 }
 
-__device__ float block_cutoff(const float* __restrict__ x, const uint16_t* __restrict__ probes,
-                              int quantile, float* s_red, int* s_cnt, float* s_cand)
+__device__ __forceinline__ void load16_acc(const double* __restrict__ p, double (&v)[kCutVPT])
 {
-    float xs[kCutVPT];
-    uint4 pr[2];
-    load_probes(probes, pr);
-    load16(x, xs);
-    return block_cutoff_x(xs, pr, quantile, s_red, s_cnt, s_cand);
+    const double2* pv = reinterpret_cast<const double2*>(p + threadIdx.x * kCutVPT);
+#pragma unroll
+    for (int k = 0; k < kCutVPT / 2; k++) {
+        const double2 a = pv[k];
+        v[2 * k] = a.x;
+        v[2 * k + 1] = a.y;
+    }
 }
 
-// rmsNorm32fast (aux.cl:156-196) of a 4096-vector by one 256-thread
-// workgroup, in the reference's fp32 order: 16 consecutive squares per
-// thread summed in order, then the 256-way tree (pairs tid, tid + st for st =
-// 128 .. 1: the thread sums through LDS, then the tree by every wave on its
-// own), scale = 1/sqrt(sum/4096 + eps) rounded from double, then the fp16 gain
-// (mul16x32, aux.cl:434-440).  v holds h[16*tid ..] on entry and the
-// normalized values on exit; gr the thread's 16 gains (gain[16*tid ..]).
-// s_part: kCutThreads floats of scratch that nothing writes again before a
-// later barrier (each wave reads it after the one barrier here).
+// imp = 1e5 * |x * probe| (bucketMul.cl:101-117) of thread tid's 16 inputs
+__device__ __forceinline__ void importances(const float (&xs)[kCutVPT], const uint4 (&pr)[2], float (&v)[kCutVPT])
+{
+#pragma clang fp contract(off)
+    const uint32_t ps[8] = {pr[0].x, pr[0].y, pr[0].z, pr[0].w, pr[1].x, pr[1].y, pr[1].z, pr[1].w};
+#pragma unroll
+    for (int k = 0; k < kCutVPT; k++) {
+        const float p = h2f(ps[k >> 1] >> ((k & 1) * 16));
+        v[k] = __fmul_rn(kScale, fabsf(__fmul_rn(xs[k], p)));
+    }
+}
+
+// rmsNorm32fast (aux.cl:156-196) of a 4096-vector by one workgroup, in the
+// reference's fp32 order: 16 consecutive squares per thread summed in order,
+// then the 256-way tree (pairs tid, tid + st for st = 128 .. 1: the partial
+// sums go through LDS, then every wave runs the tree on its own), scale =
+// 1/sqrt(sum/4096 + eps) rounded from double, then the fp16 gain (mul16x32,
+// aux.cl:434-440).  v holds h[16*tid ..] on entry (first 256 threads) and
+// the normalized values on exit; gr the thread's 16 gains.  s_part: 256
+// floats of scratch nothing writes again before a later barrier.
 __device__ __forceinline__ void block_rmsnorm4096(float (&v)[kCutVPT], const uint4 (&gr)[2], float eps, float* s_part)
 {
 #pragma clang fp contract(off)
     const int tid = threadIdx.x;
-    const uint4 g0 = gr[0], g1 = gr[1];
     float sq = 0.0f;
 #pragma unroll
     for (int k = 0; k < kCutVPT; k++) sq = __fadd_rn(sq, __fmul_rn(v[k], v[k]));
     if (tid < kCutThreads) s_part[tid] = sq;
     __syncthreads();
-    // every wave runs the tree itself (no second barrier): lane l takes
-    // part[l] + part[l+128] and part[l+64] + part[l+192] (st = 128), their
-    // sum (st = 64), then st = 32, 16 as shuffles and st = 8 .. 1 within
-    // 16-lane rows by DPP row_shl (lane l takes lane l + st); lane 0 holds
-    // the total
+    // lane l takes part[l] + part[l+128] and part[l+64] + part[l+192]
+    // (st = 128), their sum (st = 64), then st = 32, 16 as shuffles and
+    // st = 8 .. 1 within 16-lane rows by DPP row_shl; lane 0 holds the total
     const int lane = tid & 63;
     const float a = __fadd_rn(s_part[lane], s_part[lane + 128]);
     const float b = __fadd_rn(s_part[lane + 64], s_part[lane + 192]);
@@ -262,10 +123,9 @@ __device__ __forceinline__ void block_rmsnorm4096(float (&v)[kCutVPT], const uin
     const float total = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sq)));
     const float mean = __fdiv_rn(total, 4096.0f);
     const float scale = (float)(1.0 / sqrt((double)__fadd_rn(mean, eps)));
-    const uint32_t gw[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    const uint32_t gw[8] = {gr[0].x, gr[0].y, gr[0].z, gr[0].w, gr[1].x, gr[1].y, gr[1].z, gr[1].w};
 #pragma unroll
-    for (int k = 0; k < kCutVPT; k++)
-        v[k] = __fmul_rn(h2f(gw[k >> 1] >> ((k & 1) * 16)), __fmul_rn(v[k], scale));
+    for (int k = 0; k < kCutVPT; k++) v[k] = __fmul_rn(h2f(gw[k >> 1] >> ((k & 1) * 16)), __fmul_rn(v[k], scale));
 }
 
 // --------------------------------------------------------------- cutoff ---
@@ -282,17 +142,28 @@ struct CutoffArgs {
     int n;
 };
 
+__device__ __forceinline__ float block_cutoff(const float* __restrict__ x, const uint16_t* __restrict__ probes,
+                                              int quantile, SearchLds<4>& L)
+{
+    float xs[kCutVPT], v[kCutVPT];
+    uint4 pr[2];
+    load_probes(probes, pr);
+    load16(x, xs);
+    importances(xs, pr, v);
+    return search_cutoff<4>(v, quantile, L);
+}
+
 __global__ __launch_bounds__(kCutThreads) void k_cutoff(CutoffArgs a)
 {
-    __shared__ __align__(16) float s_red[16];
-    __shared__ __align__(16) int s_cnt[16];
-    __shared__ float s_cand[kCandCap];
+    __shared__ SearchLds<4> L;
     const CutoffDesc& d = a.d[blockIdx.x];
-    const float cut = block_cutoff(d.x, d.probes, d.quantile, s_red, s_cnt, s_cand);
+    const float cut = block_cutoff(d.x, d.probes, d.quantile, L);
     if (threadIdx.x == 0) d.cutoff[0] = cut;
 }
 
 // ------------------------------------------------------------- dispatch ---
+// The selected-row list of the parity queries: prepareDispatch
+// (bucketMul.cl:351-386) per chunk of 256 inputs, rows in ascending order.
 struct DispatchDesc {
     const float* x;
     const uint16_t* probes;   // already offset to the expert
@@ -306,86 +177,43 @@ struct DispatchDesc {
     uint2* list;
     uint32_t* counts;
     float* cutoff;
-    int block_base;
 };
 
-struct DispatchArgs {
-    DispatchDesc d[kMaxMulti];
-    int n;
-};
-
-__global__ __launch_bounds__(kCutThreads) void k_dispatch(DispatchArgs a)
+__global__ __launch_bounds__(kCutThreads) void k_dispatch(DispatchDesc d)
 {
 #pragma clang fp contract(off)
-    __shared__ __align__(16) float s_red[16];
-    __shared__ __align__(16) int s_cnt[16];
-    __shared__ float s_cand[kCandCap];
+    __shared__ SearchLds<4> L;
     __shared__ int s_wsum[4];
-
-    int k = 0;
-    for (int i = 1; i < a.n; i++)
-        if ((int)blockIdx.x >= a.d[i].block_base) k = i;
-    const DispatchDesc& d = a.d[k];
-    const int g = (int)blockIdx.x - d.block_base;
+    const int g = (int)blockIdx.x;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
 
-    const float cutoff = block_cutoff(d.x, d.probes, d.quantile, s_red, s_cnt, s_cand);
-    if (g == 0 && tid == 0) d.cutoff[1] = cutoff;   // cross-checked against k_cutoff's cutoff[0]
+    const float cutoff = block_cutoff(d.x, d.probes, d.quantile, L);
+    if (g == 0 && tid == 0) d.cutoff[1] = cutoff;   // cross-checked against the search launch's cutoff[0]
 
-    // prepareDispatch (bucketMul.cl:362-385) for the 16 rows of input i
     const int i = g * kChunkInputs + tid;
     const int r0 = i * 16;
     uint32_t mask = 0;
     float xi = 0.0f;
     if (i < d.in_size && r0 < d.rows) {
         xi = d.x[i];
-        // the 16 stats of this input, all loads issued before any use
         uint32_t sv[16];
         const uint16_t* st = d.stats + (size_t)r0 * d.stats_stride;
-        const bool whole = r0 + 16 <= d.rows;
-        if (whole && d.stats_stride == 1 && (((uintptr_t)st) & 15) == 0) {
-            const uint4* p4 = reinterpret_cast<const uint4*>(st);
-            const uint4 a0 = p4[0], a1 = p4[1];
-            const uint32_t w[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
 #pragma unroll
-            for (int kk = 0; kk < 16; kk++) sv[kk] = (w[kk >> 1] >> ((kk & 1) * 16)) & 0xffffu;
-        } else if (whole && d.stats_stride == 4 && d.stats_channel == 3 && (((uintptr_t)st) & 15) == 0) {
-            // reference layout: 4 equal channels per row, channel 3 read
-            const uint4* p4 = reinterpret_cast<const uint4*>(st);
-            uint4 a[8];
-#pragma unroll
-            for (int k8 = 0; k8 < 8; k8++) a[k8] = p4[k8];
-#pragma unroll
-            for (int k8 = 0; k8 < 8; k8++) {
-                sv[2 * k8] = a[k8].y >> 16;       // row 2*k8, channel 3
-                sv[2 * k8 + 1] = a[k8].w >> 16;   // row 2*k8+1, channel 3
-            }
-        } else {
-#pragma unroll
-            for (int kk = 0; kk < 16; kk++) {
-                const int rr = min(r0 + kk, d.rows - 1) - r0;
-                sv[kk] = st[(size_t)rr * d.stats_stride + d.stats_channel];
-            }
+        for (int kk = 0; kk < 16; kk++) {
+            const int rr = min(r0 + kk, d.rows - 1) - r0;
+            sv[kk] = st[(size_t)rr * d.stats_stride + d.stats_channel];
         }
 #pragma unroll
         for (int kk = 0; kk < 16; kk++) {
-            float avg = h2f(sv[kk]);
-            float prod = __fmul_rn(xi, avg);
-            float imp = __fmul_rn(kScale, fabsf(prod));
+            const float prod = __fmul_rn(xi, h2f(sv[kk]));
+            const float imp = __fmul_rn(kScale, fabsf(prod));
             if (imp >= cutoff && r0 + kk < d.rows) mask |= 1u << kk;   // bucketMul.cl:380
         }
     }
-    // ordered compaction: block exclusive scan of the per-thread counts
     const int cnt = __popc(mask);
-    int incl = cnt;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        int t = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += t;
-    }
-    __syncthreads();   // s_cnt/s_red reads of the search are done
+    const int incl = wave_incl_sum(cnt);
     if (lane == 63) s_wsum[wave] = incl;
     __syncthreads();
     int woff = 0;
@@ -394,7 +222,7 @@ __global__ __launch_bounds__(kCutThreads) void k_dispatch(DispatchArgs a)
     uint2* out = d.list + (size_t)g * kChunkRows + (woff + incl - cnt);
     const uint32_t xb = __float_as_uint(xi);
     while (mask) {
-        int kk = __ffs(mask) - 1;
+        const int kk = __ffs(mask) - 1;
         mask &= mask - 1;
         *out++ = make_uint2((uint32_t)(r0 + kk), xb);
     }
@@ -404,8 +232,8 @@ __global__ __launch_bounds__(kCutThreads) void k_dispatch(DispatchArgs a)
 // ----------------------------------------------------------------- walk ---
 // Blocks are dealt to the 8 XCDs round robin (block b -> XCD b % 8).  Remap
 // so that consecutive work items (the column tiles of one row slice, which
-// share 128-byte lines at misaligned row starts) land on the same XCD and so
-// share its L2.
+// read the same stats, inputs and neighbouring lines of the same rows) land
+// on the same XCD and share its L2.
 __device__ __forceinline__ int xcd_remap(int b, int nblocks)
 {
     const int q = nblocks >> 3, r = nblocks & 7;
@@ -413,75 +241,36 @@ __device__ __forceinline__ int xcd_remap(int b, int nblocks)
     return xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
 }
 
-template <int VEC>
-struct VecLoad;
-template <>
-struct VecLoad<4> {
-    using T = uint2;
-    __device__ static void split(const T& v, uint32_t* w) { w[0] = v.x; w[1] = v.y; }
-};
-template <>
-struct VecLoad<2> {
-    using T = uint32_t;
-    __device__ static void split(const T& v, uint32_t* w) { w[0] = v; }
-};
-template <>
-struct VecLoad<1> {
-    using T = uint16_t;
-    __device__ static void split(const T& v, uint32_t* w) { w[0] = v; }
-};
-
-// acc + x * w in the accumulator type: an fp32 product added in fp32
-// (bucketMul.cl:430-434), or in fp64, where the product of an fp32 x and an
-// fp16 w is exact (24 + 11 significant bits fit in 53).
-template <typename Acc>
-__device__ __forceinline__ Acc walk_acc(Acc x, Acc w, Acc old);
-template <>
-__device__ __forceinline__ float walk_acc<float>(float x, float w, float old)
+// LDS addresses as 32-bit byte offsets (a generic pointer into LDS makes the
+// compiler form every slot address with a 64-bit multiply-add)
+template <typename T>
+using lds_ptr = __attribute__((address_space(3))) T*;
+template <typename T>
+__device__ __forceinline__ uint32_t lds_offset(T* p)
 {
-    return __fadd_rn(old, __fmul_rn(x, w));   // bucketMul.cl:430-434: fp32 product, then the add
+    return (uint32_t)(uintptr_t)(lds_ptr<T>)p;
 }
-template <>
-__device__ __forceinline__ double walk_acc<double>(double x, double w, double old)
+template <typename T>
+__device__ __forceinline__ void lds_add(uint32_t byte_offset, int elem, T v)
 {
-    return fma(x, w, old);   // the product is exact in fp64, so this is one rounded add
+    __hip_atomic_fetch_add((lds_ptr<T>)(uintptr_t)byte_offset + elem, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// Selection + walk.  Workgroup (input slice p, column tile t) owns the
-// inputs [p*IPS, (p+1)*IPS) and the 64 columns of tile t.
-//
-// Selection (prepareDispatch, bucketMul.cl:351-386): thread i takes input
-// p*IPS + i, loads its x and the stats of its 16 rows, and marks the rows
-// with 1e5 * |x * stat| >= cutoff -- the same fp32 operations as the
-// dispatch kernel, so the selected set is the same.  A block scan compacts
-// the selected rows in ascending order into LDS.
-//
-// Walk: lane = q*NJ + j: j picks VEC consecutive columns (NJ = 64/VEC lanes
-// cover the 128-byte tile segment of one row), q one of NQ = VEC rows read
-// by the same instruction.  Every lane owns private accumulators for its VEC
-// columns x 16 output positions at acc[wave][(pos*VEC + e)*64 + lane]: the
-// scatter of a packed weight to its position (bucketMul.cl:430-445) is a
-// plain LDS read-add-write, with no atomics, and the 64 lanes of one access
-// fall in 64 different banks.  Each lane adds its rows in order and the
-// flush sums waves and row slots in a fixed order, so the result does not
-// depend on scheduling.  The VEC elements of one row go to distinct
-// addresses (different e), so their reads are issued together, then their
-// writes; the next row's reads follow in the wave's LDS order.  All UNR
-// weight loads of a batch are unconditional (past the end a lane re-reads
-// the last selected row with x = 0), so they are in flight together.
+constexpr int kTileCols = 128;
+constexpr int kTileOut = kTileCols * 16;     // outputs per column tile
+constexpr int kTilePitch = kTileCols + 1;    // LDS slots per position row (one pad)
+
 struct WalkDesc {
     const uint16_t* W;        // rows of the expert: W[row * C + col]
-    float* x;
+    float* x;                 // the input (kInX/kInCutoff) or where block 0 stores the computed one
     const uint16_t* stats;    // row 0 of the expert
+    const uint16_t* probes;   // probes of the expert
     float* cutoff;
-    uint32_t* slice_count;    // [P]: rows selected per slice (tile-0 workgroups)
-    void* part;               // [P][16*C] partial sums (Acc), one row per slice
-    const float* h;           // kInNorm: the vector to normalize
-    const uint16_t* gain;     // kInNorm: fp16 gain
-    const uint16_t* probes;   // kInX / kInNorm: probes of the expert
-    float eps;
+    uint32_t* slice_count;    // [P]: rows selected per slice (written by the tile-0 workgroups)
+    void* acc;                // [16*C] accumulators
+    float* y;                 // kFinStore: outputs; kFinSilu: gate / up values (may be null)
+    uint32_t* tile_ctr;       // [T] arrival counters (finalize modes)
     int quantile;
-    int in_mode;              // WalkIn
     int stats_stride;
     int stats_channel;
     int rows;                 // R
@@ -491,19 +280,46 @@ struct WalkDesc {
     int P;                    // slices
     int T;                    // column tiles
     int block_base;
+    int expected;             // workgroups that flush into one tile (finalize modes)
 };
 
 struct WalkArgs {
     WalkDesc d[kMaxMulti];
     int n;
+    int in_mode;
+    const float* h;
+    const void* res_acc;
+    float* h_out;
+    const uint16_t* gain;
+    float eps;
+    const uint16_t* embed;
+    const int* token;
+    const float* embed_scale;
+    int vocab;
+    const void* attn_acc;
+    int attn_lofs;            // offset of the softmax denominators in attn_acc
+    int fin;
+    float* silu_out;
+    uint32_t* pick_ctr;
+    uint2* tile_cand;
+    int* token_out;
+    int* pos;
+    int* hist;
+    int hist_len;
+    void* final_zero;
+    int final_zero_n;
+    void* zero_p[2];
+    int zero_n[2];
+    unsigned long long* counters;
 };
 
 // Loads of the selection: the 16 stats (channel stats_channel) of input
-// i0 + tid's rows and, unless x_lds, its x.  Issued before the cutoff is
-// known so that their latency overlaps the search; the raw words are kept
-// (unpacked by select_finish) so that nothing waits for them here.  Layouts:
-// compact stats (stride 1, 2 x 16 bytes), the reference's [R][4] with channel
-// 3 (8 x 16 bytes), otherwise 16 scalar loads.
+// i0 + tid's rows and, when the slice's inputs are not computed in
+// registers, its x (from memory, or from the attention accumulators).
+// Issued before the cutoff is known so that their latency overlaps the
+// search; the raw words are kept.  Layouts: compact stats (stride 1, 2 x 16
+// bytes), the reference's [R][4] with channel 3 (8 x 16 bytes), otherwise
+// 16 scalar loads.
 struct SelLoads {
     uint4 raw[8];
     uint32_t sv[16];
@@ -511,7 +327,10 @@ struct SelLoads {
     int kind;   // 0: stride 1, 1: stride 4 channel 3, 2: scalar
 };
 
-__device__ __forceinline__ void select_load(const WalkDesc& d, int i0, int ni, bool x_lds, SelLoads& L)
+enum XSrc : int { kXRegs = 0, kXMem = 1, kXAttn = 2 };
+
+__device__ __forceinline__ void select_load(const WalkDesc& d, const WalkArgs& a, int i0, int ni, int xsrc,
+                                            SelLoads& L)
 {
     const int tid = threadIdx.x;
     L.xi = 0.0f;
@@ -519,7 +338,12 @@ __device__ __forceinline__ void select_load(const WalkDesc& d, int i0, int ni, b
     const int r0 = i * 16;
     const uint16_t* base = d.stats + (size_t)i0 * 16 * d.stats_stride;
     const bool aligned = (((uintptr_t)base) & 15) == 0 && (d.rows & 15) == 0;
-    if (!x_lds) L.xi = d.x[i];
+    if (xsrc == kXMem) {
+        L.xi = d.x[i];
+    } else if (xsrc == kXAttn) {
+        const double* A = reinterpret_cast<const double*>(a.attn_acc);
+        L.xi = (float)(A[i] / A[a.attn_lofs + (i >> 7)]);
+    }
     const uint16_t* st = d.stats + (size_t)r0 * d.stats_stride;
     if (aligned && d.stats_stride == 1) {
         L.kind = 0;
@@ -547,12 +371,10 @@ __device__ __forceinline__ void select_load(const WalkDesc& d, int i0, int ni, b
 // the same.  A block scan compacts the selected rows in ascending order into
 // s_row (slice-local ids input*16 + rank); s_x[i] = x[i0 + i] (with x_lds it
 // already holds them, written before a barrier).  Ends with a barrier;
-// returns the number of selected rows, which the tile-0 workgroup of the
-// slice also stores in slice_count[p].
+// returns the number of selected rows.
 template <int NT>
-__device__ __forceinline__ uint32_t select_finish(const WalkDesc& d, float cutoff, int p, int t, int i0, int ni,
-                                                  const SelLoads& L, uint16_t* s_row, float* s_x, uint32_t* s_wsum,
-                                                  bool x_lds)
+__device__ __forceinline__ uint32_t select_finish(const WalkDesc& d, float cutoff, int i0, int ni, const SelLoads& L,
+                                                  uint16_t* s_row, float* s_x, uint32_t* s_wsum, bool x_lds)
 {
 #pragma clang fp contract(off)
     constexpr int NW = NT / 64;
@@ -582,8 +404,7 @@ __device__ __forceinline__ uint32_t select_finish(const WalkDesc& d, float cutof
         const int r0 = (i0 + tid) * 16;
 #pragma unroll
         for (int kk = 0; kk < 16; kk++) {
-            const float avg = h2f(sv[kk]);
-            const float prod = __fmul_rn(xi, avg);
+            const float prod = __fmul_rn(xi, h2f(sv[kk]));
             const float imp = __fmul_rn(kScale, fabsf(prod));
             if (imp >= cutoff && r0 + kk < d.rows) mask |= 1u << kk;   // bucketMul.cl:380
         }
@@ -595,6 +416,7 @@ __device__ __forceinline__ uint32_t select_finish(const WalkDesc& d, float cutof
     __syncthreads();
     uint32_t off = incl - cnt;
     uint32_t n_sel = 0;
+#pragma unroll
     for (int i = 0; i < NW; i++) {
         if (i < wave) off += s_wsum[i];
         n_sel += s_wsum[i];
@@ -605,183 +427,61 @@ __device__ __forceinline__ uint32_t select_finish(const WalkDesc& d, float cutof
         s_row[off++] = (uint16_t)(tid * 16 + kk);
     }
     __syncthreads();
-    if (t == 0 && tid == 0) d.slice_count[p] = n_sel;
     return n_sel;
 }
 
-template <int NT>
-__device__ uint32_t select_slice(const WalkDesc& d, float cutoff, int p, int t, int i0, int ni, uint16_t* s_row,
-                                 float* s_x, uint32_t* s_wsum)
+// first maximum (test_generation.cpp:235, 276) of (value, index) pairs
+__device__ __forceinline__ void take_max(float& bv, int& bi, float v, int i)
 {
-    SelLoads L;
-    select_load(d, i0, ni, false, L);
-    return select_finish<NT>(d, cutoff, p, t, i0, ni, L, s_row, s_x, s_wsum, false);
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
 }
 
-template <int VEC, typename Acc, int NW, int UNR>
+// Selection + walk + flush.  Workgroup (input slice p, column tile t) owns
+// the inputs [p*IPS, (p+1)*IPS) and the 128 columns [128t, 128t + 128).
+//
+// Walk: lane = q*16 + j reads 16 bytes (columns 8j..8j+7) of row q of a
+// group of 4 selected rows, so one load instruction fetches the 256-byte tile
+// segments of 4 rows (narrower segments cost HBM efficiency on these
+// scattered rows).  Wave w takes the groups w, w + NW, w + 2NW, ...  Each
+// packed weight is added, as the product x * w in the accumulator type (exact
+// in fp64), to the wave's own accumulator of its output (column c, position
+// bits & 15) with a non-returning LDS atomic add (bucketMul.cl:430-445 adds
+// the product with a plain += per work-item).  The accumulator of (column
+// 8j+e, position pos) is slot pos*129 + e*16 + j: the 16 lanes of a row (one
+// position) hit 16 consecutive slots, and the 16 positions of one column hit
+// 16 different bank pairs, so both the walk and the flush below are free of
+// bank conflicts.  Rows past the end of the list re-read the last selected
+// row with x = 0, so every load of a batch is unconditional.
+//
+// Flush: thread -> output (column-major, col*16 + pos, the reference's output
+// index, bucketMul.cl:442-445), sum of the wave tiles in wave order, one
+// atomic add per output and workgroup.
+template <typename Acc, int NW, int UNR>
 __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
 {
 #pragma clang fp contract(off)
     constexpr int NT = 64 * NW;
-    constexpr int NJ = 64 / VEC, NQ = VEC, TW = 64;
-    constexpr int PER = 16 * VEC * 64;         // accumulators per wave
-    constexpr int STRIDE = NW * NQ;            // rows per workgroup instruction
-    __shared__ Acc acc[NW * PER];
-    __shared__ uint16_t s_row[NT * 16];        // selected rows, slice-local (input*16 + rank)
-    __shared__ float s_x[NT];
-    __shared__ uint32_t s_wsum[NW];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int b = xcd_remap((int)blockIdx.x, (int)gridDim.x);
-    int k = 0;
-    for (int i = 1; i < a.n; i++)
-        if (b >= a.d[i].block_base) k = i;
-    const WalkDesc& d = a.d[k];
-    const int w = b - d.block_base;
-    const int p = w / d.T;
-    const int t = w - p * d.T;
-
-    Acc* my = acc + wave * PER + lane;
-#pragma unroll
-    for (int i = 0; i < 16 * VEC; i++) my[i * 64] = (Acc)0;
-
-    // ---- selection of the slice's rows
-    const int i0 = p * d.IPS;
-    const int ni = min(d.IPS, d.n_in - i0);
-    const uint32_t n_sel = select_slice<NT>(d, *d.cutoff, p, t, i0, ni, s_row, s_x, s_wsum);
-
-    // ---- walk of the selected rows
-    const int q = lane / NJ;
-    const int j = lane - q * NJ;
-    const int col0 = t * TW + j * VEC;
-    // Lanes past the last column read column 0 and add zeros.
-    const int colc = col0 < d.C ? col0 : 0;
-    const float xmask = col0 < d.C ? 1.0f : 0.0f;
-    using LT = typename VecLoad<VEC>::T;
-    const uint16_t* wb = d.W + (size_t)i0 * 16 * d.C + colc;
-    const int ns = (int)n_sel;
-    // batch k: the wave's rows base_k + q + u*STRIDE, u < UNR; the loads of
-    // batch k+1 are issued before the accumulation of batch k
-    int rl[UNR];
-    float xl[UNR];
-    LT v[UNR];
-    auto issue = [&](int base) {
-#pragma unroll
-        for (int u = 0; u < UNR; u++) rl[u] = s_row[min(base + q + u * STRIDE, ns - 1)];
-#pragma unroll
-        for (int u = 0; u < UNR; u++) xl[u] = s_x[rl[u] >> 4];
-#pragma unroll
-        for (int u = 0; u < UNR; u++) v[u] = *reinterpret_cast<const LT*>(wb + (size_t)rl[u] * d.C);
-    };
-    const int first = wave * NQ;
-    if (first < ns) issue(first);
-    for (int base = first; base < ns; base += STRIDE * UNR) {
-        LT vc[UNR];
-        Acc xc[UNR];
-#pragma unroll
-        for (int u = 0; u < UNR; u++) {
-            vc[u] = v[u];
-            xc[u] = (Acc)(base + q + u * STRIDE < ns ? xl[u] * xmask : 0.0f);
-        }
-        if (base + STRIDE * UNR < ns) issue(base + STRIDE * UNR);
-        // keep the next batch's loads ahead of this batch's accumulation
-        asm volatile("" ::: "memory");
-#pragma unroll
-        for (int u = 0; u < UNR; u++) {
-            uint32_t words[(VEC + 1) / 2];
-            VecLoad<VEC>::split(vc[u], words);
-            int ad[VEC];
-            Acc wv[VEC], old[VEC];
-#pragma unroll
-            for (int e = 0; e < VEC; e++) {
-                const uint32_t h = (words[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-                ad[e] = ((int)(h & 15u) * VEC + e) * 64;
-                wv[e] = (Acc)h2f(h);
-            }
-#pragma unroll
-            for (int e = 0; e < VEC; e++) old[e] = my[ad[e]];
-#pragma unroll
-            for (int e = 0; e < VEC; e++) my[ad[e]] = walk_acc<Acc>(xc[u], wv[e], old[e]);
-        }
-    }
-    __syncthreads();
-    // ---- flush.  Thread -> (pos, e, jj) with jj fastest, so the reads of the
-    // NW*NQ private copies are lane-contiguous; the sums go through a padded
-    // staging copy (one pad per 32 entries) into output order col*16 + pos
-    // (bucketMul.cl:442-445), written as one contiguous run of the slice's
-    // partial row.
-    constexpr int NOUT = TW * 16;
-    constexpr int OPT = NOUT / NT;             // outputs per thread
-    static_assert(NOUT % NT == 0 && NW * PER >= NOUT + NOUT / 32, "flush staging does not fit");
-    Acc sum[OPT];
-#pragma unroll
-    for (int k2 = 0; k2 < OPT; k2++) {
-        const int idx = tid + k2 * NT;
-        const int jj = idx % NJ;
-        const int pe = idx / NJ;               // pos*VEC + e
-        const int ai = pe * 64 + jj;
-        Acc s2 = (Acc)0;
-        for (int ww = 0; ww < NW; ww++)
-#pragma unroll
-            for (int qq = 0; qq < NQ; qq++) s2 += acc[ww * PER + ai + qq * NJ];
-        sum[k2] = s2;
-    }
-    __syncthreads();
-    Acc* stage = acc;                          // NOUT + NOUT/32 entries, reused
-#pragma unroll
-    for (int k2 = 0; k2 < OPT; k2++) {
-        const int idx = tid + k2 * NT;
-        const int jj = idx % NJ;
-        const int pe = idx / NJ;
-        const int pos = pe / VEC, e = pe - pos * VEC;
-        const int o = (jj * VEC + e) * 16 + pos;
-        stage[o + (o >> 5)] = sum[k2];
-    }
-    __syncthreads();
-    Acc* prow = reinterpret_cast<Acc*>(d.part) + (size_t)p * d.C * 16 + (size_t)t * NOUT;
-    const int nout = min(NOUT, (d.C - t * TW) * 16);
-    for (int o = tid; o < nout; o += NT) prow[o] = stage[o + (o >> 5)];
-}
-
-// Selection + walk with fp64 accumulation in wave-private LDS tiles.
-// Workgroup (input slice p, column tile t) owns the inputs [p*IPS,
-// (p+1)*IPS) and the 128 columns [128t, 128t + 128).
-//
-// Walk: lane = q*16 + j reads 16 bytes (8 columns 8j..8j+7) of row q of a
-// group of 4 selected rows, so one load instruction fetches the 256-byte tile
-// segments of 4 rows.  Wave w takes the groups w, w + NW, w + 2NW, ...  Each
-// packed weight is added, as the exact fp64 product x * w, to the wave's own
-// accumulator of its output (column c, position bits & 15) with a
-// non-returning LDS fp64 atomic add (bucketMul.cl:430-445 adds the fp32
-// product with a plain += per work-item).  Accumulator slot of (8j+e, pos) is
-// pos*128 + e*16 + j: for one element e the 16 lanes of a row hit 16
-// different bank pairs whatever their positions.  A wave's atomics are
-// applied in instruction order and, within an instruction, in lane order, so
-// the sums do not depend on scheduling; the flush adds the NW wave tiles in
-// wave order.  Rows past the end of the list re-read the last selected row
-// with x = 0, so every load of a batch is unconditional.
-template <int NW, int UNR>
-__global__ __launch_bounds__(64 * NW) void k_walk64(WalkArgs a)
-{
-#pragma clang fp contract(off)
-    constexpr int NT = 64 * NW;
-    constexpr int TW = 128;
-    constexpr int SLOTS = TW * 16;             // accumulators per wave
-    constexpr int GSTRIDE = NW * UNR;          // groups per workgroup batch
+    constexpr int TSLOTS = 16 * kTilePitch;                 // one wave's tile
+    constexpr int GSTRIDE = NW * UNR;                       // groups per workgroup batch
     static_assert(NT == kCutThreads || NT == 2 * kCutThreads, "4 or 8 waves");
-    // the norm and the search hold x[16*tid ..] in the first kCutThreads threads
-    __shared__ double acc[NW * SLOTS];
+    static_assert(kTileOut % NT == 0, "flush mapping");
+    static_assert(sizeof(Acc) * NW * TSLOTS >= sizeof(SearchLds<NW>), "the search scratch lives in the tiles");
+    __shared__ __align__(16) Acc tiles[NW * TSLOTS];   // the search's scratch, then the wave tiles
     __shared__ __align__(16) uint16_t s_row[NT * 16];
-    __shared__ float s_x[NT];
+    __shared__ __align__(16) float s_x[NT];
     __shared__ uint32_t s_wsum[NW];
-    __shared__ __align__(16) float s_red[260];
-    __shared__ __align__(16) int s_cnt[32];
+    __shared__ int s_last;
+    __shared__ float s_bv[NW];
+    __shared__ int s_bi[NW];
+    SearchLds<NW>& SL = *reinterpret_cast<SearchLds<NW>*>(tiles);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
+
     const int b = xcd_remap((int)blockIdx.x, (int)gridDim.x);
     int k = 0;
     for (int i = 1; i < a.n; i++)
@@ -790,64 +490,129 @@ __global__ __launch_bounds__(64 * NW) void k_walk64(WalkArgs a)
     const int w = b - d.block_base;
     const int p = w / d.T;
     const int t = w - p * d.T;
-
-    // every global load of the prologue is issued before any of it is used
     const int i0 = p * d.IPS;
     const int ni = min(d.IPS, d.n_in - i0);
-    const bool x_lds = d.in_mode == kInNorm;
+    const int mode = a.in_mode;
     const bool cut_thread = tid < kCutThreads;
+    const bool norm = mode == kInNorm || mode == kInResNorm || mode == kInEmbedNorm;
+    const bool regs = norm || mode == kInAttn;           // x[0:4096] computed in registers
+    const bool slice_regs = regs && i0 + ni <= kProbes;  // ... and the slice among them
+    const bool first = w == 0 && k == 0;
+
+    // ---- prologue: every global load is issued before any is used
     float xs[kCutVPT];
-    uint4 pr[2], gr[2];
+    double ra[kCutVPT];
+    uint4 pr[2], gr[2], er[2];
+    float sc[kCutVPT];
 #pragma unroll
-    for (int k2 = 0; k2 < kCutVPT; k2++) xs[k2] = 0.0f;
-    pr[0] = pr[1] = gr[0] = gr[1] = make_uint4(0u, 0u, 0u, 0u);
+    for (int k2 = 0; k2 < kCutVPT; k2++) {
+        xs[k2] = 0.0f;
+        ra[k2] = 0.0;
+        sc[k2] = 1.0f;
+    }
+    pr[0] = pr[1] = gr[0] = gr[1] = er[0] = er[1] = make_uint4(0u, 0u, 0u, 0u);
+    double lsum = 1.0;
     float cutoff = 0.0f;
-    if (d.in_mode == kInCutoff) {
+    if (mode == kInCutoff) {
         cutoff = *d.cutoff;
     } else if (cut_thread) {
         load_probes(d.probes, pr);
-        load16(d.in_mode == kInNorm ? d.h : d.x, xs);
-        if (d.in_mode == kInNorm) {
-            gr[0] = reinterpret_cast<const uint4*>(d.gain + tid * kCutVPT)[0];
-            gr[1] = reinterpret_cast<const uint4*>(d.gain + tid * kCutVPT)[1];
+        if (mode == kInX) load16(d.x, xs);
+        if (mode == kInNorm || mode == kInResNorm) load16(a.h, xs);
+        if (mode == kInResNorm && a.res_acc) load16_acc(reinterpret_cast<const double*>(a.res_acc), ra);
+        if (mode == kInEmbedNorm) {
+            const int tok = *a.token;
+            if (tok >= 0 && tok < a.vocab) {
+                const uint4* ev = reinterpret_cast<const uint4*>(a.embed + (size_t)tok * kProbes + tid * kCutVPT);
+                er[0] = ev[0];
+                er[1] = ev[1];
+            }
+            if (a.embed_scale) load16(a.embed_scale, sc);
+        }
+        if (norm) {
+            gr[0] = reinterpret_cast<const uint4*>(a.gain + tid * kCutVPT)[0];
+            gr[1] = reinterpret_cast<const uint4*>(a.gain + tid * kCutVPT)[1];
+        }
+        if (mode == kInAttn) {
+            const double* A = reinterpret_cast<const double*>(a.attn_acc);
+            load16_acc(A, ra);
+            lsum = A[a.attn_lofs + ((tid * kCutVPT) >> 7)];
         }
     }
     SelLoads L;
-    select_load(d, i0, ni, x_lds, L);
-    {
-        double2* z = reinterpret_cast<double2*>(acc + wave * SLOTS);
+    select_load(d, a, i0, ni, slice_regs ? kXRegs : (mode == kInAttn ? kXAttn : kXMem), L);
+
+    // ---- the input
+    if (mode != kInCutoff && cut_thread) {
+        if (mode == kInResNorm && a.res_acc) {
 #pragma unroll
-        for (int i = 0; i < SLOTS / 128; i++) z[i * 64 + lane] = make_double2(0.0, 0.0);
+            for (int k2 = 0; k2 < kCutVPT; k2++) xs[k2] = __fadd_rn(xs[k2], (float)ra[k2]);   // add32
+        }
+        if (mode == kInEmbedNorm) {   // fetchRow16to32 (aux.cl:442-452), then the optional channel scale
+            const uint32_t ew[8] = {er[0].x, er[0].y, er[0].z, er[0].w, er[1].x, er[1].y, er[1].z, er[1].w};
+#pragma unroll
+            for (int k2 = 0; k2 < kCutVPT; k2++) xs[k2] = __fmul_rn(h2f(ew[k2 >> 1] >> ((k2 & 1) * 16)), sc[k2]);
+        }
+        if (mode == kInAttn) {
+#pragma unroll
+            for (int k2 = 0; k2 < kCutVPT; k2++) xs[k2] = (float)(ra[k2] / lsum);
+        }
+        if ((mode == kInResNorm || mode == kInEmbedNorm) && first && a.h_out) {
+            float4* ho = reinterpret_cast<float4*>(a.h_out + tid * kCutVPT);
+#pragma unroll
+            for (int k4 = 0; k4 < 4; k4++) ho[k4] = make_float4(xs[4 * k4], xs[4 * k4 + 1], xs[4 * k4 + 2], xs[4 * k4 + 3]);
+        }
     }
-    if (d.in_mode != kInCutoff) {
-        if (d.in_mode == kInNorm) {
-            block_rmsnorm4096(xs, gr, d.eps, reinterpret_cast<float*>(s_row));
-            if (w == 0 && k == 0 && cut_thread) {
-                float4* xo = reinterpret_cast<float4*>(d.x + tid * kCutVPT);
+    if (norm) block_rmsnorm4096(xs, gr, a.eps, reinterpret_cast<float*>(s_row));
+    if (regs && cut_thread) {
+        if (first && d.x) {
+            float4* xo = reinterpret_cast<float4*>(d.x + tid * kCutVPT);
 #pragma unroll
-                for (int k4 = 0; k4 < 4; k4++)
-                    xo[k4] = make_float4(xs[4 * k4], xs[4 * k4 + 1], xs[4 * k4 + 2], xs[4 * k4 + 3]);
-            }
-            // the slice's inputs for the selection (4096 inputs: all in xs)
+            for (int k4 = 0; k4 < 4; k4++) xo[k4] = make_float4(xs[4 * k4], xs[4 * k4 + 1], xs[4 * k4 + 2], xs[4 * k4 + 3]);
+        }
+        if (slice_regs) {
 #pragma unroll
             for (int k2 = 0; k2 < kCutVPT; k2++) {
                 const int i = tid * kCutVPT + k2 - i0;
-                if (cut_thread && i >= 0 && i < ni) s_x[i] = xs[k2];
+                if (i >= 0 && i < ni) s_x[i] = xs[k2];
             }
         }
-        // s_row is free until the selection: it holds the search's bracket values
-        static_assert(sizeof(uint16_t) * NT * 16 >= sizeof(float) * kCandCap, "s_row too small");
-        cutoff = block_cutoff_x<NW>(xs, pr, d.quantile, s_red, s_cnt, reinterpret_cast<float*>(s_row));
-        if (w == 0 && tid == 0) d.cutoff[0] = cutoff;
     }
-    const int ns = (int)select_finish<NT>(d, cutoff, p, t, i0, ni, L, s_row, s_x, s_wsum, x_lds);
 
+    // ---- cutoff
+    if (mode != kInCutoff) {
+        float v[kCutVPT];
+        importances(xs, pr, v);
+        cutoff = search_cutoff<NW>(v, d.quantile, SL);
+        if (w == 0 && tid == 0) d.cutoff[0] = cutoff;
+        __syncthreads();   // the search scratch becomes the wave tiles
+    }
+    for (int i = lane; i < TSLOTS; i += 64) tiles[wave * TSLOTS + i] = (Acc)0;
+
+    // ---- selection of the slice's rows
+    const int ns = (int)select_finish<NT>(d, cutoff, i0, ni, L, s_row, s_x, s_wsum, slice_regs);
+    if (t == 0 && tid == 0) {
+        d.slice_count[p] = (uint32_t)ns;
+        if (a.counters) {
+            unsigned long long* cr = a.counters + (p % kCounterLanes) * 4;
+            atomicAdd(cr + 0, (unsigned long long)ns * (unsigned long long)d.C * 2ull);
+            atomicAdd(cr + 1, (unsigned long long)ns);
+            if (p == 0) atomicAdd(cr + 2, 1ull);
+        }
+    }
+
+    // ---- walk of the selected rows
     const int j = lane & 15;
     const int q = lane >> 4;
-    const int col0 = t * TW + j * 8;
-    if (col0 < d.C) {   // C % 8 == 0: the lane's 8 columns are all in range
+    const int col0 = t * kTileCols + j * 8;
+    if (col0 < d.C) {
+        // C % 8 == 0: one 16-byte load per row; otherwise (rows only 2-byte
+        // aligned, a lane's last columns may lie past C) eight 2-byte loads,
+        // zero past C (they land in slots the flush does not store)
+        const bool whole = (d.C & 7) == 0;
+        const int nc = min(8, d.C - col0);
         const uint16_t* wb = d.W + (size_t)i0 * 16 * d.C + col0;
-        double* accw = acc + wave * SLOTS + j;
+        const uint32_t tbase = lds_offset(tiles) + (uint32_t)(wave * TSLOTS + j) * (uint32_t)sizeof(Acc);
         const int ng = (ns + 3) >> 2;
         int rl[UNR];
         float xl[UNR];
@@ -861,18 +626,28 @@ __global__ __launch_bounds__(64 * NW) void k_walk64(WalkArgs a)
             }
 #pragma unroll
             for (int u = 0; u < UNR; u++) xl[u] *= s_x[rl[u] >> 4];
+            if (whole) {
 #pragma unroll
-            for (int u = 0; u < UNR; u++)
-                v[u] = *reinterpret_cast<const uint4*>(wb + (size_t)rl[u] * d.C);
+                for (int u = 0; u < UNR; u++) v[u] = *reinterpret_cast<const uint4*>(wb + __umul24(rl[u], d.C));
+            } else {
+#pragma unroll
+                for (int u = 0; u < UNR; u++) {
+                    const uint16_t* rp = wb + __umul24(rl[u], d.C);
+                    uint32_t e[8];
+#pragma unroll
+                    for (int c = 0; c < 8; c++) e[c] = c < nc ? rp[c] : 0u;
+                    v[u] = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
+                }
+            }
         };
         if (wave < ng) issue(wave);
         for (int g0 = wave; g0 < ng; g0 += GSTRIDE) {
             uint4 vc[UNR];
-            double xc[UNR];
+            Acc xc[UNR];
 #pragma unroll
             for (int u = 0; u < UNR; u++) {
                 vc[u] = v[u];
-                xc[u] = (double)xl[u];
+                xc[u] = (Acc)xl[u];
             }
             if (g0 + GSTRIDE < ng) issue(g0 + GSTRIDE);
             asm volatile("" ::: "memory");
@@ -881,266 +656,125 @@ __global__ __launch_bounds__(64 * NW) void k_walk64(WalkArgs a)
                 const uint32_t words[4] = {vc[u].x, vc[u].y, vc[u].z, vc[u].w};
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
-                    const uint32_t h = (words[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-                    const double wv = (double)h2f(h);
-                    // position bits by one bit-field extract (kept as one
-                    // instruction), then one shift-add into the address
+                    const uint32_t hw = words[e >> 1] >> ((e & 1) * 16);
+                    // position bits by one bit-field extract, then one
+                    // multiply-add into the slot address
                     uint32_t pos;
                     asm("v_bfe_u32 %0, %1, %2, 4" : "=v"(pos) : "v"(words[e >> 1]), "i"((e & 1) * 16));
-                    atomicAdd(accw + pos * TW + e * 16, xc[u] * wv);
+                    lds_add<Acc>(__umul24(pos, kTilePitch * (uint32_t)sizeof(Acc)) + tbase, e * 16, xc[u] * (Acc)h2f(hw));
                 }
             }
         }
     }
     __syncthreads();
-    // ---- flush: thread -> slots tid + k*NT (slot order, conflict-free), sum
-    // of the NW wave tiles in wave order, through a padded staging copy (one
-    // pad per 128 entries) into output order col*16 + pos (bucketMul.cl:
-    // 442-445), written as one contiguous run of the slice's partial row.
-    constexpr int OPT = SLOTS / NT;
-    static_assert(SLOTS % NT == 0 && NW * SLOTS >= SLOTS + SLOTS / 128, "flush staging does not fit");
-    double sum[OPT];
+
+    // ---- flush
+    constexpr int OPT = kTileOut / NT;
+    double* out = reinterpret_cast<double*>(d.acc) + (size_t)t * kTileOut;
+    const int nout = min(kTileOut, (d.C - t * kTileCols) * 16);
+    // In the finalize modes the additions return the old values, and the
+    // workgroup waits for all of them before it arrives at the tile
+    // counter: every addition is then performed, at the one place where all
+    // atomics on that address are ordered, before the last workgroup to
+    // arrive takes the sums there with atomic exchanges.
+    const bool ret = a.fin != kFinNone;
+    double sink = 0.0;
 #pragma unroll
     for (int k2 = 0; k2 < OPT; k2++) {
-        const int sl = tid + k2 * NT;
-        double s2 = acc[sl];
+        const int o = tid + k2 * NT;                      // col_local*16 + pos
+        const int cl = o >> 4, pos = o & 15;
+        const int slot = pos * kTilePitch + (cl & 7) * 16 + (cl >> 3);
+        Acc s = tiles[slot];
 #pragma unroll
-        for (int ww = 1; ww < NW; ww++) s2 += acc[ww * SLOTS + sl];
-        sum[k2] = s2;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k2 = 0; k2 < OPT; k2++) {
-        const int sl = tid + k2 * NT;
-        const int pos = sl >> 7, e = (sl >> 4) & 7, jj = sl & 15;
-        const int o = (jj * 8 + e) * 16 + pos;
-        acc[o + (o >> 7)] = sum[k2];
-    }
-    __syncthreads();
-    double* prow = reinterpret_cast<double*>(d.part) + (size_t)p * d.C * 16 + (size_t)t * SLOTS;
-    const int nout = min(SLOTS, (d.C - t * TW) * 16);
-    for (int o = tid; o < nout; o += NT) prow[o] = acc[o + (o >> 7)];
-}
-
-// y[o] = sum over the P row slices of part[p][o] (bucketIntegrate,
-// bucketMul.cl:453-497, sums 64 fixed slices), then the epilogue of the op
-// that consumes y.  Workgroup = 128 outputs; thread (ol, pg) sums outputs
-// 4ol..4ol+3 over slices pg, pg+8, ...; the 8 group sums are added in group
-// order.  The order is fixed, so y is the same on every run.  Block 0 of each
-// matrix adds up the per-slice selected-row counts.
-struct ReduceDesc {
-    const void* part;              // [P][m] of Acc
-    float* y;
-    const uint32_t* slice_count;   // [P]
-    uint32_t* count;               // total selected rows
-    const void* part2;             // kEpSilu: the up projection's partials, counts and output
-    float* y2;
-    const uint32_t* slice_count2;
-    uint32_t* count2;
-    float* out;
-    const float* table;            // RoPE table [max_ctx][hd/2][2]
-    const int* pos;
-    uint16_t* cache;               // fp16 rows [max_ctx][m]
-    int P, P2, m, C;
-    int ep;
-    int max_ctx;
-    int block_base;
-};
-
-struct ReduceArgs {
-    ReduceDesc d[kMaxMulti];
-    int n;
-    unsigned long long* counters;  // walk bytes, rows, matrices (null: no counting)
-};
-
-constexpr int kRedThreads = 256;
-constexpr int kRedHead = 128;    // the RoPE epilogues need a head of 128 outputs in one workgroup
-
-// Workgroup of OUT outputs: thread (ol, pg) sums outputs 4ol..4ol+3 over the
-// slices pg, pg + G, ... (G = 256 / (OUT/4) slice groups) in slice order,
-// U loads at a time; the G group sums are then added in group order by
-// threads 0..OUT-1.
-template <typename Acc, int OUT>
-struct RedShape {
-    static constexpr int QUADS = OUT / 4;
-    static constexpr int G = kRedThreads / QUADS;
-    static constexpr int U = OUT == kRedHead ? 8 : 4;
-};
-
-template <typename Acc, int G, int U>
-__device__ __forceinline__ void slice_loads(const Acc* __restrict__ part, int P, int m, int o, int p0, Acc (&r)[U][4])
-{
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-        const int p = min(p0 + u * G, P - 1);
-#pragma unroll
-        for (int i = 0; i < 4; i++) r[u][i] = part[(size_t)p * m + o + i];
-    }
-}
-
-template <typename Acc, int G, int U>
-__device__ __forceinline__ void slice_adds(int P, int p0, const Acc (&r)[U][4], Acc (&s)[4])
-{
-#pragma unroll
-    for (int u = 0; u < U; u++)
-        if (p0 + u * G < P)
-#pragma unroll
-            for (int i = 0; i < 4; i++) s[i] += r[u][i];
-}
-
-template <typename Acc, int G, int U>
-__device__ __forceinline__ void thread_sums(const Acc* __restrict__ part, int P, int m, int o, int pg, Acc (&s)[4])
-{
-    for (int p0 = pg; p0 < P; p0 += U * G) {
-        Acc r[U][4];
-        slice_loads<Acc, G, U>(part, P, m, o, p0, r);
-        slice_adds<Acc, G, U>(P, p0, r, s);
-    }
-}
-
-// the G group sums of output tid (< OUT) in group order
-template <typename Acc, int OUT>
-__device__ __forceinline__ Acc group_total(const Acc (*red)[OUT])
-{
-    constexpr int G = RedShape<Acc, OUT>::G;
-    const int tid = threadIdx.x;
-    Acc t = (Acc)0;
-    if (tid < OUT) {
-        t = red[0][tid];
-#pragma unroll
-        for (int g = 1; g < G; g++) t += red[g][tid];
-    }
-    return t;
-}
-
-template <typename Acc, int OUT>
-__device__ __forceinline__ Acc group_sums(const Acc* __restrict__ part, int P, int m, int o, int pg,
-                                          Acc (*red)[OUT], int ol)
-{
-    using S = RedShape<Acc, OUT>;
-    Acc s[4] = {(Acc)0, (Acc)0, (Acc)0, (Acc)0};
-    if (o < m) thread_sums<Acc, S::G, S::U>(part, P, m, o, pg, s);
-#pragma unroll
-    for (int i = 0; i < 4; i++) red[pg][ol * 4 + i] = s[i];
-    __syncthreads();
-    return group_total<Acc, OUT>(red);
-}
-
-// two matrices of the same output size at once (the gate and up
-// projections): when both fit one batch of loads, all loads of both are
-// issued together
-template <typename Acc, int OUT>
-__device__ __forceinline__ void group_sums2(const Acc* __restrict__ part, int P, const Acc* __restrict__ part2,
-                                            int P2, int m, int o, int pg, Acc (*red)[OUT], Acc (*red2)[OUT],
-                                            int ol, Acc& t1, Acc& t2)
-{
-    using S = RedShape<Acc, OUT>;
-    Acc s[4] = {(Acc)0, (Acc)0, (Acc)0, (Acc)0};
-    Acc s2[4] = {(Acc)0, (Acc)0, (Acc)0, (Acc)0};
-    if (o < m) {
-        if (P <= S::U * S::G && P2 <= S::U * S::G) {
-            Acc r[S::U][4], r2[S::U][4];
-            slice_loads<Acc, S::G, S::U>(part, P, m, o, pg, r);
-            slice_loads<Acc, S::G, S::U>(part2, P2, m, o, pg, r2);
-            slice_adds<Acc, S::G, S::U>(P, pg, r, s);
-            slice_adds<Acc, S::G, S::U>(P2, pg, r2, s2);
-        } else {
-            thread_sums<Acc, S::G, S::U>(part, P, m, o, pg, s);
-            thread_sums<Acc, S::G, S::U>(part2, P2, m, o, pg, s2);
+        for (int ww = 1; ww < NW; ww++) s += tiles[ww * TSLOTS + slot];
+        if (o < nout && s != (Acc)0) {
+            if (ret) sink += __hip_atomic_fetch_add(out + o, (double)s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else acc_add(out + o, (double)s);
         }
     }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        red[pg][ol * 4 + i] = s[i];
-        red2[pg][ol * 4 + i] = s2[i];
-    }
+    // accumulators of earlier launches that are read no more (after the
+    // prologue: their stores would queue ahead of its loads)
+    zero_share<double>(a.zero_p[0], a.zero_n[0], NT);
+    zero_share<double>(a.zero_p[1], a.zero_n[1], NT);
+    if (a.fin == kFinNone) return;
+
+    // ---- finalize: the last workgroup to flush into tile t
+    asm volatile("" ::"v"(sink));   // the returned values are in: every addition is performed
     __syncthreads();
-    t1 = group_total<Acc, OUT>(red);
-    t2 = group_total<Acc, OUT>(red2);
-}
-
-// total selected rows of a matrix (by one wave, no barrier) into count and
-// the context's counters
-__device__ void sum_counts(const uint32_t* __restrict__ sc, int P, int C, uint32_t* count,
-                           unsigned long long* counters)
-{
-    const int lane = threadIdx.x & 63;
-    unsigned long long v = 0;
-    for (int p = lane; p < P; p += 64) v += sc[p];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    if (lane == 0) {
-        count[0] = (uint32_t)v;
-        atomicAdd(counters + 0, v * (unsigned long long)C * 2ull);
-        atomicAdd(counters + 1, v);
-        atomicAdd(counters + 2, 1ull);
-    }
-}
-
-template <typename Acc, int OUT>
-__global__ __launch_bounds__(kRedThreads) void k_reduce(ReduceArgs a)
-{
-#pragma clang fp contract(off)
-    using S = RedShape<Acc, OUT>;
-    __shared__ Acc red[S::G][OUT];
-    __shared__ Acc red2[S::G][OUT];
-    __shared__ float sy[OUT];
-    const int b = (int)blockIdx.x;
-    int k = 0;
-    for (int i = 1; i < a.n; i++)
-        if (b >= a.d[i].block_base) k = i;
-    const ReduceDesc& d = a.d[k];
-    const int lb = b - d.block_base;
-    const int o0 = lb * OUT;
-    const int tid = threadIdx.x;
-    const int ol = tid % S::QUADS, pg = tid / S::QUADS;
-    const int o = o0 + ol * 4;   // m is a multiple of 16: o..o+3 are in range together
-    if (a.counters && lb == 0 && tid >= kRedThreads - 64) sum_counts(d.slice_count, d.P, d.C, d.count, a.counters);
-    if (a.counters && lb == 0 && d.ep == kEpSilu && tid >= kRedThreads - 128 && tid < kRedThreads - 64)
-        sum_counts(d.slice_count2, d.P2, d.C, d.count2, a.counters);
-    const int oo = o0 + tid;
-    const bool in = tid < OUT && oo < d.m;
-    // the epilogue's own loads go out with the partial loads (a RoPE
-    // epilogue comes with OUT = kRedHead)
-    const bool rope = OUT == kRedHead && (d.ep == kEpRopeQ || d.ep == kEpRopeK);
-    const int pos = rope || d.ep == kEpV ? *d.pos : 0;
-    const bool pos_ok = pos >= 0 && pos < d.max_ctx;
-    float rc = 0.0f, rsn = 0.0f, resid = 0.0f;
-    if (rope && in && pos_ok) {
-        const int fi = tid < OUT / 2 ? tid : tid - OUT / 2;
-        rc = d.table[(size_t)pos * OUT + 2 * fi];
-        rsn = d.table[(size_t)pos * OUT + 2 * fi + 1];
-    }
-    if (d.ep == kEpResid && in) resid = d.out[oo];
-    if (d.ep == kEpSilu) {
-        Acc t1, t2;
-        group_sums2<Acc, OUT>(reinterpret_cast<const Acc*>(d.part), d.P, reinterpret_cast<const Acc*>(d.part2),
-                              d.P2, d.m, o, pg, red, red2, ol, t1, t2);
-        const float yv = (float)t1, uv = (float)t2;
-        if (in) {
-            d.y[oo] = yv;
-            d.y2[oo] = uv;
-            const double x1 = (double)yv;
-            d.out[oo] = (float)((double)uv * x1 / (1.0 + exp(-x1)));
+    if (tid == 0)
+        s_last = __hip_atomic_fetch_add(d.tile_ctr + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (uint32_t)(d.expected - 1);
+    __syncthreads();
+    if (!s_last) return;
+    if (tid == 0) d.tile_ctr[t] = 0u;
+    if (a.fin == kFinSilu) {
+        double* g_acc = reinterpret_cast<double*>(a.d[0].acc) + (size_t)t * kTileOut;
+        double* u_acc = reinterpret_cast<double*>(a.d[1].acc) + (size_t)t * kTileOut;
+        for (int o = tid; o < nout; o += NT) {
+            const float gv = (float)acc_take(g_acc + o), uv = (float)acc_take(u_acc + o);
+            const size_t oo = (size_t)t * kTileOut + o;
+            if (a.d[0].y) a.d[0].y[oo] = gv;
+            if (a.d[1].y) a.d[1].y[oo] = uv;
+            const double x1 = (double)gv;
+            a.silu_out[oo] = (float)((double)uv * x1 / (1.0 + exp(-x1)));   // silu32, matrix.cl:27-32
         }
         return;
     }
-    const float yv = (float)group_sums<Acc, OUT>(reinterpret_cast<const Acc*>(d.part), d.P, d.m, o, pg, red, ol);
-    if (in) d.y[oo] = yv;
-    if (d.ep == kEpResid) {
-        if (in) d.out[oo] = __fadd_rn(resid, yv);
-    } else if (d.ep != kEpStore) {
-        if (d.ep == kEpV) {
-            if (in && pos_ok) d.cache[(size_t)pos * d.m + oo] = __half_as_ushort(__float2half_rn(yv));
-        } else if (rope) {
-            if (tid < OUT) sy[tid] = yv;
-            __syncthreads();
-            if (in && pos_ok) {
-                const float r = rope_cs(sy, tid, OUT / 2, rc, rsn);
-                if (d.ep == kEpRopeQ) d.out[oo] = r;
-                else d.cache[(size_t)pos * d.m + oo] = __half_as_ushort(__float2half_rn(r));
+    // kFinStore
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int o = tid; o < nout; o += NT) {
+        const float yv = (float)acc_take(out + o);
+        const int oo = t * kTileOut + o;
+        d.y[oo] = yv;
+        take_max(bv, bi, yv, oo);
+    }
+    if (!a.pick_ctr) return;
+    // the tile's first maximum, then the last tile to finish picks the token
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        take_max(bv, bi, ov, oi);
+    }
+    if (lane == 0) {
+        s_bv[wave] = bv;
+        s_bi[wave] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int ww = 1; ww < NW; ww++) take_max(bv, bi, s_bv[ww], s_bi[ww]);
+        // the candidate goes to the place the final reader's atomic loads
+        // read, and is there before this tile arrives
+        const unsigned long long cw = ((unsigned long long)(uint32_t)bi << 32) | __float_as_uint(bv);
+        const unsigned long long prev = __hip_atomic_exchange(reinterpret_cast<unsigned long long*>(a.tile_cand + t),
+                                                              cw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("" ::"v"(prev));
+        s_last = __hip_atomic_fetch_add(a.pick_ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (uint32_t)(d.T - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    if (tid == 0) {
+        if (a.token_out) {
+            float v = -INFINITY;
+            int idx = 0x7fffffff;
+            for (int tt = 0; tt < d.T; tt++) {
+                const unsigned long long cw = __hip_atomic_load(reinterpret_cast<unsigned long long*>(a.tile_cand + tt),
+                                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                take_max(v, idx, __uint_as_float((uint32_t)cw), (int)(cw >> 32));
             }
+            const int tok = idx < d.C * 16 ? idx : 0;
+            a.token_out[0] = tok;
+            const int ps = a.pos[0];
+            if (ps + 1 >= 0 && ps + 1 < a.hist_len) a.hist[ps + 1] = tok;
+            a.pos[0] = ps + 1;
         }
+        a.pick_ctr[0] = 0u;
+    }
+    if (a.final_zero) {
+        double* fz = reinterpret_cast<double*>(a.final_zero);
+        for (int i = tid; i < a.final_zero_n; i += NT) fz[i] = 0.0;
     }
 }
 
@@ -1162,99 +796,64 @@ static double est_fraction(float effort)
 
 double est_rows(int rows, float effort) { return std::max(1.0, rows * est_fraction(effort)); }
 
-// Walk launch shapes: a launch whose expected weight bytes are below
-// kWalkWideBytes uses 4 waves per workgroup and 16 rows in flight per lane
-// (more waves per slice: these launches are latency bound), a larger one 2
-// waves and 8 rows (more workgroups in flight).  Each wave holds 16 KB of
-// private accumulators (fp32: 4 columns per lane; fp64: 2); a slice holds at
-// most 64 inputs per wave.  A launch gets about one workgroup per
-// kWalkWgBytes of expected weight bytes, at least kWalkMinWgs.
-#ifndef IAM_WALK_WIDE_BYTES
-#define IAM_WALK_WIDE_BYTES 40e6
+// Walk launch shapes: below IAM_WALK_WIDE_BYTES of expected weight bytes 4
+// waves per workgroup and about one workgroup per IAM_WALK_WG_BYTES (at least
+// IAM_WALK_MIN_WGS; two or three fit a CU); above it 8 waves and one
+// workgroup per CU (IAM_WALK_WIDE_WGS), so that no CU holds more work than
+// another.
+#ifndef IAM_WALK_UNR
+#define IAM_WALK_UNR 4
 #endif
 #ifndef IAM_WALK_WG_BYTES
-#define IAM_WALK_WG_BYTES 98304.0
+#define IAM_WALK_WG_BYTES 131072.0
 #endif
 #ifndef IAM_WALK_MIN_WGS
 #define IAM_WALK_MIN_WGS 256.0
 #endif
-#ifndef IAM_WALK_SMALL_NW
-#define IAM_WALK_SMALL_NW 4
+#ifndef IAM_WALK_WIDE_BYTES
+#define IAM_WALK_WIDE_BYTES 40e6
 #endif
-#ifndef IAM_WALK_SMALL_UNR
-#define IAM_WALK_SMALL_UNR 16
+#ifndef IAM_WALK_WIDE_WGS
+#define IAM_WALK_WIDE_WGS 256
 #endif
-#ifndef IAM_WALK_BIG_NW
-#define IAM_WALK_BIG_NW 2
-#endif
-#ifndef IAM_WALK_BIG_UNR
-#define IAM_WALK_BIG_UNR 8
-#endif
-constexpr double kWalkWideBytes = IAM_WALK_WIDE_BYTES;
-constexpr double kWalkWgBytes = IAM_WALK_WG_BYTES;
-constexpr double kWalkMinWgs = IAM_WALK_MIN_WGS;
-constexpr double kWalkMaxWgs = 3072.0;
-
-// k_walk64 launch shapes: below IAM_W64_WIDE_BYTES of expected weight bytes
-// 4 waves per workgroup and about one workgroup per IAM_W64_WG_BYTES (at
-// least 256; two fit a CU); above it 8 waves and one workgroup per CU
-// (IAM_W64_WIDE_WGS), so that no CU holds more work than another.
-#ifndef IAM_W64_UNR
-#define IAM_W64_UNR 4
-#endif
-#ifndef IAM_W64_WG_BYTES
-#define IAM_W64_WG_BYTES 131072.0
-#endif
-#ifndef IAM_W64_WIDE_BYTES
-#define IAM_W64_WIDE_BYTES 40e6
-#endif
-#ifndef IAM_W64_WIDE_WGS
-#define IAM_W64_WIDE_WGS 256
-#endif
-
-// 8: the fp64 walk with 16-byte loads and 128-column tiles (k_walk64);
-// otherwise the columns per lane load of k_walk.
-static int vec_of(int C, bool acc64)
-{
-    if (acc64 && C % 8 == 0) return 8;
-    if (C % 4 == 0 && !acc64) return 4;
-    if (C % 2 == 0) return 2;
-    return 1;
-}
+constexpr double kWalkMaxWgs = 2048.0;
 
 // Slices per matrix (only the performance depends on them): the launch's
 // workgroups are shared by the matrices in proportion to their bytes.
-void plan_walk(int n, const MatOp* ops, float effort, bool acc64, WalkPlan* plan)
+void plan_walk(int n, const MatOp* ops, float effort, WalkPlan* plan)
 {
     double bytes[kMaxMulti], tot = 0;
-    bool all64 = true;
     for (int i = 0; i < n; i++) {
         const iam_bucket_matrix& M = ops[i].mat;
         WalkPlan& pl = plan[i];
-        pl.V = vec_of(M.bucket_cols, acc64);
-        all64 = all64 && pl.V == 8;
-        const int tw = pl.V == 8 ? 128 : 64;
-        pl.T = (M.bucket_cols + tw - 1) / tw;
+        pl.T = (M.bucket_cols + kTileCols - 1) / kTileCols;
         pl.n_in = std::min((M.expert_rows + 15) / 16, ops[i].in_size);
-        // the cost of a row is its tiles' width: a k_walk64 workgroup spends
-        // the same on a 64-column matrix's half-empty tile as on a full one
-        bytes[i] = est_rows(pl.n_in * 16, effort) * (pl.V == 8 ? pl.T * tw : M.bucket_cols) * 2.0;
+        // the cost of a row is its tiles' width
+        bytes[i] = est_rows(pl.n_in * 16, effort) * pl.T * kTileCols * 2.0;
         tot += bytes[i];
     }
-    const bool wide64 = all64 && tot >= IAM_W64_WIDE_BYTES;
-    const int nw = all64 ? (wide64 ? 8 : 4) : tot < kWalkWideBytes ? IAM_WALK_SMALL_NW : IAM_WALK_BIG_NW;
-    const double wg_bytes = all64 ? IAM_W64_WG_BYTES : kWalkWgBytes;
-    double target = std::min(kWalkMaxWgs, std::max(kWalkMinWgs, tot / wg_bytes));
-    const bool fit = wide64;   // at most target workgroups
-    if (wide64) target = IAM_W64_WIDE_WGS;
+    const bool wide = tot >= IAM_WALK_WIDE_BYTES;
+    const int nw = wide ? 8 : 4;
+    const double target = wide ? IAM_WALK_WIDE_WGS : std::min(kWalkMaxWgs, std::max(IAM_WALK_MIN_WGS, tot / IAM_WALK_WG_BYTES));
     for (int i = 0; i < n; i++) {
         WalkPlan& pl = plan[i];
         pl.NW = nw;
         const double wgs = tot > 0 ? target * bytes[i] / tot : target / n;
-        const int slices = std::max(1, fit ? (int)std::floor(wgs / pl.T + 1e-9) : (int)std::lround(wgs / pl.T));
+        const int slices = std::max(1, wide ? (int)std::floor(wgs / pl.T + 1e-9) : (int)std::lround(wgs / pl.T));
         pl.IPS = std::min(64 * pl.NW, std::max(1, (pl.n_in + slices - 1) / slices));
         pl.P = (pl.n_in + pl.IPS - 1) / pl.IPS;
     }
+}
+
+int walk_tiles(int bucket_cols) { return (bucket_cols + kTileCols - 1) / kTileCols; }
+
+int max_slices(int n, const MatOp* ops, float effort)
+{
+    WalkPlan plan[kMaxMulti];
+    plan_walk(n, ops, effort, plan);
+    int P = 1;
+    for (int i = 0; i < n; i++) P = std::max(P, plan[i].P);
+    return P;
 }
 
 // Validate the n matrix ops and record their selection problems in slots
@@ -1322,9 +921,7 @@ static int bucketmul_list(Ctx* c, int i)
     const int inputs = (s.rows + 15) / 16;
     const int G = std::max(1, (std::min(inputs, s.in_size) + kChunkInputs - 1) / kChunkInputs);
     IAM_TRY(ensure_list(c, i, G));
-    DispatchArgs args{};
-    args.n = 1;
-    DispatchDesc& d = args.d[0];
+    DispatchDesc d{};
     d.x = s.x;
     d.probes = s.probes;
     d.stats = s.stats;
@@ -1337,60 +934,126 @@ static int bucketmul_list(Ctx* c, int i)
     d.list = s.list;
     d.counts = s.counts;
     d.cutoff = s.cutoff;
-    d.block_base = 0;
     s.G = G;
-    return launch(c, "bucket_list", k_dispatch, dim3(G), dim3(kCutThreads), 0, args);
-}
-
-template <typename Acc, int NW, int UNR>
-static int launch_walk_shape(Ctx* c, int vec, int blocks, const WalkArgs& args)
-{
-    const dim3 g(blocks), t(64 * NW);
-    if constexpr (sizeof(Acc) == 4) {
-        if (vec >= 4) return launch(c, "bucket_walk", k_walk<4, Acc, NW, UNR>, g, t, 0, args);
-    }
-    if (vec >= 2) return launch(c, "bucket_walk", k_walk<2, Acc, NW, UNR>, g, t, 0, args);
-    return launch(c, "bucket_walk", k_walk<1, Acc, NW, UNR>, g, t, 0, args);
+    return launch(c, "bucket_list", k_dispatch, dim3(G), dim3(kCutThreads), 0, d);
 }
 
 template <typename Acc>
-static int launch_walk(Ctx* c, int nw, int vec, int blocks, const WalkArgs& args)
+static int launch_walk(Ctx* c, int nw, int blocks, const WalkArgs& args)
 {
-    if (nw == IAM_WALK_SMALL_NW) return launch_walk_shape<Acc, IAM_WALK_SMALL_NW, IAM_WALK_SMALL_UNR>(c, vec, blocks, args);
-    return launch_walk_shape<Acc, IAM_WALK_BIG_NW, IAM_WALK_BIG_UNR>(c, vec, blocks, args);
+    if (nw == 8) return launch(c, "bucket_walk", k_walk<Acc, 8, IAM_WALK_UNR>, dim3(blocks), dim3(512), 0, args);
+    return launch(c, "bucket_walk", k_walk<Acc, 4, IAM_WALK_UNR>, dim3(blocks), dim3(256), 0, args);
 }
 
-// Partial sums [P][m] of the accumulator type, then the per-slice selected
-// row counts [P].
-static size_t partial_bytes(const WalkPlan& pl, int C, bool acc64)
+int walk_group(Ctx* c, const WalkGroup& g)
 {
-    return (size_t)pl.P * C * 16 * (acc64 ? 8 : 4) + (size_t)pl.P * sizeof(uint32_t);
-}
-
-static uint32_t* slice_counts(const DispatchSlot& s, const WalkPlan& pl, bool acc64)
-{
-    return reinterpret_cast<uint32_t*>(static_cast<char*>(s.part) + (size_t)pl.P * s.bucket_cols * 16 * (acc64 ? 8 : 4));
-}
-
-int reserve_walk(Ctx* c, int n, const MatOp* ops, float effort)
-{
-    WalkPlan plan[kMaxMulti];
-    plan_walk(n, ops, effort, c->acc64, plan);
-    for (int i = 0; i < n; i++) {
-        IAM_TRY(ensure_slot(c, i));
-        IAM_TRY(ensure_partials(c, i, partial_bytes(plan[i], ops[i].mat.bucket_cols, c->acc64)));
+    IAM_REQUIRE(g.n >= 1 && g.n <= kMaxMulti, "walk: 1..3 matrices per launch");
+    IAM_REQUIRE(!std::isnan(g.effort), "walk: effort is NaN");
+    MatOp ops[kMaxMulti];
+    for (int i = 0; i < g.n; i++) {
+        const WalkMat& wm = g.m[i];
+        IAM_REQUIRE(((uintptr_t)wm.mat.buckets & 7) == 0, "walk: buckets must be 8-byte aligned");
+        // slice-local row offsets (row < 8192) times bucket_cols are formed with 24-bit multiplies
+        IAM_REQUIRE(wm.mat.bucket_cols > 0 && wm.mat.bucket_cols < (1 << 18), "walk: bucket_cols out of range");
+        IAM_REQUIRE(wm.acc && wm.cutoff && wm.slice_count, "walk: missing scratch");
+        IAM_REQUIRE(g.fin == kFinNone || wm.tile_ctr, "walk: missing tile counters");
+        IAM_REQUIRE(g.fin != kFinStore || wm.y, "walk: missing outputs");
+        ops[i].mat = wm.mat;
+        ops[i].in_size = wm.in_size;
+        ops[i].x = wm.x;
+        ops[i].y = wm.y;
     }
-    return IAM_OK;
+    WalkPlan plan[kMaxMulti];
+    plan_walk(g.n, ops, g.effort, plan);
+    WalkArgs args{};
+    args.n = g.n;
+    const int qv = quantile_of(g.effort);
+    int blocks = 0;
+    for (int i = 0; i < g.n; i++) {
+        const WalkMat& wm = g.m[i];
+        const iam_bucket_matrix& M = wm.mat;
+        WalkDesc& d = args.d[i];
+        d.W = M.buckets + (size_t)g.expert_no * (size_t)M.expert_rows * M.bucket_cols;
+        d.x = const_cast<float*>(wm.x);
+        d.stats = M.stats + (size_t)g.expert_no * (size_t)M.expert_rows * M.stats_stride;
+        d.probes = M.probes + (size_t)g.expert_no * kProbes;
+        d.cutoff = wm.cutoff;
+        d.slice_count = wm.slice_count;
+        d.acc = wm.acc;
+        d.y = wm.y;
+        d.tile_ctr = wm.tile_ctr;
+        d.quantile = qv;
+        d.stats_stride = M.stats_stride;
+        d.stats_channel = M.stats_channel;
+        d.rows = M.expert_rows;
+        d.n_in = plan[i].n_in;
+        d.C = M.bucket_cols;
+        d.IPS = plan[i].IPS;
+        d.P = plan[i].P;
+        d.T = plan[i].T;
+        d.block_base = blocks;
+        d.expected = plan[i].P;
+        blocks += plan[i].P * plan[i].T;
+    }
+    if (g.fin == kFinSilu) {
+        IAM_REQUIRE(g.n == 2 && g.m[0].mat.bucket_cols == g.m[1].mat.bucket_cols && g.silu_out,
+                    "walk: the SiLU gate pairs two matrices of one shape");
+        args.d[0].expected = args.d[1].expected = plan[0].P + plan[1].P;
+        args.d[1].tile_ctr = args.d[0].tile_ctr;
+    }
+    args.in_mode = g.in_mode;
+    args.h = g.h;
+    args.res_acc = g.res_acc;
+    args.h_out = g.h_out;
+    args.gain = g.gain;
+    args.eps = g.eps;
+    args.embed = g.embed;
+    args.token = g.token;
+    args.embed_scale = g.embed_scale;
+    args.vocab = g.vocab;
+    args.attn_acc = g.attn_acc;
+    args.attn_lofs = g.m[0].in_size;
+    args.fin = g.fin;
+    args.silu_out = g.silu_out;
+    args.pick_ctr = g.pick_ctr;
+    args.tile_cand = reinterpret_cast<uint2*>(g.tile_cand);
+    args.token_out = g.token_out;
+    args.pos = g.pos;
+    args.hist = g.hist;
+    args.hist_len = g.hist_len;
+    args.final_zero = g.final_zero;
+    args.final_zero_n = g.final_zero_n;
+    for (int z = 0; z < 2; z++) {
+        args.zero_p[z] = g.zero_p[z];
+        args.zero_n[z] = g.zero_n[z];
+    }
+    args.counters = c->counting ? c->counters : nullptr;
+    // walk_count reads the slice counts of the slots this launch wrote
+    for (int i = 0; i < g.n; i++)
+        if (g.m[i].slice_count == c->slots[i].slice_count) c->slots[i].walked_P = plan[i].P;
+    return c->acc64 ? launch_walk<double>(c, plan[0].NW, blocks, args) : launch_walk<float>(c, plan[0].NW, blocks, args);
 }
 
-// Walk and reduce of slots 0..n-1 (recorded by record_slots).  in_mode is how
-// the k_walk64 launches get x and the cutoff (k_walk always reads the
-// cutoff of a preceding k_cutoff launch); ep (null: store y) the epilogue of
-// each op, kEpSilu pairing ops 0 (gate) and 1 (up).
-static int walk_and_reduce(Ctx* c, int n, const MatOp* ops, int in_mode, const float* h, const uint16_t* gain,
-                           float eps, const ReduceEp* ep)
+// The standalone walk of the n matrices recorded in slots 0..n-1: the
+// slots' scratch, fp32 outputs stored by the tiles' last workgroups.
+static int walk_slots(Ctx* c, int n, const MatOp* ops, int in_mode, const float* h, const uint16_t* gain, float eps)
 {
-    IAM_REQUIRE(n >= 1 && n <= kMaxMulti, "bucketmul: 1..3 matrices per launch");
+    WalkGroup g;
+    g.n = n;
+    g.in_mode = in_mode;
+    g.effort = c->slots[0].effort;
+    g.expert_no = c->slots[0].expert_no;
+    g.h = h;
+    g.gain = gain;
+    g.eps = eps;
+    g.fin = kFinStore;
+    MatOp wops[kMaxMulti];
+    for (int i = 0; i < n; i++) {
+        wops[i] = ops[i];
+        wops[i].x = c->slots[i].x;
+        wops[i].in_size = c->slots[i].in_size;
+    }
+    const int P = max_slices(n, wops, g.effort);
     for (int i = 0; i < n; i++) {
         const iam_bucket_matrix& M = ops[i].mat;
         const DispatchSlot& s = c->slots[i];
@@ -1403,130 +1066,37 @@ static int walk_and_reduce(Ctx* c, int n, const MatOp* ops, int in_mode, const f
         IAM_TRY(check_dev_range(c, M.buckets, (size_t)(s.expert_no + 1) * M.expert_rows * M.bucket_cols * 2,
                                 "bucketmul buckets"));
         IAM_TRY(check_dev_range(c, ops[i].y, (size_t)M.bucket_cols * 16 * sizeof(float), "bucketmul y"));
-        IAM_REQUIRE(s.effort == c->slots[0].effort, "bucketmul: slots dispatched at different efforts");
+        IAM_REQUIRE(s.effort == c->slots[0].effort && s.expert_no == c->slots[0].expert_no,
+                    "bucketmul: slots dispatched at different efforts or experts");
+        const size_t m = (size_t)M.bucket_cols * 16;
+        IAM_TRY(ensure_walk_scratch(c, i, m, (m + kTileOut - 1) / kTileOut, (size_t)P));
+        WalkMat& wm = g.m[i];
+        wm.mat = M;
+        wm.mat.stats = s.stats - (size_t)s.expert_no * (size_t)M.expert_rows * s.stats_stride;
+        wm.mat.probes = s.probes - (size_t)s.expert_no * kProbes;
+        wm.mat.stats_stride = s.stats_stride;
+        wm.mat.stats_channel = s.stats_channel;
+        wm.in_size = s.in_size;
+        wm.x = s.x;
+        wm.cutoff = s.cutoff;
+        wm.slice_count = s.slice_count;
+        wm.acc = s.acc;
+        wm.tile_ctr = s.tile_ctr;
+        wm.y = ops[i].y;
     }
-    // the walk reads x and in_size from the slots (the dispatch's inputs)
-    MatOp wops[kMaxMulti];
-    for (int i = 0; i < n; i++) {
-        wops[i] = ops[i];
-        wops[i].x = c->slots[i].x;
-        wops[i].in_size = c->slots[i].in_size;
-    }
-    WalkPlan plan[kMaxMulti];
-    plan_walk(n, wops, c->slots[0].effort, c->acc64, plan);
-    for (int i = 0; i < n; i++)
-        IAM_TRY(ensure_partials(c, i, partial_bytes(plan[i], ops[i].mat.bucket_cols, c->acc64)));
-    const int qv = quantile_of(c->slots[0].effort);
-
-    // walk: one launch per kernel variant (the model's matrices all share one)
-    bool used[kMaxMulti] = {false, false, false};
-    for (int done = 0; done < n;) {
-        int vec = 0, blocks = 0, cnt = 0, nw = 0;
-        WalkArgs args{};
-        for (int i = 0; i < n; i++) {
-            if (used[i] || (vec != 0 && plan[i].V != vec)) continue;
-            vec = plan[i].V;
-            nw = plan[i].NW;
-            const DispatchSlot& s = c->slots[i];
-            WalkDesc& d = args.d[cnt++];
-            d.W = ops[i].mat.buckets + (size_t)s.expert_no * (size_t)ops[i].mat.expert_rows * ops[i].mat.bucket_cols;
-            d.x = const_cast<float*>(s.x);
-            d.stats = s.stats;
-            d.cutoff = s.cutoff;
-            d.slice_count = slice_counts(s, plan[i], c->acc64);
-            d.part = s.part;
-            d.h = h;
-            d.gain = gain;
-            d.probes = s.probes;
-            d.eps = eps;
-            d.quantile = qv;
-            d.in_mode = vec == 8 ? in_mode : kInCutoff;
-            d.stats_stride = s.stats_stride;
-            d.stats_channel = s.stats_channel;
-            d.rows = s.rows;
-            d.n_in = plan[i].n_in;
-            d.C = ops[i].mat.bucket_cols;
-            d.IPS = plan[i].IPS;
-            d.P = plan[i].P;
-            d.T = plan[i].T;
-            d.block_base = blocks;
-            blocks += plan[i].P * plan[i].T;
-            used[i] = true;
-            done++;
-        }
-        args.n = cnt;
-        if (vec == 8 && nw == 8)
-            IAM_TRY(launch(c, "bucket_walk", k_walk64<8, IAM_W64_UNR>, dim3(blocks), dim3(512), 0, args));
-        else if (vec == 8)
-            IAM_TRY(launch(c, "bucket_walk", k_walk64<4, IAM_W64_UNR>, dim3(blocks), dim3(256), 0, args));
-        else
-            IAM_TRY(c->acc64 ? launch_walk<double>(c, nw, vec, blocks, args)
-                             : launch_walk<float>(c, nw, vec, blocks, args));
-    }
-    // fixed-order sum of the slices into y, with the epilogue
-    ReduceArgs ra{};
-    ra.counters = c->counting ? c->counters : nullptr;   // null: no counting
-    for (int i = 0; i < n; i++) c->slots[i].counted = c->counting;
-    int rblocks = 0, nd = 0;
-    int rout = 32;
-    for (int i = 0; ep && i < n; i++)
-        if (ep[i].ep == kEpRopeQ || ep[i].ep == kEpRopeK) rout = kRedHead;
-    for (int i = 0; i < n; i++) {
-        const DispatchSlot& s = c->slots[i];
-        ReduceDesc& d = ra.d[nd++];
-        d.part = s.part;
-        d.y = ops[i].y;
-        d.slice_count = slice_counts(s, plan[i], c->acc64);
-        d.count = s.count;
-        d.P = plan[i].P;
-        d.m = ops[i].mat.bucket_cols * 16;
-        d.C = ops[i].mat.bucket_cols;
-        d.ep = ep ? ep[i].ep : kEpStore;
-        if (ep) {
-            d.out = ep[i].out;
-            d.table = ep[i].table;
-            d.pos = ep[i].pos;
-            d.max_ctx = ep[i].max_ctx;
-            d.cache = ep[i].cache;
-        }
-        if (d.ep == kEpSilu) {
-            IAM_REQUIRE(i == 0 && n == 2 && ops[1].mat.bucket_cols == ops[0].mat.bucket_cols,
-                        "bucketmul: the SiLU epilogue pairs two matrices of one shape");
-            const DispatchSlot& s2 = c->slots[1];
-            d.part2 = s2.part;
-            d.y2 = ops[1].y;
-            d.slice_count2 = slice_counts(s2, plan[1], c->acc64);
-            d.count2 = s2.count;
-            d.P2 = plan[1].P;
-            i = n;   // the pair is one descriptor
-        }
-        d.block_base = rblocks;
-        rblocks += (d.m + rout - 1) / rout;
-    }
-    ra.n = nd;
-    // a head of 128 outputs per workgroup for RoPE, else 32 outputs (more
-    // workgroups, fewer partials per thread)
-    if (rout == kRedHead)
-        return c->acc64 ? launch(c, "bucket_reduce", k_reduce<double, kRedHead>, dim3(rblocks), dim3(kRedThreads), 0, ra)
-                        : launch(c, "bucket_reduce", k_reduce<float, kRedHead>, dim3(rblocks), dim3(kRedThreads), 0, ra);
-    return c->acc64 ? launch(c, "bucket_reduce", k_reduce<double, 32>, dim3(rblocks), dim3(kRedThreads), 0, ra)
-                    : launch(c, "bucket_reduce", k_reduce<float, 32>, dim3(rblocks), dim3(kRedThreads), 0, ra);
+    return walk_group(c, g);
 }
 
-int bucketmul_walk(Ctx* c, int n, const MatOp* ops) { return walk_and_reduce(c, n, ops, kInCutoff, nullptr, nullptr, 0.0f, nullptr); }
+int bucketmul_walk(Ctx* c, int n, const MatOp* ops) { return walk_slots(c, n, ops, kInCutoff, nullptr, nullptr, 0.0f); }
 
-// One fused matrix group: record the slots, then either (all matrices on
-// k_walk64) a walk in which every workgroup computes its input (norm) and
-// cutoff itself, or the separate norm / cutoff launches before the walk;
-// then the reduce with its epilogue.  in_mode kInNorm: x = rmsnorm(h) *
-// gain is written to ops[0].x (every op must name the same x, 4096 inputs).
+// One matrix group in one launch: every workgroup computes the input (x, or
+// the norm of h written to x) and the cutoff itself.  A norm input of other
+// than 4096 values is normalized by the RMSNorm kernel first.
 int bucketmul_fused(Ctx* c, int n, const MatOp* ops, int expert_no, float effort, int in_mode, const float* h,
-                    const uint16_t* gain, float eps, const ReduceEp* ep)
+                    const uint16_t* gain, float eps)
 {
     CutoffArgs args{};
     IAM_TRY(record_slots(c, n, ops, expert_no, effort, args));
-    bool all64 = true;
-    for (int i = 0; i < n; i++) all64 = all64 && vec_of(ops[i].mat.bucket_cols, c->acc64) == 8;
     if (in_mode == kInNorm) {
         IAM_REQUIRE(h && gain, "bucketmul: norm input without h/gain");
         const int ni = ops[0].in_size;
@@ -1537,18 +1107,12 @@ int bucketmul_fused(Ctx* c, int n, const MatOp* ops, int expert_no, float effort
         IAM_TRY(check_dev_range(c, gain, (size_t)ni * 2, "bucketmul gain"));
         IAM_REQUIRE(((uintptr_t)h & 15) == 0 && ((uintptr_t)gain & 15) == 0, "bucketmul: h and gain must be 16-byte aligned");
         if (ni != kProbes) {
-            // the walk's own norm covers 4096 inputs: a wider vector is
-            // normalized by the RMSNorm kernel first (same order of sums)
             IAM_REQUIRE(ni % 1024 == 0, "bucketmul: a norm input must be a multiple of 1024 long");
             IAM_TRY(rmsnorm(c, const_cast<float*>(h), nullptr, gain, ni, eps, const_cast<float*>(ops[0].x)));
             in_mode = kInX;
         }
     }
-    if (all64) return walk_and_reduce(c, n, ops, in_mode, h, gain, eps, ep);
-    if (in_mode == kInNorm)
-        IAM_TRY(rmsnorm(c, const_cast<float*>(h), nullptr, gain, ops[0].in_size, eps, const_cast<float*>(ops[0].x)));
-    IAM_TRY(launch(c, "bucket_cutoff", k_cutoff, dim3(n), dim3(kCutThreads), 0, args));
-    return walk_and_reduce(c, n, ops, kInCutoff, nullptr, nullptr, 0.0f, ep);
+    return walk_slots(c, n, ops, in_mode, h, gain, eps);
 }
 
 __global__ void k_stats_compact(const uint16_t* __restrict__ s, size_t rows, int stride, int ch,
@@ -1651,11 +1215,12 @@ int iam_bucketmul_fused(iam_ctx* c, int n, const iam_bucket_matrix* mats, float*
         ops[i].y = ys[i];
         IAM_REQUIRE(ys[i] && mats[i].buckets, "fused: null y/buckets");
     }
-    return bucketmul_fused(c, n, ops, expert_no, effort, h ? kInNorm : kInX, h, gain, eps, nullptr);
+    return bucketmul_fused(c, n, ops, expert_no, effort, h ? kInNorm : kInX, h, gain, eps);
 }
 
-// The cutoff comes from k_cutoff; the selection is re-run by the list kernel
-// (which recomputes the cutoff on its own; the two must agree bit for bit).
+// The cutoff comes from the last search of the slot; the selection is re-run
+// by the list kernel (which recomputes the cutoff on its own; the two must
+// agree bit for bit).
 static int dispatch_query(Ctx* c, int slot, float* cutoff, std::vector<uint32_t>* rows, uint32_t* count)
 {
     if (slot < 0 || slot >= kMaxMulti) return fail(IAM_E_INVALID, "dispatch query: bad slot");
@@ -1711,9 +1276,13 @@ int iam_bucketmul_walk_count(iam_ctx* c, int slot, uint32_t* count)
     if (!c || !count || slot < 0 || slot >= kMaxMulti) return fail(IAM_E_INVALID, "walk_count: bad argument");
     const DispatchSlot& s = c->slots[slot];
     if (!s.valid) return fail(IAM_E_STATE, "walk_count: no dispatch in this slot");
-    if (!s.counted) return fail(IAM_E_STATE, "walk_count: the last walk of this slot ran with counting off");
+    if (s.walked_P <= 0) return fail(IAM_E_STATE, "walk_count: no walk in this slot");
     IAM_CHECK_HIP(hipStreamSynchronize(c->stream));
-    IAM_CHECK_HIP(hipMemcpy(count, s.count, sizeof(uint32_t), hipMemcpyDeviceToHost));
+    std::vector<uint32_t> sc((size_t)s.walked_P);
+    IAM_CHECK_HIP(hipMemcpy(sc.data(), s.slice_count, sc.size() * sizeof(uint32_t), hipMemcpyDeviceToHost));
+    uint64_t S = 0;
+    for (uint32_t v : sc) S += v;
+    *count = (uint32_t)S;
     return IAM_OK;
 }
 

@@ -44,11 +44,13 @@ constexpr int kMaxChunks = 256;             // in_dim up to 65536 per expert
 constexpr int kMaxMulti = 3;                // matrices per fused launch
 
 // ------------------------------------------------------- dispatch state ---
-// One matrix of the last cutoff launch: the selection problem (recorded by
-// bucketmul_dispatch, re-evaluated by the walk), the device cutoff and the
-// walk's selected-row counter, and the walk partials.  The selected-row
-// list (per chunk of 4096 rows, ascending {row id, bits of x[row/16]}) is
-// only built for the blocking parity queries.
+// One matrix of the last cutoff / walk launch: the selection problem
+// (recorded by bucketmul_dispatch, re-evaluated by the walk), the device
+// cutoff, and the walk's scratch: the output accumulator (zero between
+// calls: the walk's last workgroup per column tile reads and clears it),
+// the tiles' arrival counters and the per-slice selected-row counts.  The
+// selected-row list (per chunk of 4096 rows, ascending {row id, bits of
+// x[row/16]}) is only built for the blocking parity queries.
 struct DispatchSlot {
     const float* x = nullptr;
     const uint16_t* stats = nullptr;   // row 0 of the expert
@@ -61,15 +63,18 @@ struct DispatchSlot {
     int expert_no = 0;
     float effort = 1.0f;
     bool valid = false;
-    float* cutoff = nullptr;     // device [2]: k_cutoff's value, the list kernel's value
-    uint32_t* count = nullptr;   // device [1]: rows selected by the last walk
-    bool counted = false;        // the last walk counted its rows (counting was on)
+    float* cutoff = nullptr;     // device [2]: the search's value, the list kernel's value
     uint2* list = nullptr;       // [G][kChunkRows]
     uint32_t* counts = nullptr;  // [kMaxChunks]
     size_t cap_chunks = 0;
     int G = 0;                   // chunks of the last list
-    void* part = nullptr;        // walk partial sums [P][m] of the accumulator type
-    size_t part_cap = 0;         // bytes
+    void* acc = nullptr;         // [acc_cap] accumulators (8 bytes each), zero between calls
+    size_t acc_cap = 0;
+    uint32_t* tile_ctr = nullptr;     // [tile_cap] arrival counters, zero between calls
+    size_t tile_cap = 0;
+    uint32_t* slice_count = nullptr;  // [slice_cap] rows selected per slice by the last walk
+    size_t slice_cap = 0;
+    int walked_P = 0;            // slices of the last walk of this slot (0: none)
 };
 
 struct KernelStat {
@@ -96,15 +101,21 @@ struct Ctx {
     std::vector<hipEvent_t> event_pool;
     std::map<std::string, KernelStat> stats;
     DispatchSlot slots[kMaxMulti];
-    float* attn_ws = nullptr;          // split-context attention partials
-    size_t attn_ws_floats = 0;
-    // bumped whenever a context-owned scratch buffer (dispatch lists, walk
-    // partials, attention workspace) is reallocated: captured graphs hold
-    // those addresses and must be re-captured when it changes
+    // attention: accumulators (o per head and dimension, then the softmax
+    // denominator per head; zero between calls) and per-KV-head arrival
+    // counters of the standalone entry point
+    void* attn_acc = nullptr;
+    size_t attn_acc_cap = 0;
+    uint32_t* attn_ctr = nullptr;
+    // bumped whenever a context-owned scratch buffer is reallocated:
+    // captured graphs hold those addresses and must be re-captured
     uint64_t scratch_gen = 0;
-    unsigned long long* counters = nullptr;   // device: walk bytes, rows, matrices
-    // the reduce adds up the walk's selected rows into the slot counts and
-    // the counters (off: neither is updated, and the reduce is shorter)
+    // device walk counters, kCounterLanes rows of {weight bytes, rows,
+    // matrices, pad}: each walk adds to row (slice % kCounterLanes), so the
+    // additions of one launch do not queue on one address
+    unsigned long long* counters = nullptr;
+    // the walk adds its selected rows and bytes to the counters (off: it
+    // does not touch them)
     bool counting = true;
     // accumulate the walk in fp64 (sums round once to fp32) instead of fp32
     bool acc64 = true;
@@ -116,7 +127,10 @@ int check_dev_range(Ctx* c, const void* p, size_t bytes, const char* what);
 int ctx_free(Ctx* c, void* p);
 int ensure_slot(Ctx* c, int slot);
 int ensure_list(Ctx* c, int slot, int chunks);
-int ensure_partials(Ctx* c, int slot, size_t bytes);
+// the walk scratch of a slot: accumulators for m outputs, T tile counters,
+// P slice counts (grown as needed; new memory is zeroed)
+int ensure_walk_scratch(Ctx* c, int slot, size_t m, size_t T, size_t P);
+constexpr int kCounterLanes = 64;
 
 // Launch bookkeeping: with profiling on (and no graph capture in progress)
 // each launch is bracketed by a pair of pooled events.
@@ -158,54 +172,97 @@ struct MatOp {
 // record the selection problems of n matrices in slots 0..n-1 and compute
 // their cutoffs
 int bucketmul_dispatch(Ctx* c, int n, const MatOp* ops, int expert_no, float effort);
-// selection + walk of slots 0..n-1 into per-slice partial sums, then the
-// fixed-order reduction into each y (overwritten)
+// selection + walk of slots 0..n-1 with the cutoffs of the last dispatch,
+// y overwritten
 int bucketmul_walk(Ctx* c, int n, const MatOp* ops);
 
-// How a fused walk gets its input and cutoff.
+// How a walk gets its input (x[0:4096] for the cutoff, and its slice).
 enum WalkIn : int {
-    kInCutoff = 0,   // x in memory, cutoff from a preceding cutoff launch
-    kInX = 1,        // x in memory; every walk workgroup runs the cutoff search itself
-    kInNorm = 2,     // x = rmsnorm(h) * gain (4096 inputs) computed by every
-                     // walk workgroup (the first one stores it to x), then the search
+    kInCutoff = 0,     // x in memory, cutoff from a preceding cutoff launch
+    kInX = 1,          // x in memory; every walk workgroup runs the cutoff search
+    kInNorm = 2,       // x = rmsnorm(h) * gain (4096 inputs), then the search
+    kInResNorm = 3,    // h = h + (float)delta accumulator (add32), stored; x = rmsnorm(h) * gain
+    kInEmbedNorm = 4,  // h = embedding row of the device token (optionally scaled), stored; x = rmsnorm(h) * gain
+    kInAttn = 5,       // x = o / l from the attention accumulators
 };
 
-// What the reduce does with y after storing it.
-enum Epi : int {
-    kEpStore = 0,   // nothing more
-    kEpResid = 1,   // out += y (add32, bucketMul.cl:517-520)
-    kEpRopeQ = 2,   // out = rope(y) at *pos (rope_mx, aux.cl:227-248)
-    kEpRopeK = 3,   // cache row *pos = fp16(rope(y)) (attention.hpp:172-189, 281-309)
-    kEpV = 4,       // cache row *pos = fp16(y)
-    kEpSilu = 5,    // ops 0 (gate g) and 1 (up u): out = u * g / (1 + exp(-g)) (silu32, matrix.cl:27-32)
+// What happens to the outputs after the flush into the accumulators.
+enum WalkFin : int {
+    kFinNone = 0,    // they stay in the accumulators (the consumer reads them)
+    kFinStore = 1,   // the last workgroup of each column tile stores them as fp32 and clears them
+    kFinSilu = 2,    // matrices 0 (gate) and 1 (up): the last workgroup of each tile stores
+                     // up * gate / (1 + exp(-gate)) (silu32, matrix.cl:27-32) and clears both
 };
 
-struct ReduceEp {
-    int ep = kEpStore;
-    float* out = nullptr;
-    const float* table = nullptr;   // RoPE table [max_ctx][64][2]
-    const int* pos = nullptr;       // device position
-    int max_ctx = 0;
-    uint16_t* cache = nullptr;      // fp16 rows [max_ctx][m]
-};
-
-// record + (norm, cutoff) + walk + reduce with epilogues of one matrix group;
-// ep may be null (store y)
-int bucketmul_fused(Ctx* c, int n, const MatOp* ops, int expert_no, float effort, int in_mode, const float* h,
-                    const uint16_t* gain, float eps, const ReduceEp* ep);
-// size the slots and partial buffers of a group so a later call allocates nothing
-int reserve_walk(Ctx* c, int n, const MatOp* ops, float effort);
 // grid plan of one matrix in a walk launch
 struct WalkPlan {
     int NW;     // waves per workgroup (the same for every matrix of a launch)
-    int V;      // columns per lane load
-    int T;      // column tiles (128 columns for k_walk64, 64 for k_walk)
+    int T;      // column tiles of 128 columns
     int n_in;   // inputs walked
     int IPS;    // inputs per slice
     int P;      // slices
 };
-void plan_walk(int n, const MatOp* ops, float effort, bool acc64, WalkPlan* plan);
-int ensure_attn_ws(Ctx* c, size_t floats);
+void plan_walk(int n, const MatOp* ops, float effort, WalkPlan* plan);
+
+// A matrix group of the decode step (or of a standalone call): up to 3
+// matrices sharing one input mode.  Per matrix: the accumulator (zero on
+// entry), and for the finalize modes the tile counters (zero on entry) and
+// the fp32 outputs.
+struct WalkMat {
+    iam_bucket_matrix mat;
+    int in_size;
+    const float* x;          // kInX / kInCutoff: the input; norm and attention modes: where block 0
+                             // stores the computed input (may be null)
+    float* cutoff;           // the search's result is stored here (kInCutoff: read from here)
+    uint32_t* slice_count;   // [P]
+    void* acc;               // [16 * bucket_cols] of the accumulator type
+    uint32_t* tile_ctr;      // [T]
+    float* y;                // kFinStore: outputs; kFinSilu: the gate / up values (may be null)
+};
+struct WalkGroup {
+    int n = 0;
+    WalkMat m[kMaxMulti];
+    int in_mode = kInX;
+    float effort = 1.0f;
+    int expert_no = 0;
+    const float* h = nullptr;          // kInNorm / kInResNorm
+    const void* res_acc = nullptr;     // kInResNorm (may be null)
+    float* h_out = nullptr;            // kInResNorm / kInEmbedNorm (may be null)
+    const uint16_t* gain = nullptr;
+    float eps = 1e-5f;
+    const uint16_t* embed = nullptr;   // kInEmbedNorm
+    const int* token = nullptr;
+    const float* embed_scale = nullptr;
+    int vocab = 0;
+    const void* attn_acc = nullptr;    // kInAttn
+    int fin = kFinNone;
+    float* silu_out = nullptr;         // kFinSilu
+    // the last finalizing workgroup (kFinStore with pick_ctr): greedy pick
+    // of the stored outputs when token_out is set, then the final clear
+    uint32_t* pick_ctr = nullptr;
+    void* tile_cand = nullptr;         // [T] (value, index)
+    int* token_out = nullptr;
+    int* pos = nullptr;
+    int* hist = nullptr;
+    int hist_len = 0;
+    void* final_zero = nullptr;
+    int final_zero_n = 0;
+    // accumulators cleared by the launch (spread over its workgroups)
+    void* zero_p[2] = {nullptr, nullptr};
+    int zero_n[2] = {0, 0};
+};
+// one walk launch of the group (plan from the matrices and effort)
+int walk_group(Ctx* c, const WalkGroup& g);
+// column tiles of a matrix in a walk launch
+int walk_tiles(int bucket_cols);
+// the largest slice count any plan gives a group of these matrices
+int max_slices(int n, const MatOp* ops, float effort);
+
+// standalone calls: dispatch + walk with fp32 outputs (y), in_mode kInX or
+// kInNorm (the norm of h written to ops[0].x)
+int bucketmul_fused(Ctx* c, int n, const MatOp* ops, int expert_no, float effort, int in_mode, const float* h,
+                    const uint16_t* gain, float eps);
+int ensure_attn_scratch(Ctx* c, size_t acc_words, int n_kv);
 
 int quantile_of(float effort);
 double est_rows(int rows, float effort);

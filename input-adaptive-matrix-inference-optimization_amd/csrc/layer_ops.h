@@ -26,9 +26,27 @@ int add(Ctx* c, const float* a, const float* b, int n, float* out);
 int silu_mul(Ctx* c, const float* g, const float* u, int n, float* out);
 int rope_kv(Ctx* c, const float* q, const float* k, const float* v, const float* table, const int* pos,
             int n_heads, int n_kv, int hd, int max_ctx, float* q_out, uint16_t* kc, uint16_t* vc);
-int attention(Ctx* c, const float* q, const uint16_t* kc, const uint16_t* vc, const int* pos, int n_heads,
-              int n_kv, int max_ctx, float* ws, float* out);
-size_t attention_ws_floats(int n_heads, int max_ctx);
+// one launch of the split-context attention (see k_attn)
+struct AttnLaunch {
+    const float* q = nullptr;          // queries after RoPE, or null: from qkv_acc (RoPE and KV append applied)
+    const void* qkv_acc = nullptr;
+    const float* rope = nullptr;
+    uint16_t* kc = nullptr;
+    uint16_t* vc = nullptr;
+    const int* pos = nullptr;
+    int n_heads = 0, n_kv = 0, max_ctx = 0;
+    void* acc = nullptr;               // o then l accumulators, zero on entry
+    float* out = nullptr;              // standalone: out = o / l
+    uint32_t* head_ctr = nullptr;
+    void* zero_p = nullptr;
+    int zero_n = 0;
+};
+int attention_launch(Ctx* c, const AttnLaunch& L);
+size_t attention_acc_words(int n_heads);
+// h_out = h + (float)delta accumulator (add32), then RMSNorm + gain into out
+// (n = 1024 .. 16384, multiple of 1024); delta may be null
+int resnorm(Ctx* c, const float* h, const void* delta_acc, float* h_out, const uint16_t* gain, int n, float eps,
+            float* out);
 int embed(Ctx* c, const uint16_t* table, int cols, int vocab, const int* tok, float* out);
 // first-max argmax into out[0]; if pos_inc is non-null, *pos_inc += 1
 int argmax(Ctx* c, const float* v, int n, int* out, int* pos_inc);

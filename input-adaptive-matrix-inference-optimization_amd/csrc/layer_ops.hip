@@ -5,6 +5,7 @@
 
 #include <cmath>
 
+#include "accum.h"
 #include "internal.h"
 #include "layer_ops.h"
 #include "wave.h"
@@ -82,6 +83,42 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float* __restrict__ h, const fl
     }
 }
 
+// h_out = h + (float)delta (add32 of an accumulated delta, bucketMul.cl:517-520),
+// then RMSNorm + gain of h_out into out, for any n = 256 * PER (PER <= 64):
+// the same order of sums as k_rmsnorm, two passes over memory.  Used by
+// models wider than the 4096 inputs the walk normalises itself.
+template <typename Dt>
+__global__ __launch_bounds__(256) void k_resnorm(const float* __restrict__ h, const Dt* __restrict__ delta,
+                                                 float* __restrict__ h_out, const uint16_t* __restrict__ gain,
+                                                 float eps, int n, float* __restrict__ out)
+{
+#pragma clang fp contract(off)
+    __shared__ float part[256];
+    const int tid = threadIdx.x;
+    const int per = n / 256;
+    const int b0 = tid * per;
+    float s = 0.0f;
+    for (int k = 0; k < per; k++) {
+        float v = h[b0 + k];
+        if (delta) v = __fadd_rn(v, (float)delta[b0 + k]);
+        if (h_out) h_out[b0 + k] = v;
+        s = __fadd_rn(s, __fmul_rn(v, v));
+    }
+    part[tid] = s;
+    __syncthreads();
+    for (int st = 128; st > 0; st >>= 1) {
+        if (tid < st) part[tid] = __fadd_rn(part[tid], part[tid + st]);
+        __syncthreads();
+    }
+    const float mean = __fdiv_rn(part[0], (float)n);
+    const float scale = (float)(1.0 / sqrt((double)__fadd_rn(mean, eps)));
+    for (int k = 0; k < per; k++) {
+        float v = h[b0 + k];
+        if (delta) v = __fadd_rn(v, (float)delta[b0 + k]);
+        out[b0 + k] = __fmul_rn(h2f(gain[b0 + k]), __fmul_rn(v, scale));
+    }
+}
+
 // ------------------------------------------------------------ residual ---
 __global__ void k_add(const float* __restrict__ a, const float* __restrict__ b, int n,
                       float* __restrict__ out)
@@ -146,23 +183,27 @@ __global__ void k_rope_kv(const float* __restrict__ q, const float* __restrict__
 }
 
 // ------------------------------------------------------------ attention ---
-// Decode attention over an fp16 GQA cache, split over the context
-// ("flash-decoding").  Workgroup (kv head, split) handles kAttnChunk = 64
-// positions for the rep = n_heads/n_kv query heads that read this KV head
-// (repeat4x32, aux.cl:266-275, without materialising the repeat): wave r is
-// query head kvh*rep + r % rep, half r / rep of the head dimension, and lane
-// i position t0 + i.  Each lane computes its position's half dot product
-// (dotSetScore2, aux.cl:497-540, s = q.k / sqrt(hd)) with q broadcast from
-// LDS, and the halves are added through LDS; the softmax of aux.cl:204-225
-// (exp(s)/sum exp(s)) is evaluated with the split's maximum subtracted, which
-// leaves p unchanged; then lane (g, j) accumulates 8 dimensions of the
-// wave's half of sum p*V over every eighth position.  The split's K and V
-// rows are loaded once per workgroup, 16 bytes per thread, into LDS; the
-// split writes its max m, sum l of exp(s - m) and unnormalised o, and
-// k_attn_combine merges the splits (a second launch costs less than a
-// release/acquire handoff between the splits' workgroups).  Acc = double
-// evaluates every product (exact: fp32 x fp16), exponential and sum in fp64
-// and the output is rounded once; Acc = float is the fp32 evaluation.
+// Decode attention over an fp16 GQA cache, split over the context.
+// Workgroup (kv head, split) handles kAttnChunk = 64 positions for the rep =
+// n_heads/n_kv query heads that read this KV head (repeat4x32,
+// aux.cl:266-275, without materialising the repeat): wave r is query head
+// kvh*rep + r % rep and half r / rep of the head dimension, lane i position
+// t0 + i.  Each lane computes its position's half dot product (dotSetScore2,
+// aux.cl:497-540, s = q.k / sqrt(hd)) with q broadcast from LDS, and the
+// halves are added through LDS; p = exp(s) (sum_of_exps32_mx /
+// softmax_add32_mx, aux.cl:204-225: the reference's softmax has no maximum
+// subtracted, so the splits' sums add up directly); then lane (g, j)
+// accumulates 8 dimensions of the wave's half of sum p*V over every eighth
+// position.  The split adds sum p*V and sum p to the accumulators o and l
+// with atomics; out = o / l (sumScores32, aux.cl:370-384) is formed by the
+// consumer (the o projection's walk) or, for the standalone call, by the
+// last split of each KV head.  The split's K and V rows are loaded once per
+// workgroup, 16 bytes per thread, into LDS.  With the projection
+// accumulators as input the workgroup also applies RoPE to q and k (rope_mx,
+// aux.cl:227-248, table row of the position) and the split holding the
+// position appends the new K and V rows to the cache (attention.hpp:281-309)
+// and uses them from LDS.  Acc = double evaluates every product (exact:
+// fp32 x fp16), exponential and sum in fp64; Acc = float in fp32.
 constexpr int kAttnChunk = 64;
 constexpr int kAttnMaxRep = 8;
 constexpr int kMaxAttnSplits = 128;   // max_ctx up to 8192
@@ -174,168 +215,108 @@ __device__ __forceinline__ float acc_exp<float>(float x) { return expf(x); }
 template <>
 __device__ __forceinline__ double acc_exp<double>(double x) { return exp(x); }
 
-template <typename T>
-__device__ __forceinline__ T readlane_t(T v, int l);
-template <>
-__device__ __forceinline__ float readlane_t<float>(float v, int l)
-{
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
-}
-template <>
-__device__ __forceinline__ double readlane_t<double>(double v, int l)
-{
-    const long long b = __double_as_longlong(v);
-    const int lo = __builtin_amdgcn_readlane((int)b, l);
-    const int hi = __builtin_amdgcn_readlane((int)(b >> 32), l);
-    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
-}
-
-// Merge of the na <= kMaxAttnSplits splits of query head h.  Every wave
-// that takes part loads all (m_s, l_s) (lane s holds splits s and s + 64)
-// and computes M, the maximum of the m_s, and w_s = exp(m_s - M); a wave
-// sums l_s * w_s and o_s * w_s over a contiguous range of splits in split
-// order, 16 o loads in flight at a time; out = O / L, lane j writing
-// dimensions 2j, 2j+1.  Up to 16 splits (1024 positions) wave 0 takes them
-// all in one batch and the other waves return; beyond that each of the
-// kCombWaves waves takes a contiguous share and the shares are added in wave
-// order, so the o loads of a long context go out at once instead of in
-// sequential batches.
-constexpr int kCombWaves = 4;
-constexpr int kCombBatch = 16;
-
-template <typename Acc>
-__device__ __forceinline__ void combine_range(const Acc* __restrict__ base, int sb, int se, const Acc (&wv)[2],
-                                              const Acc (&lv)[2], Acc& L, Acc& O0, Acc& O1)
-{
-    constexpr int HD = 128, B = kCombBatch;
-    const int lane = threadIdx.x & 63;
-    L = O0 = O1 = (Acc)0;
-    for (int s0 = sb; s0 < se; s0 += B) {
-        Acc o0[B], o1[B];
-#pragma unroll
-        for (int i = 0; i < B; i++) {
-            const Acc* row = base + (size_t)min(s0 + i, se - 1) * (HD + 2);
-            o0[i] = row[2 * lane];
-            o1[i] = row[2 * lane + 1];
-        }
-#pragma unroll
-        for (int i = 0; i < B; i++) {
-            const int s = s0 + i;
-            if (s < se) {
-                const Acc w = readlane_t(s < 64 ? wv[0] : wv[1], s & 63);
-                L += readlane_t(s < 64 ? lv[0] : lv[1], s & 63) * w;
-                O0 += o0[i] * w;
-                O1 += o1[i] * w;
-            }
-        }
-    }
-}
-
-template <typename Acc>
-__device__ void combine_head(const Acc* __restrict__ ws, int h, int n_split, int na, float* __restrict__ out)
-{
-    constexpr int HD = 128;
-    static_assert(kMaxAttnSplits <= 128, "two splits per lane");
-    __shared__ Acc sO[kCombWaves][HD];
-    __shared__ Acc sL[kCombWaves];
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const bool one = na <= kCombBatch;   // uniform over the workgroup
-    if (one && wave != 0) return;
-    const Acc* base = ws + (size_t)h * n_split * (HD + 2);
-    Acc mv[2], lv[2];
-#pragma unroll
-    for (int k = 0; k < 2; k++) {
-        const int s = lane + 64 * k;
-        mv[k] = s < na ? base[(size_t)s * (HD + 2) + HD] : (Acc)-INFINITY;
-        lv[k] = s < na ? base[(size_t)s * (HD + 2) + HD + 1] : (Acc)0;
-    }
-    const Acc M = wave_max_t(mv[0] > mv[1] ? mv[0] : mv[1]);
-    Acc wv[2];
-#pragma unroll
-    for (int k = 0; k < 2; k++) wv[k] = lane + 64 * k < na ? acc_exp<Acc>(mv[k] - M) : (Acc)0;
-    Acc L, O0, O1;
-    if (one) {
-        combine_range<Acc>(base, 0, na, wv, lv, L, O0, O1);
-        out[h * HD + 2 * lane] = (float)(O0 / L);
-        out[h * HD + 2 * lane + 1] = (float)(O1 / L);
-        return;
-    }
-    const int per = (na + kCombWaves - 1) / kCombWaves;
-    const int sb = wave * per;
-    combine_range<Acc>(base, sb, min(na, sb + per), wv, lv, L, O0, O1);
-    sO[wave][2 * lane] = O0;
-    sO[wave][2 * lane + 1] = O1;
-    if (lane == 0) sL[wave] = L;
-    __syncthreads();
-    if (wave == 0) {
-        Acc Lt = sL[0], Ot0 = sO[0][2 * lane], Ot1 = sO[0][2 * lane + 1];
-#pragma unroll
-        for (int w = 1; w < kCombWaves; w++) {
-            Lt += sL[w];
-            Ot0 += sO[w][2 * lane];
-            Ot1 += sO[w][2 * lane + 1];
-        }
-        out[h * HD + 2 * lane] = (float)(Ot0 / Lt);
-        out[h * HD + 2 * lane + 1] = (float)(Ot1 / Lt);
-    }
-}
+struct AttnArgs {
+    const float* q;          // queries after RoPE (fp32), or null: from qkv_acc
+    const void* qkv_acc;     // the q | k | v accumulators of the projection walk (fp64)
+    const float* rope;       // RoPE table [max_ctx][64][2] (qkv_acc mode)
+    uint16_t* kc;            // fp16 K rows [max_ctx][n_kv][128] of the layer
+    uint16_t* vc;            // fp16 V rows, same layout
+    const int* pos;
+    int n_heads, n_kv, max_ctx;
+    void* acc;               // o [n_heads][128], then l [n_heads] (fp64); zero on entry
+    float* out;              // standalone: out = o / l, stored by the last split of each KV head
+    uint32_t* head_ctr;      // [n_kv] arrival counters (standalone)
+    void* zero_p;            // accumulator words cleared by this launch
+    int zero_n;
+};
 
 // LDS copies of the split's K and V rows: 128 fp16 + 8 fp16 of padding, so
 // that lanes reading 16 bytes of consecutive rows start on different banks.
 constexpr int kAttnRowStride = 128 + 8;
 
-// Two waves per query head: wave r is head hr = r % rep, half hf = r / rep,
-// and takes dimensions [64 hf, 64 hf + 64) of the scores' dot products and
-// of sum p*V.
 template <typename Acc>
-__global__ __launch_bounds__(128 * kAttnMaxRep) void k_attn_partial(const float* __restrict__ q,
-                                                                    const uint16_t* __restrict__ kc,
-                                                                    const uint16_t* __restrict__ vc,
-                                                                    const int* __restrict__ pos_p, int n_heads,
-                                                                    int n_kv, int max_ctx, Acc scale,
-                                                                    Acc* __restrict__ ws, int n_split)
+__global__ __launch_bounds__(128 * kAttnMaxRep) void k_attn(AttnArgs a, Acc scale)
 {
+#pragma clang fp contract(off)
     constexpr int HD = 128, RS = kAttnRowStride, DH = HD / 2;
     __shared__ __align__(16) uint16_t sk[kAttnChunk * RS];
     __shared__ __align__(16) uint16_t sv[kAttnChunk * RS];
     __shared__ Acc sq[kAttnMaxRep][HD];
     __shared__ Acc ss[2][kAttnMaxRep][kAttnChunk];          // half-dot products
     __shared__ Acc sp[2 * kAttnMaxRep][kAttnChunk];         // p, one copy per wave
+    __shared__ double sl[kAttnMaxRep];
+    __shared__ int s_last;
+    const int rep = a.n_heads / a.n_kv;
+    const int nthr = 128 * rep;
+    zero_share<double>(a.zero_p, a.zero_n, nthr);
     const int kvh = blockIdx.x;
     const int split = blockIdx.y;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int r = tid >> 6;
-    const int rep = n_heads / n_kv;
     const int hr = r % rep, hf = r / rep;
-    const int nthr = 128 * rep;
-    int n_tok = *pos_p + 1;
-    if (n_tok > max_ctx) n_tok = max_ctx;
+    const int pos = *a.pos;
+    const int n_tok = min(pos + 1, a.max_ctx);
     const int t0 = split * kAttnChunk;
     const int nt = min(kAttnChunk, max(0, n_tok - t0));
     if (nt == 0) return;   // past the context: neither written nor counted
-    // the split's K and V rows, 16 bytes per thread and load, into LDS
-    const float qv = q[(size_t)(kvh * rep + hr) * HD + hf * DH + lane];
+    const bool pos_ok = pos >= 0 && pos < a.max_ctx;
+    const int h = kvh * rep + hr;
+    const double* A = reinterpret_cast<const double*>(a.qkv_acc);
+    const bool fresh = A && pos_ok && pos >= t0 && pos < t0 + kAttnChunk;   // this split holds the new row
+    float c = 1.0f, sn = 0.0f;
+    if (A && pos_ok) {
+        c = a.rope[(size_t)pos * HD + 2 * lane];
+        sn = a.rope[(size_t)pos * HD + 2 * lane + 1];
+    }
+    // q of dimension hf*64 + lane
+    float qv;
+    if (A) {
+        const float lo = (float)A[(size_t)h * HD + lane], hi = (float)A[(size_t)h * HD + DH + lane];
+        qv = hf == 0 ? __fsub_rn(__fmul_rn(lo, c), __fmul_rn(hi, sn))    // rope_mx: d < 64
+                     : __fadd_rn(__fmul_rn(hi, c), __fmul_rn(lo, sn));   // d >= 64
+    } else {
+        qv = a.q[(size_t)h * HD + hf * DH + lane];
+    }
+    // the split's K and V rows (the fresh row comes from the accumulators)
     const int pieces = nt * (HD / 8);
     for (int b0 = 0; b0 < pieces; b0 += 4 * nthr) {
         uint4 kq[4], vq[4];
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const int idx = min(b0 + u * nthr + tid, pieces - 1);
-            const size_t g = ((size_t)(t0 + (idx >> 4)) * n_kv + kvh) * HD + (idx & 15) * 8;
-            kq[u] = *reinterpret_cast<const uint4*>(kc + g);
-            vq[u] = *reinterpret_cast<const uint4*>(vc + g);
+            const size_t g = ((size_t)(t0 + (idx >> 4)) * a.n_kv + kvh) * HD + (idx & 15) * 8;
+            kq[u] = *reinterpret_cast<const uint4*>(a.kc + g);
+            vq[u] = *reinterpret_cast<const uint4*>(a.vc + g);
         }
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const int idx = b0 + u * nthr + tid;
-            if (idx < pieces) {
+            if (idx < pieces && !(fresh && t0 + (idx >> 4) == pos)) {
                 const int o = (idx >> 4) * RS + (idx & 15) * 8;
                 *reinterpret_cast<uint4*>(sk + o) = kq[u];
                 *reinterpret_cast<uint4*>(sv + o) = vq[u];
             }
         }
+    }
+    if (fresh && r < 2) {
+        // wave 0: k after RoPE; wave 1: v; both rounded to fp16 into the
+        // cache row and the LDS row
+        const int nq = a.n_heads * HD, nk = a.n_kv * HD;
+        const size_t base = (size_t)(r == 0 ? nq : nq + nk) + (size_t)kvh * HD;
+        const float lo = (float)A[base + lane], hi = (float)A[base + DH + lane];
+        float o0 = lo, o1 = hi;
+        if (r == 0) {
+            o0 = __fsub_rn(__fmul_rn(lo, c), __fmul_rn(hi, sn));
+            o1 = __fadd_rn(__fmul_rn(hi, c), __fmul_rn(lo, sn));
+        }
+        const uint16_t h0 = __half_as_ushort(__float2half_rn(o0)), h1 = __half_as_ushort(__float2half_rn(o1));
+        uint16_t* crow = (r == 0 ? a.kc : a.vc) + ((size_t)pos * a.n_kv + kvh) * HD;
+        crow[lane] = h0;
+        crow[DH + lane] = h1;
+        uint16_t* lrow = (r == 0 ? sk : sv) + (pos - t0) * RS;
+        lrow[lane] = h0;
+        lrow[DH + lane] = h1;
     }
     sq[hr][hf * DH + lane] = (Acc)qv;
     __syncthreads();
@@ -354,10 +335,8 @@ __global__ __launch_bounds__(128 * kAttnMaxRep) void k_attn_partial(const float*
         ss[hf][hr][lane] = sh;
     }
     __syncthreads();
-    Acc s = ss[0][hr][lane] + ss[1][hr][lane];
-    s = lane < nt ? s * scale : (Acc)-INFINITY;
-    const Acc m = wave_max_t(s);
-    const Acc p = lane < nt ? acc_exp<Acc>(s - m) : (Acc)0;
+    const Acc s = (ss[0][hr][lane] + ss[1][hr][lane]) * scale;
+    const Acc p = lane < nt ? acc_exp<Acc>(s) : (Acc)0;
     const Acc l = wave_sum(p);
     sp[r][lane] = p;   // read back by this wave only: no barrier
     // sum of p * V over this half's dimensions: lane (g, j) takes dimensions
@@ -385,26 +364,43 @@ __global__ __launch_bounds__(128 * kAttnMaxRep) void k_attn_partial(const float*
         o[e] += __shfl_xor(o[e], 16, 64);
         o[e] += __shfl_xor(o[e], 32, 64);
     }
-    // workspace row of query head h = kvh*rep + hr, split s: ws[(h*n_split + s)*(HD+2)]
-    Acc* wrow = ws + ((size_t)(kvh * rep + hr) * n_split + split) * (HD + 2);
+    double* O = reinterpret_cast<double*>(a.acc);
+    double* Ls = O + (size_t)a.n_heads * HD;
+    if (!a.out) {
+        if (g == 0) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc_add(O + (size_t)h * HD + hf * DH + j * 8 + e, (double)o[e]);
+        }
+        if (hf == 0 && lane == 0) acc_add(Ls + h, (double)l);
+        return;
+    }
+    // standalone: the last split of this KV head forms out = o / l.  The
+    // additions return the old values and the split waits for them before it
+    // arrives, so all are performed where the final atomic reads take them.
+    double sink = 0.0;
     if (g == 0) {
 #pragma unroll
-        for (int e = 0; e < 8; e++) wrow[hf * DH + j * 8 + e] = o[e];
+        for (int e = 0; e < 8; e++)
+            sink += __hip_atomic_fetch_add(O + (size_t)h * HD + hf * DH + j * 8 + e, (double)o[e], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (hf == 0 && lane == 0) {
-        wrow[HD] = m;
-        wrow[HD + 1] = l;
+    if (hf == 0 && lane == 0)
+        sink += __hip_atomic_fetch_add(Ls + h, (double)l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("" ::"v"(sink));
+    __syncthreads();
+    if (tid == 0)
+        s_last = __hip_atomic_fetch_add(a.head_ctr + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (uint32_t)((n_tok + kAttnChunk - 1) / kAttnChunk - 1);
+    __syncthreads();
+    if (!s_last) return;
+    if (tid < rep) sl[tid] = acc_peek(Ls + kvh * rep + tid);
+    __syncthreads();
+    for (int i = tid; i < rep * HD; i += nthr) {
+        const int hh = kvh * rep + i / HD;
+        a.out[(size_t)hh * HD + (i % HD)] = (float)(acc_take(O + (size_t)hh * HD + (i % HD)) / sl[i / HD]);
     }
-}
-
-// Merge of the splits: one wave per query head.
-template <typename Acc>
-__global__ __launch_bounds__(64 * kCombWaves) void k_attn_combine(const Acc* __restrict__ ws, const int* __restrict__ pos_p,
-                                                    int max_ctx, int n_split, float* __restrict__ out)
-{
-    int n_tok = *pos_p + 1;
-    if (n_tok > max_ctx) n_tok = max_ctx;
-    combine_head<Acc>(ws, blockIdx.x, n_split, (n_tok + kAttnChunk - 1) / kAttnChunk, out);
+    if (tid < rep) (void)acc_take(Ls + kvh * rep + tid);
+    if (tid == 0) a.head_ctr[kvh] = 0u;
 }
 
 // ---------------------------------------------------------------- embed ---
@@ -494,6 +490,15 @@ int rmsnorm(Ctx* c, float* h, const float* delta, const uint16_t* gain, int n, f
     }
 }
 
+int resnorm(Ctx* c, const float* h, const void* delta_acc, float* h_out, const uint16_t* gain, int n, float eps,
+            float* out)
+{
+    IAM_REQUIRE(n % 1024 == 0 && n >= 1024 && n <= 256 * kNormMaxPer,
+                "resnorm: n must be a multiple of 1024 in [1024, 16384]");
+    return launch(c, "resnorm", k_resnorm<double>, dim3(1), dim3(256), 0, h, (const double*)delta_acc, h_out, gain,
+                  eps, n, out);
+}
+
 int add(Ctx* c, const float* a, const float* b, int n, float* out)
 {
     return launch(c, "add32", k_add, dim3((n + 255) / 256), dim3(256), 0, a, b, n, out);
@@ -512,35 +517,30 @@ int rope_kv(Ctx* c, const float* q, const float* k, const float* v, const float*
                   n_heads, n_kv, hd, max_ctx, q_out, kc, vc);
 }
 
-// The workspace holds the partials (o[128], m, l) per head and split.
-static size_t attn_partial_floats(int n_heads, int max_ctx)
-{
-    const int n_split = (max_ctx + kAttnChunk - 1) / kAttnChunk;
-    return (size_t)n_heads * n_split * (128 + 2) * 2;
-}
+size_t attention_acc_words(int n_heads) { return (size_t)n_heads * 128 + (size_t)n_heads; }
 
-int attention(Ctx* c, const float* q, const uint16_t* kc, const uint16_t* vc, const int* pos, int n_heads,
-              int n_kv, int max_ctx, float* ws, float* out)
+int attention_launch(Ctx* c, const AttnLaunch& L)
 {
-    const int n_split = (max_ctx + kAttnChunk - 1) / kAttnChunk;
+    const int n_split = (L.max_ctx + kAttnChunk - 1) / kAttnChunk;
     IAM_REQUIRE(n_split <= kMaxAttnSplits, "attention: max_ctx above 8192");
-    if (c->acc64) {
-        const double scale = 1.0 / std::sqrt(128.0);
-        IAM_TRY(launch(c, "attn_partial", k_attn_partial<double>, dim3(n_kv, n_split), dim3(128 * (n_heads / n_kv)),
-                       0, q, kc, vc, pos, n_heads, n_kv, max_ctx, scale, (double*)ws, n_split));
-        return launch(c, "attn_combine", k_attn_combine<double>, dim3(n_heads), dim3(64 * kCombWaves), 0, (const double*)ws, pos,
-                      max_ctx, n_split, out);
-    }
-    const float scale = 1.0f / std::sqrt(128.0f);
-    IAM_TRY(launch(c, "attn_partial", k_attn_partial<float>, dim3(n_kv, n_split), dim3(128 * (n_heads / n_kv)), 0, q,
-                   kc, vc, pos, n_heads, n_kv, max_ctx, scale, ws, n_split));
-    return launch(c, "attn_combine", k_attn_combine<float>, dim3(n_heads), dim3(64 * kCombWaves), 0, (const float*)ws, pos,
-                  max_ctx, n_split, out);
-}
-
-size_t attention_ws_floats(int n_heads, int max_ctx)
-{
-    return attn_partial_floats(n_heads, max_ctx);
+    AttnArgs a{};
+    a.q = L.q;
+    a.qkv_acc = L.qkv_acc;
+    a.rope = L.rope;
+    a.kc = L.kc;
+    a.vc = L.vc;
+    a.pos = L.pos;
+    a.n_heads = L.n_heads;
+    a.n_kv = L.n_kv;
+    a.max_ctx = L.max_ctx;
+    a.acc = L.acc;
+    a.out = L.out;
+    a.head_ctr = L.head_ctr;
+    a.zero_p = L.zero_p;
+    a.zero_n = L.zero_n;
+    const dim3 grid(L.n_kv, n_split), block(128 * (L.n_heads / L.n_kv));
+    if (c->acc64) return launch(c, "attention", k_attn<double>, grid, block, 0, a, 1.0 / std::sqrt(128.0));
+    return launch(c, "attention", k_attn<float>, grid, block, 0, a, 1.0f / std::sqrt(128.0f));
 }
 
 int embed(Ctx* c, const uint16_t* table, int cols, int vocab, const int* tok, float* out)
@@ -681,8 +681,19 @@ int iam_attention_decode(iam_ctx* c, const float* q, const uint16_t* kc, const u
     IAM_TRY(check_dev_range(c, vc, (size_t)max_ctx * nk * 2, "attention vcache"));
     IAM_TRY(check_dev_range(c, out, (size_t)n_heads * head_dim * 4, "attention out"));
     IAM_TRY(check_dev_range(c, pos, 4, "attention pos"));
-    IAM_TRY(ensure_attn_ws(c, attention_ws_floats(n_heads, max_ctx)));
-    return attention(c, q, kc, vc, pos, n_heads, n_kv, max_ctx, c->attn_ws, out);
+    IAM_TRY(ensure_attn_scratch(c, attention_acc_words(n_heads), n_kv));
+    AttnLaunch L{};
+    L.q = q;
+    L.kc = const_cast<uint16_t*>(kc);
+    L.vc = const_cast<uint16_t*>(vc);
+    L.pos = pos;
+    L.n_heads = n_heads;
+    L.n_kv = n_kv;
+    L.max_ctx = max_ctx;
+    L.acc = c->attn_acc;
+    L.out = out;
+    L.head_ctr = c->attn_ctr;
+    return attention_launch(c, L);
 }
 
 int iam_embed_gather(iam_ctx* c, const uint16_t* table, int cols, int vocab, const int* tok, float* out)

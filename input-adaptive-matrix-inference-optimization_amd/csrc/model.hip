@@ -3,14 +3,21 @@
 // MistralModel::forward (model.hpp:152-231) = embedding gather, 32 x
 // TransformerLayer::forward (transformer_layer.hpp:75-122: norm -> attention
 // -> +res -> norm -> FFN -> +res), final norm, LM head, greedy argmax
-// (test_generation.cpp:235/276).  Differences that are the point of the
-// build: q/k/v and gate/up run as one walk launch and one reduce launch per
-// group; the walk computes the RMSNorm of its input and the cutoff itself;
-// the reduce applies the residual add, RoPE with the fp16 KV append, or the
-// SiLU gate to its sums; attention is split over the context (partials, then
-// their merge); the position and token live in device memory, so a whole
-// step is captured once as a HIP graph and replayed per token with no host
-// round trip.
+// (test_generation.cpp:235/276).  A decode step is 5 launches per layer and
+// one for the LM head:
+//   q/k/v walk  (input: residual add of the previous FFN + attention norm;
+//                the first layer gathers the embedding row instead)
+//   attention   (RoPE of q and k and the fp16 KV append in its prologue)
+//   o walk      (input: the attention output o / l)
+//   w1/w3 walk  (input: residual add of o + FFN norm; its tiles' last
+//                workgroups store the SiLU gate)
+//   w2 walk     (input: the gate)
+//   LM head walk (input: residual add + final norm; its last workgroup picks
+//                the next token and advances the position)
+// Each walk flushes its sums into fp64 accumulators with atomics; the next
+// launch reads them, and a later launch clears them (see step()).  The
+// position and token live in device memory, so a whole step is captured
+// once as a HIP graph and replayed per token with no host round trip.
 #include <hip/hip_fp16.h>
 
 #include <cstring>
@@ -54,13 +61,28 @@ struct iam_model {
     float* rope = nullptr;
     float* embed_scale = nullptr;   // optional per-channel scale of the gathered embedding
     bool use_scale = false;
-    // activations
-    float *h = nullptr, *hn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *qr = nullptr;
-    float *att = nullptr, *o = nullptr, *g = nullptr, *u = nullptr, *s = nullptr, *d = nullptr;
+    // residual stream: ha[L] enters layer L, hb[L] enters its FFN block
+    float* ha = nullptr;
+    float* hb = nullptr;
+    float* hidden = nullptr;        // after the last layer
+    float* hn = nullptr;            // the last normalized input (the LM head's, after a step)
+    float* att_x = nullptr;         // the attention output o / l of the last layer
+    float* s = nullptr;             // SiLU gate output [ffn]
+    float* hidden_in = nullptr;     // embedding override staging
+    // accumulators (8 bytes per value): q|k|v, attention o|l, o, gate, up,
+    // down, logits; zero between steps
+    void *acc_qkv = nullptr, *acc_att = nullptr, *acc_o = nullptr, *acc_g = nullptr, *acc_u = nullptr,
+         *acc_d = nullptr, *acc_lm = nullptr;
+    uint32_t* tile_ctr = nullptr;   // gate/up tiles, then LM head tiles, then the pick counter
+    uint2* cand = nullptr;          // LM head tile maxima
+    float* cut = nullptr;           // cutoffs of the last group [3]
+    uint32_t* slice_counts = nullptr;   // [3][slice_cap]
+    int slice_cap = 0;
     float* logits = nullptr;
     int* token = nullptr;
     int* pos = nullptr;
-    int* hist = nullptr;             // token history [max_ctx + 1]
+    int* hist = nullptr;            // token history [max_ctx + 1]
+    int host_pos = 0;               // the position the next step computes
     // captured step
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
@@ -112,184 +134,208 @@ __global__ void k_copy_f32(const float* __restrict__ a, float* __restrict__ b, i
     if (i < n) b[i] = a[i];
 }
 
-// argmax + token history + position advance for the device-driven step
-__global__ __launch_bounds__(1024) void k_pick(const float* __restrict__ v, int n, int* __restrict__ tok,
-                                               int* __restrict__ pos, int* __restrict__ hist, int hist_len)
+static size_t acc_bytes(size_t n) { return n * 8; }
+
+static WalkMat walk_mat(iam_model* m, const Mat& w, int slot, int in_size, void* acc)
 {
-    __shared__ float sv[16];
-    __shared__ int si[16];
-    const int tid = threadIdx.x;
-    float bv = -INFINITY;
-    int bi = n;
-    auto take = [&](float x, int i) {
-        if (x > bv || (x == bv && i < bi)) {
-            bv = x;
-            bi = i;
-        }
-    };
-    // 16-byte loads, 8 per thread in flight (the order of the candidates a
-    // thread sees does not matter: ties go to the smaller index)
-    const int n4 = (reinterpret_cast<uintptr_t>(v) & 15) == 0 ? n >> 2 : 0;
-    const float4* v4 = reinterpret_cast<const float4*>(v);
-    constexpr int U = 8;
-    for (int b0 = 0; b0 < n4; b0 += U * 1024) {
-        float4 r[U];
-#pragma unroll
-        for (int u = 0; u < U; u++) r[u] = v4[min(b0 + u * 1024 + tid, n4 - 1)];
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int j = b0 + u * 1024 + tid;
-            if (j < n4) {
-                take(r[u].x, 4 * j);
-                take(r[u].y, 4 * j + 1);
-                take(r[u].z, 4 * j + 2);
-                take(r[u].w, 4 * j + 3);
-            }
-        }
-    }
-    for (int i = 4 * n4 + tid; i < n; i += 1024) take(v[i], i);
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o, 64);
-        const int oi = __shfl_xor(bi, o, 64);
-        if (ov > bv || (ov == bv && oi < bi)) {
-            bv = ov;
-            bi = oi;
-        }
-    }
-    if ((tid & 63) == 0) {
-        sv[tid >> 6] = bv;
-        si[tid >> 6] = bi;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        for (int w = 1; w < 16; w++)
-            if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) {
-                bv = sv[w];
-                bi = si[w];
-            }
-        const int t = bi < n ? bi : 0;
-        tok[0] = t;
-        const int p = pos[0];
-        if (p + 1 >= 0 && p + 1 < hist_len) hist[p + 1] = t;
-        pos[0] = p + 1;
-    }
+    WalkMat wm{};
+    wm.mat = w.desc();
+    wm.in_size = in_size;
+    wm.cutoff = m->cut + slot;
+    wm.slice_count = m->slice_counts + (size_t)slot * m->slice_cap;
+    wm.acc = acc;
+    return wm;
 }
 
-// One matrix group through bucketmul_fused: x (in memory, or the norm of h
-// written to x), cutoff, walk, reduce with the epilogues ep (null: store).
-static int mat_group(iam_model* m, int n, const Mat* const* mats, float* x, int in_size, float* const* ys,
-                     float effort, int in_mode, const float* h, const uint16_t* gain, const ReduceEp* ep)
-{
-    MatOp ops[kMaxMulti];
-    for (int i = 0; i < n; i++) {
-        ops[i].mat = mats[i]->desc();
-        ops[i].x = x;
-        ops[i].in_size = in_size;
-        ops[i].y = ys[i];
-    }
-    return bucketmul_fused(m->c, n, ops, 0, effort, in_mode, h, gain, m->cfg.norm_eps, ep);
-}
-
-// One decode step reading token/pos from device memory.  logits_out may be
-// the model's own buffer or a caller buffer of vocab floats.  Per layer:
-//   q/k/v walk (attention norm of h fused in) -> reduce + RoPE + fp16 KV append
-//   -> attention -> o walk -> reduce + residual (h += o)
-//   -> w1/w3 walk (FFN norm of h fused in) -> reduce + SiLU gate
-//   -> w2 walk -> reduce + residual (h += d)
-// (transformer_layer.hpp:75-122, attention.hpp:135-202, feedforward.hpp:46-86).
+// One decode step reading token/pos from device memory; logits_out is the
+// model's own buffer or a caller buffer of vocab floats.  With pick, the LM
+// head's last workgroup writes the next token, the history and pos + 1.
+//
+// Accumulators: each is written by one launch and read by the next one(s);
+// the launch after its last reader clears it, so all are zero between steps:
+//   qkv  written by the q/k/v walk, read by attention, cleared by the o walk
+//   att  written by attention, read by the o walk, cleared by the w1/w3 walk
+//   o    written by the o walk, read by the w1/w3 walk, cleared by the w2 walk
+//   gate/up  written by the w1/w3 walk, taken (read and cleared) by its own
+//        tiles' last workgroups
+//   down written by the w2 walk, read by the next q/k/v walk (or the LM
+//        head), cleared by the next attention (or the LM head's last
+//        workgroup)
+//   logits   taken by the LM head's tiles' last workgroups
+// Models wider than 4096 (the walk normalises 4096 inputs itself) run the
+// residual add + norm as a kernel of its own before the walk.
 static int step(iam_model* m, float effort, const float* hidden_override, float* logits_out, bool pick)
 {
     Ctx* c = m->c;
     const iam_model_config& C = m->cfg;
-    const int D = C.dim, F = C.ffn_dim;
-    if (hidden_override) {
-        IAM_TRY(launch(c, "copy_hidden", k_copy_f32, dim3((D + 255) / 256), dim3(256), 0, hidden_override, m->h, D));
-    } else {
-        IAM_TRY(embed(c, m->embed, D, C.vocab, m->token, m->h));
-        if (m->use_scale)
-            IAM_TRY(launch(c, "embed_scale", k_scale_vec, dim3((D + 255) / 256), dim3(256), 0, m->h,
-                           (const float*)m->embed_scale, D));
-    }
-    const size_t kv_layer = (size_t)C.max_ctx * C.n_kv_heads * C.head_dim;
+    const int D = C.dim, F = C.ffn_dim, KVD = C.n_kv_heads * C.head_dim;
+    const bool wide = D != kProbes;
+    const size_t kv_layer = (size_t)C.max_ctx * KVD;
+    char* qkv = static_cast<char*>(m->acc_qkv);
+    const int T13 = walk_tiles(F / 16);
     for (int L = 0; L < C.n_layers; L++) {
         Layer& ly = m->layers[L];
         uint16_t* kc = m->kcache + (size_t)L * kv_layer;
         uint16_t* vc = m->vcache + (size_t)L * kv_layer;
+        float* ha = m->ha + (size_t)L * D;
+        float* hb = m->hb + (size_t)L * D;
+        const float* hprev = L == 0 ? nullptr : m->hb + (size_t)(L - 1) * D;
+        // ---- q, k, v (attention.hpp:160-170) with the attention norm
+        // (transformer_layer.hpp:96-100) and the previous FFN's residual
         {
-            const Mat* mats[3] = {&ly.wq, &ly.wk, &ly.wv};
-            float* ys[3] = {m->q, m->k, m->v};
-            ReduceEp ep[3];
-            ep[0].ep = kEpRopeQ;
-            ep[0].out = m->qr;
-            ep[1].ep = kEpRopeK;
-            ep[1].cache = kc;
-            ep[2].ep = kEpV;
-            ep[2].cache = vc;
-            for (int i = 0; i < 3; i++) {
-                ep[i].table = m->rope;
-                ep[i].pos = m->pos;
-                ep[i].max_ctx = C.max_ctx;
+            WalkGroup g;
+            g.n = 3;
+            g.m[0] = walk_mat(m, ly.wq, 0, D, qkv);
+            g.m[1] = walk_mat(m, ly.wk, 1, D, qkv + acc_bytes(D));
+            g.m[2] = walk_mat(m, ly.wv, 2, D, qkv + acc_bytes(D + KVD));
+            g.effort = effort;
+            g.gain = ly.attn_gain;
+            g.eps = C.norm_eps;
+            if (!wide) {
+                for (int i = 0; i < 3; i++) g.m[i].x = m->hn;
+                if (L > 0) {
+                    g.in_mode = kInResNorm;
+                    g.h = hprev;
+                    g.res_acc = m->acc_d;
+                } else if (hidden_override) {
+                    g.in_mode = kInResNorm;
+                    g.h = hidden_override;
+                } else {
+                    g.in_mode = kInEmbedNorm;
+                    g.embed = m->embed;
+                    g.token = m->token;
+                    g.embed_scale = m->use_scale ? m->embed_scale : nullptr;
+                    g.vocab = C.vocab;
+                }
+                g.h_out = ha;
+            } else {
+                if (L > 0) {
+                    IAM_TRY(resnorm(c, hprev, m->acc_d, ha, ly.attn_gain, D, C.norm_eps, m->hn));
+                } else {
+                    if (hidden_override) {
+                        IAM_TRY(launch(c, "copy_hidden", k_copy_f32, dim3((D + 255) / 256), dim3(256), 0,
+                                       hidden_override, ha, D));
+                    } else {
+                        IAM_TRY(embed(c, m->embed, D, C.vocab, m->token, ha));
+                        if (m->use_scale)
+                            IAM_TRY(launch(c, "embed_scale", k_scale_vec, dim3((D + 255) / 256), dim3(256), 0, ha,
+                                           (const float*)m->embed_scale, D));
+                    }
+                    IAM_TRY(resnorm(c, ha, nullptr, nullptr, ly.attn_gain, D, C.norm_eps, m->hn));
+                }
+                for (int i = 0; i < 3; i++) g.m[i].x = m->hn;
+                g.in_mode = kInX;
             }
-            IAM_TRY(mat_group(m, 3, mats, m->hn, D, ys, effort, kInNorm, m->h, ly.attn_gain, ep));
+            IAM_TRY(walk_group(c, g));
         }
-        IAM_TRY(attention(c, m->qr, kc, vc, m->pos, C.n_heads, C.n_kv_heads, C.max_ctx, c->attn_ws, m->att));
+        // ---- attention (attention.hpp:172-200): RoPE, KV append, split
+        // attention into o|l; clears the previous FFN's down accumulator
         {
-            const Mat* mats[1] = {&ly.wo};
-            float* ys[1] = {m->o};
-            ReduceEp ep[1];
-            ep[0].ep = kEpResid;
-            ep[0].out = m->h;
-            IAM_TRY(mat_group(m, 1, mats, m->att, D, ys, effort, kInX, nullptr, nullptr, ep));
+            AttnLaunch A{};
+            A.qkv_acc = m->acc_qkv;
+            A.rope = m->rope;
+            A.kc = kc;
+            A.vc = vc;
+            A.pos = m->pos;
+            A.n_heads = C.n_heads;
+            A.n_kv = C.n_kv_heads;
+            A.max_ctx = C.max_ctx;
+            A.acc = m->acc_att;
+            A.zero_p = m->acc_d;
+            A.zero_n = D;
+            IAM_TRY(attention_launch(c, A));
         }
+        // ---- o projection (attention.hpp:198-200)
         {
-            const Mat* mats[2] = {&ly.w1, &ly.w3};
-            float* ys[2] = {m->g, m->u};
-            ReduceEp ep[2];
-            ep[0].ep = kEpSilu;
-            ep[0].out = m->s;
-            IAM_TRY(mat_group(m, 2, mats, m->hn, D, ys, effort, kInNorm, m->h, ly.ffn_gain, ep));
+            WalkGroup g;
+            g.n = 1;
+            g.m[0] = walk_mat(m, ly.wo, 0, D, m->acc_o);
+            g.m[0].x = m->att_x;
+            g.effort = effort;
+            g.in_mode = kInAttn;
+            g.attn_acc = m->acc_att;
+            g.zero_p[0] = m->acc_qkv;
+            g.zero_n[0] = D + 2 * KVD;
+            IAM_TRY(walk_group(c, g));
         }
+        // ---- gate and up (feedforward.hpp:60-78) with the residual add of o
+        // and the FFN norm (transformer_layer.hpp:104-112); SiLU gate
         {
-            const Mat* mats[1] = {&ly.w2};
-            float* ys[1] = {m->d};
-            ReduceEp ep[1];
-            ep[0].ep = kEpResid;
-            ep[0].out = m->h;
-            IAM_TRY(mat_group(m, 1, mats, m->s, F, ys, effort, kInX, nullptr, nullptr, ep));
+            WalkGroup g;
+            g.n = 2;
+            g.m[0] = walk_mat(m, ly.w1, 0, D, m->acc_g);
+            g.m[1] = walk_mat(m, ly.w3, 1, D, m->acc_u);
+            g.m[0].tile_ctr = g.m[1].tile_ctr = m->tile_ctr;
+            g.effort = effort;
+            g.gain = ly.ffn_gain;
+            g.eps = C.norm_eps;
+            if (!wide) {
+                g.in_mode = kInResNorm;
+                g.h = ha;
+                g.res_acc = m->acc_o;
+                g.h_out = hb;
+                g.m[0].x = g.m[1].x = m->hn;
+            } else {
+                IAM_TRY(resnorm(c, ha, m->acc_o, hb, ly.ffn_gain, D, C.norm_eps, m->hn));
+                g.in_mode = kInX;
+                g.m[0].x = g.m[1].x = m->hn;
+            }
+            g.fin = kFinSilu;
+            g.silu_out = m->s;
+            g.zero_p[0] = m->acc_att;
+            g.zero_n[0] = (int)attention_acc_words(C.n_heads);
+            IAM_TRY(walk_group(c, g));
+        }
+        // ---- down (feedforward.hpp:82-84)
+        {
+            WalkGroup g;
+            g.n = 1;
+            g.m[0] = walk_mat(m, ly.w2, 0, F, m->acc_d);
+            g.m[0].x = m->s;
+            g.effort = effort;
+            g.in_mode = kInX;
+            g.zero_p[0] = m->acc_o;
+            g.zero_n[0] = D;
+            IAM_TRY(walk_group(c, g));
         }
     }
+    // ---- final norm + LM head (model.hpp:181-227) + greedy pick
     {
-        const Mat* mats[1] = {&m->lm};
-        float* ys[1] = {logits_out};
-        IAM_TRY(mat_group(m, 1, mats, m->hn, D, ys, effort, kInNorm, m->h, m->final_gain, nullptr));
-    }
-    if (pick)
-        IAM_TRY(launch(c, "pick", k_pick, dim3(1), dim3(1024), 0, (const float*)logits_out, C.vocab, m->token,
-                       m->pos, m->hist, C.max_ctx + 1));
-    return IAM_OK;
-}
-
-// size the dispatch slots, walk partials and attention workspace for every
-// matrix group of a step at this effort, so a step never allocates (which
-// graph capture requires)
-static int reserve(iam_model* m, float effort)
-{
-    Ctx* c = m->c;
-    const iam_model_config& C = m->cfg;
-    for (int s = 0; s < kMaxMulti; s++) IAM_TRY(ensure_slot(c, s));
-    const Layer& ly = m->layers[0];
-    const Mat* groups[5][3] = {{&ly.wq, &ly.wk, &ly.wv}, {&ly.wo}, {&ly.w1, &ly.w3}, {&ly.w2}, {&m->lm}};
-    const int sizes[5] = {3, 1, 2, 1, 1};
-    const int ins[5] = {C.dim, C.dim, C.dim, C.ffn_dim, C.dim};
-    for (int gi = 0; gi < 5; gi++) {
-        MatOp ops[kMaxMulti];
-        for (int i = 0; i < sizes[gi]; i++) {
-            ops[i].mat = groups[gi][i]->desc();
-            ops[i].in_size = ins[gi];
+        const float* hlast = m->hb + (size_t)(C.n_layers - 1) * D;
+        WalkGroup g;
+        g.n = 1;
+        g.m[0] = walk_mat(m, m->lm, 0, D, m->acc_lm);
+        g.m[0].tile_ctr = m->tile_ctr + T13;
+        g.m[0].y = logits_out;
+        g.m[0].x = m->hn;
+        g.effort = effort;
+        g.gain = m->final_gain;
+        g.eps = C.norm_eps;
+        if (!wide) {
+            g.in_mode = kInResNorm;
+            g.h = hlast;
+            g.res_acc = m->acc_d;
+            g.h_out = m->hidden;
+        } else {
+            IAM_TRY(resnorm(c, hlast, m->acc_d, m->hidden, m->final_gain, D, C.norm_eps, m->hn));
+            g.in_mode = kInX;
         }
-        IAM_TRY(reserve_walk(c, sizes[gi], ops, effort));
+        g.fin = kFinStore;
+        const int Tlm = walk_tiles(C.vocab / 16);
+        g.pick_ctr = m->tile_ctr + T13 + Tlm;
+        g.tile_cand = m->cand;
+        if (pick) {
+            g.token_out = m->token;
+            g.pos = m->pos;
+            g.hist = m->hist;
+            g.hist_len = C.max_ctx + 1;
+        }
+        g.final_zero = m->acc_d;
+        g.final_zero_n = D;
+        IAM_TRY(walk_group(c, g));
     }
-    return ensure_attn_ws(c, attention_ws_floats(C.n_heads, C.max_ctx));
+    (void)T13;
+    return IAM_OK;
 }
 
 static int drop_graph(iam_model* m)
@@ -306,11 +352,10 @@ static int capture_step(iam_model* m, float effort, bool override_hidden)
 {
     Ctx* c = m->c;
     IAM_TRY(drop_graph(m));
-    IAM_TRY(reserve(m, effort));
     IAM_CHECK_HIP(hipStreamSynchronize(c->stream));
     IAM_CHECK_HIP(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
     c->capturing = true;
-    int rc = step(m, effort, override_hidden ? m->s : nullptr, m->logits, true);
+    int rc = step(m, effort, override_hidden ? m->hidden_in : nullptr, m->logits, true);
     c->capturing = false;
     hipGraph_t g = nullptr;
     hipError_t e = hipStreamEndCapture(c->stream, &g);
@@ -369,9 +414,11 @@ static bool lookup(iam_model* m, const std::string& name, TensorRef* out, const 
     else if (head == "logits") *out = {m->logits, V * 4};
     else if (head == "token") *out = {m->token, 4};
     else if (head == "pos") *out = {m->pos, 4};
-    else if (head == "hidden") *out = {m->h, D * 4};
-    else if (head == "hidden_in") *out = {m->s, D * 4};
+    else if (head == "hidden") *out = {m->hidden, D * 4};
+    else if (head == "hidden_in") *out = {m->hidden_in, D * 4};
     else if (head == "hidden_norm") *out = {m->hn, D * 4};
+    else if (head == "attention_out") *out = {m->att_x, D * 4};
+    else if (head == "ffn_act") *out = {m->s, (size_t)C.ffn_dim * 4};
     else if (head == "embed_scale") *out = {m->embed_scale, D * 4};
     else if (head == "history") *out = {m->hist, (size_t)(C.max_ctx + 1) * 4};
     else if (head.rfind("layer", 0) == 0) {
@@ -386,6 +433,8 @@ static bool lookup(iam_model* m, const std::string& name, TensorRef* out, const 
         std::string w, part;
         split(rest, w, part);
         if (w == "attn_gain") *out = {ly.attn_gain, D * 2};
+        else if (w == "h_in") *out = {m->ha + (size_t)L * D, D * 4};
+        else if (w == "h_mid") *out = {m->hb + (size_t)L * D, D * 4};
         else if (w == "ffn_gain") *out = {ly.ffn_gain, D * 2};
         else if (w == "wq") return matparts(ly.wq, part);
         else if (w == "wk") return matparts(ly.wk, part);
@@ -466,10 +515,23 @@ int iam_model_create(iam_ctx* c, const iam_model_config* cfg, iam_model** out)
     T(alloc_t(m, kv, &m->vcache));
     T(alloc_t(m, (size_t)C.max_ctx * C.head_dim, &m->rope));
     T(alloc_t(m, D, &m->embed_scale));
-    for (float** p : {&m->h, &m->hn, &m->q, &m->qr, &m->att, &m->o, &m->d}) T(alloc_t(m, D, p));
-    T(alloc_t(m, KVD, &m->k));
-    T(alloc_t(m, KVD, &m->v));
-    for (float** p : {&m->g, &m->u, &m->s}) T(alloc_t(m, F, p));
+    T(alloc_t(m, (size_t)C.n_layers * D, &m->ha));
+    T(alloc_t(m, (size_t)C.n_layers * D, &m->hb));
+    for (float** p : {&m->hidden, &m->hn, &m->att_x, &m->hidden_in}) T(alloc_t(m, D, p));
+    T(alloc_t(m, F, &m->s));
+    T(alloc_owned(m, acc_bytes(D + 2 * KVD), &m->acc_qkv));
+    T(alloc_owned(m, acc_bytes(attention_acc_words(C.n_heads)), &m->acc_att));
+    T(alloc_owned(m, acc_bytes(D), &m->acc_o));
+    T(alloc_owned(m, acc_bytes(F), &m->acc_g));
+    T(alloc_owned(m, acc_bytes(F), &m->acc_u));
+    T(alloc_owned(m, acc_bytes(D), &m->acc_d));
+    T(alloc_owned(m, acc_bytes(C.vocab), &m->acc_lm));
+    const int T13 = walk_tiles(F / 16), Tlm = walk_tiles(C.vocab / 16);
+    T(alloc_t(m, (size_t)T13 + Tlm + 1, &m->tile_ctr));
+    T(alloc_t(m, (size_t)Tlm, &m->cand));
+    T(alloc_t(m, 3, &m->cut));
+    m->slice_cap = std::max(D, F);   // a slice holds at least one input
+    T(alloc_t(m, (size_t)3 * m->slice_cap, &m->slice_counts));
     T(alloc_t(m, C.vocab, &m->logits));
     T(alloc_t(m, 1, &m->token));
     T(alloc_t(m, 1, &m->pos));
@@ -538,7 +600,18 @@ int iam_model_reset_caches(iam_model* m)
     IAM_TRY(zero_async(m->c, m->hist, (size_t)(C.max_ctx + 1) * 4));
     IAM_TRY(zero_async(m->c, m->pos, 4));
     IAM_TRY(zero_async(m->c, m->token, 4));
+    // the accumulators and counters are zero between steps; clear them
+    // anyway, so that a reset also recovers from an interrupted step
+    const int D = C.dim, F = C.ffn_dim, KVD = C.n_kv_heads * C.head_dim;
+    IAM_TRY(zero_async(m->c, m->acc_qkv, acc_bytes(D + 2 * KVD)));
+    IAM_TRY(zero_async(m->c, m->acc_att, acc_bytes(attention_acc_words(C.n_heads))));
+    for (void* p : {m->acc_o, m->acc_d}) IAM_TRY(zero_async(m->c, p, acc_bytes(D)));
+    for (void* p : {m->acc_g, m->acc_u}) IAM_TRY(zero_async(m->c, p, acc_bytes(F)));
+    IAM_TRY(zero_async(m->c, m->acc_lm, acc_bytes(C.vocab)));
+    const int T13 = walk_tiles(F / 16), Tlm = walk_tiles(C.vocab / 16);
+    IAM_TRY(zero_async(m->c, m->tile_ctr, ((size_t)T13 + Tlm + 1) * 4));
     IAM_CHECK_HIP(hipStreamSynchronize(m->c->stream));
+    m->host_pos = 0;
     return IAM_OK;
 }
 
@@ -550,9 +623,10 @@ int iam_model_forward(iam_model* m, int token, int pos, float effort, float* log
     IAM_REQUIRE(token >= 0 && token < C.vocab, "model_forward: token outside the vocabulary");
     IAM_REQUIRE(!std::isnan(effort), "model_forward: effort is NaN");
     IAM_TRY(check_dev_range(m->c, logits, (size_t)C.vocab * 4, "model_forward logits"));
-    IAM_TRY(reserve(m, effort));
+    IAM_REQUIRE(((uintptr_t)logits & 15) == 0, "model_forward: logits must be 16-byte aligned");
     IAM_TRY(launch(m->c, "set_int", k_set_int, dim3(1), dim3(1), 0, m->token, token));
     IAM_TRY(launch(m->c, "set_int", k_set_int, dim3(1), dim3(1), 0, m->pos, pos));
+    m->host_pos = pos;   // forward does not advance the position
     return step(m, effort, nullptr, logits, false);
 }
 
@@ -560,9 +634,15 @@ int iam_model_step_device(iam_model* m, float effort, const float* hidden_overri
 {
     if (!m) return fail(IAM_E_INVALID, "model_step: null model");
     IAM_REQUIRE(!std::isnan(effort), "model_step: effort is NaN");
-    if (hidden_override) IAM_TRY(check_dev_range(m->c, hidden_override, (size_t)m->cfg.dim * 4, "model_step hidden"));
-    IAM_TRY(reserve(m, effort));
-    return step(m, effort, hidden_override, m->logits, true);
+    if (hidden_override) {
+        IAM_TRY(check_dev_range(m->c, hidden_override, (size_t)m->cfg.dim * 4, "model_step hidden"));
+        IAM_REQUIRE(((uintptr_t)hidden_override & 15) == 0, "model_step: hidden must be 16-byte aligned");
+    }
+    IAM_REQUIRE(m->host_pos >= 0 && m->host_pos < m->cfg.max_ctx,
+                "model_step: the position has reached the KV capacity");
+    IAM_TRY(step(m, effort, hidden_override, m->logits, true));
+    m->host_pos++;
+    return IAM_OK;
 }
 
 int iam_model_generate(iam_model* m, const int* prompt, int n_prompt, int n_new, float effort, int use_graph,
@@ -576,8 +656,8 @@ int iam_model_generate(iam_model* m, const int* prompt, int n_prompt, int n_new,
     for (int i = 0; i < n_prompt; i++)
         IAM_REQUIRE(prompt[i] >= 0 && prompt[i] < C.vocab, "generate: prompt token outside the vocabulary");
     Ctx* c = m->c;
-    IAM_TRY(reserve(m, effort));
     IAM_TRY(launch(c, "set_int", k_set_int, dim3(1), dim3(1), 0, m->pos, 0));
+    m->host_pos = 0;
     if (use_graph && (m->exec == nullptr || m->graph_effort != effort || m->graph_override ||
                       m->graph_gen != c->scratch_gen))
         IAM_TRY(capture_step(m, effort, false));
@@ -596,6 +676,7 @@ int iam_model_generate(iam_model* m, const int* prompt, int n_prompt, int n_new,
     // the pick of the last prompt step is the first new token; each further
     // step consumes the token the previous step picked
     for (int t = 1; t < n_new; t++) IAM_TRY(one());
+    m->host_pos = n_prompt + std::max(n_new - 1, 0);
     if (n_new > 0) {
         std::vector<int> hist(C.max_ctx + 1);
         IAM_CHECK_HIP(hipMemcpyAsync(hist.data(), m->hist, hist.size() * 4, hipMemcpyDeviceToHost, c->stream));
@@ -611,7 +692,9 @@ int iam_model_decode(iam_model* m, int n_steps, float effort, int use_graph)
     IAM_REQUIRE(n_steps >= 0, "decode: negative step count");
     IAM_REQUIRE(!std::isnan(effort), "decode: effort is NaN");
     Ctx* c = m->c;
-    IAM_TRY(reserve(m, effort));
+    // positions host_pos .. host_pos + n_steps - 1 must fit the KV cache
+    IAM_REQUIRE(m->host_pos >= 0 && (int64_t)m->host_pos + n_steps <= m->cfg.max_ctx,
+                "decode: the steps would pass the KV capacity");
     if (use_graph && (m->exec == nullptr || m->graph_effort != effort || m->graph_override ||
                       m->graph_gen != c->scratch_gen))
         IAM_TRY(capture_step(m, effort, false));
@@ -619,6 +702,7 @@ int iam_model_decode(iam_model* m, int n_steps, float effort, int use_graph)
         if (use_graph) IAM_CHECK_HIP(hipGraphLaunch(m->exec, c->stream));
         else IAM_TRY(step(m, effort, nullptr, m->logits, true));
     }
+    m->host_pos += n_steps;
     return IAM_OK;
 }
 
@@ -639,6 +723,15 @@ int iam_model_matrix(iam_model* m, const char* name, iam_bucket_matrix* out)
     const Mat* w = nullptr;
     if (!lookup(m, name, &r, &w) || !w) return fail(IAM_E_INVALID, std::string("model_matrix: unknown ") + name);
     *out = w->desc();
+    return IAM_OK;
+}
+
+int iam_model_set_position(iam_model* m, int pos)
+{
+    if (!m) return fail(IAM_E_INVALID, "set_position: null model");
+    IAM_REQUIRE(pos >= 0 && pos <= m->cfg.max_ctx, "set_position: pos outside [0, max_ctx]");
+    IAM_TRY(launch(m->c, "set_int", k_set_int, dim3(1), dim3(1), 0, m->pos, pos));
+    m->host_pos = pos;
     return IAM_OK;
 }
 

@@ -72,7 +72,6 @@ int ensure_slot(Ctx* c, int slot)
     if (!s.cutoff) {
         if (c->capturing) return fail(IAM_E_STATE, "dispatch buffer allocation during graph capture");
         IAM_TRY(ctx_alloc(c, 16, (void**)&s.cutoff));
-        IAM_TRY(ctx_alloc(c, 16, (void**)&s.count));
         c->scratch_gen++;
     }
     return IAM_OK;
@@ -91,31 +90,37 @@ int ensure_list(Ctx* c, int slot, int chunks)
     return IAM_OK;
 }
 
-int ensure_partials(Ctx* c, int slot, size_t bytes)
+// Grow a zero-initialised scratch buffer of `count` elements of `elem` bytes.
+static int grow_zeroed(Ctx* c, void** p, size_t* cap, size_t count, size_t elem, const char* what)
 {
-    DispatchSlot& s = c->slots[slot];
-    if (bytes <= s.part_cap) return IAM_OK;
-    if (c->capturing) return fail(IAM_E_STATE, "partial buffer growth during graph capture");
-    if (s.part) IAM_TRY(ctx_free(c, s.part));
-    s.part = nullptr;
-    s.part_cap = 0;
-    IAM_TRY(ctx_alloc(c, bytes, &s.part));
-    s.part_cap = bytes;
+    if (count <= *cap && *p) return IAM_OK;
+    if (c->capturing) return fail(IAM_E_STATE, std::string(what) + " growth during graph capture");
+    if (*p) IAM_TRY(ctx_free(c, *p));
+    *p = nullptr;
+    *cap = 0;
+    const size_t n = std::max<size_t>(count, 1);
+    IAM_TRY(ctx_alloc(c, n * elem, p));
+    IAM_TRY(zero_async(c, *p, n * elem));
+    *cap = n;
     c->scratch_gen++;
     return IAM_OK;
 }
 
-int ensure_attn_ws(Ctx* c, size_t floats)
+int ensure_walk_scratch(Ctx* c, int slot, size_t m, size_t T, size_t P)
 {
-    if (floats <= c->attn_ws_floats) return IAM_OK;
-    if (c->capturing) return fail(IAM_E_STATE, "attention workspace growth during graph capture");
-    if (c->attn_ws) IAM_TRY(ctx_free(c, c->attn_ws));
-    c->attn_ws = nullptr;
-    c->attn_ws_floats = 0;
-    IAM_TRY(ctx_alloc(c, floats * sizeof(float), (void**)&c->attn_ws));
-    c->attn_ws_floats = floats;
-    c->scratch_gen++;
+    DispatchSlot& s = c->slots[slot];
+    IAM_TRY(grow_zeroed(c, &s.acc, &s.acc_cap, m, 8, "walk accumulator"));
+    IAM_TRY(grow_zeroed(c, (void**)&s.tile_ctr, &s.tile_cap, T, sizeof(uint32_t), "walk tile counter"));
+    IAM_TRY(grow_zeroed(c, (void**)&s.slice_count, &s.slice_cap, P, sizeof(uint32_t), "walk slice count"));
     return IAM_OK;
+}
+
+int ensure_attn_scratch(Ctx* c, size_t acc_words, int n_kv)
+{
+    IAM_TRY(grow_zeroed(c, &c->attn_acc, &c->attn_acc_cap, acc_words, 8, "attention accumulator"));
+    size_t cap = c->attn_ctr ? 64 : 0;
+    IAM_REQUIRE(n_kv <= 64, "attention: at most 64 KV heads");
+    return grow_zeroed(c, (void**)&c->attn_ctr, &cap, 64, sizeof(uint32_t), "attention counter");
 }
 
 int begin_launch(Ctx* c, const char* name, PendingEvent* ev)
@@ -217,8 +222,9 @@ int iam_ctx_create(int device, iam_ctx** out)
     c->total_mem = total_b;
     const size_t margin = 512ull << 20;   // gpu.hpp:28 safety margin
     c->usable = total_b > margin ? total_b - margin : total_b;
-    int rc = ctx_alloc(c, 4 * sizeof(unsigned long long), (void**)&c->counters);
-    if (rc == IAM_OK) rc = zero_async(c, c->counters, 4 * sizeof(unsigned long long));
+    const size_t cbytes = kCounterLanes * 4 * sizeof(unsigned long long);
+    int rc = ctx_alloc(c, cbytes, (void**)&c->counters);
+    if (rc == IAM_OK) rc = zero_async(c, c->counters, cbytes);
     if (rc == IAM_OK && hipStreamSynchronize(c->stream) != hipSuccess) rc = fail(IAM_E_HIP, "ctx_create: sync");
     if (rc != IAM_OK) {
         std::string err = g_last_error;
@@ -433,12 +439,15 @@ int iam_kernel_stats(iam_ctx* c, char* buf, size_t len)
 int iam_walk_counters(iam_ctx* c, uint64_t* bytes, uint64_t* rows, uint64_t* mats, int reset)
 {
     if (!c) return fail(IAM_E_INVALID, "walk_counters: null context");
-    unsigned long long h[4] = {0, 0, 0, 0};
+    unsigned long long h[kCounterLanes * 4];
     IAM_CHECK_HIP(hipMemcpyAsync(h, c->counters, sizeof(h), hipMemcpyDeviceToHost, c->stream));
     IAM_CHECK_HIP(hipStreamSynchronize(c->stream));
-    if (bytes) *bytes = h[0];
-    if (rows) *rows = h[1];
-    if (mats) *mats = h[2];
+    unsigned long long t[3] = {0, 0, 0};
+    for (int l = 0; l < kCounterLanes; l++)
+        for (int i = 0; i < 3; i++) t[i] += h[l * 4 + i];
+    if (bytes) *bytes = t[0];
+    if (rows) *rows = t[1];
+    if (mats) *mats = t[2];
     if (reset) {
         IAM_TRY(zero_async(c, c->counters, sizeof(h)));
         IAM_CHECK_HIP(hipStreamSynchronize(c->stream));
@@ -472,7 +481,7 @@ int iam_set_walk_counting(iam_ctx* c, int on)
     IAM_REQUIRE(!c->capturing, "set_walk_counting: not allowed during graph capture");
     if ((on != 0) != c->counting) {
         c->counting = on != 0;
-        c->scratch_gen++;   // captured graphs hold reduce launches of the other setting
+        c->scratch_gen++;   // captured graphs hold walk launches of the other setting
     }
     return IAM_OK;
 }

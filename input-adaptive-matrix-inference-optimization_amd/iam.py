@@ -350,6 +350,9 @@ class Model:
     def decode(self, n_steps, effort, use_graph=True):
         check(lib().iam_model_decode(self.h, n_steps, C.c_float(effort), 1 if use_graph else 0))
 
+    def set_position(self, pos):
+        check(lib().iam_model_set_position(self.h, int(pos)))
+
     def set_embed_scale(self, scale):
         if scale is None:
             check(lib().iam_model_set_embed_scale(self.h, None))
