@@ -29,6 +29,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <type_traits>
 #include <vector>
 
 #include "accum.h"
@@ -258,7 +259,7 @@ __device__ __forceinline__ void lds_add(uint32_t byte_offset, int elem, T v)
 
 constexpr int kTileCols = 128;
 constexpr int kTileOut = kTileCols * 16;     // outputs per column tile
-constexpr int kTilePitch = kTileCols + 1;    // LDS slots per position row (one pad)
+constexpr int kTilePitch = kTileCols;        // LDS slots per position row
 
 struct WalkDesc {
     const uint16_t* W;        // rows of the expert: W[row * C + col]
@@ -450,15 +451,17 @@ __device__ __forceinline__ void take_max(float& bv, int& bi, float v, int i)
 // in fp64), to the wave's own accumulator of its output (column c, position
 // bits & 15) with a non-returning LDS atomic add (bucketMul.cl:430-445 adds
 // the product with a plain += per work-item).  The accumulator of (column
-// 8j+e, position pos) is slot pos*129 + e*16 + j: the 16 lanes of a row (one
-// position) hit 16 consecutive slots, and the 16 positions of one column hit
-// 16 different bank pairs, so both the walk and the flush below are free of
-// bank conflicts.  Rows past the end of the list re-read the last selected
+// 8j+e, position pos) is slot pos*128 + e*16 + j: whatever the positions of
+// the 64 lanes' weights (each weight carries its own), an instruction's
+// lanes j of the 4 rows map to 16 bank pairs set by j alone, so the walk's
+// LDS atomics never conflict beyond the 4 rows sharing a bank pair (the
+// fewest passes 64 8-byte accumulators need).  Two batches of rows are in
+// flight per wave.  Rows past the end of the list re-read the last selected
 // row with x = 0, so every load of a batch is unconditional.
 //
-// Flush: thread -> output (column-major, col*16 + pos, the reference's output
-// index, bucketMul.cl:442-445), sum of the wave tiles in wave order, one
-// atomic add per output and workgroup.
+// Flush: sums of the wave tiles in wave order, staged in output order
+// (column-major, col*16 + pos, the reference's output index,
+// bucketMul.cl:442-445), one atomic add per output and workgroup.
 template <typename Acc, int NW, int UNR>
 __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
 {
@@ -614,10 +617,14 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
         const uint16_t* wb = d.W + (size_t)i0 * 16 * d.C + col0;
         const uint32_t tbase = lds_offset(tiles) + (uint32_t)(wave * TSLOTS + j) * (uint32_t)sizeof(Acc);
         const int ng = (ns + 3) >> 2;
-        int rl[UNR];
-        float xl[UNR];
-        uint4 v[UNR];
-        auto issue = [&](int g0) {
+        // one instance of the loop per row load shape, so that no branch sits
+        // in its steady state
+        auto walk_rows = [&](auto whole_tag) {
+        constexpr bool WHOLE = decltype(whole_tag)::value;
+        // batch g0: rows (g0 + u*NW)*4 + q, u < UNR, into one register set
+        auto issue = [&](int g0, uint4 (&v)[UNR], Acc (&xc)[UNR]) {
+            int rl[UNR];
+            float xl[UNR];
 #pragma unroll
             for (int u = 0; u < UNR; u++) {
                 const int idx = (g0 + u * NW) * 4 + q;
@@ -625,8 +632,8 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
                 xl[u] = idx < ns ? 1.0f : 0.0f;
             }
 #pragma unroll
-            for (int u = 0; u < UNR; u++) xl[u] *= s_x[rl[u] >> 4];
-            if (whole) {
+            for (int u = 0; u < UNR; u++) xc[u] = (Acc)(xl[u] * s_x[rl[u] >> 4]);
+            if constexpr (WHOLE) {
 #pragma unroll
                 for (int u = 0; u < UNR; u++) v[u] = *reinterpret_cast<const uint4*>(wb + __umul24(rl[u], d.C));
             } else {
@@ -640,20 +647,10 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
                 }
             }
         };
-        if (wave < ng) issue(wave);
-        for (int g0 = wave; g0 < ng; g0 += GSTRIDE) {
-            uint4 vc[UNR];
-            Acc xc[UNR];
+        auto consume = [&](const uint4 (&v)[UNR], const Acc (&xc)[UNR]) {
 #pragma unroll
             for (int u = 0; u < UNR; u++) {
-                vc[u] = v[u];
-                xc[u] = (Acc)xl[u];
-            }
-            if (g0 + GSTRIDE < ng) issue(g0 + GSTRIDE);
-            asm volatile("" ::: "memory");
-#pragma unroll
-            for (int u = 0; u < UNR; u++) {
-                const uint32_t words[4] = {vc[u].x, vc[u].y, vc[u].z, vc[u].w};
+                const uint32_t words[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
                     const uint32_t hw = words[e >> 1] >> ((e & 1) * 16);
@@ -664,14 +661,72 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
                     lds_add<Acc>(__umul24(pos, kTilePitch * (uint32_t)sizeof(Acc)) + tbase, e * 16, xc[u] * (Acc)h2f(hw));
                 }
             }
+        };
+        // two batches in flight: the steady state issues unconditionally
+        // (so the waits before each batch's use count exactly the other
+        // batch's loads) and keeps the phases apart; the tail takes the last
+        // one to three batches
+        uint4 va[UNR], vb[UNR];
+        Acc xa[UNR], xb[UNR];
+        int g = wave;
+        if (g + 3 * GSTRIDE < ng) {
+            issue(g, va, xa);
+            issue(g + GSTRIDE, vb, xb);
+            do {
+                consume(va, xa);
+                __builtin_amdgcn_sched_barrier(0);
+                issue(g + 2 * GSTRIDE, va, xa);
+                __builtin_amdgcn_sched_barrier(0);
+                consume(vb, xb);
+                __builtin_amdgcn_sched_barrier(0);
+                issue(g + 3 * GSTRIDE, vb, xb);
+                __builtin_amdgcn_sched_barrier(0);
+                g += 2 * GSTRIDE;
+            } while (g + 3 * GSTRIDE < ng);
+        } else {
+            if (g < ng) issue(g, va, xa);
+            if (g + GSTRIDE < ng) issue(g + GSTRIDE, vb, xb);
         }
+        if (g < ng) consume(va, xa);
+        if (g + 2 * GSTRIDE < ng) issue(g + 2 * GSTRIDE, va, xa);
+        if (g + GSTRIDE < ng) consume(vb, xb);
+        if (g + 2 * GSTRIDE < ng) consume(va, xa);
+        };
+        if (whole) walk_rows(std::true_type{});
+        else walk_rows(std::false_type{});
     }
     __syncthreads();
 
-    // ---- flush
+    // ---- flush: the wave tiles summed in wave order, read in slot order
+    // (free of bank conflicts), staged in LDS in output order (col*16 + pos,
+    // the reference's output index, bucketMul.cl:442-445; one pad per 128
+    // entries keeps the staging writes and the reads after them free of
+    // conflicts too), then one atomic add per output and workgroup over
+    // consecutive outputs.
     constexpr int OPT = kTileOut / NT;
+    static_assert(NW * TSLOTS >= kTileOut + kTileOut / 128, "the staging copy fits the tiles");
     double* out = reinterpret_cast<double*>(d.acc) + (size_t)t * kTileOut;
     const int nout = min(kTileOut, (d.C - t * kTileCols) * 16);
+    {
+        Acc sum[OPT];
+#pragma unroll
+        for (int k2 = 0; k2 < OPT; k2++) {
+            const int sl = tid + k2 * NT;
+            Acc sv = tiles[sl];
+#pragma unroll
+            for (int ww = 1; ww < NW; ww++) sv += tiles[ww * TSLOTS + sl];
+            sum[k2] = sv;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k2 = 0; k2 < OPT; k2++) {
+            const int sl = tid + k2 * NT;
+            const int pos = sl >> 7, e = (sl >> 4) & 7, jj = sl & 15;   // slot pos*128 + e*16 + j
+            const int o = (jj * 8 + e) * 16 + pos;
+            tiles[o + (o >> 7)] = sum[k2];
+        }
+        __syncthreads();
+    }
     // In the finalize modes the additions return the old values, and the
     // workgroup waits for all of them before it arrives at the tile
     // counter: every addition is then performed, at the one place where all
@@ -682,14 +737,10 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
 #pragma unroll
     for (int k2 = 0; k2 < OPT; k2++) {
         const int o = tid + k2 * NT;                      // col_local*16 + pos
-        const int cl = o >> 4, pos = o & 15;
-        const int slot = pos * kTilePitch + (cl & 7) * 16 + (cl >> 3);
-        Acc s = tiles[slot];
-#pragma unroll
-        for (int ww = 1; ww < NW; ww++) s += tiles[ww * TSLOTS + slot];
-        if (o < nout && s != (Acc)0) {
-            if (ret) sink += __hip_atomic_fetch_add(out + o, (double)s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            else acc_add(out + o, (double)s);
+        const Acc sv = tiles[o + (o >> 7)];
+        if (o < nout && sv != (Acc)0) {
+            if (ret) sink += __hip_atomic_fetch_add(out + o, (double)sv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else acc_add(out + o, (double)sv);
         }
     }
     // accumulators of earlier launches that are read no more (after the

@@ -1,27 +1,32 @@
 // Cutoff search of findCutoffBinarySearch (bucketMul.cl:68-214) for one
-// workgroup of 4 or 8 waves, resolved several bisection rounds at a time.
+// workgroup of 4 or 8 waves.
 //
 // The reference bisects [min, max] of the 4096 importances for at most 20
 // rounds: it counts c = #(imp > bound), moves max (c < target) or min
 // (otherwise) to the bound, and stops on c == target, max - min < 1e-5 or
 // |maxCount - minCount| < 3, returning the tested bound (or, after 20
-// rounds, the untested midpoint of the last bracket).  Every bound it can
-// test in the next D rounds is a node of the depth-D tree of float midpoints
-// of the current bracket, and every count it needs is a count of the
-// importances above one of those nodes.  A stage therefore:
-//   1. computes the 2^D leaf edges of that tree (each lane walks the
-//      midpoint recurrence down to its leaves, in the reference's fp32
-//      arithmetic, so the edges are the reference's bounds bit for bit);
-//   2. bins the importances inside the bracket into the leaves (LDS
-//      histogram, one per wave);
-//   3. after one barrier, turns the histogram into the count above every
-//      node (a suffix sum), finds the leaf the bisection ends in, and
-//      evaluates the stop tests of its D rounds in parallel (lane l takes
-//      round l); the first round that stops gives the cutoff.
-// Otherwise the next stage continues from that leaf's bracket.  The tested
-// bounds, counts, updates and stop decisions are those of the reference, so
-// the cutoff is the same float; two stages cover typical inputs (about 12
-// rounds), three the 20-round limit.
+// rounds, the untested midpoint of the last bracket).  With u_j the j-th
+// largest importance (NaN below every value: NaN > b is false),
+// #(imp > b) >= j exactly when u_j > b.  So every decision of the reference
+// follows from t = target and u_{t-2} .. u_{t+2}: the round moves max iff
+// u_t <= b, the count equals t iff u_t > b >= u_{t+1}, and the bracket's
+// counts differ by less than 3 only in cases that compare u_{t-2}, u_{t-1},
+// u_{t+1}, u_{t+2} with its ends.  The search therefore
+//   1. maps the importances to order-preserving 32-bit keys (NaN -> 0) and
+//      reduces their min, max and count;
+//   2. selects the key of rank a = min(t, #non-NaN) with a radix select:
+//      digits of key - min from the top bit of max - min down, 8 bits a pass,
+//      counted in per-wave LDS histograms (one barrier a pass; every wave
+//      scans the summed histogram itself); a digit bin holding one key ends
+//      it early.  Digits of the key's offset from the minimum spread a
+//      heavy-tailed distribution over many bins (the float exponent is in
+//      the top bits), which keeps LDS atomics on one address few;
+//   3. one pass for the two nearest keys on either side of u_a (the counts
+//      above and equal to it come out of the select): every rank within two
+//      of t lies in that neighbourhood;
+//   4. replays the reference's rounds in its fp32 arithmetic, lane r taking
+//      round r, and returns the first round that stops, so the cutoff is the
+//      reference's float bit for bit.
 #pragma once
 
 #include "wave.h"
@@ -30,15 +35,13 @@ namespace iam {
 
 constexpr int kCutThreads = 256;              // threads holding importances
 constexpr int kCutVPT = IAM_PROBES_COUNT / kCutThreads;   // 16 per thread
-constexpr int kMaxDepth = 8;                  // rounds per stage
-constexpr int kLeaves = 1 << kMaxDepth;
 
 template <int NW>
 struct SearchLds {
-    float E[NW][kLeaves];            // leaf upper edges, one copy per wave
-    uint32_t S[NW][kLeaves];         // counts above each leaf start, one copy per wave
-    uint32_t H[2][4][kLeaves];       // histograms of the 4 value-holding waves, two stages
-    float red[2 * NW];
+    uint32_t H[2][4][256];     // digit histograms of the 4 value-holding waves, two passes
+    uint32_t red[2][NW];       // key min - 1, key max per wave
+    uint32_t nb[4][4];         // per holder wave: the two nearest keys above u and below (as offsets)
+    uint32_t cand;             // the one key of a one-key bin
 };
 
 __device__ __forceinline__ float uniform_f(float v)
@@ -55,10 +58,53 @@ __device__ __forceinline__ float midpoint(float lo, float hi)
     return __fmul_rn(__fadd_rn(lo, hi), 0.5f);
 }
 
+// order-preserving key of a float; NaN maps below every number (to 0, whose
+// float, a NaN, compares like -inf in every v > b)
+__device__ __forceinline__ uint32_t order_key(float f)
+{
+    const uint32_t b = __float_as_uint(f);
+    const uint32_t k = b ^ ((uint32_t)((int)b >> 31) | 0x80000000u);
+    return f != f ? 0u : k;
+}
+
+__device__ __forceinline__ float key_float(uint32_t k)
+{
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// the two smallest of {a1 <= a2} and {b1 <= b2}
+__device__ __forceinline__ void merge_low2(uint32_t& a1, uint32_t& a2, uint32_t b1, uint32_t b2)
+{
+    const uint32_t n2 = min(max(a1, b1), min(a2, b2));
+    a1 = min(a1, b1);
+    a2 = n2;
+}
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ void dpp_low2(uint32_t& a1, uint32_t& a2)
+{
+    const uint32_t o1 = dpp_t<CTRL, ROW_MASK>(0xffffffffu, a1);
+    const uint32_t o2 = dpp_t<CTRL, ROW_MASK>(0xffffffffu, a2);
+    merge_low2(a1, a2, o1, o2);
+}
+
+// the two smallest of the wave's pairs, in every lane
+__device__ __forceinline__ void wave_low2(uint32_t& a1, uint32_t& a2)
+{
+    dpp_low2<0x111>(a1, a2);
+    dpp_low2<0x112>(a1, a2);
+    dpp_low2<0x114>(a1, a2);
+    dpp_low2<0x118>(a1, a2);
+    dpp_low2<0x142, 0xA>(a1, a2);
+    dpp_low2<0x143, 0xC>(a1, a2);
+    a1 = lane63(a1);
+    a2 = lane63(a2);
+}
+
 // The cutoff of the 4096 importances held 16 per thread by the first 256
-// threads (v; other threads' values are ignored).  Every thread returns it.
-// Two barriers plus one per stage; on return the scratch may be reused
-// after a further barrier.
+// threads (v: numbers >= +0 or NaN, as 1e5 * |x * probe| gives; other
+// threads' values are ignored).  Every thread returns it.  On return the
+// scratch may be reused after a further barrier.
 template <int NW>
 __device__ float search_cutoff(const float (&v)[kCutVPT], int quantile, SearchLds<NW>& L)
 {
@@ -68,163 +114,196 @@ __device__ float search_cutoff(const float (&v)[kCutVPT], int quantile, SearchLd
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const bool holder = tid < kCutThreads;
+    const int t = IAM_PROBES_COUNT - quantile;         // bucketMul.cl:81
 
-    float mn = 1e30f, mx = -1e30f;                     // bucketMul.cl:98-99
-    if (holder) {
+    // ---- 1. keys, their range and the count of numbers
+    uint32_t key[kCutVPT];
+    uint32_t kmn1 = 0xffffffffu, kmx = 0u;   // min of key - 1 (NaN keys wrap to the top), max
+    int nv = 0;
 #pragma unroll
-        for (int k = 0; k < kCutVPT; k++) {
-            mn = fminf(mn, v[k]);
-            mx = fmaxf(mx, v[k]);
-        }
+    for (int k = 0; k < kCutVPT; k++) {
+        key[k] = holder ? order_key(v[k]) : 0u;
+        kmn1 = min(kmn1, key[k] - 1u);
+        kmx = max(kmx, key[k]);
+        nv += __popcll(__ballot(key[k] != 0u));
     }
-    mn = wave_min(mn);
-    mx = wave_max(mx);
+    kmn1 = wave_reduce(kmn1, [](uint32_t a, uint32_t b) { return min(a, b); });
+    kmx = wave_reduce(kmx, [](uint32_t a, uint32_t b) { return max(a, b); });
     if (lane == 0) {
-        L.red[wave] = mn;
-        L.red[NW + wave] = mx;
+        L.red[0][wave] = kmn1;
+        L.red[1][wave] = kmx;
     }
+    // the block's count: the waves' ballots summed through the histogram
+    // scratch of pass 2 (cleared below before its use)
+    if (lane == 0) L.H[1][0][wave] = (uint32_t)nv;
+    // each holder wave clears its first histogram (its own region: program
+    // order puts the clear before its atomics)
+    if (holder) *reinterpret_cast<uint4*>(&L.H[0][wave][4 * lane]) = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
-    float gmin = 1e30f, gmax = -1e30f;
+    kmn1 = 0xffffffffu;
+    kmx = 0u;
+    nv = 0;
 #pragma unroll
     for (int w = 0; w < NW; w++) {
-        gmin = fminf(gmin, L.red[w]);
-        gmax = fmaxf(gmax, L.red[NW + w]);
+        kmn1 = min(kmn1, L.red[0][w]);
+        kmx = max(kmx, L.red[1][w]);
+        nv += (int)L.H[1][0][w];
     }
-    const int target = IAM_PROBES_COUNT - quantile;    // bucketMul.cl:81
-    float minB = uniform_f(gmin), maxB = uniform_f(gmax);
-    int minC = IAM_PROBES_COUNT, maxC = 0;             // bucketMul.cl:142-143
-    int rounds = 0, buf = 0;
-    float* E = L.E[wave];
-    uint32_t* S = L.S[wave];
-    for (;;) {
-        const int D = min(kMaxDepth, 20 - rounds);
-        const int NL = 1 << D;
-        // 1. leaf edges: lane l takes leaves 4l .. 4l+3 (their paths share
-        // all but the last two levels)
-        if (4 * lane < NL || lane == 0) {
-            float lo = minB, hi = maxB;
-            const int pre = D >= 2 ? D - 2 : 0;
-            for (int l = 0; l < pre; l++) {
-                const float b = midpoint(lo, hi);
-                if ((lane >> (pre - 1 - l)) & 1) lo = b;
-                else hi = b;
+    const uint32_t kmn = kmn1 + 1u;
+    // bucketMul.cl:98-99: min and max from 1e30 / -1e30 (fmin / fmax skip NaN)
+    const float gmin = nv ? fminf(1e30f, key_float(kmn)) : 1e30f;
+    const float gmax = nv ? fmaxf(-1e30f, key_float(kmx)) : -1e30f;
+
+    // ---- 2. radix select of the key of rank a (descending, 1-based)
+    const int a = min(t, nv);
+    uint32_t ukey = 0u;
+    int gt = 0, eq = 0;            // #(keys > ukey), #(keys == ukey)
+    uint32_t a1 = 0xffffffffu, a2 = 0xffffffffu, b1 = 0xffffffffu, b2 = 0xffffffffu;
+    if (a >= 1) {
+        const uint32_t range = kmx - kmn;
+        const int top = range ? 31 - __clz(range) : 0;
+        int s = max(top - 7, 0);       // digit = (rel >> s) & (2^w - 1)
+        int w = top + 1 - s;
+        uint32_t prefix = 0u;          // rel >> (s + w) of the keys still in the running
+        int r = a;
+        int buf = 0;
+        bool first = true;
+        for (;;) {
+            if (holder) {
+                uint32_t* H = L.H[buf][wave];
+                const uint32_t dmask = (1u << w) - 1u;
+                const int sw = first ? 0 : s + w;   // the first pass takes every number
+#pragma unroll
+                for (int k = 0; k < kCutVPT; k++) {
+                    const uint32_t rel = key[k] - kmn;
+                    const bool in = key[k] != 0u && (first || (rel >> sw) == prefix);
+                    if (in) atomicAdd(H + ((rel >> s) & dmask), 1u);
+                }
             }
-            float4 e;
-            if (D >= 2) {
-                const float mid = midpoint(lo, hi);
-                e = make_float4(midpoint(lo, mid), mid, midpoint(mid, hi), hi);
-            } else {
-                e = make_float4(midpoint(lo, hi), hi, hi, hi);
+            __syncthreads();
+            // the next pass's histogram (free: every wave has scanned it)
+            if (holder) *reinterpret_cast<uint4*>(&L.H[buf ^ 1][wave][4 * lane]) = make_uint4(0u, 0u, 0u, 0u);
+            // bins 4*lane .. 4*lane+3 summed over the holder waves
+            const uint4 h0 = *reinterpret_cast<const uint4*>(&L.H[buf][0][4 * lane]);
+            const uint4 h1 = *reinterpret_cast<const uint4*>(&L.H[buf][1][4 * lane]);
+            const uint4 h2 = *reinterpret_cast<const uint4*>(&L.H[buf][2][4 * lane]);
+            const uint4 h3 = *reinterpret_cast<const uint4*>(&L.H[buf][3][4 * lane]);
+            const int c0 = (int)(h0.x + h1.x + h2.x + h3.x);
+            const int c1 = (int)(h0.y + h1.y + h2.y + h3.y);
+            const int c2 = (int)(h0.z + h1.z + h2.z + h3.z);
+            const int c3 = (int)(h0.w + h1.w + h2.w + h3.w);
+            const int incl = wave_incl_sum(c0 + c1 + c2 + c3);
+            const int above3 = __builtin_amdgcn_readlane(incl, 63) - incl;   // keys in bins above 4*lane+3
+            const int above2 = above3 + c3, above1 = above2 + c2, above0 = above1 + c1;
+            // the bin d with above(d) < r <= above(d) + count(d)
+            const bool f3 = above3 < r && r <= above2, f2 = above2 < r && r <= above1;
+            const bool f1 = above1 < r && r <= above0, f0 = above0 < r && r <= above0 + c0;
+            const int d = 4 * lane + (f3 ? 3 : f2 ? 2 : f1 ? 1 : 0);
+            const int ab = f3 ? above3 : f2 ? above2 : f1 ? above1 : above0;
+            const int cd = f3 ? c3 : f2 ? c2 : f1 ? c1 : c0;
+            const int src = __ffsll((long long)__ballot(f3 | f2 | f1 | f0)) - 1;
+            const uint32_t dd = (uint32_t)__builtin_amdgcn_readlane(d, src);
+            r -= __builtin_amdgcn_readlane(ab, src);
+            const int cnt = __builtin_amdgcn_readlane(cd, src);
+            prefix = (prefix << w) | dd;
+            if (s == 0) {              // prefix is the key's offset: cnt keys equal it
+                ukey = kmn + prefix;
+                eq = cnt;
+                break;
             }
-            *reinterpret_cast<float4*>(E + 4 * lane) = e;
-        }
-        // 2. histogram of the bracket (minB, maxB] over the leaves
-        if (holder) {
-            uint32_t* H = L.H[buf][wave];
-            *reinterpret_cast<uint4*>(H + 4 * lane) = make_uint4(0u, 0u, 0u, 0u);
-            // Binning by position: the edges lie within a small fraction of
-            // a leaf of their dyadic positions when the bracket is wide
-            // against the float spacing at maxB (and no midpoint sum
-            // overflows), so the estimated leaf is off by at most one and one
-            // comparison on each side fixes it; otherwise a binary search.
-            const float w = __fsub_rn(maxB, minB);
-            const bool guess = w > 0.0f && maxB < 1.0e38f && w > __fmul_rn(fmaxf(maxB, 1e-30f), 0.00025f);
-            const float scale = guess ? __fdiv_rn((float)NL, w) : 0.0f;
-            // every value gets a leaf (those outside the bracket are not
-            // counted), so the LDS reads of all 16 go out together
-            int g[kCutVPT];
-            if (guess) {
-                float eg[kCutVPT], em[kCutVPT];
-#pragma unroll
-                for (int k = 0; k < kCutVPT; k++) {
-                    const float f = __fmul_rn(__fsub_rn(v[k], minB), scale);
-                    g[k] = (int)fminf(fmaxf(f, 0.0f), (float)(NL - 1));   // NaN -> 0
-                }
-#pragma unroll
-                for (int k = 0; k < kCutVPT; k++) {
-                    eg[k] = E[g[k]];
-                    em[k] = E[g[k] > 0 ? g[k] - 1 : 0];
-                }
-#pragma unroll
-                for (int k = 0; k < kCutVPT; k++) {
-                    if (g[k] < NL - 1 && eg[k] < v[k]) g[k]++;
-                    else if (g[k] > 0 && em[k] >= v[k]) g[k]--;
-                }
-            } else {
-#pragma unroll
-                for (int k = 0; k < kCutVPT; k++) g[k] = 0;   // #(edges E[0 .. NL-2] below the value)
-                for (int st = NL >> 1; st > 0; st >>= 1) {
-                    float e[kCutVPT];
-#pragma unroll
-                    for (int k = 0; k < kCutVPT; k++) e[k] = E[min(g[k] + st - 1, NL - 2)];
+            if (cnt == 1) {
+                // the one key whose offset from the minimum starts with prefix
+                if (holder) {
 #pragma unroll
                     for (int k = 0; k < kCutVPT; k++)
-                        if (g[k] + st <= NL - 1 && e[k] < v[k]) g[k] += st;
+                        if (key[k] != 0u && ((key[k] - kmn) >> s) == prefix) L.cand = key[k];
                 }
+                __syncthreads();
+                ukey = L.cand;
+                eq = 1;
+                break;
             }
+            w = min(8, s);
+            s -= w;
+            buf ^= 1;
+            first = false;
+        }
+        gt = a - r;                    // r is the rank left within the keys equal to ukey
+
+        // ---- 3. the nearest keys on either side of ukey: the smallest of
+        // key - (ukey + 1) (keys <= ukey wrap above every key > ukey) and of
+        // (ukey - 1) - key (keys >= ukey wrap above every key < ukey)
+        if (holder) {
 #pragma unroll
-            for (int k = 0; k < kCutVPT; k++)
-                if (v[k] > minB && v[k] <= maxB) atomicAdd(H + g[k], 1u);
+            for (int k = 0; k < kCutVPT; k++) {
+                const uint32_t da = key[k] - (ukey + 1u), db = (ukey - 1u) - key[k];
+                a2 = min(a2, max(a1, da));
+                a1 = min(a1, da);
+                b2 = min(b2, max(b1, db));
+                b1 = min(b1, db);
+            }
         }
+        wave_low2(a1, a2);
+        wave_low2(b1, b2);
+        if (holder && lane == 0) *reinterpret_cast<uint4*>(L.nb[wave]) = make_uint4(a1, a2, b1, b2);
         __syncthreads();
-        // 3. S[j] = #(bracket values in leaves >= j), every wave for itself
-        uint32_t c0, c1, c2, c3;
-        {
-            const uint4 h0 = *reinterpret_cast<const uint4*>(L.H[buf][0] + 4 * lane);
-            const uint4 h1 = *reinterpret_cast<const uint4*>(L.H[buf][1] + 4 * lane);
-            const uint4 h2 = *reinterpret_cast<const uint4*>(L.H[buf][2] + 4 * lane);
-            const uint4 h3 = *reinterpret_cast<const uint4*>(L.H[buf][3] + 4 * lane);
-            c0 = h0.x + h1.x + h2.x + h3.x;
-            c1 = h0.y + h1.y + h2.y + h3.y;
-            c2 = h0.z + h1.z + h2.z + h3.z;
-            c3 = h0.w + h1.w + h2.w + h3.w;
+        a1 = a2 = b1 = b2 = 0xffffffffu;
+#pragma unroll
+        for (int w2 = 0; w2 < 4; w2++) {
+            const uint4 q = *reinterpret_cast<const uint4*>(L.nb[w2]);
+            merge_low2(a1, a2, q.x, q.y);
+            merge_low2(b1, b2, q.z, q.w);
         }
-        const uint32_t s3 = c3, s2 = c2 + s3, s1 = c1 + s2, s0 = c0 + s1;
-        const int incl = wave_incl_sum((int)s0);
-        const uint32_t above = (uint32_t)(__builtin_amdgcn_readlane(incl, 63) - incl);   // lanes > this one
-        const uint32_t S0 = s0 + above, S1 = s1 + above, S2 = s2 + above, S3 = s3 + above;
-        *reinterpret_cast<uint4*>(S + 4 * lane) = make_uint4(S0, S1, S2, S3);
-        // the leaf the rounds end in: count(imp > E[m-1]) = maxC + S[m] >=
-        // target exactly for m <= js (going up the tree at that node)
-        const int m0 = 4 * lane;
-        int js = __popcll(__ballot(m0 >= 1 && m0 < NL && maxC + (int)S0 >= target)) +
-                 __popcll(__ballot(m0 + 1 < NL && maxC + (int)S1 >= target)) +
-                 __popcll(__ballot(m0 + 2 < NL && maxC + (int)S2 >= target)) +
-                 __popcll(__ballot(m0 + 3 < NL && maxC + (int)S3 >= target));
-        js = uniform_i(js);
-        // the stop tests of rounds 0 .. D-1 of this stage (bucketMul.cl:178-200)
-        bool stop = false;
-        float tested = 0.0f;
-        if (lane < D) {
-            const int sh = D - lane;                     // the round's node covers 2^sh leaves
-            const int half = 1 << (sh - 1);
-            const int a = (js >> sh) << sh;
-            const int m = a + half;
-            tested = E[m - 1];
-            const int c = maxC + (int)S[m];
-            const int a1 = (js >> (sh - 1)) << (sh - 1);   // the bracket after the update
-            const float lo = a1 == 0 ? minB : E[a1 - 1];
-            const float hi = a1 + half == NL ? maxB : E[a1 + half - 1];
-            const int lc = a1 == 0 ? minC : maxC + (int)S[a1];
-            const int hc = a1 + half == NL ? maxC : maxC + (int)S[a1 + half];
-            const int gap = hc - lc;
-            stop = c == target || __fsub_rn(hi, lo) < 0.00001f || (gap < 0 ? -gap : gap) < 3;
-        }
-        const uint64_t sm = __ballot(stop);
-        if (sm) return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tested), __ffsll((long long)sm) - 1));
-        // continue from leaf js's bracket
-        const float nlo = js == 0 ? minB : E[js - 1];
-        const float nhi = js == NL - 1 ? maxB : E[js];
-        const int nlc = js == 0 ? minC : maxC + (int)S[js];
-        const int nhc = js == NL - 1 ? maxC : maxC + (int)S[js + 1];
-        minB = uniform_f(nlo);
-        maxB = uniform_f(nhi);
-        minC = uniform_i(nlc);
-        maxC = uniform_i(nhc);
-        rounds += D;
-        buf ^= 1;
-        if (rounds >= 20) return midpoint(minB, maxB);   // bucketMul.cl:211-213: the untested midpoint
     }
+
+    // ---- 4. u_{t+o}, o = -2 .. 2, lane o + 2 computing one (ranks within two
+    // of t lie within two of the tie group of u_a; ranks past the numbers
+    // compare like -inf; ranks below 1 are above every bound, flagged)
+    float U[5];
+    {
+        const int k = t + lane - 2;
+        const uint32_t kk = (k > gt && k <= gt + eq) ? ukey
+                          : k == gt ? ukey + 1u + a1
+                          : k == gt - 1 ? ukey + 1u + a2
+                          : k == gt + eq + 1 ? ukey - 1u - b1
+                                             : ukey - 1u - b2;
+        const float uk = k > nv ? -INFINITY : key_float(kk);
+#pragma unroll
+        for (int o = 0; o < 5; o++) U[o] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(uk), o));
+    }
+    const bool top_m1 = t - 1 < 1, top_m2 = t - 2 < 1;   // (U[0], U[1] unused then)
+
+    // ---- 5. the reference's rounds (bucketMul.cl:139-213), lane r keeping
+    // the state after round r (its tested bound, bracket and counts' side);
+    // straight-line selects, no branches
+    float lo = gmin, hi = gmax;
+    float b = midpoint(gmin, gmax);
+    bool min_init = true;          // minB is still the minimum: its count is the reference's 4096 (:142)
+    bool ge = false;
+#pragma unroll
+    for (int rd = 0; rd < 20; rd++) {
+        const bool act = rd <= lane;
+        const bool g = U[2] > b;             // count >= target: min moves
+        const bool up = act && g, down = act && !g;
+        ge = act ? g : ge;
+        lo = up ? b : lo;
+        hi = down ? b : hi;
+        min_init = min_init && !up;
+        const float nb = midpoint(lo, hi);
+        b = rd < lane ? nb : b;
+    }
+    // lane r < 20: the stop tests of round r (bucketMul.cl:195-200)
+    const bool eq_t = ge && !(U[3] > b);                          // count == target
+    const bool am1 = top_m1 || U[1] > hi, am2 = top_m2 || U[0] > hi;
+    const int dmax = am1 ? 1 : am2 ? 2 : 3;                       // target - maxCount (3: 3 or more)
+    const int dmin = !(U[3] > lo) ? 0 : !(U[4] > lo) ? 1 : 2;     // minCount - target (2: 2 or more)
+    const bool gap_small = min_init ? (dmax <= 2 && t - dmax >= IAM_PROBES_COUNT - 2)   // 4096 - maxCount < 3
+                                    : dmin + dmax < 3;
+    const bool stop = lane < 20 && (eq_t || __fsub_rn(hi, lo) < 0.00001f || gap_small);
+    const uint64_t sm = __ballot(stop);
+    // no stop: the untested midpoint after round 20 (lane 20's b), :211-213
+    const int src = sm ? __ffsll((long long)sm) - 1 : 20;
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(b), src));
 }
 
 }  // namespace iam

@@ -47,6 +47,17 @@ __device__ __forceinline__ double lane63<double>(double v)
     return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
 }
 
+template <>
+__device__ __forceinline__ uint32_t lane63<uint32_t>(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_t(uint32_t old, uint32_t v)
+{
+    return (uint32_t)dpp_i<CTRL, ROW_MASK>((int)old, (int)v);
+}
 template <int CTRL, int ROW_MASK = 0xF>
 __device__ __forceinline__ float dpp_t(float old, float v) { return dpp_f<CTRL, ROW_MASK>(old, v); }
 template <int CTRL, int ROW_MASK = 0xF>

@@ -175,6 +175,95 @@ def test_cutoff_edge_paths(O, iam, ctx, pattern):
     check_against_oracle(O, ctx, b, s, probes, x, effort, fused=iam)
 
 
+def _search_input(kind, rng):
+    """(x, probes) of one importance pattern of the search: heavy-tailed,
+    skewed, tied, constant, an outlier, tiny, with infinities or NaNs,
+    overflowing midpoints, two adjacent floats, zero, bimodal."""
+    n = 4096
+    p = rng.normal(0, 0.02, n).astype(np.float16).view(np.uint16)
+    const_p = np.full(n, 0x2400, np.uint16)          # 2^-6
+    z = rng.normal(0, 1, n).astype(np.float32)
+    x = z.copy()
+    if kind == "skew":
+        x[rng.choice(n, 41, replace=False)] *= 20.0
+    elif kind == "ties":
+        x, p = np.floor(np.abs(z) * 4).astype(np.float32), const_p
+    elif kind == "constant":
+        x, p = np.full(n, 0.64, np.float32), const_p
+    elif kind == "outlier":
+        x[7] = 1e4
+    elif kind == "tiny":
+        x = (z * np.float32(1e-38)).astype(np.float32)
+    elif kind == "inf":
+        x[::3] = np.inf
+    elif kind == "nan":
+        x[::5] = np.nan
+    elif kind == "huge":
+        x = (rng.random(n) * 1e36).astype(np.float32)
+    elif kind == "adjacent":
+        x = np.where(np.arange(n) < 2048, np.float32(0.64), np.nextafter(np.float32(0.64), np.float32(1)))
+        x, p = x.astype(np.float32), const_p
+    elif kind == "zero":
+        x = np.zeros(n, np.float32)
+    elif kind == "all_nan":
+        x = np.full(n, np.nan, np.float32)
+    elif kind == "nan_inf":
+        x = np.where(np.arange(n) % 2 == 1, np.float32(np.nan), np.float32(np.inf)).astype(np.float32)
+    elif kind == "few_nans":
+        x[: 1 + int(rng.integers(0, 4))] = np.nan
+    elif kind == "bimodal":
+        x = (z + np.where(rng.random(n) < 0.5, 10.0, 0.0)).astype(np.float32)
+    return x, p
+
+
+_SEARCH_KINDS = ["normal", "skew", "ties", "constant", "outlier", "tiny", "inf", "nan", "huge",
+                 "adjacent", "zero", "all_nan", "nan_inf", "few_nans", "bimodal"]
+
+
+@pytest.mark.parametrize("kind", _SEARCH_KINDS)
+def test_cutoff_search_kinds(O, iam, ctx, kind):
+    """The cutoff search bit-exact against the oracle on 15 importance
+    patterns at efforts that give the quantiles 0..3, 4092..4095 and the
+    usual ones: the standalone cutoff kernel, and the walk's own search in
+    4-wave (256 outputs) and 8-wave (32000 outputs) workgroups; the selected
+    row count matches too."""
+    rng = np.random.default_rng(100 + _SEARCH_KINDS.index(kind))
+    x, p = _search_input(kind, rng)
+    quants = [0, 1, 2, 3, 100, 1023, 2047, 3071, 3583, 3890, 4092, 4093, 4094, 4095]
+    efforts = sorted({float(np.float32(1.0 - (q + 0.5) / 4095.0)) for q in quants} | {1.0, 0.0})
+    mats = []
+    for out_dim, tid in ((256, 9), (32000, 5)):
+        b, s, _ = make_matrix(O, out_dim, 4096, tid=tid)
+        db, ds = ctx.upload(b), ctx.upload(s)
+        mats.append((b, s, db, ds))
+    dp, dx = ctx.upload(p), ctx.upload(x)
+    with np.errstate(all="ignore"):
+        for effort in efforts:
+            q = O.effort_quantile(effort)
+            ocut = O.find_cutoff(x, p, q)
+            for mi, (b, s, db, ds) in enumerate(mats):
+                R, C = b.shape
+                _, oS = O.select_rows(x, s, ocut, R, R // 16)
+                runs = ["split", "fused"] if mi == 0 else ["fused"]
+                for how in runs:
+                    dy = ctx.empty(16 * C, np.float32)
+                    if how == "split":
+                        ctx.calc_dispatch(dx, ds, dp, 0, R // 16, C, R, effort)
+                        ctx.mul(db, C, dy)
+                    else:
+                        ctx.fused([iam.BucketMatrix(db.ptr, ds.ptr, dp.ptr, R, C, 4, 3)], dx, R // 16, [dy], effort)
+                    cut, S = ctx.dispatch_info(0)
+                    assert np.float32(cut).view(np.uint32) == np.float32(ocut).view(np.uint32), \
+                        (kind, effort, q, how, C, cut, ocut)
+                    assert S == oS and ctx.walk_count(0) == S, (kind, effort, how, S, oS)
+                    dy.free()
+    for _, _, db, ds in mats:
+        db.free()
+        ds.free()
+    dp.free()
+    dx.free()
+
+
 @pytest.mark.parametrize("in_dim", [4096, 8192])
 def test_fused_norm_input(O, iam, ctx, in_dim):
     """iam_bucketmul_fused with a norm input: x = RMSNorm(h) * gain is the
