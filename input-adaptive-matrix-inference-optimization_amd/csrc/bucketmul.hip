@@ -27,6 +27,7 @@
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstring>
 #include <type_traits>
@@ -47,66 +48,102 @@ __device__ __forceinline__ float h2f(uint32_t bits16)
     return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xffffu)));
 }
 
-// The 16 probes of thread tid (probes[16*tid ..]).
-__device__ __forceinline__ void load_probes(const uint16_t* __restrict__ probes, uint4 (&pr)[2])
+// A workgroup of NT threads holds the 4096 inputs the cutoff sees, VPT =
+// 4096 / NT consecutive ones per thread (thread tid: [VPT*tid, VPT*tid+VPT)).
+template <int VPT>
+__device__ __forceinline__ void load_f32(const float* __restrict__ p, float (&v)[VPT])
 {
-    const uint4* pv = reinterpret_cast<const uint4*>(probes + threadIdx.x * kCutVPT);
-    pr[0] = pv[0];
-    pr[1] = pv[1];
-}
-
-__device__ __forceinline__ void load16(const float* __restrict__ x, float (&xs)[kCutVPT])
-{
-    const float4* xv = reinterpret_cast<const float4*>(x + threadIdx.x * kCutVPT);
+    const float4* q = reinterpret_cast<const float4*>(p + threadIdx.x * VPT);
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const float4 a = xv[k];
-        xs[4 * k] = a.x;
-        xs[4 * k + 1] = a.y;
-        xs[4 * k + 2] = a.z;
-        xs[4 * k + 3] = a.w;
+    for (int k = 0; k < VPT / 4; k++) {
+        const float4 a = q[k];
+        v[4 * k] = a.x;
+        v[4 * k + 1] = a.y;
+        v[4 * k + 2] = a.z;
+        v[4 * k + 3] = a.w;
     }
 }
 
-__device__ __forceinline__ void load16_acc(const double* __restrict__ p, double (&v)[kCutVPT])
+template <int VPT>
+__device__ __forceinline__ void load_f64(const double* __restrict__ p, double (&v)[VPT])
 {
-    const double2* pv = reinterpret_cast<const double2*>(p + threadIdx.x * kCutVPT);
+    const double2* q = reinterpret_cast<const double2*>(p + threadIdx.x * VPT);
 #pragma unroll
-    for (int k = 0; k < kCutVPT / 2; k++) {
-        const double2 a = pv[k];
+    for (int k = 0; k < VPT / 2; k++) {
+        const double2 a = q[k];
         v[2 * k] = a.x;
         v[2 * k + 1] = a.y;
     }
 }
 
-// imp = 1e5 * |x * probe| (bucketMul.cl:101-117) of thread tid's 16 inputs
-__device__ __forceinline__ void importances(const float (&xs)[kCutVPT], const uint4 (&pr)[2], float (&v)[kCutVPT])
+// VPT fp16 values as VPT/2 words (value k in the half k & 1 of word k >> 1)
+template <int VPT>
+__device__ __forceinline__ void load_h16(const uint16_t* __restrict__ p, uint32_t (&w)[VPT / 2])
 {
-#pragma clang fp contract(off)
-    const uint32_t ps[8] = {pr[0].x, pr[0].y, pr[0].z, pr[0].w, pr[1].x, pr[1].y, pr[1].z, pr[1].w};
+    const uint4* q = reinterpret_cast<const uint4*>(p + threadIdx.x * VPT);
 #pragma unroll
-    for (int k = 0; k < kCutVPT; k++) {
-        const float p = h2f(ps[k >> 1] >> ((k & 1) * 16));
-        v[k] = __fmul_rn(kScale, fabsf(__fmul_rn(xs[k], p)));
+    for (int k = 0; k < VPT / 8; k++) {
+        const uint4 a = q[k];
+        w[4 * k] = a.x;
+        w[4 * k + 1] = a.y;
+        w[4 * k + 2] = a.z;
+        w[4 * k + 3] = a.w;
     }
 }
 
-// rmsNorm32fast (aux.cl:156-196) of a 4096-vector by one workgroup, in the
-// reference's fp32 order: 16 consecutive squares per thread summed in order,
-// then the 256-way tree (pairs tid, tid + st for st = 128 .. 1: the partial
-// sums go through LDS, then every wave runs the tree on its own), scale =
-// 1/sqrt(sum/4096 + eps) rounded from double, then the fp16 gain (mul16x32,
-// aux.cl:434-440).  v holds h[16*tid ..] on entry (first 256 threads) and
-// the normalized values on exit; gr the thread's 16 gains.  s_part: 256
-// floats of scratch nothing writes again before a later barrier.
-__device__ __forceinline__ void block_rmsnorm4096(float (&v)[kCutVPT], const uint4 (&gr)[2], float eps, float* s_part)
+template <int VPT>
+__device__ __forceinline__ float half_at(const uint32_t (&w)[VPT / 2], int k)
+{
+    return h2f(w[k >> 1] >> ((k & 1) * 16));
+}
+
+template <int VPT>
+__device__ __forceinline__ void store_f32(float* __restrict__ p, const float (&v)[VPT])
+{
+    float4* q = reinterpret_cast<float4*>(p + threadIdx.x * VPT);
+#pragma unroll
+    for (int k = 0; k < VPT / 4; k++) q[k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+}
+
+// imp = 1e5 * |x * probe| (bucketMul.cl:101-117) of the thread's inputs
+template <int VPT>
+__device__ __forceinline__ void importances(const float (&xs)[VPT], const uint32_t (&pw)[VPT / 2], float (&v)[VPT])
 {
 #pragma clang fp contract(off)
+#pragma unroll
+    for (int k = 0; k < VPT; k++) v[k] = __fmul_rn(kScale, fabsf(__fmul_rn(xs[k], half_at<VPT>(pw, k))));
+}
+
+// rmsNorm32fast (aux.cl:156-196) of a 4096-vector by one workgroup, in the
+// reference's fp32 order: 16 consecutive squares summed in order (with 8
+// values per thread, the even lane's running sum continues in the odd
+// lane), then the 256-way tree (pairs j, j + st for st = 128 .. 1: the
+// partial sums go through LDS, then every wave runs the tree on its own),
+// scale = 1/sqrt(sum/4096 + eps) rounded from double, then the fp16 gain
+// (mul16x32, aux.cl:434-440).  v holds the thread's inputs on entry and the
+// normalized values on exit; gw its gains.  s_part: 256 floats of scratch
+// nothing writes again before a later barrier.
+template <int VPT>
+__device__ __forceinline__ void block_rmsnorm4096(float (&v)[VPT], const uint32_t (&gw)[VPT / 2], float eps,
+                                                  float* s_part)
+{
+#pragma clang fp contract(off)
+    static_assert(VPT == 16 || VPT == 8, "16 or 8 values per thread");
     const int tid = threadIdx.x;
     float sq = 0.0f;
+    if constexpr (VPT == 8) {
+        float lo = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kCutVPT; k++) sq = __fadd_rn(sq, __fmul_rn(v[k], v[k]));
-    if (tid < kCutThreads) s_part[tid] = sq;
+        for (int k = 0; k < VPT; k++) lo = __fadd_rn(lo, __fmul_rn(v[k], v[k]));
+        sq = dpp_f<0x111>(0.0f, lo);   // the even neighbour's sum (row_shr:1)
+#pragma unroll
+        for (int k = 0; k < VPT; k++) sq = __fadd_rn(sq, __fmul_rn(v[k], v[k]));
+        if (tid & 1) s_part[tid >> 1] = sq;
+    } else {
+#pragma unroll
+        for (int k = 0; k < VPT; k++) sq = __fadd_rn(sq, __fmul_rn(v[k], v[k]));
+        s_part[tid] = sq;
+    }
     __syncthreads();
     // lane l takes part[l] + part[l+128] and part[l+64] + part[l+192]
     // (st = 128), their sum (st = 64), then st = 32, 16 as shuffles and
@@ -124,9 +161,8 @@ __device__ __forceinline__ void block_rmsnorm4096(float (&v)[kCutVPT], const uin
     const float total = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sq)));
     const float mean = __fdiv_rn(total, 4096.0f);
     const float scale = (float)(1.0 / sqrt((double)__fadd_rn(mean, eps)));
-    const uint32_t gw[8] = {gr[0].x, gr[0].y, gr[0].z, gr[0].w, gr[1].x, gr[1].y, gr[1].z, gr[1].w};
 #pragma unroll
-    for (int k = 0; k < kCutVPT; k++) v[k] = __fmul_rn(h2f(gw[k >> 1] >> ((k & 1) * 16)), __fmul_rn(v[k], scale));
+    for (int k = 0; k < VPT; k++) v[k] = __fmul_rn(half_at<VPT>(gw, k), __fmul_rn(v[k], scale));
 }
 
 // --------------------------------------------------------------- cutoff ---
@@ -146,11 +182,12 @@ struct CutoffArgs {
 __device__ __forceinline__ float block_cutoff(const float* __restrict__ x, const uint16_t* __restrict__ probes,
                                               int quantile, SearchLds<4>& L)
 {
-    float xs[kCutVPT], v[kCutVPT];
-    uint4 pr[2];
-    load_probes(probes, pr);
-    load16(x, xs);
-    importances(xs, pr, v);
+    constexpr int VPT = kCutVPT;
+    float xs[VPT], v[VPT];
+    uint32_t pw[VPT / 2];
+    load_h16<VPT>(probes, pw);
+    load_f32<VPT>(x, xs);
+    importances<VPT>(xs, pw, v);
     return search_cutoff<4>(v, quantile, L);
 }
 
@@ -280,7 +317,7 @@ struct WalkDesc {
     int IPS;                  // inputs per slice (<= threads per workgroup)
     int P;                    // slices
     int T;                    // column tiles
-    int block_base;
+    int nblocks;              // blocks of this matrix (P * T); the grid's x may be larger
     int expected;             // workgroups that flush into one tile (finalize modes)
 };
 
@@ -314,6 +351,24 @@ struct WalkArgs {
     unsigned long long* counters;
 };
 
+// A pointer the compiler no longer sees as global (after an asm) marked
+// global again, so that its loads stay global loads (a flat load also counts
+// against the LDS wait counter)
+template <typename T>
+__device__ __forceinline__ T* as_global(uint64_t u)
+{
+    return (T*)(__attribute__((address_space(1))) T*)u;
+}
+
+// The arguments the first vector loads of a walk block need (the matrices'
+// probes and x, the input mode's pointers, the block bases) are read from
+// fixed argument offsets and pinned in scalar registers, so they arrive in
+// one batch of scalar loads with one wait; the block's matrix then picks
+// among them.  A field read through the block's matrix index would cost a
+// second round trip before the first vector load; the other fields are read
+// that way, and used only once the input and the search are under way.
+
+
 // Loads of the selection: the 16 stats (channel stats_channel) of input
 // i0 + tid's rows and, when the slice's inputs are not computed in
 // registers, its x (from memory, or from the attention accumulators).
@@ -325,33 +380,48 @@ struct SelLoads {
     uint4 raw[8];
     uint32_t sv[16];
     float xi;
-    int kind;   // 0: stride 1, 1: stride 4 channel 3, 2: scalar
+    double an, ad;   // attention input: o and the softmax denominator (divided after the search)
+    bool attn;
+    int kind;        // 0: stride 1, 1: stride 4 channel 3, 2: scalar
+};
+
+// where the selection reads the stats and x of the block's matrix
+struct SelSrc {
+    const uint16_t* stats;
+    const float* x;
+    int stride;
+    int channel;
+    int rows;
 };
 
 enum XSrc : int { kXRegs = 0, kXMem = 1, kXAttn = 2 };
 
-__device__ __forceinline__ void select_load(const WalkDesc& d, const WalkArgs& a, int i0, int ni, int xsrc,
+__device__ __forceinline__ void select_load(const SelSrc& d, const WalkArgs& a, int i0, int ni, int xsrc,
                                             SelLoads& L)
 {
     const int tid = threadIdx.x;
     L.xi = 0.0f;
+    L.an = 0.0;
+    L.ad = 1.0;
+    L.attn = xsrc == kXAttn;
     const int i = i0 + min(tid, ni - 1);   // threads past the slice re-read its last input
     const int r0 = i * 16;
-    const uint16_t* base = d.stats + (size_t)i0 * 16 * d.stats_stride;
+    const uint16_t* base = d.stats + (size_t)i0 * 16 * d.stride;
     const bool aligned = (((uintptr_t)base) & 15) == 0 && (d.rows & 15) == 0;
     if (xsrc == kXMem) {
         L.xi = d.x[i];
     } else if (xsrc == kXAttn) {
         const double* A = reinterpret_cast<const double*>(a.attn_acc);
-        L.xi = (float)(A[i] / A[a.attn_lofs + (i >> 7)]);
+        L.an = A[i];
+        L.ad = A[a.attn_lofs + (i >> 7)];
     }
-    const uint16_t* st = d.stats + (size_t)r0 * d.stats_stride;
-    if (aligned && d.stats_stride == 1) {
+    const uint16_t* st = d.stats + (size_t)r0 * d.stride;
+    if (aligned && d.stride == 1) {
         L.kind = 0;
         const uint4* p4 = reinterpret_cast<const uint4*>(st);
         L.raw[0] = p4[0];
         L.raw[1] = p4[1];
-    } else if (aligned && d.stats_stride == 4 && d.stats_channel == 3) {
+    } else if (aligned && d.stride == 4 && d.channel == 3) {
         L.kind = 1;
         const uint4* p4 = reinterpret_cast<const uint4*>(st);
 #pragma unroll
@@ -361,7 +431,7 @@ __device__ __forceinline__ void select_load(const WalkDesc& d, const WalkArgs& a
 #pragma unroll
         for (int kk = 0; kk < 16; kk++) {
             const int rr = min(r0 + kk, d.rows - 1) - r0;
-            L.sv[kk] = st[(size_t)rr * d.stats_stride + d.stats_channel];
+            L.sv[kk] = st[(size_t)rr * d.stride + d.channel];
         }
     }
 }
@@ -374,7 +444,7 @@ __device__ __forceinline__ void select_load(const WalkDesc& d, const WalkArgs& a
 // already holds them, written before a barrier).  Ends with a barrier;
 // returns the number of selected rows.
 template <int NT>
-__device__ __forceinline__ uint32_t select_finish(const WalkDesc& d, float cutoff, int i0, int ni, const SelLoads& L,
+__device__ __forceinline__ uint32_t select_finish(const SelSrc& d, float cutoff, int i0, int ni, const SelLoads& L,
                                                   uint16_t* s_row, float* s_x, uint32_t* s_wsum, bool x_lds)
 {
 #pragma clang fp contract(off)
@@ -386,6 +456,7 @@ __device__ __forceinline__ uint32_t select_finish(const WalkDesc& d, float cutof
     uint32_t mask = 0;
     if (tid < ni) {
         if (x_lds) xi = s_x[tid];
+        else if (L.attn) xi = (float)(L.an / L.ad);
         uint32_t sv[16];
         if (L.kind == 0) {
             const uint32_t ww[8] = {L.raw[0].x, L.raw[0].y, L.raw[0].z, L.raw[0].w,
@@ -469,7 +540,8 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     constexpr int NT = 64 * NW;
     constexpr int TSLOTS = 16 * kTilePitch;                 // one wave's tile
     constexpr int GSTRIDE = NW * UNR;                       // groups per workgroup batch
-    static_assert(NT == kCutThreads || NT == 2 * kCutThreads, "4 or 8 waves");
+    static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+    constexpr int VPT = IAM_PROBES_COUNT / NT;              // inputs of the cutoff per thread
     static_assert(kTileOut % NT == 0, "flush mapping");
     static_assert(sizeof(Acc) * NW * TSLOTS >= sizeof(SearchLds<NW>), "the search scratch lives in the tiles");
     __shared__ __align__(16) Acc tiles[NW * TSLOTS];   // the search's scratch, then the wave tiles
@@ -485,98 +557,99 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     const int lane = tid & 63;
     const int wave = tid >> 6;
 
-    const int b = xcd_remap((int)blockIdx.x, (int)gridDim.x);
-    int k = 0;
-    for (int i = 1; i < a.n; i++)
-        if (b >= a.d[i].block_base) k = i;
+    // The block's matrix is blockIdx.y, so the reads of its descriptor (at an
+    // offset known when the wave starts) and of the input mode's arguments
+    // go out as one batch of scalar loads; the ones the first vector loads
+    // need are pinned there (a later first use would cost another round trip
+    // to the arguments, which the weight stream keeps out of the caches).
+    const int k = (int)blockIdx.y;
+    int nb = a.d[k].nblocks, mode = a.in_mode, attn_lofs = a.attn_lofs;
+    uint64_t u_pr = (uint64_t)a.d[k].probes, u_x = (uint64_t)a.d[k].x;
+    uint64_t u_h = (uint64_t)a.h, u_res = (uint64_t)a.res_acc, u_gain = (uint64_t)a.gain, u_attn = (uint64_t)a.attn_acc;
+    asm volatile("" : "+s"(nb), "+s"(mode), "+s"(attn_lofs), "+s"(u_pr), "+s"(u_x), "+s"(u_h), "+s"(u_res), "+s"(u_gain),
+                 "+s"(u_attn));
+    if ((int)blockIdx.x >= nb) return;   // the grid's x covers the largest matrix
+    const uint16_t* probes = as_global<const uint16_t>(u_pr);
+    float* dx = as_global<float>(u_x);
+    const float* a_h = as_global<const float>(u_h);
+    const void* a_res = as_global<const double>(u_res);
+    const uint16_t* a_gain = as_global<const uint16_t>(u_gain);
+    const void* a_attn = as_global<const double>(u_attn);
+    const int b = xcd_remap((int)blockIdx.x, nb);
     const WalkDesc& d = a.d[k];
-    const int w = b - d.block_base;
-    const int p = w / d.T;
-    const int t = w - p * d.T;
-    const int i0 = p * d.IPS;
-    const int ni = min(d.IPS, d.n_in - i0);
-    const int mode = a.in_mode;
-    const bool cut_thread = tid < kCutThreads;
     const bool norm = mode == kInNorm || mode == kInResNorm || mode == kInEmbedNorm;
     const bool regs = norm || mode == kInAttn;           // x[0:4096] computed in registers
-    const bool slice_regs = regs && i0 + ni <= kProbes;  // ... and the slice among them
-    const bool first = w == 0 && k == 0;
 
     // ---- prologue: every global load is issued before any is used
-    float xs[kCutVPT];
-    double ra[kCutVPT];
-    uint4 pr[2], gr[2], er[2];
-    float sc[kCutVPT];
+    float xs[VPT];
+    double ra[VPT];
+    uint32_t pw[VPT / 2], gw[VPT / 2], ew[VPT / 2];
+    float sc[VPT];
 #pragma unroll
-    for (int k2 = 0; k2 < kCutVPT; k2++) {
+    for (int k2 = 0; k2 < VPT; k2++) {
         xs[k2] = 0.0f;
         ra[k2] = 0.0;
         sc[k2] = 1.0f;
     }
-    pr[0] = pr[1] = gr[0] = gr[1] = er[0] = er[1] = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+    for (int k2 = 0; k2 < VPT / 2; k2++) pw[k2] = gw[k2] = ew[k2] = 0u;
     double lsum = 1.0;
     float cutoff = 0.0f;
     if (mode == kInCutoff) {
         cutoff = *d.cutoff;
-    } else if (cut_thread) {
-        load_probes(d.probes, pr);
-        if (mode == kInX) load16(d.x, xs);
-        if (mode == kInNorm || mode == kInResNorm) load16(a.h, xs);
-        if (mode == kInResNorm && a.res_acc) load16_acc(reinterpret_cast<const double*>(a.res_acc), ra);
+    } else {
+        load_h16<VPT>(probes, pw);
+        if (mode == kInX) load_f32<VPT>(dx, xs);
+        if (mode == kInNorm || mode == kInResNorm) load_f32<VPT>(a_h, xs);
+        if (mode == kInResNorm && a_res) load_f64<VPT>(reinterpret_cast<const double*>(a_res), ra);
         if (mode == kInEmbedNorm) {
             const int tok = *a.token;
-            if (tok >= 0 && tok < a.vocab) {
-                const uint4* ev = reinterpret_cast<const uint4*>(a.embed + (size_t)tok * kProbes + tid * kCutVPT);
-                er[0] = ev[0];
-                er[1] = ev[1];
-            }
-            if (a.embed_scale) load16(a.embed_scale, sc);
+            if (tok >= 0 && tok < a.vocab) load_h16<VPT>(a.embed + (size_t)tok * kProbes, ew);
+            if (a.embed_scale) load_f32<VPT>(a.embed_scale, sc);
         }
-        if (norm) {
-            gr[0] = reinterpret_cast<const uint4*>(a.gain + tid * kCutVPT)[0];
-            gr[1] = reinterpret_cast<const uint4*>(a.gain + tid * kCutVPT)[1];
-        }
+        if (norm) load_h16<VPT>(a_gain, gw);
         if (mode == kInAttn) {
-            const double* A = reinterpret_cast<const double*>(a.attn_acc);
-            load16_acc(A, ra);
-            lsum = A[a.attn_lofs + ((tid * kCutVPT) >> 7)];
+            const double* A = reinterpret_cast<const double*>(a_attn);
+            load_f64<VPT>(A, ra);
+            lsum = A[attn_lofs + ((tid * VPT) >> 7)];   // the head of the thread's inputs
         }
     }
+    // the block's slice and column tile (from the descriptor read through k)
+    const int w = b;
+    const int p = w / d.T;
+    const int t = w - p * d.T;
+    const int i0 = p * d.IPS;
+    const int ni = min(d.IPS, d.n_in - i0);
+    const SelSrc ss{d.stats, dx, d.stats_stride, d.stats_channel, d.rows};
+    const int quantile = d.quantile;
+    const bool slice_regs = regs && i0 + ni <= kProbes;  // x of the slice among the computed ones
+    const bool first = w == 0 && k == 0;
     SelLoads L;
-    select_load(d, a, i0, ni, slice_regs ? kXRegs : (mode == kInAttn ? kXAttn : kXMem), L);
+    select_load(ss, a, i0, ni, slice_regs ? kXRegs : (mode == kInAttn ? kXAttn : kXMem), L);
 
     // ---- the input
-    if (mode != kInCutoff && cut_thread) {
-        if (mode == kInResNorm && a.res_acc) {
+    if (mode != kInCutoff) {
+        if (mode == kInResNorm && a_res) {
 #pragma unroll
-            for (int k2 = 0; k2 < kCutVPT; k2++) xs[k2] = __fadd_rn(xs[k2], (float)ra[k2]);   // add32
+            for (int k2 = 0; k2 < VPT; k2++) xs[k2] = __fadd_rn(xs[k2], (float)ra[k2]);   // add32
         }
         if (mode == kInEmbedNorm) {   // fetchRow16to32 (aux.cl:442-452), then the optional channel scale
-            const uint32_t ew[8] = {er[0].x, er[0].y, er[0].z, er[0].w, er[1].x, er[1].y, er[1].z, er[1].w};
 #pragma unroll
-            for (int k2 = 0; k2 < kCutVPT; k2++) xs[k2] = __fmul_rn(h2f(ew[k2 >> 1] >> ((k2 & 1) * 16)), sc[k2]);
+            for (int k2 = 0; k2 < VPT; k2++) xs[k2] = __fmul_rn(half_at<VPT>(ew, k2), sc[k2]);
         }
         if (mode == kInAttn) {
 #pragma unroll
-            for (int k2 = 0; k2 < kCutVPT; k2++) xs[k2] = (float)(ra[k2] / lsum);
+            for (int k2 = 0; k2 < VPT; k2++) xs[k2] = (float)(ra[k2] / lsum);
         }
-        if ((mode == kInResNorm || mode == kInEmbedNorm) && first && a.h_out) {
-            float4* ho = reinterpret_cast<float4*>(a.h_out + tid * kCutVPT);
-#pragma unroll
-            for (int k4 = 0; k4 < 4; k4++) ho[k4] = make_float4(xs[4 * k4], xs[4 * k4 + 1], xs[4 * k4 + 2], xs[4 * k4 + 3]);
-        }
+        if ((mode == kInResNorm || mode == kInEmbedNorm) && first && a.h_out) store_f32<VPT>(a.h_out, xs);
     }
-    if (norm) block_rmsnorm4096(xs, gr, a.eps, reinterpret_cast<float*>(s_row));
-    if (regs && cut_thread) {
-        if (first && d.x) {
-            float4* xo = reinterpret_cast<float4*>(d.x + tid * kCutVPT);
-#pragma unroll
-            for (int k4 = 0; k4 < 4; k4++) xo[k4] = make_float4(xs[4 * k4], xs[4 * k4 + 1], xs[4 * k4 + 2], xs[4 * k4 + 3]);
-        }
+    if (norm) block_rmsnorm4096<VPT>(xs, gw, a.eps, reinterpret_cast<float*>(s_row));
+    if (regs) {
+        if (first && dx) store_f32<VPT>(dx, xs);
         if (slice_regs) {
 #pragma unroll
-            for (int k2 = 0; k2 < kCutVPT; k2++) {
-                const int i = tid * kCutVPT + k2 - i0;
+            for (int k2 = 0; k2 < VPT; k2++) {
+                const int i = tid * VPT + k2 - i0;
                 if (i >= 0 && i < ni) s_x[i] = xs[k2];
             }
         }
@@ -584,16 +657,16 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
 
     // ---- cutoff
     if (mode != kInCutoff) {
-        float v[kCutVPT];
-        importances(xs, pr, v);
-        cutoff = search_cutoff<NW>(v, d.quantile, SL);
+        float v[VPT];
+        importances<VPT>(xs, pw, v);
+        cutoff = search_cutoff<NW>(v, quantile, SL);
         if (w == 0 && tid == 0) d.cutoff[0] = cutoff;
         __syncthreads();   // the search scratch becomes the wave tiles
     }
     for (int i = lane; i < TSLOTS; i += 64) tiles[wave * TSLOTS + i] = (Acc)0;
 
     // ---- selection of the slice's rows
-    const int ns = (int)select_finish<NT>(d, cutoff, i0, ni, L, s_row, s_x, s_wsum, slice_regs);
+    const int ns = (int)select_finish<NT>(ss, cutoff, i0, ni, L, s_row, s_x, s_wsum, slice_regs);
     if (t == 0 && tid == 0) {
         d.slice_count[p] = (uint32_t)ns;
         if (a.counters) {
@@ -847,30 +920,18 @@ static double est_fraction(float effort)
 
 double est_rows(int rows, float effort) { return std::max(1.0, rows * est_fraction(effort)); }
 
-// Walk launch shapes: below IAM_WALK_WIDE_BYTES of expected weight bytes 4
-// waves per workgroup and about one workgroup per IAM_WALK_WG_BYTES (at least
-// IAM_WALK_MIN_WGS; two or three fit a CU); above it 8 waves and one
-// workgroup per CU (IAM_WALK_WIDE_WGS), so that no CU holds more work than
-// another.
+// Walk launch shape: 8-wave workgroups (each CU holds one: 128 KB of fp64
+// tiles), about IAM_WALK_WGS of them, shared among the matrices in
+// proportion to their expected weight bytes (at least one slice each), so
+// that no CU holds more work than another.
 #ifndef IAM_WALK_UNR
 #define IAM_WALK_UNR 4
 #endif
-#ifndef IAM_WALK_WG_BYTES
-#define IAM_WALK_WG_BYTES 131072.0
+#ifndef IAM_WALK_WGS
+#define IAM_WALK_WGS 256
 #endif
-#ifndef IAM_WALK_MIN_WGS
-#define IAM_WALK_MIN_WGS 256.0
-#endif
-#ifndef IAM_WALK_WIDE_BYTES
-#define IAM_WALK_WIDE_BYTES 40e6
-#endif
-#ifndef IAM_WALK_WIDE_WGS
-#define IAM_WALK_WIDE_WGS 256
-#endif
-constexpr double kWalkMaxWgs = 2048.0;
+constexpr int kWalkWaves = 8;
 
-// Slices per matrix (only the performance depends on them): the launch's
-// workgroups are shared by the matrices in proportion to their bytes.
 void plan_walk(int n, const MatOp* ops, float effort, WalkPlan* plan)
 {
     double bytes[kMaxMulti], tot = 0;
@@ -883,14 +944,11 @@ void plan_walk(int n, const MatOp* ops, float effort, WalkPlan* plan)
         bytes[i] = est_rows(pl.n_in * 16, effort) * pl.T * kTileCols * 2.0;
         tot += bytes[i];
     }
-    const bool wide = tot >= IAM_WALK_WIDE_BYTES;
-    const int nw = wide ? 8 : 4;
-    const double target = wide ? IAM_WALK_WIDE_WGS : std::min(kWalkMaxWgs, std::max(IAM_WALK_MIN_WGS, tot / IAM_WALK_WG_BYTES));
     for (int i = 0; i < n; i++) {
         WalkPlan& pl = plan[i];
-        pl.NW = nw;
-        const double wgs = tot > 0 ? target * bytes[i] / tot : target / n;
-        const int slices = std::max(1, wide ? (int)std::floor(wgs / pl.T + 1e-9) : (int)std::lround(wgs / pl.T));
+        pl.NW = kWalkWaves;
+        const double wgs = tot > 0 ? IAM_WALK_WGS * bytes[i] / tot : (double)IAM_WALK_WGS / n;
+        const int slices = std::max(1, (int)std::floor(wgs / pl.T + 1e-9));
         pl.IPS = std::min(64 * pl.NW, std::max(1, (pl.n_in + slices - 1) / slices));
         pl.P = (pl.n_in + pl.IPS - 1) / pl.IPS;
     }
@@ -990,10 +1048,9 @@ static int bucketmul_list(Ctx* c, int i)
 }
 
 template <typename Acc>
-static int launch_walk(Ctx* c, int nw, int blocks, const WalkArgs& args)
+static int launch_walk(Ctx* c, dim3 grid, const WalkArgs& args)
 {
-    if (nw == 8) return launch(c, "bucket_walk", k_walk<Acc, 8, IAM_WALK_UNR>, dim3(blocks), dim3(512), 0, args);
-    return launch(c, "bucket_walk", k_walk<Acc, 4, IAM_WALK_UNR>, dim3(blocks), dim3(256), 0, args);
+    return launch(c, "bucket_walk", k_walk<Acc, kWalkWaves, IAM_WALK_UNR>, grid, dim3(64 * kWalkWaves), 0, args);
 }
 
 int walk_group(Ctx* c, const WalkGroup& g)
@@ -1019,7 +1076,6 @@ int walk_group(Ctx* c, const WalkGroup& g)
     WalkArgs args{};
     args.n = g.n;
     const int qv = quantile_of(g.effort);
-    int blocks = 0;
     for (int i = 0; i < g.n; i++) {
         const WalkMat& wm = g.m[i];
         const iam_bucket_matrix& M = wm.mat;
@@ -1042,10 +1098,14 @@ int walk_group(Ctx* c, const WalkGroup& g)
         d.IPS = plan[i].IPS;
         d.P = plan[i].P;
         d.T = plan[i].T;
-        d.block_base = blocks;
+        d.nblocks = plan[i].P * plan[i].T;
         d.expected = plan[i].P;
-        blocks += plan[i].P * plan[i].T;
     }
+    // grid: x over the largest matrix (a multiple of 8, so that block x of
+    // every matrix sits on XCD x % 8), y over the matrices
+    int gx = 0;
+    for (int i = 0; i < g.n; i++) gx = std::max(gx, args.d[i].nblocks);
+    gx = (gx + 7) & ~7;
     if (g.fin == kFinSilu) {
         IAM_REQUIRE(g.n == 2 && g.m[0].mat.bucket_cols == g.m[1].mat.bucket_cols && g.silu_out,
                     "walk: the SiLU gate pairs two matrices of one shape");
@@ -1082,7 +1142,8 @@ int walk_group(Ctx* c, const WalkGroup& g)
     // walk_count reads the slice counts of the slots this launch wrote
     for (int i = 0; i < g.n; i++)
         if (g.m[i].slice_count == c->slots[i].slice_count) c->slots[i].walked_P = plan[i].P;
-    return c->acc64 ? launch_walk<double>(c, plan[0].NW, blocks, args) : launch_walk<float>(c, plan[0].NW, blocks, args);
+    const dim3 grid((unsigned)gx, (unsigned)g.n);
+    return c->acc64 ? launch_walk<double>(c, grid, args) : launch_walk<float>(c, grid, args);
 }
 
 // The standalone walk of the n matrices recorded in slots 0..n-1: the

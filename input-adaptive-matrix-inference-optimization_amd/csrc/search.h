@@ -33,14 +33,14 @@
 
 namespace iam {
 
-constexpr int kCutThreads = 256;              // threads holding importances
-constexpr int kCutVPT = IAM_PROBES_COUNT / kCutThreads;   // 16 per thread
+constexpr int kCutThreads = 256;              // threads of the standalone cutoff kernels
+constexpr int kCutVPT = IAM_PROBES_COUNT / kCutThreads;   // 16 importances per thread there
 
 template <int NW>
 struct SearchLds {
-    uint32_t H[2][4][256];     // digit histograms of the 4 value-holding waves, two passes
+    uint32_t H[2][NW][256];    // digit histograms of the waves, two passes
     uint32_t red[2][NW];       // key min - 1, key max per wave
-    uint32_t nb[4][4];         // per holder wave: the two nearest keys above u and below (as offsets)
+    uint32_t nb[NW][4];        // per wave: the two nearest keys above u and below (as offsets)
     uint32_t cand;             // the one key of a one-key bin
 };
 
@@ -101,28 +101,27 @@ __device__ __forceinline__ void wave_low2(uint32_t& a1, uint32_t& a2)
     a2 = lane63(a2);
 }
 
-// The cutoff of the 4096 importances held 16 per thread by the first 256
-// threads (v: numbers >= +0 or NaN, as 1e5 * |x * probe| gives; other
-// threads' values are ignored).  Every thread returns it.  On return the
-// scratch may be reused after a further barrier.
+// The cutoff of the 4096 importances held VPT = 4096 / (64 NW) per thread
+// (v: numbers >= +0 or NaN, as 1e5 * |x * probe| gives).  Every thread
+// returns it.  On return the scratch may be reused after a further barrier.
 template <int NW>
-__device__ float search_cutoff(const float (&v)[kCutVPT], int quantile, SearchLds<NW>& L)
+__device__ float search_cutoff(const float (&v)[IAM_PROBES_COUNT / (64 * NW)], int quantile, SearchLds<NW>& L)
 {
 #pragma clang fp contract(off)
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+    constexpr int VPT = IAM_PROBES_COUNT / (64 * NW);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const bool holder = tid < kCutThreads;
     const int t = IAM_PROBES_COUNT - quantile;         // bucketMul.cl:81
 
     // ---- 1. keys, their range and the count of numbers
-    uint32_t key[kCutVPT];
+    uint32_t key[VPT];
     uint32_t kmn1 = 0xffffffffu, kmx = 0u;   // min of key - 1 (NaN keys wrap to the top), max
     int nv = 0;
 #pragma unroll
-    for (int k = 0; k < kCutVPT; k++) {
-        key[k] = holder ? order_key(v[k]) : 0u;
+    for (int k = 0; k < VPT; k++) {
+        key[k] = order_key(v[k]);
         kmn1 = min(kmn1, key[k] - 1u);
         kmx = max(kmx, key[k]);
         nv += __popcll(__ballot(key[k] != 0u));
@@ -136,9 +135,9 @@ __device__ float search_cutoff(const float (&v)[kCutVPT], int quantile, SearchLd
     // the block's count: the waves' ballots summed through the histogram
     // scratch of pass 2 (cleared below before its use)
     if (lane == 0) L.H[1][0][wave] = (uint32_t)nv;
-    // each holder wave clears its first histogram (its own region: program
-    // order puts the clear before its atomics)
-    if (holder) *reinterpret_cast<uint4*>(&L.H[0][wave][4 * lane]) = make_uint4(0u, 0u, 0u, 0u);
+    // each wave clears its first histogram (its own region: program order
+    // puts the clear before its atomics)
+    *reinterpret_cast<uint4*>(&L.H[0][wave][4 * lane]) = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
     kmn1 = 0xffffffffu;
     kmx = 0u;
@@ -169,12 +168,12 @@ __device__ float search_cutoff(const float (&v)[kCutVPT], int quantile, SearchLd
         int buf = 0;
         bool first = true;
         for (;;) {
-            if (holder) {
+            {
                 uint32_t* H = L.H[buf][wave];
                 const uint32_t dmask = (1u << w) - 1u;
                 const int sw = first ? 0 : s + w;   // the first pass takes every number
 #pragma unroll
-                for (int k = 0; k < kCutVPT; k++) {
+                for (int k = 0; k < VPT; k++) {
                     const uint32_t rel = key[k] - kmn;
                     const bool in = key[k] != 0u && (first || (rel >> sw) == prefix);
                     if (in) atomicAdd(H + ((rel >> s) & dmask), 1u);
@@ -182,16 +181,17 @@ __device__ float search_cutoff(const float (&v)[kCutVPT], int quantile, SearchLd
             }
             __syncthreads();
             // the next pass's histogram (free: every wave has scanned it)
-            if (holder) *reinterpret_cast<uint4*>(&L.H[buf ^ 1][wave][4 * lane]) = make_uint4(0u, 0u, 0u, 0u);
-            // bins 4*lane .. 4*lane+3 summed over the holder waves
-            const uint4 h0 = *reinterpret_cast<const uint4*>(&L.H[buf][0][4 * lane]);
-            const uint4 h1 = *reinterpret_cast<const uint4*>(&L.H[buf][1][4 * lane]);
-            const uint4 h2 = *reinterpret_cast<const uint4*>(&L.H[buf][2][4 * lane]);
-            const uint4 h3 = *reinterpret_cast<const uint4*>(&L.H[buf][3][4 * lane]);
-            const int c0 = (int)(h0.x + h1.x + h2.x + h3.x);
-            const int c1 = (int)(h0.y + h1.y + h2.y + h3.y);
-            const int c2 = (int)(h0.z + h1.z + h2.z + h3.z);
-            const int c3 = (int)(h0.w + h1.w + h2.w + h3.w);
+            *reinterpret_cast<uint4*>(&L.H[buf ^ 1][wave][4 * lane]) = make_uint4(0u, 0u, 0u, 0u);
+            // bins 4*lane .. 4*lane+3 summed over the waves
+            int c0 = 0, c1 = 0, c2 = 0, c3 = 0;
+#pragma unroll
+            for (int w2 = 0; w2 < NW; w2++) {
+                const uint4 h = *reinterpret_cast<const uint4*>(&L.H[buf][w2][4 * lane]);
+                c0 += (int)h.x;
+                c1 += (int)h.y;
+                c2 += (int)h.z;
+                c3 += (int)h.w;
+            }
             const int incl = wave_incl_sum(c0 + c1 + c2 + c3);
             const int above3 = __builtin_amdgcn_readlane(incl, 63) - incl;   // keys in bins above 4*lane+3
             const int above2 = above3 + c3, above1 = above2 + c2, above0 = above1 + c1;
@@ -213,11 +213,9 @@ __device__ float search_cutoff(const float (&v)[kCutVPT], int quantile, SearchLd
             }
             if (cnt == 1) {
                 // the one key whose offset from the minimum starts with prefix
-                if (holder) {
 #pragma unroll
-                    for (int k = 0; k < kCutVPT; k++)
-                        if (key[k] != 0u && ((key[k] - kmn) >> s) == prefix) L.cand = key[k];
-                }
+                for (int k = 0; k < VPT; k++)
+                    if (key[k] != 0u && ((key[k] - kmn) >> s) == prefix) L.cand = key[k];
                 __syncthreads();
                 ukey = L.cand;
                 eq = 1;
@@ -233,23 +231,21 @@ __device__ float search_cutoff(const float (&v)[kCutVPT], int quantile, SearchLd
         // ---- 3. the nearest keys on either side of ukey: the smallest of
         // key - (ukey + 1) (keys <= ukey wrap above every key > ukey) and of
         // (ukey - 1) - key (keys >= ukey wrap above every key < ukey)
-        if (holder) {
 #pragma unroll
-            for (int k = 0; k < kCutVPT; k++) {
-                const uint32_t da = key[k] - (ukey + 1u), db = (ukey - 1u) - key[k];
-                a2 = min(a2, max(a1, da));
-                a1 = min(a1, da);
-                b2 = min(b2, max(b1, db));
-                b1 = min(b1, db);
-            }
+        for (int k = 0; k < VPT; k++) {
+            const uint32_t da = key[k] - (ukey + 1u), db = (ukey - 1u) - key[k];
+            a2 = min(a2, max(a1, da));
+            a1 = min(a1, da);
+            b2 = min(b2, max(b1, db));
+            b1 = min(b1, db);
         }
         wave_low2(a1, a2);
         wave_low2(b1, b2);
-        if (holder && lane == 0) *reinterpret_cast<uint4*>(L.nb[wave]) = make_uint4(a1, a2, b1, b2);
+        if (lane == 0) *reinterpret_cast<uint4*>(L.nb[wave]) = make_uint4(a1, a2, b1, b2);
         __syncthreads();
         a1 = a2 = b1 = b2 = 0xffffffffu;
 #pragma unroll
-        for (int w2 = 0; w2 < 4; w2++) {
+        for (int w2 = 0; w2 < NW; w2++) {
             const uint4 q = *reinterpret_cast<const uint4*>(L.nb[w2]);
             merge_low2(a1, a2, q.x, q.y);
             merge_low2(b1, b2, q.z, q.w);

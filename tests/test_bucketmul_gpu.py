@@ -161,9 +161,9 @@ def _cutoff_patterns():
 @pytest.mark.parametrize("pattern", [p[0] for p in _cutoff_patterns()])
 def test_cutoff_edge_paths(O, iam, ctx, pattern):
     """The search's edge paths on the GPU, bit-exact against the oracle: the
-    standalone cutoff kernel (calc_dispatch + mul), and the walk's own search
-    (iam_bucketmul_fused) with 4-wave workgroups (256 outputs) and with
-    8-wave workgroups (the LM-head shape)."""
+    standalone cutoff kernel (calc_dispatch + mul, 4 waves, 16 importances
+    per thread), and the walk's own search (iam_bucketmul_fused, 8 waves, 8
+    per thread) on a 256-output matrix and on the LM-head shape."""
     name, x, effort, (rounds, conv) = next(p for p in _cutoff_patterns() if p[0] == pattern)
     probes = np.full(4096, 0x2400, np.uint16)
     _, tr = O.find_cutoff(x, probes, O.effort_quantile(effort), trace=True)
@@ -224,9 +224,9 @@ _SEARCH_KINDS = ["normal", "skew", "ties", "constant", "outlier", "tiny", "inf",
 def test_cutoff_search_kinds(O, iam, ctx, kind):
     """The cutoff search bit-exact against the oracle on 15 importance
     patterns at efforts that give the quantiles 0..3, 4092..4095 and the
-    usual ones: the standalone cutoff kernel, and the walk's own search in
-    4-wave (256 outputs) and 8-wave (32000 outputs) workgroups; the selected
-    row count matches too."""
+    usual ones: the standalone cutoff kernel (4 waves) and the walk's own
+    search (8 waves) on 256 and 32000 outputs; the selected row count
+    matches too."""
     rng = np.random.default_rng(100 + _SEARCH_KINDS.index(kind))
     x, p = _search_input(kind, rng)
     quants = [0, 1, 2, 3, 100, 1023, 2047, 3071, 3583, 3890, 4092, 4093, 4094, 4095]
