@@ -227,7 +227,9 @@ __global__ __launch_bounds__(kCutThreads) void k_dispatch(DispatchDesc d)
     const int lane = tid & 63;
     const int wave = tid >> 6;
 
-    const float cutoff = block_cutoff(d.x, d.probes, d.quantile, L);
+    block_cutoff(d.x, d.probes, d.quantile, L);
+    __syncthreads();
+    const float cutoff = L.cut;
     if (g == 0 && tid == 0) d.cutoff[1] = cutoff;   // cross-checked against the search launch's cutoff[0]
 
     const int i = g * kChunkInputs + tid;
@@ -543,15 +545,18 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     constexpr int VPT = IAM_PROBES_COUNT / NT;              // inputs of the cutoff per thread
     static_assert(kTileOut % NT == 0, "flush mapping");
-    static_assert(sizeof(Acc) * NW * TSLOTS >= sizeof(SearchLds<NW>), "the search scratch lives in the tiles");
-    __shared__ __align__(16) Acc tiles[NW * TSLOTS];   // the search's scratch, then the wave tiles
-    __shared__ __align__(16) uint16_t s_row[NT * 16];
+    __shared__ __align__(16) Acc tiles[NW * TSLOTS];   // the wave tiles
+    // the search's scratch, then the selected rows
+    constexpr int kSearchBytes = sizeof(SearchLds<NW>) > NT * 16 * 2 ? sizeof(SearchLds<NW>) : NT * 16 * 2;
+    __shared__ __align__(16) uint4 s_search[(kSearchBytes + 15) / 16];
+    uint16_t* s_row = reinterpret_cast<uint16_t*>(s_search);
     __shared__ __align__(16) float s_x[NT];
+    __shared__ float s_part[256];
     __shared__ uint32_t s_wsum[NW];
     __shared__ int s_last;
     __shared__ float s_bv[NW];
     __shared__ int s_bi[NW];
-    SearchLds<NW>& SL = *reinterpret_cast<SearchLds<NW>*>(tiles);
+    SearchLds<NW>& SL = *reinterpret_cast<SearchLds<NW>*>(s_search);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -614,6 +619,13 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
             lsum = A[attn_lofs + ((tid * VPT) >> 7)];   // the head of the thread's inputs
         }
     }
+    // each wave clears its own tile while the loads are in flight
+    {
+        uint4* tz = reinterpret_cast<uint4*>(tiles + wave * TSLOTS);
+        constexpr int kTileVecs = TSLOTS * (int)sizeof(Acc) / 16;
+#pragma unroll
+        for (int i = 0; i < kTileVecs / 64; i++) tz[i * 64 + lane] = make_uint4(0u, 0u, 0u, 0u);
+    }
     // the block's slice and column tile (from the descriptor read through k)
     const int w = b;
     const int p = w / d.T;
@@ -643,7 +655,7 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
         }
         if ((mode == kInResNorm || mode == kInEmbedNorm) && first && a.h_out) store_f32<VPT>(a.h_out, xs);
     }
-    if (norm) block_rmsnorm4096<VPT>(xs, gw, a.eps, reinterpret_cast<float*>(s_row));
+    if (norm) block_rmsnorm4096<VPT>(xs, gw, a.eps, s_part);
     if (regs) {
         if (first && dx) store_f32<VPT>(dx, xs);
         if (slice_regs) {
@@ -659,11 +671,11 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     if (mode != kInCutoff) {
         float v[VPT];
         importances<VPT>(xs, pw, v);
-        cutoff = search_cutoff<NW>(v, quantile, SL);
+        search_cutoff<NW>(v, quantile, SL);
+        __syncthreads();   // wave 0 has stored the cutoff; the search scratch becomes the row list
+        cutoff = SL.cut;
         if (w == 0 && tid == 0) d.cutoff[0] = cutoff;
-        __syncthreads();   // the search scratch becomes the wave tiles
     }
-    for (int i = lane; i < TSLOTS; i += 64) tiles[wave * TSLOTS + i] = (Acc)0;
 
     // ---- selection of the slice's rows
     const int ns = (int)select_finish<NT>(ss, cutoff, i0, ni, L, s_row, s_x, s_wsum, slice_regs);

@@ -40,8 +40,9 @@ template <int NW>
 struct SearchLds {
     uint32_t H[2][NW][256];    // digit histograms of the waves, two passes
     uint32_t red[2][NW];       // key min - 1, key max per wave
-    uint32_t nb[NW][4];        // per wave: the two nearest keys above u and below (as offsets)
-    uint32_t cand;             // the one key of a one-key bin
+    uint32_t nb[NW][4];        // per wave: the two smallest keys above u's bin, and of ~key below it
+    uint32_t tie[NW];          // per wave: the largest key in u's bin
+    float cut;                 // the cutoff (wave 0 writes it)
 };
 
 __device__ __forceinline__ float uniform_f(float v)
@@ -102,8 +103,11 @@ __device__ __forceinline__ void wave_low2(uint32_t& a1, uint32_t& a2)
 }
 
 // The cutoff of the 4096 importances held VPT = 4096 / (64 NW) per thread
-// (v: numbers >= +0 or NaN, as 1e5 * |x * probe| gives).  Every thread
-// returns it.  On return the scratch may be reused after a further barrier.
+// (v: numbers >= +0 or NaN, as 1e5 * |x * probe| gives).  Wave 0 finishes
+// the search after its last barrier: its threads return the cutoff and lane
+// 0 stores it in L.cut; the other waves return 0 there, so a caller that
+// needs the cutoff in every wave reads L.cut after a barrier.  The scratch
+// may be reused after that barrier.
 template <int NW>
 __device__ float search_cutoff(const float (&v)[IAM_PROBES_COUNT / (64 * NW)], int quantile, SearchLds<NW>& L)
 {
@@ -137,7 +141,7 @@ __device__ float search_cutoff(const float (&v)[IAM_PROBES_COUNT / (64 * NW)], i
     if (lane == 0) L.H[1][0][wave] = (uint32_t)nv;
     // each wave clears its first histogram (its own region: program order
     // puts the clear before its atomics)
-    *reinterpret_cast<uint4*>(&L.H[0][wave][4 * lane]) = make_uint4(0u, 0u, 0u, 0u);
+    reinterpret_cast<uint4*>(L.H[0][wave])[lane] = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
     kmn1 = 0xffffffffu;
     kmx = 0u;
@@ -153,7 +157,9 @@ __device__ float search_cutoff(const float (&v)[IAM_PROBES_COUNT / (64 * NW)], i
     const float gmin = nv ? fminf(1e30f, key_float(kmn)) : 1e30f;
     const float gmax = nv ? fmaxf(-1e30f, key_float(kmx)) : -1e30f;
 
-    // ---- 2. radix select of the key of rank a (descending, 1-based)
+    // ---- 2. radix select of the key of rank a (descending, 1-based): after
+    // it, the keys whose offset from the minimum has the top bits `prefix`
+    // (shift s) are the tie group of u_a: equal keys (s == 0) or one key
     const int a = min(t, nv);
     uint32_t ukey = 0u;
     int gt = 0, eq = 0;            // #(keys > ukey), #(keys == ukey)
@@ -181,12 +187,12 @@ __device__ float search_cutoff(const float (&v)[IAM_PROBES_COUNT / (64 * NW)], i
             }
             __syncthreads();
             // the next pass's histogram (free: every wave has scanned it)
-            *reinterpret_cast<uint4*>(&L.H[buf ^ 1][wave][4 * lane]) = make_uint4(0u, 0u, 0u, 0u);
+            reinterpret_cast<uint4*>(L.H[buf ^ 1][wave])[lane] = make_uint4(0u, 0u, 0u, 0u);
             // bins 4*lane .. 4*lane+3 summed over the waves
             int c0 = 0, c1 = 0, c2 = 0, c3 = 0;
 #pragma unroll
             for (int w2 = 0; w2 < NW; w2++) {
-                const uint4 h = *reinterpret_cast<const uint4*>(&L.H[buf][w2][4 * lane]);
+                const uint4 h = reinterpret_cast<const uint4*>(L.H[buf][w2])[lane];
                 c0 += (int)h.x;
                 c1 += (int)h.y;
                 c2 += (int)h.z;
@@ -206,19 +212,8 @@ __device__ float search_cutoff(const float (&v)[IAM_PROBES_COUNT / (64 * NW)], i
             r -= __builtin_amdgcn_readlane(ab, src);
             const int cnt = __builtin_amdgcn_readlane(cd, src);
             prefix = (prefix << w) | dd;
-            if (s == 0) {              // prefix is the key's offset: cnt keys equal it
-                ukey = kmn + prefix;
+            if (s == 0 || cnt == 1) {  // the bin holds cnt equal keys, or one key
                 eq = cnt;
-                break;
-            }
-            if (cnt == 1) {
-                // the one key whose offset from the minimum starts with prefix
-#pragma unroll
-                for (int k = 0; k < VPT; k++)
-                    if (key[k] != 0u && ((key[k] - kmn) >> s) == prefix) L.cand = key[k];
-                __syncthreads();
-                ukey = L.cand;
-                eq = 1;
                 break;
             }
             w = min(8, s);
@@ -228,12 +223,18 @@ __device__ float search_cutoff(const float (&v)[IAM_PROBES_COUNT / (64 * NW)], i
         }
         gt = a - r;                    // r is the rank left within the keys equal to ukey
 
-        // ---- 3. the nearest keys on either side of ukey: the smallest of
-        // key - (ukey + 1) (keys <= ukey wrap above every key > ukey) and of
-        // (ukey - 1) - key (keys >= ukey wrap above every key < ukey)
+        // ---- 3. the tie group's key, the two smallest keys above its bin and
+        // the two largest below it (as the two smallest ~key; NaN keys, 0,
+        // lie below every bin, and an absent one decodes to the NaN key,
+        // which compares like -inf)
+        uint32_t tmax = 0u;
 #pragma unroll
         for (int k = 0; k < VPT; k++) {
-            const uint32_t da = key[k] - (ukey + 1u), db = (ukey - 1u) - key[k];
+            const uint32_t kb = (key[k] - kmn) >> s;
+            const bool num = key[k] != 0u;
+            const uint32_t da = num && kb > prefix ? key[k] : 0xffffffffu;
+            const uint32_t db = num && kb >= prefix ? 0xffffffffu : ~key[k];
+            tmax = max(tmax, num && kb == prefix ? key[k] : 0u);
             a2 = min(a2, max(a1, da));
             a1 = min(a1, da);
             b2 = min(b2, max(b1, db));
@@ -241,15 +242,25 @@ __device__ float search_cutoff(const float (&v)[IAM_PROBES_COUNT / (64 * NW)], i
         }
         wave_low2(a1, a2);
         wave_low2(b1, b2);
-        if (lane == 0) *reinterpret_cast<uint4*>(L.nb[wave]) = make_uint4(a1, a2, b1, b2);
+        tmax = wave_reduce(tmax, [](uint32_t x, uint32_t y) { return max(x, y); });
+        if (lane == 0) {
+            *reinterpret_cast<uint4*>(L.nb[wave]) = make_uint4(a1, a2, b1, b2);
+            L.tie[wave] = tmax;
+        }
         __syncthreads();
+        if (wave != 0) return 0.0f;    // wave 0 finishes the search and writes the cutoff
         a1 = a2 = b1 = b2 = 0xffffffffu;
 #pragma unroll
         for (int w2 = 0; w2 < NW; w2++) {
             const uint4 q = *reinterpret_cast<const uint4*>(L.nb[w2]);
             merge_low2(a1, a2, q.x, q.y);
             merge_low2(b1, b2, q.z, q.w);
+            ukey = max(ukey, L.tie[w2]);
         }
+        b1 = ~b1;
+        b2 = ~b2;
+    } else if (wave != 0) {
+        return 0.0f;
     }
 
     // ---- 4. u_{t+o}, o = -2 .. 2, lane o + 2 computing one (ranks within two
@@ -259,47 +270,54 @@ __device__ float search_cutoff(const float (&v)[IAM_PROBES_COUNT / (64 * NW)], i
     {
         const int k = t + lane - 2;
         const uint32_t kk = (k > gt && k <= gt + eq) ? ukey
-                          : k == gt ? ukey + 1u + a1
-                          : k == gt - 1 ? ukey + 1u + a2
-                          : k == gt + eq + 1 ? ukey - 1u - b1
-                                             : ukey - 1u - b2;
+                          : k == gt ? a1
+                          : k == gt - 1 ? a2
+                          : k == gt + eq + 1 ? b1
+                                             : b2;
         const float uk = k > nv ? -INFINITY : key_float(kk);
 #pragma unroll
         for (int o = 0; o < 5; o++) U[o] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(uk), o));
     }
     const bool top_m1 = t - 1 < 1, top_m2 = t - 2 < 1;   // (U[0], U[1] unused then)
 
-    // ---- 5. the reference's rounds (bucketMul.cl:139-213), lane r keeping
-    // the state after round r (its tested bound, bracket and counts' side);
-    // straight-line selects, no branches
+    // ---- 5. the reference's rounds (bucketMul.cl:139-213): one chain of
+    // bounds (each round's next bound is the midpoint on the side its count
+    // picks, both computed while the count is compared), lane r keeping round
+    // r's tested bound, bracket, side and min-count state
     float lo = gmin, hi = gmax;
     float b = midpoint(gmin, gmax);
     bool min_init = true;          // minB is still the minimum: its count is the reference's 4096 (:142)
-    bool ge = false;
+    float cb = 0.0f, clo = 0.0f, chi = 0.0f;
+    bool cge = false, cmi = true;
 #pragma unroll
     for (int rd = 0; rd < 20; rd++) {
-        const bool act = rd <= lane;
         const bool g = U[2] > b;             // count >= target: min moves
-        const bool up = act && g, down = act && !g;
-        ge = act ? g : ge;
-        lo = up ? b : lo;
-        hi = down ? b : hi;
-        min_init = min_init && !up;
-        const float nb = midpoint(lo, hi);
-        b = rd < lane ? nb : b;
+        const float mh = midpoint(b, hi), ml = midpoint(lo, b);
+        const float nlo = g ? b : lo, nhi = g ? hi : b;
+        min_init = min_init && !g;
+        const bool me = lane == rd;
+        cb = me ? b : cb;
+        clo = me ? nlo : clo;
+        chi = me ? nhi : chi;
+        cge = me ? g : cge;
+        cmi = me ? min_init : cmi;
+        lo = nlo;
+        hi = nhi;
+        b = g ? mh : ml;
     }
     // lane r < 20: the stop tests of round r (bucketMul.cl:195-200)
-    const bool eq_t = ge && !(U[3] > b);                          // count == target
-    const bool am1 = top_m1 || U[1] > hi, am2 = top_m2 || U[0] > hi;
+    const bool eq_t = cge && !(U[3] > cb);                        // count == target
+    const bool am1 = top_m1 || U[1] > chi, am2 = top_m2 || U[0] > chi;
     const int dmax = am1 ? 1 : am2 ? 2 : 3;                       // target - maxCount (3: 3 or more)
-    const int dmin = !(U[3] > lo) ? 0 : !(U[4] > lo) ? 1 : 2;     // minCount - target (2: 2 or more)
-    const bool gap_small = min_init ? (dmax <= 2 && t - dmax >= IAM_PROBES_COUNT - 2)   // 4096 - maxCount < 3
-                                    : dmin + dmax < 3;
-    const bool stop = lane < 20 && (eq_t || __fsub_rn(hi, lo) < 0.00001f || gap_small);
+    const int dmin = !(U[3] > clo) ? 0 : !(U[4] > clo) ? 1 : 2;   // minCount - target (2: 2 or more)
+    const bool gap_small = cmi ? (dmax <= 2 && t - dmax >= IAM_PROBES_COUNT - 2)   // 4096 - maxCount < 3
+                               : dmin + dmax < 3;
+    const bool stop = lane < 20 && (eq_t || __fsub_rn(chi, clo) < 0.00001f || gap_small);
     const uint64_t sm = __ballot(stop);
-    // no stop: the untested midpoint after round 20 (lane 20's b), :211-213
-    const int src = sm ? __ffsll((long long)sm) - 1 : 20;
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(b), src));
+    // no stop: the untested midpoint after round 20 (:211-213)
+    const float cut = sm ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cb), __ffsll((long long)sm) - 1)) : b;
+    if (lane == 0) L.cut = cut;
+    return cut;
 }
 
 }  // namespace iam
