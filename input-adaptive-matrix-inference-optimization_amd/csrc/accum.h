@@ -38,7 +38,8 @@ __device__ __forceinline__ float acc_peek(float* p)
                                              __HIP_MEMORY_SCOPE_AGENT));
 }
 
-// zero n accumulator words, shared out over the grid's workgroups
+// zero n accumulator words, shared out over every workgroup of the grid (x
+// and y): each one must call it, including those with no other work
 template <typename Acc>
 __device__ __forceinline__ void zero_share(void* p, int n, int nt)
 {

@@ -573,7 +573,13 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     uint64_t u_h = (uint64_t)a.h, u_res = (uint64_t)a.res_acc, u_gain = (uint64_t)a.gain, u_attn = (uint64_t)a.attn_acc;
     asm volatile("" : "+s"(nb), "+s"(mode), "+s"(attn_lofs), "+s"(u_pr), "+s"(u_x), "+s"(u_h), "+s"(u_res), "+s"(u_gain),
                  "+s"(u_attn));
-    if ((int)blockIdx.x >= nb) return;   // the grid's x covers the largest matrix
+    if ((int)blockIdx.x >= nb) {
+        // the grid's x covers the largest matrix: a block past this matrix's
+        // count only clears its share of the earlier launches' accumulators
+        zero_share<double>(a.zero_p[0], a.zero_n[0], NT);
+        zero_share<double>(a.zero_p[1], a.zero_n[1], NT);
+        return;
+    }
     const uint16_t* probes = as_global<const uint16_t>(u_pr);
     float* dx = as_global<float>(u_x);
     const float* a_h = as_global<const float>(u_h);

@@ -223,3 +223,27 @@ def test_wide_model_logits_and_tokens_match_oracle(O, iam, ctx):
         dlog.free()
     finally:
         m.close()
+
+
+FFN_WIDE = dict(n_layers=1, dim=4096, ffn_dim=14336, n_heads=32, n_kv_heads=8, head_dim=128, vocab=32000,
+                max_ctx=64, rope_theta=10000.0, norm_eps=1e-5)
+
+
+def test_mistral_width_layer_matches_oracle_every_position(O, iam, ctx):
+    """One layer at the Mistral-7B widths (FFN 14336, vocabulary 32000): the
+    walk grids of these launches carry blocks past the smaller matrices'
+    counts, which must still clear their share of the previous launches'
+    accumulators.  Logits within 1 ulp of the oracle model's at 12
+    consecutive positions (eager steps on the same tokens)."""
+    m = iam.Model(ctx, iam.ModelConfig(**FFN_WIDE))
+    try:
+        m.synthesize(0)
+        orc = O.OracleModel(FFN_WIDE, m.read_tensor)
+        m.reset_caches()
+        dlog = ctx.empty(FFN_WIDE["vocab"], np.float32)
+        for pos, tok in enumerate(O.gen_tokens(0, 90, 12, FFN_WIDE["vocab"]).tolist()):
+            m.forward(tok, pos, 0.25, dlog)
+            assert ulps(dlog.read(), orc.forward(tok, pos, 0.25)).max() <= 1, pos
+        dlog.free()
+    finally:
+        m.close()
