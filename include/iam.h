@@ -83,7 +83,10 @@ int iam_profiling(iam_ctx* ctx, int enable);
 /* Gpu::printKernelStats (gpu.hpp:190-234) into a text buffer. */
 int iam_kernel_stats(iam_ctx* ctx, char* buf, size_t len);
 int iam_kernel_stats_reset(iam_ctx* ctx);
-/* total time (ms) and launch count of one kernel name since the last reset */
+/* total time (ms) and launch count of one kernel name since the last reset.
+ * The model's walk launches are labelled by matrix group ("bucket_walk.qkv",
+ * ".o", ".ffn13", ".ffn2", ".lm"); a name without a dot also sums its
+ * labelled launches ("bucket_walk" = every walk); "*" sums every kernel. */
 int iam_kernel_stat(iam_ctx* ctx, const char* name, double* total_ms, int* calls);
 
 /* --------------------------------------------------------------- bucketMul */
@@ -130,13 +133,14 @@ int iam_bucketmul_full(iam_ctx* ctx, const float* x_dev, const uint16_t* stats_d
 int iam_bucketmul_multi(iam_ctx* ctx, int n, const iam_bucket_matrix* mats,
                         const float* const* xs_dev, const int* in_sizes, float* const* ys_dev,
                         int expert_no, float effort);
-/* One matrix group (1..3 matrices sharing one input) in two launches, as
- * the model's decode step runs it: every walk workgroup computes the input
+/* One matrix group (1..3 matrices sharing one input) in one launch, as the
+ * model's decode step runs it: every walk workgroup computes the input
  * itself -- x_dev as given, or, when h_dev is not null, x = RMSNorm(h) * gain
  * (rmsNorm32fast + mul16x32, aux.cl:156-196, :434-440; written to x_dev) --
  * then the cutoff (the same bisection as calc_dispatch, in every workgroup),
- * selects and walks its input slice; the second launch sums the slices into
- * ys_dev[i].  Results equal calc_dispatch + mul.  A norm input of other than
+ * selects and walks its input slice into fp64 (or fp32) accumulators; the
+ * last workgroup to finish a column tile stores that tile of ys_dev[i].
+ * Results equal calc_dispatch + mul.  A norm input of other than
  * 4096 values is normalized by a separate RMSNorm launch first.  No
  * counterpart in the reference, which runs the cutoff as a launch of its
  * own (bucket_mul.hpp:147-176). */
@@ -164,11 +168,21 @@ int iam_effort_quantile(float effort);
  * the walk kernel, so graph replays count too.  Blocking. */
 int iam_walk_counters(iam_ctx* ctx, uint64_t* weight_bytes, uint64_t* rows, uint64_t* matrices,
                       int reset);
-/* Counting of the walk's selected rows (default on): the reduce adds up the
- * per-slice counts into the slot count (iam_bucketmul_walk_count) and the
- * counters above.  Off, neither is updated (walk_count then fails with
- * IAM_E_STATE for the slots walked) and each reduce launch is shorter: its
- * first workgroup no longer waits for the counts and the counter atomics.
+/* The model's walk launches by matrix group: the counters above split by the
+ * group that streamed them (IAM_WALK_GROUP_NONE: standalone calls).  Reset
+ * with iam_walk_counters.  Blocking.  No counterpart in the reference. */
+#define IAM_WALK_GROUP_NONE 0
+#define IAM_WALK_GROUP_QKV 1
+#define IAM_WALK_GROUP_O 2
+#define IAM_WALK_GROUP_FFN13 3
+#define IAM_WALK_GROUP_FFN2 4
+#define IAM_WALK_GROUP_LM 5
+int iam_walk_group_counters(iam_ctx* ctx, int group, uint64_t* weight_bytes, uint64_t* rows,
+                            uint64_t* matrices);
+/* Counting of the walk's selected rows (default on): the first column tile
+ * of each input slice adds its row count to the counters above (three
+ * 64-bit atomics per slice).  Off, the counters are not updated.  The
+ * per-slice counts behind iam_bucketmul_walk_count are stored either way.
  * Changing it re-captures the model's decode graph.  Not during capture.
  * No counterpart in the reference. */
 int iam_set_walk_counting(iam_ctx* ctx, int on);

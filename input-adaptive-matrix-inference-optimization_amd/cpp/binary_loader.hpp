@@ -54,7 +54,7 @@ public:
     static WeightMetadata readMetadata(const std::string& meta_file)
     {
         std::ifstream file(meta_file);
-        if (!file) throw std::runtime_error("Cannot open metadata file: " + meta_file);
+        if (!file) throw std::runtime_error("weight metadata not readable (" + meta_file + ")");
         WeightMetadata meta;
         std::string line;
         while (std::getline(file, line)) {
@@ -69,13 +69,13 @@ public:
             else if (key == "out_dim:") iss >> meta.out_dim;
             else if (key == "bsize:") iss >> meta.bsize;
         }
-        if (meta.in_dim == 0 || meta.out_dim == 0) throw std::runtime_error("Invalid metadata - missing dimensions");
+        if (meta.in_dim == 0 || meta.out_dim == 0) throw std::runtime_error("weight metadata lacks in_dim or out_dim");
         // the shapes must describe the layout of preprocess_layer_fixed_gpu.py:226-228
         const size_t bs = meta.bsize ? meta.bsize : 16;
         if (meta.buckets_shape.dim0 < 1 || meta.buckets_shape.dim1 != meta.in_dim * bs ||
             meta.buckets_shape.dim2 * bs != meta.out_dim || meta.stats_shape.dim0 != meta.buckets_shape.dim0 ||
             meta.stats_shape.dim1 != meta.buckets_shape.dim1 || meta.stats_shape.dim2 != 4)
-            throw std::runtime_error("Invalid metadata - inconsistent shapes in " + meta_file);
+            throw std::runtime_error("weight metadata shapes do not describe a bucket layout (" + meta_file + ")");
         return meta;
     }
 
@@ -83,19 +83,19 @@ public:
     static std::vector<uint16_t> readBinary(const std::string& bin_file, size_t expected_elements)
     {
         std::ifstream file(bin_file, std::ios::binary);
-        if (!file) throw std::runtime_error("Cannot open binary file: " + bin_file);
+        if (!file) throw std::runtime_error("weight array not readable (" + bin_file + ")");
         file.seekg(0, std::ios::end);
         const size_t file_size = (size_t)file.tellg();
         file.seekg(0, std::ios::beg);
         const size_t expected_size = expected_elements * sizeof(uint16_t);
         if (file_size != expected_size) {
             std::ostringstream oss;
-            oss << "File size mismatch: " << bin_file << " has " << file_size << " bytes, expected " << expected_size;
+            oss << bin_file << ": " << file_size << " bytes on disk, the metadata asks for " << expected_size;
             throw std::runtime_error(oss.str());
         }
         std::vector<uint16_t> data(expected_elements);
         file.read(reinterpret_cast<char*>(data.data()), (std::streamsize)file_size);
-        if (!file) throw std::runtime_error("Failed to read data from: " + bin_file);
+        if (!file) throw std::runtime_error("short read of weight array (" + bin_file + ")");
         return data;
     }
 
@@ -122,10 +122,10 @@ public:
     static std::vector<uint16_t> loadNpyF16(const std::string& path, std::vector<size_t>* shape = nullptr)
     {
         std::ifstream f(path, std::ios::binary);
-        if (!f) throw std::runtime_error("Cannot open: " + path);
+        if (!f) throw std::runtime_error("npy file not readable (" + path + ")");
         char magic[6];
         f.read(magic, 6);
-        if (!f || std::memcmp(magic, "\x93NUMPY", 6) != 0) throw std::runtime_error("Not a .npy file: " + path);
+        if (!f || std::memcmp(magic, "\x93NUMPY", 6) != 0) throw std::runtime_error("no npy magic at the start of " + path);
         uint8_t major = 0, minor = 0;
         f.read(reinterpret_cast<char*>(&major), 1);
         f.read(reinterpret_cast<char*>(&minor), 1);
@@ -139,11 +139,11 @@ public:
         }
         std::string header(hlen, '\0');
         f.read(&header[0], hlen);
-        if (!f) throw std::runtime_error("Truncated .npy header: " + path);
+        if (!f) throw std::runtime_error("npy header cut short in " + path);
         if (header.find("'<f2'") == std::string::npos && header.find("'float16'") == std::string::npos)
-            throw std::runtime_error("Expected an fp16 .npy: " + path);
+            throw std::runtime_error("npy array is not little-endian fp16: " + path);
         if (header.find("'fortran_order': True") != std::string::npos)
-            throw std::runtime_error("Fortran-ordered .npy not supported: " + path);
+            throw std::runtime_error("npy array is column-major (only row-major is read): " + path);
         std::vector<size_t> shp;
         const size_t l = header.find('('), r = header.find(')');
         if (l != std::string::npos && r != std::string::npos) {
@@ -158,7 +158,7 @@ public:
         for (size_t d : shp) n *= d;
         std::vector<uint16_t> data(n);
         f.read(reinterpret_cast<char*>(data.data()), (std::streamsize)(n * 2));
-        if (!f) throw std::runtime_error("Truncated .npy data: " + path);
+        if (!f) throw std::runtime_error("npy data cut short in " + path);
         if (shape) *shape = shp;
         return data;
     }

@@ -20,15 +20,15 @@ public:
     size_t byte_size;
     Gpu* gpu_ref;
 
-    // bucket_mul.hpp:22-24
-    BufferWrapper(Gpu* gpu, size_t size)
+    // bucket_mul.hpp:22-24 (the access flags are ignored)
+    BufferWrapper(Gpu* gpu, size_t size, cl_mem_flags /*flags*/ = CL_MEM_READ_WRITE)
         : MTLBufferable(gpu->createBuffer(size * sizeof(T)), 0), count(size), rows(size), cols(1),
           byte_size(size * sizeof(T)), gpu_ref(gpu)
     {
     }
 
     // bucket_mul.hpp:26-32 (rows = shape[0], cols = shape[1])
-    BufferWrapper(Gpu* gpu, const std::vector<size_t>& shape)
+    BufferWrapper(Gpu* gpu, const std::vector<size_t>& shape, cl_mem_flags /*flags*/ = CL_MEM_READ_WRITE)
         : MTLBufferable(gpu->createBuffer(calculateSize(shape) * sizeof(T)), 0), count(calculateSize(shape)),
           rows(shape.size() > 0 ? shape[0] : 1), cols(shape.size() > 1 ? shape[1] : 1),
           byte_size(calculateSize(shape) * sizeof(T)), gpu_ref(gpu)

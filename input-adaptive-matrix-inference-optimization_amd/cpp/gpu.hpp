@@ -7,6 +7,7 @@
 #ifndef IAM_GPU_HPP
 #define IAM_GPU_HPP
 
+#include <cstdint>
 #include <cstdio>
 #include <iostream>
 #include <stdexcept>
@@ -15,12 +16,23 @@
 
 #include "../../include/iam.h"
 
+// Memory access flags the reference's call sites pass when they create
+// buffers (the OpenCL specification's values).  HIP device memory takes no
+// access flags: they are accepted and ignored.
+#ifndef CL_MEM_READ_WRITE
+typedef uint64_t cl_mem_flags;
+#define CL_MEM_READ_WRITE ((cl_mem_flags)1 << 0)
+#define CL_MEM_WRITE_ONLY ((cl_mem_flags)1 << 1)
+#define CL_MEM_READ_ONLY ((cl_mem_flags)1 << 2)
+#define CL_MEM_COPY_HOST_PTR ((cl_mem_flags)1 << 5)
+#endif
+
 namespace iam_cpp {
 
 inline void check(int rc, const char* what)
 {
     if (rc != IAM_OK)
-        throw std::runtime_error(std::string(what) + " (error code: " + std::to_string(rc) + "): " +
+        throw std::runtime_error(std::string(what) + " failed, iam code " + std::to_string(rc) + ": " +
                                  iam_last_error());
 }
 
@@ -48,11 +60,11 @@ public:
     // Gpu::Gpu (gpu.hpp:109-159): picks a device and creates the queue
     explicit Gpu(int device = 0)
     {
-        iam_cpp::check(iam_ctx_create(device, &ctx), "Failed to create context");
+        iam_cpp::check(iam_ctx_create(device, &ctx), "context creation");
         char name[256];
         int cus = 0;
         size_t mem = 0;
-        iam_cpp::check(iam_device_info(ctx, name, sizeof(name), &cus, &mem), "Failed to get device");
+        iam_cpp::check(iam_device_info(ctx, name, sizeof(name), &cus, &mem), "device query");
         deviceName = name;
         computeUnits = cus;
         globalMem = mem;
@@ -67,58 +79,66 @@ public:
     Gpu(const Gpu&) = delete;
     Gpu& operator=(const Gpu&) = delete;
 
-    // gpu.hpp:236-248
-    void* createBuffer(size_t size)
+    // gpu.hpp:236-248 (the access flags are ignored)
+    void* createBuffer(size_t size, cl_mem_flags /*flags*/ = CL_MEM_READ_WRITE)
     {
         void* p = nullptr;
-        iam_cpp::check(iam_alloc(ctx, size, &p), "Failed to create buffer");
+        iam_cpp::check(iam_alloc(ctx, size, &p), "device allocation");
+        return p;
+    }
+
+    // gpu.hpp:250-262: a buffer initialised from host memory
+    void* createBuffer(size_t size, const void* data, cl_mem_flags /*flags*/ = CL_MEM_READ_WRITE)
+    {
+        void* p = createBuffer(size);
+        if (data) iam_cpp::check(iam_write(ctx, p, 0, data, size), "host-to-device write");
         return p;
     }
 
     // gpu.hpp:264-269
     void releaseBuffer(void* buffer)
     {
-        if (buffer) iam_cpp::check(iam_free(ctx, buffer), "Failed to release buffer");
+        if (buffer) iam_cpp::check(iam_free(ctx, buffer), "device free");
     }
 
     // gpu.hpp:399-447: wait for the queue; kernel timings are folded in
     void eval(bool noWarn = false)
     {
         evalCount++;
-        if (warnOfEvals && !noWarn) std::cout << "warn: EVAL #" << evalCount << std::endl;
-        iam_cpp::check(iam_sync(ctx), "Failed to finish command queue");
+        if (warnOfEvals && !noWarn) std::cout << "note: synchronizing evaluation " << evalCount << std::endl;
+        iam_cpp::check(iam_sync(ctx), "stream synchronization");
     }
 
     // gpu.hpp:449-455
     void copyBuffer(MTLBufferable* src, MTLBufferable* dst, size_t size)
     {
         iam_cpp::check(iam_copy(ctx, dst->buffer, dst->offsetBytes, src->buffer, src->offsetBytes, size),
-                       "Failed to copy buffer");
+                       "device copy");
     }
 
     // gpu.hpp:457-462 (blocking)
     void readBuffer(const void* buffer, size_t size, void* hostPtr, size_t offset = 0)
     {
         blockingReadCount++;
-        iam_cpp::check(iam_read(ctx, hostPtr, buffer, offset, size), "Failed to read buffer");
+        iam_cpp::check(iam_read(ctx, hostPtr, buffer, offset, size), "device-to-host read");
     }
 
     // gpu.hpp:464-469 (blocking)
     void writeBuffer(void* buffer, size_t size, const void* hostPtr, size_t offset = 0)
     {
         blockingWriteCount++;
-        iam_cpp::check(iam_write(ctx, buffer, offset, hostPtr, size), "Failed to write buffer");
+        iam_cpp::check(iam_write(ctx, buffer, offset, hostPtr, size), "host-to-device write");
     }
 
     void zeroBuffer(void* buffer, size_t size, size_t offset = 0)
     {
-        iam_cpp::check(iam_zero(ctx, buffer, offset, size), "Failed to fill buffer");
+        iam_cpp::check(iam_zero(ctx, buffer, offset, size), "device clear");
     }
 
     void setProfiling(bool on)
     {
         enableKernelProfiling = on;
-        iam_cpp::check(iam_profiling(ctx, on ? 1 : 0), "Failed to set profiling");
+        iam_cpp::check(iam_profiling(ctx, on ? 1 : 0), "profiling switch");
     }
 
     // gpu.hpp:190-234
@@ -126,8 +146,8 @@ public:
     {
         std::vector<char> buf(1 << 16);
         if (iam_kernel_stats(ctx, buf.data(), buf.size()) == IAM_OK) {
-            std::cout << "\n========== PER-KERNEL PROFILING ==========\n" << buf.data()
-                      << "==========================================\n";
+            std::cout << "\n-- kernel times (HIP events per launch) --\n" << buf.data()
+                      << "-- end of kernel times --\n";
         }
     }
 

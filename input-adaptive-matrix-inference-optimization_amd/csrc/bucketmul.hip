@@ -1066,14 +1066,15 @@ static int bucketmul_list(Ctx* c, int i)
 }
 
 template <typename Acc>
-static int launch_walk(Ctx* c, dim3 grid, const WalkArgs& args)
+static int launch_walk(Ctx* c, const char* name, dim3 grid, const WalkArgs& args)
 {
-    return launch(c, "bucket_walk", k_walk<Acc, kWalkWaves, IAM_WALK_UNR>, grid, dim3(64 * kWalkWaves), 0, args);
+    return launch(c, name, k_walk<Acc, kWalkWaves, IAM_WALK_UNR>, grid, dim3(64 * kWalkWaves), 0, args);
 }
 
 int walk_group(Ctx* c, const WalkGroup& g)
 {
     IAM_REQUIRE(g.n >= 1 && g.n <= kMaxMulti, "walk: 1..3 matrices per launch");
+    IAM_REQUIRE(g.label >= 0 && g.label < kWalkLabels, "walk: bad group label");
     IAM_REQUIRE(!std::isnan(g.effort), "walk: effort is NaN");
     MatOp ops[kMaxMulti];
     for (int i = 0; i < g.n; i++) {
@@ -1156,12 +1157,15 @@ int walk_group(Ctx* c, const WalkGroup& g)
         args.zero_p[z] = g.zero_p[z];
         args.zero_n[z] = g.zero_n[z];
     }
-    args.counters = c->counting ? c->counters : nullptr;
+    args.counters = c->counting ? c->counters + (size_t)g.label * kCounterLanes * 4 : nullptr;
     // walk_count reads the slice counts of the slots this launch wrote
     for (int i = 0; i < g.n; i++)
         if (g.m[i].slice_count == c->slots[i].slice_count) c->slots[i].walked_P = plan[i].P;
     const dim3 grid((unsigned)gx, (unsigned)g.n);
-    return c->acc64 ? launch_walk<double>(c, grid, args) : launch_walk<float>(c, grid, args);
+    static const char* const names[kWalkLabels] = {"bucket_walk", "bucket_walk.qkv", "bucket_walk.o",
+                                                    "bucket_walk.ffn13", "bucket_walk.ffn2", "bucket_walk.lm"};
+    const char* name = names[g.label];
+    return c->acc64 ? launch_walk<double>(c, name, grid, args) : launch_walk<float>(c, name, grid, args);
 }
 
 // The standalone walk of the n matrices recorded in slots 0..n-1: the

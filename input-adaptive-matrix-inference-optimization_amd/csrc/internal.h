@@ -110,8 +110,9 @@ struct Ctx {
     // bumped whenever a context-owned scratch buffer is reallocated:
     // captured graphs hold those addresses and must be re-captured
     uint64_t scratch_gen = 0;
-    // device walk counters, kCounterLanes rows of {weight bytes, rows,
-    // matrices, pad}: each walk adds to row (slice % kCounterLanes), so the
+    // device walk counters, one block per walk label (kWalkLabels), each of
+    // kCounterLanes rows of {weight bytes, rows, matrices, pad}: each walk
+    // adds to row (slice % kCounterLanes) of its label's block, so the
     // additions of one launch do not queue on one address
     unsigned long long* counters = nullptr;
     // the walk adds its selected rows and bytes to the counters (off: it
@@ -131,6 +132,8 @@ int ensure_list(Ctx* c, int slot, int chunks);
 // P slice counts (grown as needed; new memory is zeroed)
 int ensure_walk_scratch(Ctx* c, int slot, size_t m, size_t T, size_t P);
 constexpr int kCounterLanes = 64;
+constexpr int kWalkLabels = 6;   // standalone, q/k/v, o, w1/w3, w2, LM head
+constexpr size_t kCounterWords = (size_t)kWalkLabels * kCounterLanes * 4;
 
 // Launch bookkeeping: with profiling on (and no graph capture in progress)
 // each launch is bracketed by a pair of pooled events.
@@ -220,6 +223,9 @@ struct WalkMat {
     float* y;                // kFinStore: outputs; kFinSilu: the gate / up values (may be null)
 };
 struct WalkGroup {
+    // the model's matrix group of the launch (IAM_WALK_GROUP_*; 0: a
+    // standalone call): picks the kernel-statistics name and the counter block
+    int label = 0;
     int n = 0;
     WalkMat m[kMaxMulti];
     int in_mode = kInX;

@@ -184,6 +184,7 @@ static int step(iam_model* m, float effort, const float* hidden_override, float*
         // (transformer_layer.hpp:96-100) and the previous FFN's residual
         {
             WalkGroup g;
+            g.label = IAM_WALK_GROUP_QKV;
             g.n = 3;
             g.m[0] = walk_mat(m, ly.wq, 0, D, qkv);
             g.m[1] = walk_mat(m, ly.wk, 1, D, qkv + acc_bytes(D));
@@ -248,6 +249,7 @@ static int step(iam_model* m, float effort, const float* hidden_override, float*
         // ---- o projection (attention.hpp:198-200)
         {
             WalkGroup g;
+            g.label = IAM_WALK_GROUP_O;
             g.n = 1;
             g.m[0] = walk_mat(m, ly.wo, 0, D, m->acc_o);
             g.m[0].x = m->att_x;
@@ -262,6 +264,7 @@ static int step(iam_model* m, float effort, const float* hidden_override, float*
         // and the FFN norm (transformer_layer.hpp:104-112); SiLU gate
         {
             WalkGroup g;
+            g.label = IAM_WALK_GROUP_FFN13;
             g.n = 2;
             g.m[0] = walk_mat(m, ly.w1, 0, D, m->acc_g);
             g.m[1] = walk_mat(m, ly.w3, 1, D, m->acc_u);
@@ -289,6 +292,7 @@ static int step(iam_model* m, float effort, const float* hidden_override, float*
         // ---- down (feedforward.hpp:82-84)
         {
             WalkGroup g;
+            g.label = IAM_WALK_GROUP_FFN2;
             g.n = 1;
             g.m[0] = walk_mat(m, ly.w2, 0, F, m->acc_d);
             g.m[0].x = m->s;
@@ -303,6 +307,7 @@ static int step(iam_model* m, float effort, const float* hidden_override, float*
     {
         const float* hlast = m->hb + (size_t)(C.n_layers - 1) * D;
         WalkGroup g;
+        g.label = IAM_WALK_GROUP_LM;
         g.n = 1;
         g.m[0] = walk_mat(m, m->lm, 0, D, m->acc_lm);
         g.m[0].tile_ctr = m->tile_ctr + T13;

@@ -222,7 +222,7 @@ int iam_ctx_create(int device, iam_ctx** out)
     c->total_mem = total_b;
     const size_t margin = 512ull << 20;   // gpu.hpp:28 safety margin
     c->usable = total_b > margin ? total_b - margin : total_b;
-    const size_t cbytes = kCounterLanes * 4 * sizeof(unsigned long long);
+    const size_t cbytes = kCounterWords * sizeof(unsigned long long);
     int rc = ctx_alloc(c, cbytes, (void**)&c->counters);
     if (rc == IAM_OK) rc = zero_async(c, c->counters, cbytes);
     if (rc == IAM_OK && hipStreamSynchronize(c->stream) != hipSuccess) rc = fail(IAM_E_HIP, "ctx_create: sync");
@@ -436,23 +436,38 @@ int iam_kernel_stats(iam_ctx* c, char* buf, size_t len)
     return IAM_OK;
 }
 
-int iam_walk_counters(iam_ctx* c, uint64_t* bytes, uint64_t* rows, uint64_t* mats, int reset)
+// sums of the counter rows of labels [g0, g1)
+static int read_counters(Ctx* c, int g0, int g1, uint64_t* bytes, uint64_t* rows, uint64_t* mats, int reset)
 {
-    if (!c) return fail(IAM_E_INVALID, "walk_counters: null context");
-    unsigned long long h[kCounterLanes * 4];
-    IAM_CHECK_HIP(hipMemcpyAsync(h, c->counters, sizeof(h), hipMemcpyDeviceToHost, c->stream));
+    std::vector<unsigned long long> h(kCounterWords);
+    IAM_CHECK_HIP(hipMemcpyAsync(h.data(), c->counters, kCounterWords * sizeof(unsigned long long),
+                                 hipMemcpyDeviceToHost, c->stream));
     IAM_CHECK_HIP(hipStreamSynchronize(c->stream));
     unsigned long long t[3] = {0, 0, 0};
-    for (int l = 0; l < kCounterLanes; l++)
-        for (int i = 0; i < 3; i++) t[i] += h[l * 4 + i];
+    for (int l = g0 * kCounterLanes; l < g1 * kCounterLanes; l++)
+        for (int i = 0; i < 3; i++) t[i] += h[(size_t)l * 4 + i];
     if (bytes) *bytes = t[0];
     if (rows) *rows = t[1];
     if (mats) *mats = t[2];
     if (reset) {
-        IAM_TRY(zero_async(c, c->counters, sizeof(h)));
+        IAM_TRY(zero_async(c, c->counters, kCounterWords * sizeof(unsigned long long)));
         IAM_CHECK_HIP(hipStreamSynchronize(c->stream));
     }
     return IAM_OK;
+}
+
+int iam_walk_counters(iam_ctx* c, uint64_t* bytes, uint64_t* rows, uint64_t* mats, int reset)
+{
+    if (!c) return fail(IAM_E_INVALID, "walk_counters: null context");
+    return read_counters(c, 0, kWalkLabels, bytes, rows, mats, reset);
+}
+
+int iam_walk_group_counters(iam_ctx* c, int group, uint64_t* bytes, uint64_t* rows, uint64_t* mats)
+{
+    if (!c) return fail(IAM_E_INVALID, "walk_group_counters: null context");
+    if (group < 0 || group >= kWalkLabels)
+        return fail(IAM_E_INVALID, "walk_group_counters: group must be one of IAM_WALK_GROUP_*");
+    return read_counters(c, group, group + 1, bytes, rows, mats, 0);
 }
 
 int iam_kernel_stats_reset(iam_ctx* c)
@@ -496,9 +511,19 @@ int iam_get_accumulation(iam_ctx* c, int* mode)
 int iam_kernel_stat(iam_ctx* c, const char* name, double* total_ms, int* calls)
 {
     if (!c || !name) return fail(IAM_E_INVALID, "kernel_stat: bad argument");
-    auto it = c->stats.find(name);
-    if (total_ms) *total_ms = it == c->stats.end() ? 0.0 : it->second.total_ms;
-    if (calls) *calls = it == c->stats.end() ? 0 : it->second.calls;
+    // "bucket_walk" also sums the labelled launches "bucket_walk.<group>";
+    // "*" sums every kernel
+    const std::string key(name), sub = key + ".";
+    const bool all = key == "*";
+    double t = 0.0;
+    int n = 0;
+    for (const auto& kv : c->stats)
+        if (all || kv.first == key || (key.find('.') == std::string::npos && kv.first.rfind(sub, 0) == 0)) {
+            t += kv.second.total_ms;
+            n += kv.second.calls;
+        }
+    if (total_ms) *total_ms = t;
+    if (calls) *calls = n;
     return IAM_OK;
 }
 

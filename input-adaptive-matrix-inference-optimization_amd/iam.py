@@ -255,6 +255,16 @@ class Ctx:
         check(lib().iam_walk_counters(self.h, C.byref(b), C.byref(r), C.byref(m), 1 if reset else 0))
         return b.value, r.value, m.value
 
+    WALK_GROUPS = {"none": 0, "qkv": 1, "o": 2, "ffn13": 3, "ffn2": 4, "lm": 5}
+
+    def walk_group_counters(self, group):
+        """(weight bytes, rows, matrices) the model's walks of one matrix group
+        ('qkv', 'o', 'ffn13', 'ffn2', 'lm'; 'none': standalone calls) added."""
+        b, r, m = C.c_uint64(), C.c_uint64(), C.c_uint64()
+        check(lib().iam_walk_group_counters(self.h, self.WALK_GROUPS[group], C.byref(b), C.byref(r),
+                                            C.byref(m)))
+        return b.value, r.value, m.value
+
     def stats_compact(self, stats, rows, stride=4, channel=3, out=None):
         if out is None:
             out = self.empty(rows, np.uint16)

@@ -44,6 +44,9 @@
 #include "oracle.h"
 
 #include <math.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
 #include <stdlib.h>
 #include <string.h>
 
@@ -419,6 +422,7 @@ int64_t orc_select_rows(const float* x, const uint16_t* stats, int stats_channel
 {
     int64_t s = 0;
     const size_t off = (size_t)expert_rows * (size_t)exp_no;
+    #pragma omp parallel for schedule(static) reduction(+ : s)
     for (int r = 0; r < expert_rows; r++) {
         size_t gi = off + (size_t)r;
         float avg = orc_f16_to_f32(stats[gi * (size_t)stats_channels + 3]);
@@ -444,27 +448,41 @@ void orc_bucket_walk(const uint16_t* buckets, int bucket_cols, int exp_no, int e
     const int C = bucket_cols;
     const int m = C * 16;
     const size_t off = (size_t)expert_rows * (size_t)exp_no;
+    /* threads own column ranges (the outputs c*16 .. c*16+15 of column c
+     * only receive weights of column c) and each walks the rows in
+     * ascending order, so every output is summed in the same order as with
+     * one thread */
+    const int CB = 16;
+    const int nblk = (C + CB - 1) / CB;
     if (acc64) {
         double* acc = (double*)calloc((size_t)m, sizeof(double));
-        for (int r = 0; r < expert_rows; r++) {
-            if (!mask[r]) continue;
-            double xv = (double)x[r / 16];
-            const uint16_t* w = buckets + (off + (size_t)r) * (size_t)C;
-            for (int c = 0; c < C; c++) {
-                acc[c * 16 + (w[c] & 15)] += xv * (double)orc_f16_to_f32(w[c]);
+        #pragma omp parallel for schedule(static)
+        for (int cb = 0; cb < nblk; cb++) {
+            const int c0 = cb * CB, c1 = c0 + CB < C ? c0 + CB : C;
+            for (int r = 0; r < expert_rows; r++) {
+                if (!mask[r]) continue;
+                double xv = (double)x[r / 16];
+                const uint16_t* w = buckets + (off + (size_t)r) * (size_t)C;
+                for (int c = c0; c < c1; c++) {
+                    acc[c * 16 + (w[c] & 15)] += xv * (double)orc_f16_to_f32(w[c]);
+                }
             }
         }
         for (int o = 0; o < m; o++) y[o] = (float)acc[o];
         free(acc);
     } else {
         for (int o = 0; o < m; o++) y[o] = 0.0f;
-        for (int r = 0; r < expert_rows; r++) {
-            if (!mask[r]) continue;
-            float xv = x[r / 16];
-            const uint16_t* w = buckets + (off + (size_t)r) * (size_t)C;
-            for (int c = 0; c < C; c++) {
-                float prod = xv * orc_f16_to_f32(w[c]);
-                y[c * 16 + (w[c] & 15)] += prod;
+        #pragma omp parallel for schedule(static)
+        for (int cb = 0; cb < nblk; cb++) {
+            const int c0 = cb * CB, c1 = c0 + CB < C ? c0 + CB : C;
+            for (int r = 0; r < expert_rows; r++) {
+                if (!mask[r]) continue;
+                float xv = x[r / 16];
+                const uint16_t* w = buckets + (off + (size_t)r) * (size_t)C;
+                for (int c = c0; c < c1; c++) {
+                    float prod = xv * orc_f16_to_f32(w[c]);
+                    y[c * 16 + (w[c] & 15)] += prod;
+                }
             }
         }
     }
@@ -590,9 +608,11 @@ void orc_attention_f16kv(const float* q, const uint16_t* kcache, const uint16_t*
                          int n_tok, int n_heads, int n_kv, int head_dim, float* out)
 {
     int rep = n_heads / n_kv;
-    double* sc = (double*)malloc(sizeof(double) * (size_t)(n_tok > 0 ? n_tok : 1));
     double inv = 1.0 / sqrt((double)head_dim);
+    /* heads are independent: one per thread at a time */
+    #pragma omp parallel for schedule(static)
     for (int h = 0; h < n_heads; h++) {
+        double* sc = (double*)malloc(sizeof(double) * (size_t)(n_tok > 0 ? n_tok : 1));
         int kv = h / rep;
         const float* qh = q + (size_t)h * head_dim;
         double mx = -INFINITY;
@@ -616,8 +636,8 @@ void orc_attention_f16kv(const float* q, const uint16_t* kcache, const uint16_t*
             }
             out[(size_t)h * head_dim + j] = (float)(acc / den);
         }
+        free(sc);
     }
-    free(sc);
 }
 
 int orc_argmax(const float* v, int n)
@@ -702,4 +722,14 @@ void orc_model_forward(const orc_model* m, int token, int pos, float effort,
     mat_apply(&m->lm_head, hn, effort, logits);
     free(h);
     free(hn);
+}
+
+/* threads the parallel loops above use (OpenMP's maximum; 1 without it) */
+int orc_threads(void)
+{
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
 }

@@ -149,6 +149,9 @@ void orc_layer_forward(const orc_model* m, int layer, int pos, float effort, flo
 void orc_model_forward(const orc_model* m, int token, int pos, float effort,
                        const float* hidden_in, float* logits);
 
+/* threads the OpenMP loops use (1 when built without OpenMP) */
+int orc_threads(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -106,6 +106,8 @@ def lib():
     L.orc_attention_f16kv.argtypes = [f32p, u16p, u16p, C.c_int, C.c_int, C.c_int, C.c_int, f32p]
     L.orc_argmax.restype = C.c_int
     L.orc_argmax.argtypes = [f32p, C.c_int]
+    L.orc_threads.restype = C.c_int
+    L.orc_threads.argtypes = []
     L.orc_layer_forward.argtypes = [C.POINTER(Model), C.c_int, C.c_int, C.c_float, f32p]
     L.orc_model_forward.argtypes = [C.POINTER(Model), C.c_int, C.c_int, C.c_float,
                                     C.c_void_p, f32p]
@@ -328,3 +330,8 @@ class OracleModel:
         out = np.ascontiguousarray(h, np.float32).copy()
         lib().orc_layer_forward(C.byref(self.mod), layer, pos, effort, out)
         return out
+
+
+def threads():
+    """Threads of the oracle's parallel loops (OpenMP's maximum)."""
+    return lib().orc_threads()

@@ -5,7 +5,9 @@ read by binary_loader.hpp) plus the .npy norms, embedding and dense LM head
 (transformer_layer.hpp:25-52, model.hpp:54-81).
 
 Checks: BucketMul::calcDispatch + mul on one weight file gives the oracle's
-cutoff bits, selected-row count and y (within 1 ulp); MistralModel greedy
+cutoff bits, selected-row count and y (within 1 ulp); TransformerLayer
+(Attention then FeedForward) over six positions gives the oracle layer's
+output (within 1 ulp); MistralModel greedy
 generation (graph replay and eager host argmax) gives the oracle model's
 tokens, with the dense LM head bucketized on load."""
 import os
@@ -104,3 +106,24 @@ def test_generate_from_reference_files(O, weights, eager):
         if pos >= len(prompt) - 1:
             seq.append(O.argmax(lo))
     assert toks == seq[len(prompt):]
+
+
+@pytest.mark.parametrize("effort", [0.25, 1.0])
+def test_layer_from_reference_files(O, weights, tmp_path, effort):
+    """TransformerLayer::forward (Attention then FeedForward through the
+    drop-in headers) for positions 0..5 with the same input, filling the KV
+    cache: the last output within 1 ulp of the oracle's layer."""
+    d, t = weights
+    P = 5
+    h = O.gen_f32(7, 650, 4096, 0.0, 1.0)
+    hin, yout = str(tmp_path / "h.f32"), str(tmp_path / "y.f32")
+    h.tofile(hin)
+    run(["layer", "-d", d, "-l", "0", "-e", str(effort), "--in", hin, "--out", yout, "--pos", str(P),
+         "--max-ctx", str(CFG["max_ctx"]), "--theta", "10000"])
+    y = np.fromfile(yout, np.float32)
+    orc = O.OracleModel(CFG, lambda name, dtype: np.ascontiguousarray(t[name]).view(dtype).ravel())
+    for p in range(P + 1):
+        want = orc.layer_forward(0, p, effort, h.copy())
+    iy = y.view(np.int32).astype(np.int64)
+    io = want.view(np.int32).astype(np.int64)
+    assert np.abs(np.where(iy < 0, -(iy & 0x7FFFFFFF), iy) - np.where(io < 0, -(io & 0x7FFFFFFF), io)).max() <= 1

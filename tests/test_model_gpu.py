@@ -197,6 +197,35 @@ def test_model_rejects_bad_config(iam, ctx):
         iam.Model(ctx, iam.ModelConfig(**bad))
 
 
+def test_model_refuses_steps_past_the_kv_capacity(iam, ctx, model):
+    """The host keeps the position of the next step: a decode, device step or
+    generate that would write K/V past max_ctx, or a position beyond
+    max_ctx (max_ctx itself is the full cache), fails with IAM_E_INVALID
+    before anything is launched; the steps up to the last slot run."""
+    cap = CFG["max_ctx"]
+    model.generate(np.arange(4, dtype=np.int32), 1, 0.25, use_graph=False)   # next step at position 4
+    model.decode(cap - 4 - 1, 0.25, use_graph=False)                         # positions 4 .. cap - 2
+    model.decode(1, 0.25, use_graph=True)                                    # cap - 1, the last slot
+    ctx.sync()
+    assert int(model.read_tensor("pos", np.int32)[0]) == cap
+    for call in (lambda: model.decode(1, 0.25, use_graph=False),
+                 lambda: model.decode(1, 0.25, use_graph=True),
+                 lambda: model.step_device(0.25),
+                 lambda: model.set_position(cap + 1),
+                 lambda: model.generate(np.zeros(cap, np.int32), 1, 0.25, use_graph=False)):
+        with pytest.raises(iam.IamError) as e:
+            call()
+        assert e.value.code == -1, e.value
+    assert int(model.read_tensor("pos", np.int32)[0]) == cap
+    model.set_position(cap)
+    with pytest.raises(iam.IamError):
+        model.step_device(0.25)
+    model.set_position(cap - 1)
+    model.decode(1, 0.25, use_graph=False)
+    with pytest.raises(iam.IamError):
+        model.decode(1, 0.25, use_graph=False)
+
+
 WIDE = dict(n_layers=1, dim=8192, ffn_dim=4096, n_heads=64, n_kv_heads=8, head_dim=128, vocab=256,
             max_ctx=16, rope_theta=10000.0, norm_eps=1e-5)
 
