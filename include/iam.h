@@ -147,6 +147,23 @@ int iam_bucketmul_multi(iam_ctx* ctx, int n, const iam_bucket_matrix* mats,
 int iam_bucketmul_fused(iam_ctx* ctx, int n, const iam_bucket_matrix* mats, float* x_dev, int in_size,
                         float* const* ys_dev, int expert_no, float effort, const float* h_dev,
                         const uint16_t* gain_dev, float eps);
+/* iam_bucketmul_fused without any device allocation at call time.  No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The walk's scratch lives in one fixed device array per GPU
+ * (about 1 MiB, held from the first call on that GPU until the process
+ * ends): at most IAM_NOALLOC_MAX_OUTPUTS outputs (16 * bucket_cols summed
+ * over the matrices), 256 column tiles and 1024 input slices per matrix;
+ * larger groups fail with IAM_E_INVALID.  A norm input (h_dev, gain_dev)
+ * must be 4096 long.  Results equal iam_bucketmul_fused's.  Every call on a
+ * GPU shares that array: calls that overlap on one GPU (other streams,
+ * contexts or threads) race.  The call is not recorded in the dispatch
+ * slots (dispatch_info / walk_count do not see it) and launches without
+ * profiling events. */
+#define IAM_NOALLOC_MAX_OUTPUTS 131072
+int iam_bucketmul_fused_noalloc(iam_ctx* ctx, int n, const iam_bucket_matrix* mats, float* x_dev,
+                                int in_size, float* const* ys_dev, int expert_no, float effort,
+                                const float* h_dev, const uint16_t* gain_dev, float eps);
 /* Parity outputs of the last calc_dispatch / multi / fused call for matrix slot
  * `slot`: the cutoff (fp32, as written by findCutoffBinarySearch) and the
  * selected-row count S.  The selection is re-run by a separate list kernel

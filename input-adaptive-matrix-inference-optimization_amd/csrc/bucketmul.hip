@@ -1066,8 +1066,15 @@ static int bucketmul_list(Ctx* c, int i)
 }
 
 template <typename Acc>
-static int launch_walk(Ctx* c, const char* name, dim3 grid, const WalkArgs& args)
+static int launch_walk(Ctx* c, const char* name, bool plain, dim3 grid, const WalkArgs& args)
 {
+    if (plain) {
+        auto kern = k_walk<Acc, kWalkWaves, IAM_WALK_UNR>;
+        hipLaunchKernelGGL(kern, grid, dim3(64 * kWalkWaves), 0, c->stream, args);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return fail(IAM_E_HIP, std::string("launch ") + name + ": " + hipGetErrorString(e));
+        return IAM_OK;
+    }
     return launch(c, name, k_walk<Acc, kWalkWaves, IAM_WALK_UNR>, grid, dim3(64 * kWalkWaves), 0, args);
 }
 
@@ -1165,7 +1172,8 @@ int walk_group(Ctx* c, const WalkGroup& g)
     static const char* const names[kWalkLabels] = {"bucket_walk", "bucket_walk.qkv", "bucket_walk.o",
                                                     "bucket_walk.ffn13", "bucket_walk.ffn2", "bucket_walk.lm"};
     const char* name = names[g.label];
-    return c->acc64 ? launch_walk<double>(c, name, grid, args) : launch_walk<float>(c, name, grid, args);
+    return c->acc64 ? launch_walk<double>(c, name, g.plain, grid, args)
+                    : launch_walk<float>(c, name, g.plain, grid, args);
 }
 
 // The standalone walk of the n matrices recorded in slots 0..n-1: the

@@ -226,6 +226,8 @@ struct WalkGroup {
     // the model's matrix group of the launch (IAM_WALK_GROUP_*; 0: a
     // standalone call): picks the kernel-statistics name and the counter block
     int label = 0;
+    // launch without the profiling events (the no-allocation entry point)
+    bool plain = false;
     int n = 0;
     WalkMat m[kMaxMulti];
     int in_mode = kInX;

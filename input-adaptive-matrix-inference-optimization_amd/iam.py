@@ -210,6 +210,16 @@ class Ctx:
                                         _vp(h) if h is not None else None,
                                         _vp(gain) if gain is not None else None, C.c_float(eps)))
 
+    def fused_noalloc(self, mats, x, in_size, ys, effort, h=None, gain=None, eps=1e-5, expert_no=0):
+        """fused() with the scratch in the library's fixed per-GPU array: no
+        device allocation during the call."""
+        n = len(mats)
+        M = (BucketMatrix * n)(*mats)
+        Y = (C.c_void_p * n)(*[y.ptr if not isinstance(y, int) else y for y in ys])
+        check(lib().iam_bucketmul_fused_noalloc(self.h, n, M, _vp(x), in_size, Y, expert_no, C.c_float(effort),
+                                                _vp(h) if h is not None else None,
+                                                _vp(gain) if gain is not None else None, C.c_float(eps)))
+
     def dispatch_info(self, slot=0):
         cut = C.c_float()
         cnt = C.c_uint32()
