@@ -35,14 +35,17 @@ struct AttnLaunch {
     uint16_t* vc = nullptr;
     const int* pos = nullptr;
     int n_heads = 0, n_kv = 0, max_ctx = 0;
-    void* acc = nullptr;               // o then l accumulators, zero on entry
+    void* acc = nullptr;               // model: o then l, written by the last split of each KV head
+    void* part = nullptr;              // the splits' partial sums (attention_part_words doubles)
     float* out = nullptr;              // standalone: out = o / l
-    uint32_t* head_ctr = nullptr;
+    uint32_t* head_ctr = nullptr;      // [n_kv], zero on entry (left zero)
     void* zero_p = nullptr;
     int zero_n = 0;
 };
 int attention_launch(Ctx* c, const AttnLaunch& L);
 size_t attention_acc_words(int n_heads);
+// doubles of the per-split partials of one attention launch
+size_t attention_part_words(int n_heads, int n_kv, int max_ctx);
 // h_out = h + (float)delta accumulator (add32), then RMSNorm + gain into out
 // (n = 1024 .. 16384, multiple of 1024); delta may be null
 int resnorm(Ctx* c, const float* h, const void* delta_acc, float* h_out, const uint16_t* gain, int n, float eps,

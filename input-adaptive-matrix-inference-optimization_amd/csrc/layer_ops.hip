@@ -207,6 +207,9 @@ __global__ void k_rope_kv(const float* __restrict__ q, const float* __restrict__
 constexpr int kAttnChunk = 64;
 constexpr int kAttnMaxRep = 8;
 constexpr int kMaxAttnSplits = 128;   // max_ctx up to 8192
+// doubles per split and KV head in the partials: o of rep heads, the rep
+// softmax sums, padded to 64 bytes
+__host__ __device__ constexpr int attn_part_stride(int rep) { return rep * 128 + 8; }
 
 template <typename Acc>
 __device__ __forceinline__ Acc acc_exp(Acc x);
@@ -223,9 +226,11 @@ struct AttnArgs {
     uint16_t* vc;            // fp16 V rows, same layout
     const int* pos;
     int n_heads, n_kv, max_ctx;
-    void* acc;               // o [n_heads][128], then l [n_heads] (fp64); zero on entry
+    void* acc;               // o [n_heads][128], then l [n_heads] (fp64): written by the last
+                             // split of each KV head (model mode)
+    void* part;              // the splits' partial sums [n_kv][splits][attn_part_stride(rep)] (fp64)
     float* out;              // standalone: out = o / l, stored by the last split of each KV head
-    uint32_t* head_ctr;      // [n_kv] arrival counters (standalone)
+    uint32_t* head_ctr;      // [n_kv] arrival counters, zero on entry (left zero)
     void* zero_p;            // accumulator words cleared by this launch
     int zero_n;
 };
@@ -233,6 +238,8 @@ struct AttnArgs {
 // LDS copies of the split's K and V rows: 128 fp16 + 8 fp16 of padding, so
 // that lanes reading 16 bytes of consecutive rows start on different banks.
 constexpr int kAttnRowStride = 128 + 8;
+static_assert(kAttnChunk * kAttnRowStride * 2 >= kMaxAttnSplits * kAttnMaxRep * 8,
+              "the K rows' LDS holds the softmax-sum partials of the last split");
 
 template <typename Acc>
 __global__ __launch_bounds__(128 * kAttnMaxRep) void k_attn(AttnArgs a, Acc scale)
@@ -364,42 +371,70 @@ __global__ __launch_bounds__(128 * kAttnMaxRep) void k_attn(AttnArgs a, Acc scal
         o[e] += __shfl_xor(o[e], 16, 64);
         o[e] += __shfl_xor(o[e], 32, 64);
     }
-    double* O = reinterpret_cast<double*>(a.acc);
-    double* Ls = O + (size_t)a.n_heads * HD;
-    if (!a.out) {
-        if (g == 0) {
+    // the split's partial sums go to its own slot of the partials (no two
+    // splits add to one address): lane (g, j) holds dimension
+    // hf*64 + j*8 + g at slot position hr*128 + hf*64 + g*8 + j, so a wave
+    // writes 64 consecutive values; then the softmax sums.  The exchanges
+    // return the old values and the split waits for them before it arrives,
+    // so all are performed where the last split's atomic loads read them.
+    const int PS = attn_part_stride(rep);
+    double* part = reinterpret_cast<double*>(a.part);
+    double* mine = part + ((size_t)kvh * gridDim.y + split) * PS;
+    Acc og = o[0];
 #pragma unroll
-            for (int e = 0; e < 8; e++) acc_add(O + (size_t)h * HD + hf * DH + j * 8 + e, (double)o[e]);
-        }
-        if (hf == 0 && lane == 0) acc_add(Ls + h, (double)l);
-        return;
-    }
-    // standalone: the last split of this KV head forms out = o / l.  The
-    // additions return the old values and the split waits for them before it
-    // arrives, so all are performed where the final atomic reads take them.
-    double sink = 0.0;
-    if (g == 0) {
-#pragma unroll
-        for (int e = 0; e < 8; e++)
-            sink += __hip_atomic_fetch_add(O + (size_t)h * HD + hf * DH + j * 8 + e, (double)o[e], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-    }
+    for (int e = 1; e < 8; e++) og = g == e ? o[e] : og;
+    unsigned long long sink = __hip_atomic_exchange(
+        reinterpret_cast<unsigned long long*>(mine + hr * HD + hf * DH + lane),
+        (unsigned long long)__double_as_longlong((double)og), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (hf == 0 && lane == 0)
-        sink += __hip_atomic_fetch_add(Ls + h, (double)l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sink += __hip_atomic_exchange(reinterpret_cast<unsigned long long*>(mine + rep * HD + hr),
+                                      (unsigned long long)__double_as_longlong((double)l), __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
     asm volatile("" ::"v"(sink));
     __syncthreads();
+    const int ns = (n_tok + kAttnChunk - 1) / kAttnChunk;   // the KV head's splits
     if (tid == 0)
         s_last = __hip_atomic_fetch_add(a.head_ctr + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                 (uint32_t)((n_tok + kAttnChunk - 1) / kAttnChunk - 1);
+                 (uint32_t)(ns - 1);
     __syncthreads();
     if (!s_last) return;
-    if (tid < rep) sl[tid] = acc_peek(Ls + kvh * rep + tid);
-    __syncthreads();
-    for (int i = tid; i < rep * HD; i += nthr) {
-        const int hh = kvh * rep + i / HD;
-        a.out[(size_t)hh * HD + (i % HD)] = (float)(acc_take(O + (size_t)hh * HD + (i % HD)) / sl[i / HD]);
+    // the last split of this KV head: the sums over the splits, in split
+    // order, of o (rep heads x 128: one value per thread, 16 splits' loads
+    // in flight) and l (thread t < rep * ns loads split t / rep's value of
+    // head t % rep into LDS, where the first threads add them up)
+    const double* first = part + (size_t)kvh * gridDim.y * PS;
+    const bool has_lp = tid < rep * ns;
+    const double lp = has_lp ? acc_peek(const_cast<double*>(first) + (size_t)(tid / rep) * PS + rep * HD + tid % rep)
+                             : 0.0;
+    double to = 0.0;
+    for (int s0 = 0; s0 < ns; s0 += 16) {
+        double vo[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++)
+            vo[u] = s0 + u < ns ? acc_peek(const_cast<double*>(first) + (size_t)(s0 + u) * PS + tid) : 0.0;
+#pragma unroll
+        for (int u = 0; u < 16; u++) to += vo[u];
     }
-    if (tid < rep) (void)acc_take(Ls + kvh * rep + tid);
+    double* s_lp = reinterpret_cast<double*>(sk);   // the K rows are read no more
+    if (has_lp) s_lp[tid] = lp;
+    __syncthreads();
+    if (tid < rep) {
+        double tl = 0.0;
+        for (int sp_ = 0; sp_ < ns; sp_++) tl += s_lp[sp_ * rep + tid];
+        sl[tid] = tl;
+    }
+    // slot position tid -> head and dimension
+    const int hh = tid / HD, pp = tid % HD;
+    const int d = (pp / DH) * DH + (pp % 8) * 8 + (pp % DH) / 8;
+    const size_t oi = (size_t)(kvh * rep + hh) * HD + d;
+    double* O = reinterpret_cast<double*>(a.acc);
+    if (a.out) {
+        __syncthreads();
+        a.out[oi] = (float)(to / sl[hh]);
+    } else {
+        O[oi] = to;
+        if (tid < rep) O[(size_t)a.n_heads * HD + kvh * rep + tid] = sl[tid];
+    }
     if (tid == 0) a.head_ctr[kvh] = 0u;
 }
 
@@ -519,10 +554,16 @@ int rope_kv(Ctx* c, const float* q, const float* k, const float* v, const float*
 
 size_t attention_acc_words(int n_heads) { return (size_t)n_heads * 128 + (size_t)n_heads; }
 
+size_t attention_part_words(int n_heads, int n_kv, int max_ctx)
+{
+    return (size_t)n_kv * (size_t)((max_ctx + kAttnChunk - 1) / kAttnChunk) * attn_part_stride(n_heads / n_kv);
+}
+
 int attention_launch(Ctx* c, const AttnLaunch& L)
 {
     const int n_split = (L.max_ctx + kAttnChunk - 1) / kAttnChunk;
     IAM_REQUIRE(n_split <= kMaxAttnSplits, "attention: max_ctx above 8192");
+    IAM_REQUIRE(L.part && L.head_ctr && (L.out || L.acc), "attention: missing scratch");
     AttnArgs a{};
     a.q = L.q;
     a.qkv_acc = L.qkv_acc;
@@ -534,6 +575,7 @@ int attention_launch(Ctx* c, const AttnLaunch& L)
     a.n_kv = L.n_kv;
     a.max_ctx = L.max_ctx;
     a.acc = L.acc;
+    a.part = L.part;
     a.out = L.out;
     a.head_ctr = L.head_ctr;
     a.zero_p = L.zero_p;
@@ -681,7 +723,7 @@ int iam_attention_decode(iam_ctx* c, const float* q, const uint16_t* kc, const u
     IAM_TRY(check_dev_range(c, vc, (size_t)max_ctx * nk * 2, "attention vcache"));
     IAM_TRY(check_dev_range(c, out, (size_t)n_heads * head_dim * 4, "attention out"));
     IAM_TRY(check_dev_range(c, pos, 4, "attention pos"));
-    IAM_TRY(ensure_attn_scratch(c, attention_acc_words(n_heads), n_kv));
+    IAM_TRY(ensure_attn_scratch(c, attention_part_words(n_heads, n_kv, max_ctx), n_kv));
     AttnLaunch L{};
     L.q = q;
     L.kc = const_cast<uint16_t*>(kc);
@@ -690,7 +732,7 @@ int iam_attention_decode(iam_ctx* c, const float* q, const uint16_t* kc, const u
     L.n_heads = n_heads;
     L.n_kv = n_kv;
     L.max_ctx = max_ctx;
-    L.acc = c->attn_acc;
+    L.part = c->attn_acc;
     L.out = out;
     L.head_ctr = c->attn_ctr;
     return attention_launch(c, L);

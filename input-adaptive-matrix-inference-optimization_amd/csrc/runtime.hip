@@ -27,7 +27,7 @@ int ctx_alloc(Ctx* c, size_t bytes, void** out)
     if (bytes == 0) bytes = 1;
     // MemoryTracker::can_allocate (gpu.hpp:40-44)
     if (c->allocated + bytes > c->usable)
-        return fail(IAM_E_NOMEM, "VRAM allocation failed - insufficient memory! (budget " +
+        return fail(IAM_E_NOMEM, "alloc: over the context's device memory budget (budget " +
                                      std::to_string(c->usable) + " bytes, in use " +
                                      std::to_string(c->allocated) + ", asked " +
                                      std::to_string(bytes) + ")");
