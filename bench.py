@@ -18,7 +18,7 @@ walk's own dispatch on the library's stream during eager steps, against the
 bandwidth measured in the same run: 16-byte loads over 2 GiB, reported as
 `stream_read_GBs`).  `traffic` is the walk's measured HBM bytes per launch
 (FETCH_SIZE + WRITE_SIZE, calibrated on a copy of known size) read from the
-committed counter summary profiles/walk_counters_mistral7b_effort025.md.
+committed counter summary profiles/walk_attention_counters_mistral7b_effort025_ctx2048.md.
 `walk_groups` splits the same steps by matrix group (q/k/v, o, w1/w3, w2, LM
 head, and the attention kernel): bytes, microseconds and fraction per launch.
 
@@ -156,7 +156,7 @@ def profiled_steps(ctx, model, n, effort):
     return b
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "walk_counters_mistral7b_effort025.md")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "walk_attention_counters_mistral7b_effort025_ctx2048.md")
 
 
 def walk_traffic():
@@ -468,23 +468,30 @@ def run_skew(args, iam, ctx):
 
 # ------------------------------------------------------------ profiling ---
 
-PROBE_CFG = dict(MISTRAL, max_ctx=1024)
+PROBE_CFG = dict(MISTRAL)
 
 
 def run_counter_probe(args, iam, ctx):
     """`--counter-probe`: the workload of the rocprofv3 counter passes.  The
-    32-layer model, an 8-token prompt and `--probe-steps` eager decode steps
-    (the same launch mix as a decode step of the default run: per layer the
+    32-layer model, an 8-token prompt, then every layer's K and V cache
+    filled with N(0,1) and the position set to `--probe-pos` (2048, the
+    layer workload's context), and `--probe-steps` eager decode steps (the
+    same launch mix as a decode step of the default run: per layer the
     q/k/v, o, w1/w3 and w2 walks and attention, then the LM head), then one
     device-to-device copy of 256 MiB that calibrates FETCH_SIZE and
     WRITE_SIZE.  Prints one JSON line with the decode steps' algorithmic
-    bytes per launch of each walk group."""
+    bytes per launch of each walk group and of attention."""
     cfg = PROBE_CFG
     model = iam.Model(ctx, iam.ModelConfig(**cfg))
     model.synthesize(0)
     prompt = np.random.default_rng(0).integers(0, cfg["vocab"], 8).astype(np.int32)
     model.generate(prompt, 1, args.effort, use_graph=False)
     ctx.sync()
+    pos0 = 8
+    if args.probe_pos > 8:
+        fill_kv_normal(ctx, model)
+        model.set_position(args.probe_pos)
+        pos0 = args.probe_pos
     n = args.probe_steps
     ctx.set_walk_counting(True)
     ctx.walk_counters(reset=True)
@@ -500,8 +507,9 @@ def run_counter_probe(args, iam, ctx):
     a, b = ctx.alloc(nbytes), ctx.alloc(nbytes)
     ctx.copy(b, a, nbytes)
     ctx.sync()
-    print(json.dumps({"steps": n, "layers": cfg["n_layers"], "effort": args.effort,
-                      "attention_context": 8 + 1 + (n - 1) / 2, "kv_bytes": kv_bytes(cfg, 8 + 1 + (n - 1) / 2),
+    actx = pos0 + 1 + (n - 1) / 2
+    print(json.dumps({"steps": n, "layers": cfg["n_layers"], "effort": args.effort, "position": pos0,
+                      "attention_context": actx, "kv_bytes": kv_bytes(cfg, actx),
                       "groups": groups, "copy_bytes": nbytes}), flush=True)
     a.free()
     b.free()
@@ -563,6 +571,20 @@ def run_counter_summary(args):
             if ctr in ("FETCH_SIZE", "WRITE_SIZE"):
                 copy = [v for _, n, v in rows if "copy" in n.lower() and "walk" not in n]
                 calib[ctr] = (max(copy), probe["copy_bytes"] / (max(copy) * 1024.0)) if copy else None
+    if args.trace:
+        c = sqlite3.connect(args.trace)
+        disp = [(d, nm, dur) for d, nm, dur in c.execute("select dispatch_id, name, duration from kernels "
+                                                         "order by dispatch_id")]
+        lab = label_dispatches(disp, steps, layers)
+        print("| kind | launches | algorithmic bytes | avg us | GB/s | fraction of 8 TB/s |")
+        print("|---|---:|---:|---:|---:|---:|")
+        for k in kinds:
+            if not lab[k]:
+                continue
+            us = sum(x for _, _, x in lab[k]) / len(lab[k]) / 1e3
+            print(f"| {k} | {len(lab[k])} | {algo[k]:.0f} | {us:.2f} | {algo[k] / us / 1e3:.0f} "
+                  f"| {algo[k] / us / 1e3 / HBM_PEAK_GBS:.3f} |")
+        print()
     print("| counter | " + " | ".join(kinds) + " |")
     print("|---|" + "---:|" * len(kinds))
     for ctr in sorted(table):
@@ -651,9 +673,12 @@ def main():
     ap.add_argument("--config1-reps", type=int, default=400, help="timed calls per mode of --config1")
     ap.add_argument("--counter-probe", action="store_true", help="run the counter passes' workload")
     ap.add_argument("--probe-steps", type=int, default=4)
+    ap.add_argument("--probe-pos", type=int, default=LAYER_CTX,
+                    help="position of the probe's decode steps (KV cache N(0,1) below it)")
     ap.add_argument("--counter-summary", nargs="+", metavar="CSV",
                     help="summarize rocprofv3 counter_collection CSVs of --counter-probe runs")
     ap.add_argument("--probe", help="the JSON line --counter-probe printed")
+    ap.add_argument("--trace", metavar="DB", help="with --counter-summary: a kernel trace of the same probe command")
     ap.add_argument("--trace-summary", metavar="DB", help="summarize a rocprofv3 kernel trace")
     ap.add_argument("--trace-steps", type=int, default=8)
     ap.add_argument("--trace-layers", type=int, default=32)

@@ -81,6 +81,7 @@ def test_counter_summary_calibrates_on_the_copy(bench, tmp_path, capsys):
     class A:
         counter_summary = paths
         probe = str(pj)
+        trace = None
     bench.run_counter_summary(A)
     out = capsys.readouterr().out
     # both counters calibrate to k KiB read and k KiB written for kind k:
