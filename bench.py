@@ -663,6 +663,10 @@ def main():
                     help="skip the config 1/2/3/5 measurements of the default run")
     ap.add_argument("--acc", choices=["fp64", "fp32"], default="fp64",
                     help="walk/attention accumulation (fp64: results equal the correctly rounded sums)")
+    ap.add_argument("--select-block", type=int, default=1,
+                    help="block-structured selection: inputs per block (1: the reference's per-row selection)")
+    ap.add_argument("--select-below", type=float, default=2.0,
+                    help="with --select-block: apply it to efforts below this one")
     ap.add_argument("--eager", action="store_true",
                     help="launch every kernel from the host instead of replaying a captured graph")
     ap.add_argument("--skew", action="store_true",
@@ -708,6 +712,8 @@ def main():
     iam = load_iam()
     ctx = iam.Ctx(0)
     ctx.set_accumulation(args.acc)
+    if args.select_block != 1:
+        ctx.set_selection_block(args.select_block, args.select_below)
     if args.counter_probe:
         run_counter_probe(args, iam, ctx)
         ctx.close()
@@ -851,6 +857,8 @@ def main():
                                "bucket-layout LM head, fp16 GQA KV cache (4096 positions)",
                    "effort": args.effort, "prompt_tokens": args.prompt, "layers": cfg["n_layers"],
                    "accumulation": args.acc, "graph_replay": use_graph,
+                   "selection": "per row" if args.select_block == 1 else
+                                f"blocks of {args.select_block} inputs below effort {args.select_below}",
                    "dim": cfg["dim"], "ffn_dim": cfg["ffn_dim"], "vocab": cfg["vocab"],
                    "global_batch": 1, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": "bucket_walk", "achieved": round(achieved, 1),

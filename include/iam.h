@@ -203,6 +203,18 @@ int iam_walk_group_counters(iam_ctx* ctx, int group, uint64_t* weight_bytes, uin
  * Changing it re-captures the model's decode graph.  Not during capture.
  * No counterpart in the reference. */
 int iam_set_walk_counting(iam_ctx* ctx, int on);
+/* Block-structured selection, the thesis's future work (THESIS p.42-43):
+ * with block_inputs B > 1, the inputs are taken in blocks of B consecutive
+ * ones, and rank k of every input of a block is selected when rank k of any
+ * of them passes the cutoff (the block's largest rank-k importance >= the
+ * cutoff); the cutoff itself is the reference's.  It applies to calls whose
+ * effort is below below_effort (the hybrid of fine selection at moderate
+ * and blocks at aggressive sparsity); B = 1 (the default) is the
+ * reference's per-row selection.  B is 1, 2, 4, 8 or 16.  Changing it
+ * re-captures a model's decode graph.  Not during capture.  No counterpart
+ * in the reference. */
+int iam_set_selection_block(iam_ctx* ctx, int block_inputs, float below_effort);
+int iam_get_selection_block(iam_ctx* ctx, int* block_inputs, float* below_effort);
 /* Accumulation of the bucket walk (and of attention) for this context:
  * IAM_ACC_FP64 (default) adds the exact fp64 products in fp64 and rounds each
  * output once, so results do not depend on the order of the additions and

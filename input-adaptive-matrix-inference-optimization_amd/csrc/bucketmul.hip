@@ -202,6 +202,19 @@ __global__ __launch_bounds__(kCutThreads) void k_cutoff(CutoffArgs a)
 // ------------------------------------------------------------- dispatch ---
 // The selected-row list of the parity queries: prepareDispatch
 // (bucketMul.cl:351-386) per chunk of 256 inputs, rows in ascending order.
+// Block-structured selection (the thesis's future work, p.42-43): rank k
+// of every input of a block of blk consecutive inputs is selected when rank
+// k of any of them passes the cutoff, i.e. when the block's largest rank-k
+// importance does.  The block's inputs sit in consecutive lanes (slices
+// start at multiples of blk), so an OR over the lane group does it; lanes
+// past the slice contribute nothing.  NaN importances pass for no input.
+__device__ __forceinline__ uint32_t block_select(uint32_t mask, int blk, bool valid)
+{
+    uint32_t m = valid ? mask : 0u;
+    for (int o = 1; o < blk; o <<= 1) m |= (uint32_t)__shfl_xor((int)m, o, 64);
+    return valid ? m : 0u;
+}
+
 struct DispatchDesc {
     const float* x;
     const uint16_t* probes;   // already offset to the expert
@@ -215,6 +228,7 @@ struct DispatchDesc {
     uint2* list;
     uint32_t* counts;
     float* cutoff;
+    int sel_block;            // inputs per selection block (1: per row)
 };
 
 __global__ __launch_bounds__(kCutThreads) void k_dispatch(DispatchDesc d)
@@ -251,6 +265,11 @@ __global__ __launch_bounds__(kCutThreads) void k_dispatch(DispatchDesc d)
             const float imp = __fmul_rn(kScale, fabsf(prod));
             if (imp >= cutoff && r0 + kk < d.rows) mask |= 1u << kk;   // bucketMul.cl:380
         }
+    }
+    if (d.sel_block > 1) {
+        mask = block_select(mask, d.sel_block, i < d.in_size && r0 < d.rows);
+        const int left = d.rows - r0;
+        if (left < 16) mask &= left > 0 ? (1u << left) - 1u : 0u;
     }
     const int cnt = __popc(mask);
     const int incl = wave_incl_sum(cnt);
@@ -351,6 +370,7 @@ struct WalkArgs {
     void* zero_p[2];
     int zero_n[2];
     unsigned long long* counters;
+    int sel_block;            // inputs per selection block (1: the reference's per-row selection)
 };
 
 // A pointer the compiler no longer sees as global (after an asm) marked
@@ -447,7 +467,8 @@ __device__ __forceinline__ void select_load(const SelSrc& d, const WalkArgs& a, 
 // returns the number of selected rows.
 template <int NT>
 __device__ __forceinline__ uint32_t select_finish(const SelSrc& d, float cutoff, int i0, int ni, const SelLoads& L,
-                                                  uint16_t* s_row, float* s_x, uint32_t* s_wsum, bool x_lds)
+                                                  uint16_t* s_row, float* s_x, uint32_t* s_wsum, bool x_lds,
+                                                  int blk)
 {
 #pragma clang fp contract(off)
     constexpr int NW = NT / 64;
@@ -482,6 +503,11 @@ __device__ __forceinline__ uint32_t select_finish(const SelSrc& d, float cutoff,
             const float imp = __fmul_rn(kScale, fabsf(prod));
             if (imp >= cutoff && r0 + kk < d.rows) mask |= 1u << kk;   // bucketMul.cl:380
         }
+    }
+    if (blk > 1) {
+        mask = block_select(mask, blk, tid < ni);
+        const int left = d.rows - (i0 + tid) * 16;          // rows of this input inside the expert
+        if (left < 16) mask &= left > 0 ? (1u << left) - 1u : 0u;
     }
     const uint32_t cnt = (uint32_t)__popc(mask);
     const uint32_t incl = (uint32_t)wave_incl_sum((int)cnt);
@@ -684,7 +710,7 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     }
 
     // ---- selection of the slice's rows
-    const int ns = (int)select_finish<NT>(ss, cutoff, i0, ni, L, s_row, s_x, s_wsum, slice_regs);
+    const int ns = (int)select_finish<NT>(ss, cutoff, i0, ni, L, s_row, s_x, s_wsum, slice_regs, a.sel_block);
     if (t == 0 && tid == 0) {
         d.slice_count[p] = (uint32_t)ns;
         if (a.counters) {
@@ -950,7 +976,9 @@ double est_rows(int rows, float effort) { return std::max(1.0, rows * est_fracti
 #endif
 constexpr int kWalkWaves = 8;
 
-void plan_walk(int n, const MatOp* ops, float effort, WalkPlan* plan)
+int sel_block_for(const Ctx* c, float effort) { return c->sel_block > 1 && effort < c->sel_below ? c->sel_block : 1; }
+
+void plan_walk(int n, const MatOp* ops, float effort, WalkPlan* plan, int blk)
 {
     double bytes[kMaxMulti], tot = 0;
     for (int i = 0; i < n; i++) {
@@ -968,6 +996,7 @@ void plan_walk(int n, const MatOp* ops, float effort, WalkPlan* plan)
         const double wgs = tot > 0 ? IAM_WALK_WGS * bytes[i] / tot : (double)IAM_WALK_WGS / n;
         const int slices = std::max(1, (int)std::floor(wgs / pl.T + 1e-9));
         pl.IPS = std::min(64 * pl.NW, std::max(1, (pl.n_in + slices - 1) / slices));
+        if (blk > 1) pl.IPS = std::min(64 * pl.NW, (pl.IPS + blk - 1) / blk * blk);   // blocks within a slice
         pl.P = (pl.n_in + pl.IPS - 1) / pl.IPS;
     }
 }
@@ -1061,6 +1090,7 @@ static int bucketmul_list(Ctx* c, int i)
     d.list = s.list;
     d.counts = s.counts;
     d.cutoff = s.cutoff;
+    d.sel_block = sel_block_for(c, s.effort);
     s.G = G;
     return launch(c, "bucket_list", k_dispatch, dim3(G), dim3(kCutThreads), 0, d);
 }
@@ -1097,9 +1127,11 @@ int walk_group(Ctx* c, const WalkGroup& g)
         ops[i].x = wm.x;
         ops[i].y = wm.y;
     }
+    const int blk = sel_block_for(c, g.effort);
     WalkPlan plan[kMaxMulti];
-    plan_walk(g.n, ops, g.effort, plan);
+    plan_walk(g.n, ops, g.effort, plan, blk);
     WalkArgs args{};
+    args.sel_block = blk;
     args.n = g.n;
     const int qv = quantile_of(g.effort);
     for (int i = 0; i < g.n; i++) {

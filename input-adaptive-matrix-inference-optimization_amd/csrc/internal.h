@@ -120,6 +120,10 @@ struct Ctx {
     bool counting = true;
     // accumulate the walk in fp64 (sums round once to fp32) instead of fp32
     bool acc64 = true;
+    // block-structured selection: inputs per block (1: the reference's
+    // per-row selection), used for efforts below sel_below
+    int sel_block = 1;
+    float sel_below = 2.0f;
 };
 
 int ctx_alloc(Ctx* c, size_t bytes, void** out);
@@ -205,7 +209,10 @@ struct WalkPlan {
     int IPS;    // inputs per slice
     int P;      // slices
 };
-void plan_walk(int n, const MatOp* ops, float effort, WalkPlan* plan);
+// blk: inputs per selection block (slices start at its multiples)
+void plan_walk(int n, const MatOp* ops, float effort, WalkPlan* plan, int blk = 1);
+// the selection block size of a walk at this effort
+int sel_block_for(const Ctx* c, float effort);
 
 // A matrix group of the decode step (or of a standalone call): up to 3
 // matrices sharing one input mode.  Per matrix: the accumulator (zero on

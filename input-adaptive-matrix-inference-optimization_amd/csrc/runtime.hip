@@ -501,6 +501,30 @@ int iam_set_walk_counting(iam_ctx* c, int on)
     return IAM_OK;
 }
 
+int iam_set_selection_block(iam_ctx* c, int block_inputs, float below_effort)
+{
+    if (!c) return fail(IAM_E_INVALID, "set_selection_block: null context");
+    IAM_REQUIRE(!c->capturing, "set_selection_block: not allowed during graph capture");
+    IAM_REQUIRE(block_inputs == 1 || block_inputs == 2 || block_inputs == 4 || block_inputs == 8 ||
+                    block_inputs == 16,
+                "set_selection_block: block_inputs must be 1, 2, 4, 8 or 16");
+    IAM_REQUIRE(below_effort > 0.0f, "set_selection_block: below_effort must be positive");
+    if (block_inputs != c->sel_block || below_effort != c->sel_below) {
+        c->sel_block = block_inputs;
+        c->sel_below = below_effort;
+        c->scratch_gen++;   // captured graphs hold walk launches of the other setting
+    }
+    return IAM_OK;
+}
+
+int iam_get_selection_block(iam_ctx* c, int* block_inputs, float* below_effort)
+{
+    if (!c || !block_inputs || !below_effort) return fail(IAM_E_INVALID, "get_selection_block: bad argument");
+    *block_inputs = c->sel_block;
+    *below_effort = c->sel_below;
+    return IAM_OK;
+}
+
 int iam_get_accumulation(iam_ctx* c, int* mode)
 {
     if (!c || !mode) return fail(IAM_E_INVALID, "get_accumulation: bad argument");

@@ -249,6 +249,17 @@ class Ctx:
         """Count the walk's selected rows (default on; off shortens each reduce)."""
         check(lib().iam_set_walk_counting(self.h, 1 if on else 0))
 
+    def set_selection_block(self, block_inputs, below_effort=2.0):
+        """Block-structured selection: blocks of `block_inputs` consecutive
+        inputs share each rank's selection, for efforts below `below_effort`
+        (1: the reference's per-row selection)."""
+        check(lib().iam_set_selection_block(self.h, int(block_inputs), C.c_float(below_effort)))
+
+    def get_selection_block(self):
+        b, e = C.c_int(), C.c_float()
+        check(lib().iam_get_selection_block(self.h, C.byref(b), C.byref(e)))
+        return b.value, e.value
+
     def get_accumulation(self):
         m = C.c_int()
         check(lib().iam_get_accumulation(self.h, C.byref(m)))

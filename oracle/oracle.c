@@ -440,6 +440,31 @@ int64_t orc_select_rows(const float* x, const uint16_t* stats, int stats_channel
     return s;
 }
 
+/* Block-structured selection (THESIS p.42-43, future work; not in the
+ * reference's code): the inputs 0.. are taken in blocks of `block`
+ * consecutive ones, and row 16*i + k (i < in_size) is selected when row
+ * 16*u + k passes the per-row test of orc_select_rows for some input u of
+ * i's block (u < in_size); rows of inputs past in_size stay unselected, as
+ * in the per-row test.  block = 1 is orc_select_rows. */
+int64_t orc_select_rows_block(const float* x, const uint16_t* stats, int stats_channels,
+                              int exp_no, int expert_rows, int in_size, float cutoff, int block,
+                              uint8_t* mask)
+{
+    int64_t s = orc_select_rows(x, stats, stats_channels, exp_no, expert_rows, in_size, cutoff, mask);
+    if (block <= 1) return s;
+    const int inputs = (expert_rows + 15) / 16;
+    uint8_t* blk = (uint8_t*)calloc((size_t)((inputs + block - 1) / block) * 16, 1);
+    for (int r = 0; r < expert_rows; r++)
+        if (mask[r]) blk[(size_t)(r / 16 / block) * 16 + (r % 16)] = 1;
+    s = 0;
+    for (int r = 0; r < expert_rows; r++) {
+        mask[r] = r / 16 < in_size ? blk[(size_t)(r / 16 / block) * 16 + (r % 16)] : 0;   /* past in_size: skipped */
+        s += mask[r];
+    }
+    free(blk);
+    return s;
+}
+
 /* bucketMul (bucketMul.cl:392-447) + bucketIntegrate (:453-497): every
  * selected row contributes x*packed_w at output col*16 + (bits & 15). */
 void orc_bucket_walk(const uint16_t* buckets, int bucket_cols, int exp_no, int expert_rows,
@@ -488,6 +513,17 @@ void orc_bucket_walk(const uint16_t* buckets, int bucket_cols, int exp_no, int e
     }
 }
 
+/* the selection used by orc_bucketmul (and so by the layer and model
+ * forwards): blocks of g_sel_block inputs for efforts below g_sel_below */
+static int g_sel_block = 1;
+static float g_sel_below = 2.0f;
+
+void orc_set_selection_block(int block, float below_effort)
+{
+    g_sel_block = block > 1 ? block : 1;
+    g_sel_below = below_effort;
+}
+
 int64_t orc_bucketmul(const float* x, const uint16_t* stats, const uint16_t* probes,
                       const uint16_t* buckets, int exp_no, int in_size, int bucket_cols,
                       int expert_rows, float effort, float* y, float* cutoff_out,
@@ -496,7 +532,8 @@ int64_t orc_bucketmul(const float* x, const uint16_t* stats, const uint16_t* pro
     int q = orc_effort_quantile(effort);
     float cutoff = orc_find_cutoff(x, probes, exp_no, q, NULL);
     uint8_t* mask = mask_out ? mask_out : (uint8_t*)malloc((size_t)expert_rows);
-    int64_t s = orc_select_rows(x, stats, 4, exp_no, expert_rows, in_size, cutoff, mask);
+    const int blk = g_sel_block > 1 && effort < g_sel_below ? g_sel_block : 1;
+    int64_t s = orc_select_rows_block(x, stats, 4, exp_no, expert_rows, in_size, cutoff, blk, mask);
     orc_bucket_walk(buckets, bucket_cols, exp_no, expert_rows, mask, x, y, acc64);
     if (cutoff_out) *cutoff_out = cutoff;
     if (!mask_out) free(mask);

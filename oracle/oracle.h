@@ -82,6 +82,11 @@ float orc_find_cutoff_imp(const float* imp, int quantile, orc_cutoff_trace* trac
 int64_t orc_select_rows(const float* x, const uint16_t* stats, int stats_channels,
                         int exp_no, int expert_rows, int in_size, float cutoff,
                         uint8_t* mask);
+/* block-structured selection: rank k of every input of a block of `block`
+ * consecutive inputs when rank k of any of them passes (block 1: the above) */
+int64_t orc_select_rows_block(const float* x, const uint16_t* stats, int stats_channels,
+                              int exp_no, int expert_rows, int in_size, float cutoff, int block,
+                              uint8_t* mask);
 
 /* ---- bucket walk + integrate (bucketMul.cl:392-497) ---------------------- */
 /* y[out_dim = 16*C] = sum over selected rows r (mask) of x[r/16]*W[r][c] at
@@ -148,6 +153,11 @@ typedef struct {
 void orc_layer_forward(const orc_model* m, int layer, int pos, float effort, float* h);
 void orc_model_forward(const orc_model* m, int token, int pos, float effort,
                        const float* hidden_in, float* logits);
+
+/* selection of orc_bucketmul and the forwards above: blocks of `block`
+ * inputs (orc_select_rows_block) for efforts below below_effort; block 1
+ * (the default) is the reference's per-row selection */
+void orc_set_selection_block(int block, float below_effort);
 
 /* threads the OpenMP loops use (1 when built without OpenMP) */
 int orc_threads(void);

@@ -93,6 +93,9 @@ def lib():
     L.orc_find_cutoff_imp.argtypes = [f32p, C.c_int, C.POINTER(CutoffTrace)]
     L.orc_select_rows.restype = C.c_int64
     L.orc_select_rows.argtypes = [f32p, u16p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, u8p]
+    L.orc_select_rows_block.restype = C.c_int64
+    L.orc_select_rows_block.argtypes = [f32p, u16p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int,
+                                        u8p]
     L.orc_bucket_walk.argtypes = [u16p, C.c_int, C.c_int, C.c_int, u8p, f32p, f32p, C.c_int]
     L.orc_bucketmul.restype = C.c_int64
     L.orc_bucketmul.argtypes = [f32p, u16p, u16p, u16p, C.c_int, C.c_int, C.c_int, C.c_int,
@@ -106,6 +109,7 @@ def lib():
     L.orc_attention_f16kv.argtypes = [f32p, u16p, u16p, C.c_int, C.c_int, C.c_int, C.c_int, f32p]
     L.orc_argmax.restype = C.c_int
     L.orc_argmax.argtypes = [f32p, C.c_int]
+    L.orc_set_selection_block.argtypes = [C.c_int, C.c_float]
     L.orc_threads.restype = C.c_int
     L.orc_threads.argtypes = []
     L.orc_layer_forward.argtypes = [C.POINTER(Model), C.c_int, C.c_int, C.c_float, f32p]
@@ -199,6 +203,16 @@ def select_rows(x, stats, cutoff, expert_rows, in_size, exp_no=0, channels=4):
     s = lib().orc_select_rows(np.ascontiguousarray(x, np.float32),
                               np.ascontiguousarray(stats, np.uint16).ravel(), channels,
                               exp_no, expert_rows, in_size, cutoff, mask)
+    return mask, s
+
+
+def select_rows_block(x, stats, cutoff, expert_rows, in_size, block, exp_no=0, channels=4):
+    """Block-structured selection: blocks of `block` consecutive inputs share
+    each rank's selection (block 1: select_rows)."""
+    mask = np.empty(expert_rows, dtype=np.uint8)
+    s = lib().orc_select_rows_block(np.ascontiguousarray(x, np.float32),
+                                    np.ascontiguousarray(stats, np.uint16).ravel(), channels,
+                                    exp_no, expert_rows, in_size, cutoff, block, mask)
     return mask, s
 
 
@@ -335,3 +349,9 @@ class OracleModel:
 def threads():
     """Threads of the oracle's parallel loops (OpenMP's maximum)."""
     return lib().orc_threads()
+
+
+def set_selection_block(block, below_effort=2.0):
+    """The selection of bucketmul and the layer/model forwards: blocks of
+    `block` inputs for efforts below `below_effort` (1: per row)."""
+    lib().orc_set_selection_block(int(block), float(below_effort))

@@ -66,7 +66,9 @@ def run_gpu(ctx, b, s, p, x, effort, in_size=None, expert_no=0, expert_rows=None
     return y, cut, S, rows
 
 
-def check_against_oracle(O, ctx, b, s, p, x, effort, **kw):
+def check_against_oracle(O, ctx, b, s, p, x, effort, block=1, **kw):
+    """block: the oracle selects in blocks of that many inputs (the GPU's
+    setting is the context's)."""
     y, cut, S, rows = run_gpu(ctx, b, s, p, x, effort, **kw)
     in_size = kw.get("in_size")
     expert_no = kw.get("expert_no", 0)
@@ -75,7 +77,7 @@ def check_against_oracle(O, ctx, b, s, p, x, effort, **kw):
         in_size = R // 16
     q = O.effort_quantile(effort)
     ocut = O.find_cutoff(x, p, q, exp_no=expert_no)
-    mask, oS = O.select_rows(x, s, ocut, R, in_size, exp_no=expert_no)
+    mask, oS = O.select_rows_block(x, s, ocut, R, in_size, block, exp_no=expert_no)
     bb = b.reshape(-1, b.shape[-1])
     oy = O.bucket_walk(bb, mask, x, R, exp_no=expert_no)
     assert np.float32(cut).view(np.uint32) == np.float32(ocut).view(np.uint32), (cut, ocut)
@@ -433,3 +435,27 @@ def test_walk_counting_switch(O, iam, ctx):
     assert ctx.walk_counters(reset=True) == (2 * S * b.shape[1], S, 1)
     for d in (db, ds, dp, dx, dy):
         d.free()
+
+
+@pytest.mark.parametrize("block", [2, 16])
+@pytest.mark.parametrize("shape,effort", [((4096, 4096), 0.25), ((14336, 4096), 0.05), ((4096, 14336), 0.125)],
+                         ids=["square", "w1", "w2"])
+def test_block_structured_selection(O, iam, ctx, block, shape, effort):
+    """Block-structured selection (opt-in, blocks of `block` inputs for
+    efforts below 0.5): cutoff bits, the selected rows, their count and y
+    against the oracle's block selection and walk, through calc_dispatch +
+    mul and through the fused walk; at effort 0.75 (above 0.5) the
+    reference's per-row selection."""
+    b, s, p = make_matrix(O, *shape, tid=40 + block)
+    x = O.gen_f32(0, 41, shape[1], 0.0, 1.0)
+    ctx.set_selection_block(block, 0.5)
+    try:
+        y, oy, cut, S = check_against_oracle(O, ctx, b, s, p, x, effort, block=block)
+        fine, _ = O.select_rows(x, s, cut, b.shape[0], shape[1])
+        assert S > int(fine.sum())                      # blocks add rows
+        yf = run_gpu(ctx, b, s, p, x, effort, fused=iam)[0]
+        assert ulps(yf, oy).max() <= 1
+        check_against_oracle(O, ctx, b, s, p, x, 0.75, block=1)
+    finally:
+        ctx.set_selection_block(1)
+    assert ctx.get_selection_block()[0] == 1

@@ -197,6 +197,37 @@ def test_model_rejects_bad_config(iam, ctx):
         iam.Model(ctx, iam.ModelConfig(**bad))
 
 
+def test_block_selection_model_logits_and_tokens(O, ctx, model):
+    """The decode step with block-structured selection (blocks of 8 inputs
+    below effort 0.5), run at effort 0.25: logits within 1 ulp of the oracle
+    model with the same selection at every step, greedy tokens identical,
+    and different from the per-row selection's logits."""
+    orc = OracleModel(O, model)
+    prompt = [5, 77, 130]
+    ctx.set_selection_block(8, 0.5)
+    O.set_selection_block(8, 0.5)
+    try:
+        toks = model.generate(np.array(prompt, np.int32), 4, 0.25, use_graph=True)
+        seq = list(prompt)
+        for pos in range(len(prompt) + 3):
+            lo = orc.forward(seq[pos], pos, 0.25)
+            if pos >= len(prompt) - 1:
+                seq.append(O.argmax(lo))
+        assert list(toks) == seq[len(prompt):]
+        gl = ctx.empty(CFG["vocab"], np.float32)
+        model.forward(seq[2], 2, 0.25, gl)
+        g = gl.read()
+        want = orc.forward(seq[2], 2, 0.25)
+        assert ulps(g, want).max() <= 1
+        O.set_selection_block(1)
+        fine = orc.forward(seq[2], 2, 0.25)
+        assert not np.array_equal(fine, want)
+        gl.free()
+    finally:
+        ctx.set_selection_block(1)
+        O.set_selection_block(1)
+
+
 def test_model_refuses_steps_past_the_kv_capacity(iam, ctx, model):
     """The host keeps the position of the next step: a decode, device step or
     generate that would write K/V past max_ctx, or a position beyond

@@ -284,6 +284,58 @@ def test_select_rows_expert_offset(O):
     assert not np.array_equal(m0, m1)
 
 
+@pytest.mark.parametrize("block", [1, 2, 8, 16])
+def test_select_rows_block_is_any_over_the_block(O, block):
+    """Block-structured selection against a numpy any-over-the-block of the
+    per-row test, with a partial last block (in_size not a multiple of the
+    block) and rows past in_size; invariants: it contains the per-row
+    selection, is constant over each block for every rank, and block 1 is
+    the per-row selection."""
+    rng = np.random.default_rng(20 + block)
+    in_dim = 100
+    R = in_dim * 16
+    in_size = 90
+    x = rng.standard_cauchy(4096).astype(np.float32)          # heavy-tailed inputs
+    stats = np.abs(rng.normal(0.02, 0.01, (R, 4))).astype(np.float16)
+    fine, s_fine = O.select_rows(x, stats.view(np.uint16), 300.0, R, in_size)
+    mask, s = O.select_rows_block(x, stats.view(np.uint16), 300.0, R, in_size, block)
+    f = fine.reshape(in_dim, 16).astype(bool)
+    nb = (in_dim + block - 1) // block
+    pad = np.zeros((nb * block, 16), bool)
+    pad[:in_dim] = f
+    want = np.repeat(pad.reshape(nb, block, 16).any(axis=1), block, axis=0)[:in_dim]
+    want[in_size:] = False                                    # rows past in_size stay skipped
+    assert np.array_equal(mask.reshape(in_dim, 16).astype(bool), want)
+    assert s == want.sum()
+    assert (mask >= fine).all()
+    if block == 1:
+        assert np.array_equal(mask, fine) and s == s_fine
+    else:
+        assert s > s_fine
+        m = mask.reshape(in_dim, 16).astype(bool)
+        assert not m[in_size:].any()
+        for b0 in range(0, in_size - in_size % block, block):   # whole blocks below in_size
+            blk = m[b0:b0 + block]
+            assert (blk == blk[0]).all()
+
+
+def test_select_rows_block_one_hot(O):
+    """x zero but for input 37: only its block's rows, with the ranks input 37
+    passes, are selected, in every input of the block."""
+    R = 64 * 16
+    x = np.zeros(4096, np.float32)
+    x[37] = 3.0
+    stats = np.full((R, 4), np.float16(0.01), np.float16)
+    stats[37 * 16:38 * 16, 3] = np.linspace(0.05, 0.001, 16).astype(np.float16)
+    cutoff = np.float32(100000.0 * 3.0 * np.float32(np.float16(0.02)))
+    mask, s = O.select_rows_block(x, stats.view(np.uint16), cutoff, R, 64, 8)
+    ranks = np.float32(100000.0) * np.abs(np.float32(3.0) * stats[37 * 16:38 * 16, 3].astype(np.float32)) >= cutoff
+    want = np.zeros((64, 16), bool)
+    want[32:40] = ranks
+    assert np.array_equal(mask.reshape(64, 16).astype(bool), want)
+    assert s == 8 * ranks.sum() and 0 < ranks.sum() < 16
+
+
 # ------------------------------------------------------------------ walk ---
 
 def _packed_dense(b, in_dim):
