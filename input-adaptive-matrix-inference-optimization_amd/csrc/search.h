@@ -281,30 +281,31 @@ __device__ float search_cutoff(const float (&v)[IAM_PROBES_COUNT / (64 * NW)], i
     const bool top_m1 = t - 1 < 1, top_m2 = t - 2 < 1;   // (U[0], U[1] unused then)
 
     // ---- 5. the reference's rounds (bucketMul.cl:139-213): one chain of
-    // bounds (each round's next bound is the midpoint on the side its count
-    // picks, both computed while the count is compared), lane r keeping round
-    // r's tested bound, bracket, side and min-count state
+    // bounds, each round's side picked by U[2] > b (count >= target); lane r
+    // keeps round r's tested bound and the decisions collect in a bit mask.
+    // Round r's bracket is then rebuilt per lane: its low end is the last
+    // tested bound at or before r whose count reached the target (else the
+    // minimum), its high end the last one whose count did not (else the
+    // maximum).
     float lo = gmin, hi = gmax;
     float b = midpoint(gmin, gmax);
-    bool min_init = true;          // minB is still the minimum: its count is the reference's 4096 (:142)
-    float cb = 0.0f, clo = 0.0f, chi = 0.0f;
-    bool cge = false, cmi = true;
+    float cb = 0.0f;
+    uint32_t gbits = 0u;
 #pragma unroll
     for (int rd = 0; rd < 20; rd++) {
         const bool g = U[2] > b;             // count >= target: min moves
-        const float mh = midpoint(b, hi), ml = midpoint(lo, b);
-        const float nlo = g ? b : lo, nhi = g ? hi : b;
-        min_init = min_init && !g;
-        const bool me = lane == rd;
-        cb = me ? b : cb;
-        clo = me ? nlo : clo;
-        chi = me ? nhi : chi;
-        cge = me ? g : cge;
-        cmi = me ? min_init : cmi;
-        lo = nlo;
-        hi = nhi;
-        b = g ? mh : ml;
+        cb = lane == rd ? b : cb;
+        gbits |= (g ? 1u : 0u) << rd;
+        lo = g ? b : lo;
+        hi = g ? hi : b;
+        b = midpoint(lo, hi);
     }
+    const uint32_t upto = lane < 20 ? (2u << lane) - 1u : 0xfffffu;    // rounds 0 .. lane
+    const uint32_t gl = gbits & upto, gh = ~gbits & upto;
+    const float clo = gl ? __shfl(cb, 31 - __clz(gl), 64) : gmin;
+    const float chi = gh ? __shfl(cb, 31 - __clz(gh), 64) : gmax;
+    const bool cge = lane < 20 && ((gbits >> lane) & 1u);
+    const bool cmi = gl == 0u;     // minB is still the minimum: its count is the reference's 4096 (:142)
     // lane r < 20: the stop tests of round r (bucketMul.cl:195-200)
     const bool eq_t = cge && !(U[3] > cb);                        // count == target
     const bool am1 = top_m1 || U[1] > chi, am2 = top_m2 || U[0] > chi;
