@@ -217,10 +217,11 @@ int iam_set_selection_block(iam_ctx* ctx, int block_inputs, float below_effort);
 int iam_get_selection_block(iam_ctx* ctx, int* block_inputs, float* below_effort);
 /* Accumulation of the bucket walk (and of attention) for this context:
  * IAM_ACC_FP64 (default) adds the exact fp64 products in fp64 and rounds each
- * output once, so results do not depend on the order of the additions and
- * equal the correctly rounded sums; IAM_ACC_FP32 accumulates in fp32 like
- * the reference's bucketMul (bucketMul.cl:430-445).  Both are deterministic.
- * No counterpart in the reference (its fp32 atomics are order dependent). */
+ * output once: every output is within an fp64 rounding of the correctly
+ * rounded sum, whatever the order of the additions.  IAM_ACC_FP32 forms the
+ * products in fp32 as the reference's bucketMul does (bucketMul.cl:430-445)
+ * and adds them in fp64; attention runs in fp32.  No counterpart in the
+ * reference (its fp32 atomics are order dependent). */
 #define IAM_ACC_FP32 0
 #define IAM_ACC_FP64 1
 int iam_set_accumulation(iam_ctx* ctx, int mode);

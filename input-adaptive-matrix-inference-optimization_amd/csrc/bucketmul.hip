@@ -571,7 +571,11 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     constexpr int VPT = IAM_PROBES_COUNT / NT;              // inputs of the cutoff per thread
     static_assert(kTileOut % NT == 0, "flush mapping");
-    __shared__ __align__(16) Acc tiles[NW * TSLOTS];   // the wave tiles
+    // the wave tiles hold fp64 sums in both modes: Acc is the precision of
+    // the products (fp32 mode: the reference's fp32 products), and LDS fp64
+    // atomic adds run many times faster than fp32 ones on this part
+    using Tile = double;
+    __shared__ __align__(16) Tile tiles[NW * TSLOTS];   // the wave tiles
     // the search's scratch, then the selected rows
     constexpr int kSearchBytes = sizeof(SearchLds<NW>) > NT * 16 * 2 ? sizeof(SearchLds<NW>) : NT * 16 * 2;
     __shared__ __align__(16) uint4 s_search[(kSearchBytes + 15) / 16];
@@ -654,7 +658,7 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     // each wave clears its own tile while the loads are in flight
     {
         uint4* tz = reinterpret_cast<uint4*>(tiles + wave * TSLOTS);
-        constexpr int kTileVecs = TSLOTS * (int)sizeof(Acc) / 16;
+        constexpr int kTileVecs = TSLOTS * (int)sizeof(Tile) / 16;
 #pragma unroll
         for (int i = 0; i < kTileVecs / 64; i++) tz[i * 64 + lane] = make_uint4(0u, 0u, 0u, 0u);
     }
@@ -732,7 +736,7 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
         const bool whole = (d.C & 7) == 0;
         const int nc = min(8, d.C - col0);
         const uint16_t* wb = d.W + (size_t)i0 * 16 * d.C + col0;
-        const uint32_t tbase = lds_offset(tiles) + (uint32_t)(wave * TSLOTS + j) * (uint32_t)sizeof(Acc);
+        const uint32_t tbase = lds_offset(tiles) + (uint32_t)(wave * TSLOTS + j) * (uint32_t)sizeof(Tile);
         const int ng = (ns + 3) >> 2;
         // one instance of the loop per row load shape, so that no branch sits
         // in its steady state
@@ -775,7 +779,8 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
                     // multiply-add into the slot address
                     uint32_t pos;
                     asm("v_bfe_u32 %0, %1, %2, 4" : "=v"(pos) : "v"(words[e >> 1]), "i"((e & 1) * 16));
-                    lds_add<Acc>(__umul24(pos, kTilePitch * (uint32_t)sizeof(Acc)) + tbase, e * 16, xc[u] * (Acc)h2f(hw));
+                    lds_add<Tile>(__umul24(pos, kTilePitch * (uint32_t)sizeof(Tile)) + tbase, e * 16,
+                                  (Tile)(xc[u] * (Acc)h2f(hw)));
                 }
             }
         };
@@ -825,11 +830,11 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     double* out = reinterpret_cast<double*>(d.acc) + (size_t)t * kTileOut;
     const int nout = min(kTileOut, (d.C - t * kTileCols) * 16);
     {
-        Acc sum[OPT];
+        Tile sum[OPT];
 #pragma unroll
         for (int k2 = 0; k2 < OPT; k2++) {
             const int sl = tid + k2 * NT;
-            Acc sv = tiles[sl];
+            Tile sv = tiles[sl];
 #pragma unroll
             for (int ww = 1; ww < NW; ww++) sv += tiles[ww * TSLOTS + sl];
             sum[k2] = sv;
@@ -854,8 +859,8 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
 #pragma unroll
     for (int k2 = 0; k2 < OPT; k2++) {
         const int o = tid + k2 * NT;                      // col_local*16 + pos
-        const Acc sv = tiles[o + (o >> 7)];
-        if (o < nout && sv != (Acc)0) {
+        const Tile sv = tiles[o + (o >> 7)];
+        if (o < nout && sv != (Tile)0) {
             if (ret) sink += __hip_atomic_fetch_add(out + o, (double)sv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             else acc_add(out + o, (double)sv);
         }

@@ -392,9 +392,9 @@ def test_invalid_arguments_raise(iam, O, ctx):
 @pytest.mark.parametrize("mode", ["fp64", "fp32"])
 def test_accumulation_modes_repeat(O, ctx, mode):
     """Repeated runs: fp64 stays within 1 ulp of the oracle on every run;
-    fp32 (products and a workgroup's sums in fp32, as the reference's walk)
-    within 1e-5 relative L2, and the runs agree to 1e-6 (the workgroups'
-    sums are added in fp64 in whatever order they arrive)."""
+    fp32 (the reference's fp32 products, added in fp64) within 1e-5 relative
+    L2 of the oracle's fp32 walk, and the runs agree to 1e-6 (the sums are
+    added in whatever order the workgroups arrive)."""
     b, s, p = make_matrix(O, 14336, 4096, tid=31)
     x = O.gen_f32(0, 32, 4096, 0.0, 1.0)
     ctx.set_accumulation(mode)
