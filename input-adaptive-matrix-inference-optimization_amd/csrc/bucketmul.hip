@@ -391,13 +391,13 @@ __device__ __forceinline__ T* as_global(uint64_t u)
 // that way, and used only once the input and the search are under way.
 
 
-// Loads of the selection: the 16 stats (channel stats_channel) of input
-// i0 + tid's rows and, when the slice's inputs are not computed in
-// registers, its x (from memory, or from the attention accumulators).
-// Issued before the cutoff is known so that their latency overlaps the
-// search; the raw words are kept.  Layouts: compact stats (stride 1, 2 x 16
-// bytes), the reference's [R][4] with channel 3 (8 x 16 bytes), otherwise
-// 16 scalar loads.
+// Loads of the selection: the 16 stats (channel stats_channel) of the rows
+// of the slice input the thread holds (sel_input) and, when the slice's
+// inputs are not computed in registers, its x (from memory, or from the
+// attention accumulators).  Issued before the cutoff is known so that their
+// latency overlaps the search; the raw words are kept.  Layouts: compact
+// stats (stride 1, 2 x 16 bytes), the reference's [R][4] with channel 3
+// (8 x 16 bytes), otherwise 16 scalar loads.
 struct SelLoads {
     uint4 raw[8];
     uint32_t sv[16];
@@ -418,36 +418,66 @@ struct SelSrc {
 
 enum XSrc : int { kXRegs = 0, kXMem = 1, kXAttn = 2 };
 
+// A load issued where the source puts it.  The barriers of the search
+// order LDS only, so a plain load whose value is first used after them is
+// moved down to that use, and its latency then follows the cutoff instead of
+// overlapping the search.  A relaxed atomic load is the same load
+// instruction (no cache bypass at workgroup scope), but the compiler keeps
+// it in place.
+template <typename T>
+__device__ __forceinline__ T load_early(const T* p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+__device__ __forceinline__ uint4 load_early16(const void* p)
+{
+    const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
+    const uint64_t lo = load_early(q), hi = load_early(q + 1);
+    return make_uint4((uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32));
+}
+
+// The slice input thread tid holds in the selection: waves 1.. take the
+// first ones and wave 0 the last, so that for slices of up to 64 * (NW - 1)
+// inputs the waves that leave the cutoff search early compute the rows'
+// importances while wave 0 finishes it.  Consecutive inputs stay in
+// consecutive lanes of one wave (blocks of block mode included).
+template <int NT>
+__device__ __forceinline__ int sel_input(int tid)
+{
+    return (tid + NT - 64) & (NT - 1);
+}
+
+template <int NT>
 __device__ __forceinline__ void select_load(const SelSrc& d, const WalkArgs& a, int i0, int ni, int xsrc,
                                             SelLoads& L)
 {
-    const int tid = threadIdx.x;
+    const int li = sel_input<NT>(threadIdx.x);
     L.xi = 0.0f;
     L.an = 0.0;
     L.ad = 1.0;
     L.attn = xsrc == kXAttn;
-    const int i = i0 + min(tid, ni - 1);   // threads past the slice re-read its last input
+    const int i = i0 + min(li, ni - 1);   // threads past the slice re-read its last input
     const int r0 = i * 16;
     const uint16_t* base = d.stats + (size_t)i0 * 16 * d.stride;
     const bool aligned = (((uintptr_t)base) & 15) == 0 && (d.rows & 15) == 0;
     if (xsrc == kXMem) {
-        L.xi = d.x[i];
+        L.xi = __uint_as_float(load_early(reinterpret_cast<const uint32_t*>(d.x) + i));
     } else if (xsrc == kXAttn) {
-        const double* A = reinterpret_cast<const double*>(a.attn_acc);
-        L.an = A[i];
-        L.ad = A[a.attn_lofs + (i >> 7)];
+        const uint64_t* A = reinterpret_cast<const uint64_t*>(a.attn_acc);
+        L.an = __longlong_as_double((long long)load_early(A + i));
+        L.ad = __longlong_as_double((long long)load_early(A + a.attn_lofs + (i >> 7)));
     }
     const uint16_t* st = d.stats + (size_t)r0 * d.stride;
     if (aligned && d.stride == 1) {
         L.kind = 0;
-        const uint4* p4 = reinterpret_cast<const uint4*>(st);
-        L.raw[0] = p4[0];
-        L.raw[1] = p4[1];
+        L.raw[0] = load_early16(st);
+        L.raw[1] = load_early16(st + 8);
     } else if (aligned && d.stride == 4 && d.channel == 3) {
         L.kind = 1;
-        const uint4* p4 = reinterpret_cast<const uint4*>(st);
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(st);
 #pragma unroll
-        for (int k8 = 0; k8 < 8; k8++) L.raw[k8] = p4[k8];
+        for (int k8 = 0; k8 < 8; k8++) L.raw[k8] = make_uint4(0u, load_early(p + 4 * k8 + 1), 0u, load_early(p + 4 * k8 + 3));
     } else {
         L.kind = 2;
 #pragma unroll
@@ -458,27 +488,25 @@ __device__ __forceinline__ void select_load(const SelSrc& d, const WalkArgs& a, 
     }
 }
 
-// The selection of slice p given its loads (prepareDispatch,
-// bucketMul.cl:351-386): a row is selected iff 1e5 * |x * stat| >= cutoff,
-// the same fp32 operations as the dispatch kernel, so the selected set is
-// the same.  A block scan compacts the selected rows in ascending order into
-// s_row (slice-local ids input*16 + rank); s_x[i] = x[i0 + i] (with x_lds it
-// already holds them, written before a barrier).  Ends with a barrier;
-// returns the number of selected rows.
+// The importances of the 16 rows of the thread's input, 1e5 * |x * stat|
+// in the fp32 operations of prepareDispatch (bucketMul.cl:351-386), and the
+// bits of its rows inside the expert (none for threads past the slice).
+// They need only the loads and x (s_x, published by an earlier barrier, when
+// x_lds), so they are computed before the cutoff is known.  Without x_lds
+// the thread's x goes to s_x[input] (0 past the slice) for the walk; a
+// barrier follows before it is read.
 template <int NT>
-__device__ __forceinline__ uint32_t select_finish(const SelSrc& d, float cutoff, int i0, int ni, const SelLoads& L,
-                                                  uint16_t* s_row, float* s_x, uint32_t* s_wsum, bool x_lds,
-                                                  int blk)
+__device__ __forceinline__ void select_prepare(const SelSrc& d, int i0, int ni, const SelLoads& L, float* s_x,
+                                               bool x_lds, float (&imp)[16], uint32_t& vbits)
 {
 #pragma clang fp contract(off)
-    constexpr int NW = NT / 64;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int li = sel_input<NT>(threadIdx.x);
     float xi = L.xi;
-    uint32_t mask = 0;
-    if (tid < ni) {
-        if (x_lds) xi = s_x[tid];
+    vbits = 0u;
+#pragma unroll
+    for (int kk = 0; kk < 16; kk++) imp[kk] = 0.0f;
+    if (li < ni) {
+        if (x_lds) xi = s_x[li];
         else if (L.attn) xi = (float)(L.an / L.ad);
         uint32_t sv[16];
         if (L.kind == 0) {
@@ -496,35 +524,56 @@ __device__ __forceinline__ uint32_t select_finish(const SelSrc& d, float cutoff,
 #pragma unroll
             for (int kk = 0; kk < 16; kk++) sv[kk] = L.sv[kk];
         }
-        const int r0 = (i0 + tid) * 16;
 #pragma unroll
         for (int kk = 0; kk < 16; kk++) {
             const float prod = __fmul_rn(xi, h2f(sv[kk]));
-            const float imp = __fmul_rn(kScale, fabsf(prod));
-            if (imp >= cutoff && r0 + kk < d.rows) mask |= 1u << kk;   // bucketMul.cl:380
+            imp[kk] = __fmul_rn(kScale, fabsf(prod));
         }
+        const int left = d.rows - (i0 + li) * 16;   // rows of this input inside the expert (>= 1)
+        vbits = left >= 16 ? 0xffffu : (1u << left) - 1u;
     }
-    if (blk > 1) {
-        mask = block_select(mask, blk, tid < ni);
-        const int left = d.rows - (i0 + tid) * 16;          // rows of this input inside the expert
-        if (left < 16) mask &= left > 0 ? (1u << left) - 1u : 0u;
-    }
+    if (!x_lds) s_x[li] = li < ni ? xi : 0.0f;
+}
+
+// The selection of slice p (prepareDispatch, bucketMul.cl:351-386): a row is
+// selected iff its importance >= cutoff (NaN never is), so the selected set
+// is the dispatch kernel's.  Block mode (blk > 1): rank k of every input of
+// a block is selected when rank k of any of them passes (block_select), rows
+// outside the expert excepted.  A scan over the waves in input order (waves
+// 1.., then 0) compacts the selected rows in ascending order into s_row
+// (slice-local ids input*16 + rank).  Ends with a barrier; returns the
+// number of selected rows.
+template <int NT>
+__device__ __forceinline__ uint32_t select_finish(float cutoff, const float (&imp)[16], uint32_t vbits,
+                                                  uint16_t* s_row, uint32_t* s_wsum, int blk)
+{
+    constexpr int NW = NT / 64;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int li = sel_input<NT>(tid);
+    uint32_t mask = 0;
+#pragma unroll
+    for (int kk = 0; kk < 16; kk++)
+        if (imp[kk] >= cutoff) mask |= 1u << kk;   // bucketMul.cl:380
+    mask &= vbits;
+    if (blk > 1) mask = block_select(mask, blk, vbits != 0u) & vbits;
     const uint32_t cnt = (uint32_t)__popc(mask);
     const uint32_t incl = (uint32_t)wave_incl_sum((int)cnt);
     if (lane == 63) s_wsum[wave] = incl;
-    if (!x_lds) s_x[tid] = tid < ni ? xi : 0.0f;
     __syncthreads();
     uint32_t off = incl - cnt;
     uint32_t n_sel = 0;
 #pragma unroll
-    for (int i = 0; i < NW; i++) {
-        if (i < wave) off += s_wsum[i];
-        n_sel += s_wsum[i];
+    for (int w = 0; w < NW; w++) {
+        const uint32_t c = s_wsum[w];
+        if (w >= 1 && (w < wave || wave == 0)) off += c;   // waves before this one in input order
+        n_sel += c;
     }
     while (mask) {
         const int kk = __ffs(mask) - 1;
         mask &= mask - 1;
-        s_row[off++] = (uint16_t)(tid * 16 + kk);
+        s_row[off++] = (uint16_t)(li * 16 + kk);
     }
     __syncthreads();
     return n_sel;
@@ -603,6 +652,12 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     uint64_t u_h = (uint64_t)a.h, u_res = (uint64_t)a.res_acc, u_gain = (uint64_t)a.gain, u_attn = (uint64_t)a.attn_acc;
     asm volatile("" : "+s"(nb), "+s"(mode), "+s"(attn_lofs), "+s"(u_pr), "+s"(u_x), "+s"(u_h), "+s"(u_res), "+s"(u_gain),
                  "+s"(u_attn));
+    // Fields read only later (the selection mode, the walk's rows, the
+    // flush's accumulators, the zeroing and counting pointers) are touched
+    // in the same batch: every 64-byte line of the block's descriptor and of
+    // the trailing arguments is then in the scalar cache, and their later
+    // reads do not each wait for a round trip to argument memory.
+    asm volatile("" ::"s"(a.d[k].W), "s"(a.d[k].acc), "s"(a.final_zero), "s"(a.counters), "s"(a.sel_block));
     if ((int)blockIdx.x >= nb) {
         // the grid's x covers the largest matrix: a block past this matrix's
         // count only clears its share of the earlier launches' accumulators
@@ -673,7 +728,7 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     const bool slice_regs = regs && i0 + ni <= kProbes;  // x of the slice among the computed ones
     const bool first = w == 0 && k == 0;
     SelLoads L;
-    select_load(ss, a, i0, ni, slice_regs ? kXRegs : (mode == kInAttn ? kXAttn : kXMem), L);
+    select_load<NT>(ss, a, i0, ni, slice_regs ? kXRegs : (mode == kInAttn ? kXAttn : kXMem), L);
 
     // ---- the input
     if (mode != kInCutoff) {
@@ -703,18 +758,24 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
         }
     }
 
-    // ---- cutoff
+    // ---- cutoff, and the importances of the slice's rows (the waves that
+    // leave the search early compute theirs while wave 0 finishes it)
+    float imp[16];
+    uint32_t vbits;
     if (mode != kInCutoff) {
         float v[VPT];
         importances<VPT>(xs, pw, v);
         search_cutoff<NW>(v, quantile, SL);
+        select_prepare<NT>(ss, i0, ni, L, s_x, slice_regs, imp, vbits);
         __syncthreads();   // wave 0 has stored the cutoff; the search scratch becomes the row list
         cutoff = SL.cut;
         if (w == 0 && tid == 0) d.cutoff[0] = cutoff;
+    } else {
+        select_prepare<NT>(ss, i0, ni, L, s_x, slice_regs, imp, vbits);
     }
 
     // ---- selection of the slice's rows
-    const int ns = (int)select_finish<NT>(ss, cutoff, i0, ni, L, s_row, s_x, s_wsum, slice_regs, a.sel_block);
+    const int ns = (int)select_finish<NT>(cutoff, imp, vbits, s_row, s_wsum, a.sel_block);
     if (t == 0 && tid == 0) {
         d.slice_count[p] = (uint32_t)ns;
         if (a.counters) {
