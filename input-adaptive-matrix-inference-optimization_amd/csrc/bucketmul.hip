@@ -315,9 +315,11 @@ __device__ __forceinline__ void lds_add(uint32_t byte_offset, int elem, T v)
     __hip_atomic_fetch_add((lds_ptr<T>)(uintptr_t)byte_offset + elem, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-constexpr int kTileCols = 128;
-constexpr int kTileOut = kTileCols * 16;     // outputs per column tile
-constexpr int kTilePitch = kTileCols;        // LDS slots per position row
+// column tiles of the walk: 128 columns (256-byte row segments) or 64
+// (half the flush's atomic adds per workgroup, for launches whose walk is
+// short next to their flush)
+constexpr int kTileColsWide = 128;
+constexpr int kTileColsNarrow = 64;
 
 struct WalkDesc {
     const uint16_t* W;        // rows of the expert: W[row * C + col]
@@ -589,37 +591,45 @@ __device__ __forceinline__ void take_max(float& bv, int& bi, float v, int i)
 }
 
 // Selection + walk + flush.  Workgroup (input slice p, column tile t) owns
-// the inputs [p*IPS, (p+1)*IPS) and the 128 columns [128t, 128t + 128).
+// the inputs [p*IPS, (p+1)*IPS) and the TC columns [TC*t, TC*t + TC)
+// (TC = 128 or 64).
 //
-// Walk: lane = q*16 + j reads 16 bytes (columns 8j..8j+7) of row q of a
-// group of 4 selected rows, so one load instruction fetches the 256-byte tile
-// segments of 4 rows (narrower segments cost HBM efficiency on these
-// scattered rows).  Wave w takes the groups w, w + NW, w + 2NW, ...  Each
-// packed weight is added, as the product x * w in the accumulator type (exact
-// in fp64), to the wave's own accumulator of its output (column c, position
-// bits & 15) with a non-returning LDS atomic add (bucketMul.cl:430-445 adds
-// the product with a plain += per work-item).  The accumulator of (column
-// 8j+e, position pos) is slot pos*128 + e*16 + j: whatever the positions of
+// Walk: lane = q*LPR + j (LPR = TC/8 lanes per row) reads 16 bytes (columns
+// 8j..8j+7) of row q of a group of RPI = 64/LPR selected rows, so one load
+// instruction fetches the 2*TC-byte tile segments of RPI rows.  Wave w takes
+// the groups w, w + NW, w + 2NW, ...  Each packed weight is added, as the
+// product x * w in the accumulator type (exact in fp64), to the wave's own
+// accumulator of its output (column c, position bits & 15) with a
+// non-returning LDS atomic add (bucketMul.cl:430-445 adds the product with a
+// plain += per work-item).  The accumulator of (column 8j+e, position pos)
+// is slot pos*TC + e*LPR + j of the wave's tile copy q % NCOPY (NCOPY =
+// 128/TC copies, 64 bytes apart in bank terms): whatever the positions of
 // the 64 lanes' weights (each weight carries its own), an instruction's
-// lanes j of the 4 rows map to 16 bank pairs set by j alone, so the walk's
-// LDS atomics never conflict beyond the 4 rows sharing a bank pair (the
-// fewest passes 64 8-byte accumulators need).  Two batches of rows are in
-// flight per wave.  Rows past the end of the list re-read the last selected
-// row with x = 0, so every load of a batch is unconditional.
+// lanes map to bank pairs set by j and the copy alone, so the walk's LDS
+// atomics never conflict beyond the 4 rows sharing a bank pair (the fewest
+// passes 64 8-byte accumulators need).  Two batches of rows are in flight
+// per wave.  Rows past the end of the list re-read the last selected row
+// with x = 0, so every load of a batch is unconditional.
 //
-// Flush: sums of the wave tiles in wave order, staged in output order
-// (column-major, col*16 + pos, the reference's output index,
+// Flush: sums of the wave tiles (waves, then copies, in order), staged in
+// output order (column-major, col*16 + pos, the reference's output index,
 // bucketMul.cl:442-445), one atomic add per output and workgroup.
-template <typename Acc, int NW, int UNR>
+template <typename Acc, int NW, int UNR, int TC>
 __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
 {
 #pragma clang fp contract(off)
     constexpr int NT = 64 * NW;
-    constexpr int TSLOTS = 16 * kTilePitch;                 // one wave's tile
+    static_assert(TC == 64 || TC == 128, "64- or 128-column tiles");
+    constexpr int TOUT = TC * 16;                           // outputs of a column tile
+    constexpr int LPR = TC / 8;                             // lanes per row
+    constexpr int RPI = 64 / LPR;                           // rows per wave load
+    constexpr int NCOPY = 128 / TC;                         // tile copies per wave
+    constexpr int CSLOTS = 16 * TC + (NCOPY > 1 ? 8 : 0);   // one copy (+64 bytes: the next one's banks)
+    constexpr int TSLOTS = NCOPY * CSLOTS;                  // one wave's tiles
     constexpr int GSTRIDE = NW * UNR;                       // groups per workgroup batch
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     constexpr int VPT = IAM_PROBES_COUNT / NT;              // inputs of the cutoff per thread
-    static_assert(kTileOut % NT == 0, "flush mapping");
+    static_assert(TOUT % NT == 0, "flush mapping");
     // the wave tiles hold fp64 sums in both modes: Acc is the precision of
     // the products (fp32 mode: the reference's fp32 products), and LDS fp64
     // atomic adds run many times faster than fp32 ones on this part
@@ -714,8 +724,10 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     {
         uint4* tz = reinterpret_cast<uint4*>(tiles + wave * TSLOTS);
         constexpr int kTileVecs = TSLOTS * (int)sizeof(Tile) / 16;
+        static_assert(TSLOTS * sizeof(Tile) % 16 == 0, "whole 16-byte stores");
 #pragma unroll
-        for (int i = 0; i < kTileVecs / 64; i++) tz[i * 64 + lane] = make_uint4(0u, 0u, 0u, 0u);
+        for (int i = 0; i < (kTileVecs + 63) / 64; i++)
+            if (i * 64 + lane < kTileVecs) tz[i * 64 + lane] = make_uint4(0u, 0u, 0u, 0u);
     }
     // the block's slice and column tile (from the descriptor read through k)
     const int w = b;
@@ -787,9 +799,9 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     }
 
     // ---- walk of the selected rows
-    const int j = lane & 15;
-    const int q = lane >> 4;
-    const int col0 = t * kTileCols + j * 8;
+    const int j = lane % LPR;
+    const int q = lane / LPR;
+    const int col0 = t * TC + j * 8;
     if (col0 < d.C) {
         // C % 8 == 0: one 16-byte load per row; otherwise (rows only 2-byte
         // aligned, a lane's last columns may lie past C) eight 2-byte loads,
@@ -797,19 +809,20 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
         const bool whole = (d.C & 7) == 0;
         const int nc = min(8, d.C - col0);
         const uint16_t* wb = d.W + (size_t)i0 * 16 * d.C + col0;
-        const uint32_t tbase = lds_offset(tiles) + (uint32_t)(wave * TSLOTS + j) * (uint32_t)sizeof(Tile);
-        const int ng = (ns + 3) >> 2;
+        const uint32_t tbase =
+            lds_offset(tiles) + (uint32_t)(wave * TSLOTS + (q % NCOPY) * CSLOTS + j) * (uint32_t)sizeof(Tile);
+        const int ng = (ns + RPI - 1) / RPI;
         // one instance of the loop per row load shape, so that no branch sits
         // in its steady state
         auto walk_rows = [&](auto whole_tag) {
         constexpr bool WHOLE = decltype(whole_tag)::value;
-        // batch g0: rows (g0 + u*NW)*4 + q, u < UNR, into one register set
+        // batch g0: rows (g0 + u*NW)*RPI + q, u < UNR, into one register set
         auto issue = [&](int g0, uint4 (&v)[UNR], Acc (&xc)[UNR]) {
             int rl[UNR];
             float xl[UNR];
 #pragma unroll
             for (int u = 0; u < UNR; u++) {
-                const int idx = (g0 + u * NW) * 4 + q;
+                const int idx = (g0 + u * NW) * RPI + q;
                 rl[u] = s_row[min(idx, ns - 1)];
                 xl[u] = idx < ns ? 1.0f : 0.0f;
             }
@@ -840,7 +853,7 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
                     // multiply-add into the slot address
                     uint32_t pos;
                     asm("v_bfe_u32 %0, %1, %2, 4" : "=v"(pos) : "v"(words[e >> 1]), "i"((e & 1) * 16));
-                    lds_add<Tile>(__umul24(pos, kTilePitch * (uint32_t)sizeof(Tile)) + tbase, e * 16,
+                    lds_add<Tile>(__umul24(pos, TC * (uint32_t)sizeof(Tile)) + tbase, e * LPR,
                                   (Tile)(xc[u] * (Acc)h2f(hw)));
                 }
             }
@@ -886,10 +899,10 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     // entries keeps the staging writes and the reads after them free of
     // conflicts too), then one atomic add per output and workgroup over
     // consecutive outputs.
-    constexpr int OPT = kTileOut / NT;
-    static_assert(NW * TSLOTS >= kTileOut + kTileOut / 128, "the staging copy fits the tiles");
-    double* out = reinterpret_cast<double*>(d.acc) + (size_t)t * kTileOut;
-    const int nout = min(kTileOut, (d.C - t * kTileCols) * 16);
+    constexpr int OPT = TOUT / NT;
+    static_assert(NW * TSLOTS >= TOUT + TOUT / 128, "the staging copy fits the tiles");
+    double* out = reinterpret_cast<double*>(d.acc) + (size_t)t * TOUT;
+    const int nout = min(TOUT, (d.C - t * TC) * 16);
     {
         Tile sum[OPT];
 #pragma unroll
@@ -897,14 +910,18 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
             const int sl = tid + k2 * NT;
             Tile sv = tiles[sl];
 #pragma unroll
-            for (int ww = 1; ww < NW; ww++) sv += tiles[ww * TSLOTS + sl];
+            for (int cc = 1; cc < NCOPY; cc++) sv += tiles[cc * CSLOTS + sl];
+#pragma unroll
+            for (int ww = 1; ww < NW; ww++)
+#pragma unroll
+                for (int cc = 0; cc < NCOPY; cc++) sv += tiles[ww * TSLOTS + cc * CSLOTS + sl];
             sum[k2] = sv;
         }
         __syncthreads();
 #pragma unroll
         for (int k2 = 0; k2 < OPT; k2++) {
             const int sl = tid + k2 * NT;
-            const int pos = sl >> 7, e = (sl >> 4) & 7, jj = sl & 15;   // slot pos*128 + e*16 + j
+            const int pos = sl / TC, e = (sl / LPR) & 7, jj = sl % LPR;   // slot pos*TC + e*LPR + j
             const int o = (jj * 8 + e) * 16 + pos;
             tiles[o + (o >> 7)] = sum[k2];
         }
@@ -942,11 +959,11 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     if (!s_last) return;
     if (tid == 0) d.tile_ctr[t] = 0u;
     if (a.fin == kFinSilu) {
-        double* g_acc = reinterpret_cast<double*>(a.d[0].acc) + (size_t)t * kTileOut;
-        double* u_acc = reinterpret_cast<double*>(a.d[1].acc) + (size_t)t * kTileOut;
+        double* g_acc = reinterpret_cast<double*>(a.d[0].acc) + (size_t)t * TOUT;
+        double* u_acc = reinterpret_cast<double*>(a.d[1].acc) + (size_t)t * TOUT;
         for (int o = tid; o < nout; o += NT) {
             const float gv = (float)acc_take(g_acc + o), uv = (float)acc_take(u_acc + o);
-            const size_t oo = (size_t)t * kTileOut + o;
+            const size_t oo = (size_t)t * TOUT + o;
             if (a.d[0].y) a.d[0].y[oo] = gv;
             if (a.d[1].y) a.d[1].y[oo] = uv;
             const double x1 = (double)gv;
@@ -959,7 +976,7 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     int bi = 0x7fffffff;
     for (int o = tid; o < nout; o += NT) {
         const float yv = (float)acc_take(out + o);
-        const int oo = t * kTileOut + o;
+        const int oo = t * TOUT + o;
         d.y[oo] = yv;
         take_max(bv, bi, yv, oo);
     }
@@ -1044,16 +1061,16 @@ constexpr int kWalkWaves = 8;
 
 int sel_block_for(const Ctx* c, float effort) { return c->sel_block > 1 && effort < c->sel_below ? c->sel_block : 1; }
 
-void plan_walk(int n, const MatOp* ops, float effort, WalkPlan* plan, int blk)
+void plan_walk(int n, const MatOp* ops, float effort, WalkPlan* plan, int blk, int tc)
 {
     double bytes[kMaxMulti], tot = 0;
     for (int i = 0; i < n; i++) {
         const iam_bucket_matrix& M = ops[i].mat;
         WalkPlan& pl = plan[i];
-        pl.T = (M.bucket_cols + kTileCols - 1) / kTileCols;
+        pl.T = (M.bucket_cols + tc - 1) / tc;
         pl.n_in = std::min((M.expert_rows + 15) / 16, ops[i].in_size);
         // the cost of a row is its tiles' width
-        bytes[i] = est_rows(pl.n_in * 16, effort) * pl.T * kTileCols * 2.0;
+        bytes[i] = est_rows(pl.n_in * 16, effort) * pl.T * tc * 2.0;
         tot += bytes[i];
     }
     for (int i = 0; i < n; i++) {
@@ -1067,7 +1084,7 @@ void plan_walk(int n, const MatOp* ops, float effort, WalkPlan* plan, int blk)
     }
 }
 
-int walk_tiles(int bucket_cols) { return (bucket_cols + kTileCols - 1) / kTileCols; }
+int walk_tiles(int bucket_cols) { return (bucket_cols + kTileColsNarrow - 1) / kTileColsNarrow; }
 
 int max_slices(int n, const MatOp* ops, float effort)
 {
@@ -1161,17 +1178,35 @@ static int bucketmul_list(Ctx* c, int i)
     return launch(c, "bucket_list", k_dispatch, dim3(G), dim3(kCutThreads), 0, d);
 }
 
-template <typename Acc>
+template <typename Acc, int TC>
 static int launch_walk(Ctx* c, const char* name, bool plain, dim3 grid, const WalkArgs& args)
 {
+    auto kern = k_walk<Acc, kWalkWaves, IAM_WALK_UNR, TC>;
     if (plain) {
-        auto kern = k_walk<Acc, kWalkWaves, IAM_WALK_UNR>;
         hipLaunchKernelGGL(kern, grid, dim3(64 * kWalkWaves), 0, c->stream, args);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return fail(IAM_E_HIP, std::string("launch ") + name + ": " + hipGetErrorString(e));
         return IAM_OK;
     }
-    return launch(c, name, k_walk<Acc, kWalkWaves, IAM_WALK_UNR>, grid, dim3(64 * kWalkWaves), 0, args);
+    return launch(c, name, kern, grid, dim3(64 * kWalkWaves), 0, args);
+}
+
+// The column tile width of a launch.  Narrow tiles halve the flush's atomic
+// adds per workgroup (4 per thread on 128-column tiles back up the memory
+// pipeline; 2 do not) for a slightly slower walk (twice the rows per
+// load, 128-byte segments), so every launch whose matrices share one shape
+// uses them.  A launch of matrices of different
+// widths (q with k and v) keeps 128 columns: its grid spans the largest
+// matrix, the smaller ones' idle blocks then outnumber the CUs, and on the
+// narrow plan some real blocks would queue behind whole walks.
+int walk_tile_cols(const WalkGroup& g)
+{
+    if (g.tile_cols == kTileColsNarrow || g.tile_cols == kTileColsWide) return g.tile_cols;
+    for (int i = 1; i < g.n; i++)
+        if (g.m[i].mat.bucket_cols != g.m[0].mat.bucket_cols || g.m[i].mat.expert_rows != g.m[0].mat.expert_rows ||
+            g.m[i].in_size != g.m[0].in_size)
+            return kTileColsWide;
+    return kTileColsNarrow;
 }
 
 int walk_group(Ctx* c, const WalkGroup& g)
@@ -1194,8 +1229,9 @@ int walk_group(Ctx* c, const WalkGroup& g)
         ops[i].y = wm.y;
     }
     const int blk = sel_block_for(c, g.effort);
+    const int tc = walk_tile_cols(g);
     WalkPlan plan[kMaxMulti];
-    plan_walk(g.n, ops, g.effort, plan, blk);
+    plan_walk(g.n, ops, g.effort, plan, blk, tc);
     WalkArgs args{};
     args.sel_block = blk;
     args.n = g.n;
@@ -1270,8 +1306,11 @@ int walk_group(Ctx* c, const WalkGroup& g)
     static const char* const names[kWalkLabels] = {"bucket_walk", "bucket_walk.qkv", "bucket_walk.o",
                                                     "bucket_walk.ffn13", "bucket_walk.ffn2", "bucket_walk.lm"};
     const char* name = names[g.label];
-    return c->acc64 ? launch_walk<double>(c, name, g.plain, grid, args)
-                    : launch_walk<float>(c, name, g.plain, grid, args);
+    if (tc == kTileColsNarrow)
+        return c->acc64 ? launch_walk<double, kTileColsNarrow>(c, name, g.plain, grid, args)
+                        : launch_walk<float, kTileColsNarrow>(c, name, g.plain, grid, args);
+    return c->acc64 ? launch_walk<double, kTileColsWide>(c, name, g.plain, grid, args)
+                    : launch_walk<float, kTileColsWide>(c, name, g.plain, grid, args);
 }
 
 // The standalone walk of the n matrices recorded in slots 0..n-1: the
@@ -1309,7 +1348,7 @@ static int walk_slots(Ctx* c, int n, const MatOp* ops, int in_mode, const float*
         IAM_REQUIRE(s.effort == c->slots[0].effort && s.expert_no == c->slots[0].expert_no,
                     "bucketmul: slots dispatched at different efforts or experts");
         const size_t m = (size_t)M.bucket_cols * 16;
-        IAM_TRY(ensure_walk_scratch(c, i, m, (m + kTileOut - 1) / kTileOut, (size_t)P));
+        IAM_TRY(ensure_walk_scratch(c, i, m, walk_tiles((m + 15) / 16), (size_t)P));
         WalkMat& wm = g.m[i];
         wm.mat = M;
         wm.mat.stats = s.stats - (size_t)s.expert_no * (size_t)M.expert_rows * s.stats_stride;

@@ -210,7 +210,9 @@ struct WalkPlan {
     int P;      // slices
 };
 // blk: inputs per selection block (slices start at its multiples)
-void plan_walk(int n, const MatOp* ops, float effort, WalkPlan* plan, int blk = 1);
+// blk: inputs per selection block; tc: columns per tile (128 gives the
+// most slices, the bound the scratch is sized for)
+void plan_walk(int n, const MatOp* ops, float effort, WalkPlan* plan, int blk = 1, int tc = 128);
 // the selection block size of a walk at this effort
 int sel_block_for(const Ctx* c, float effort);
 
@@ -235,6 +237,8 @@ struct WalkGroup {
     int label = 0;
     // launch without the profiling events (the no-allocation entry point)
     bool plain = false;
+    // columns per tile (64 or 128; 0: the group's default)
+    int tile_cols = 0;
     int n = 0;
     WalkMat m[kMaxMulti];
     int in_mode = kInX;
@@ -269,6 +273,8 @@ struct WalkGroup {
 // one walk launch of the group (plan from the matrices and effort)
 int walk_group(Ctx* c, const WalkGroup& g);
 // column tiles of a matrix in a walk launch
+// column tiles of a matrix at the narrowest tile width (the most any launch
+// uses: the size of per-tile counters and candidates)
 int walk_tiles(int bucket_cols);
 // the largest slice count any plan gives a group of these matrices
 int max_slices(int n, const MatOp* ops, float effort);
