@@ -346,6 +346,7 @@ struct WalkDesc {
 
 struct WalkArgs {
     WalkDesc d[kMaxMulti];
+    int first[kMaxMulti];     // the first work item of each matrix (the grid's total past the last matrix)
     int n;
     int in_mode;
     const float* h;
@@ -651,37 +652,39 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     const int lane = tid & 63;
     const int wave = tid >> 6;
 
-    // The block's matrix is blockIdx.y, so the reads of its descriptor (at an
-    // offset known when the wave starts) and of the input mode's arguments
-    // go out as one batch of scalar loads; the ones the first vector loads
-    // need are pinned there (a later first use would cost another round trip
-    // to the arguments, which the weight stream keeps out of the caches).
-    const int k = (int)blockIdx.y;
-    int nb = a.d[k].nblocks, mode = a.in_mode, attn_lofs = a.attn_lofs;
-    uint64_t u_pr = (uint64_t)a.d[k].probes, u_x = (uint64_t)a.d[k].x;
+    // The grid holds exactly the launch's blocks (no idle ones to take CU
+    // slots from real ones): block ids are remapped so that consecutive work
+    // items sit on one XCD, and the work items are dealt to the matrices in
+    // ranges starting at first[k].  The reads the first vector loads need --
+    // the range starts, every matrix's probes and x, the input mode's
+    // arguments -- go out as one batch of scalar loads and are pinned there
+    // (a later first use would cost another round trip to the arguments,
+    // which the weight stream keeps out of the caches); the block's matrix
+    // then picks among them.
+    int nblk = (int)gridDim.x, f1 = a.first[1], f2 = a.first[2], mode = a.in_mode, attn_lofs = a.attn_lofs;
+    uint64_t pr0 = (uint64_t)a.d[0].probes, pr1 = (uint64_t)a.d[1].probes, pr2 = (uint64_t)a.d[2].probes;
+    uint64_t x0 = (uint64_t)a.d[0].x, x1 = (uint64_t)a.d[1].x, x2 = (uint64_t)a.d[2].x;
     uint64_t u_h = (uint64_t)a.h, u_res = (uint64_t)a.res_acc, u_gain = (uint64_t)a.gain, u_attn = (uint64_t)a.attn_acc;
-    asm volatile("" : "+s"(nb), "+s"(mode), "+s"(attn_lofs), "+s"(u_pr), "+s"(u_x), "+s"(u_h), "+s"(u_res), "+s"(u_gain),
-                 "+s"(u_attn));
     // Fields read only later (the selection mode, the walk's rows, the
     // flush's accumulators, the zeroing and counting pointers) are touched
-    // in the same batch: every 64-byte line of the block's descriptor and of
-    // the trailing arguments is then in the scalar cache, and their later
-    // reads do not each wait for a round trip to argument memory.
-    asm volatile("" ::"s"(a.d[k].W), "s"(a.d[k].acc), "s"(a.final_zero), "s"(a.counters), "s"(a.sel_block));
-    if ((int)blockIdx.x >= nb) {
-        // the grid's x covers the largest matrix: a block past this matrix's
-        // count only clears its share of the earlier launches' accumulators
-        zero_share<double>(a.zero_p[0], a.zero_n[0], NT);
-        zero_share<double>(a.zero_p[1], a.zero_n[1], NT);
-        return;
-    }
+    // in the same batch: every 64-byte line of the descriptors and of the
+    // trailing arguments is then in the scalar cache, and their later reads
+    // do not each wait for a round trip to argument memory.
+    asm volatile(""
+                 : "+s"(nblk), "+s"(f1), "+s"(f2), "+s"(mode), "+s"(attn_lofs), "+s"(pr0), "+s"(pr1), "+s"(pr2), "+s"(x0), "+s"(x1),
+                   "+s"(x2), "+s"(u_h), "+s"(u_res), "+s"(u_gain), "+s"(u_attn)
+                 : "s"(a.d[0].W), "s"(a.d[0].acc), "s"(a.d[1].W), "s"(a.d[1].acc), "s"(a.d[2].W), "s"(a.d[2].acc),
+                   "s"(a.d[2].expected), "s"(a.final_zero), "s"(a.counters), "s"(a.sel_block));
+    const int wi = xcd_remap((int)blockIdx.x, nblk);
+    const int k = wi >= f2 ? 2 : wi >= f1 ? 1 : 0;
+    const int b = wi - (k == 2 ? f2 : k == 1 ? f1 : 0);
+    const uint64_t u_pr = k == 2 ? pr2 : k == 1 ? pr1 : pr0, u_x = k == 2 ? x2 : k == 1 ? x1 : x0;
     const uint16_t* probes = as_global<const uint16_t>(u_pr);
     float* dx = as_global<float>(u_x);
     const float* a_h = as_global<const float>(u_h);
     const void* a_res = as_global<const double>(u_res);
     const uint16_t* a_gain = as_global<const uint16_t>(u_gain);
     const void* a_attn = as_global<const double>(u_attn);
-    const int b = xcd_remap((int)blockIdx.x, nb);
     const WalkDesc& d = a.d[k];
     const bool norm = mode == kInNorm || mode == kInResNorm || mode == kInEmbedNorm;
     const bool regs = norm || mode == kInAttn;           // x[0:4096] computed in registers
@@ -1191,22 +1194,18 @@ static int launch_walk(Ctx* c, const char* name, bool plain, dim3 grid, const Wa
     return launch(c, name, kern, grid, dim3(64 * kWalkWaves), 0, args);
 }
 
+#ifndef IAM_WALK_TILE_COLS
+#define IAM_WALK_TILE_COLS 64
+#endif
+
 // The column tile width of a launch.  Narrow tiles halve the flush's atomic
 // adds per workgroup (4 per thread on 128-column tiles back up the memory
-// pipeline; 2 do not) for a slightly slower walk (twice the rows per
-// load, 128-byte segments), so every launch whose matrices share one shape
-// uses them.  A launch of matrices of different
-// widths (q with k and v) keeps 128 columns: its grid spans the largest
-// matrix, the smaller ones' idle blocks then outnumber the CUs, and on the
-// narrow plan some real blocks would queue behind whole walks.
+// pipeline; 2 do not) for a slightly slower walk (twice the rows per load,
+// 128-byte segments).
 int walk_tile_cols(const WalkGroup& g)
 {
     if (g.tile_cols == kTileColsNarrow || g.tile_cols == kTileColsWide) return g.tile_cols;
-    for (int i = 1; i < g.n; i++)
-        if (g.m[i].mat.bucket_cols != g.m[0].mat.bucket_cols || g.m[i].mat.expert_rows != g.m[0].mat.expert_rows ||
-            g.m[i].in_size != g.m[0].in_size)
-            return kTileColsWide;
-    return kTileColsNarrow;
+    return IAM_WALK_TILE_COLS == kTileColsWide ? kTileColsWide : kTileColsNarrow;
 }
 
 int walk_group(Ctx* c, const WalkGroup& g)
@@ -1261,11 +1260,12 @@ int walk_group(Ctx* c, const WalkGroup& g)
         d.nblocks = plan[i].P * plan[i].T;
         d.expected = plan[i].P;
     }
-    // grid: x over the largest matrix (a multiple of 8, so that block x of
-    // every matrix sits on XCD x % 8), y over the matrices
-    int gx = 0;
-    for (int i = 0; i < g.n; i++) gx = std::max(gx, args.d[i].nblocks);
-    gx = (gx + 7) & ~7;
+    // grid: every matrix's blocks, the matrices' work items in consecutive ranges
+    int total = 0;
+    for (int i = 0; i < kMaxMulti; i++) {
+        args.first[i] = total;
+        if (i < g.n) total += args.d[i].nblocks;
+    }
     if (g.fin == kFinSilu) {
         IAM_REQUIRE(g.n == 2 && g.m[0].mat.bucket_cols == g.m[1].mat.bucket_cols && g.silu_out,
                     "walk: the SiLU gate pairs two matrices of one shape");
@@ -1302,7 +1302,7 @@ int walk_group(Ctx* c, const WalkGroup& g)
     // walk_count reads the slice counts of the slots this launch wrote
     for (int i = 0; i < g.n; i++)
         if (g.m[i].slice_count == c->slots[i].slice_count) c->slots[i].walked_P = plan[i].P;
-    const dim3 grid((unsigned)gx, (unsigned)g.n);
+    const dim3 grid((unsigned)total);
     static const char* const names[kWalkLabels] = {"bucket_walk", "bucket_walk.qkv", "bucket_walk.o",
                                                     "bucket_walk.ffn13", "bucket_walk.ffn2", "bucket_walk.lm"};
     const char* name = names[g.label];
