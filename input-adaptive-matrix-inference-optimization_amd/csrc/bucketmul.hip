@@ -599,12 +599,14 @@ __device__ __forceinline__ void take_max(float& bv, int& bi, float v, int i)
 // 8j..8j+7) of row q of a group of RPI = 64/LPR selected rows, so one load
 // instruction fetches the 2*TC-byte tile segments of RPI rows.  Wave w takes
 // the groups w, w + NW, w + 2NW, ...  Each packed weight is added, as the
-// product x * w in the accumulator type (exact in fp64), to the wave's own
+// product x * w in the accumulator type (exact in fp64), to the workgroup's
 // accumulator of its output (column c, position bits & 15) with a
 // non-returning LDS atomic add (bucketMul.cl:430-445 adds the product with a
-// plain += per work-item).  The accumulator of (column 8j+e, position pos)
-// is slot pos*TC + e*LPR + j of the wave's tile copy q % NCOPY (NCOPY =
-// 128/TC copies, 64 bytes apart in bank terms): whatever the positions of
+// plain += per work-item); the waves share the tile (LDS atomics of
+// different waves on one address cost no more than on different ones).  The
+// accumulator of (column 8j+e, position pos) is slot pos*TC + e*LPR + j of
+// tile copy q % NCOPY (NCOPY = 128/TC copies, 64 bytes apart in bank
+// terms): whatever the positions of
 // the 64 lanes' weights (each weight carries its own), an instruction's
 // lanes map to bank pairs set by j and the copy alone, so the walk's LDS
 // atomics never conflict beyond the 4 rows sharing a bank pair (the fewest
@@ -612,8 +614,7 @@ __device__ __forceinline__ void take_max(float& bv, int& bi, float v, int i)
 // per wave.  Rows past the end of the list re-read the last selected row
 // with x = 0, so every load of a batch is unconditional.
 //
-// Flush: sums of the wave tiles (waves, then copies, in order), staged in
-// output order (column-major, col*16 + pos, the reference's output index,
+// Flush: sums of the tile copies, staged in output order (column-major, col*16 + pos, the reference's output index,
 // bucketMul.cl:442-445), one atomic add per output and workgroup.
 template <typename Acc, int NW, int UNR, int TC>
 __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
@@ -624,18 +625,19 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     constexpr int TOUT = TC * 16;                           // outputs of a column tile
     constexpr int LPR = TC / 8;                             // lanes per row
     constexpr int RPI = 64 / LPR;                           // rows per wave load
-    constexpr int NCOPY = 128 / TC;                         // tile copies per wave
+    constexpr int NCOPY = 128 / TC;                         // tile copies (rows alternate)
     constexpr int CSLOTS = 16 * TC + (NCOPY > 1 ? 8 : 0);   // one copy (+64 bytes: the next one's banks)
-    constexpr int TSLOTS = NCOPY * CSLOTS;                  // one wave's tiles
+    constexpr int STAGE = TOUT + TOUT / 128;                // the flush's staging copy
+    constexpr int TSLOTS = NCOPY * CSLOTS > STAGE ? NCOPY * CSLOTS : STAGE;
     constexpr int GSTRIDE = NW * UNR;                       // groups per workgroup batch
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     constexpr int VPT = IAM_PROBES_COUNT / NT;              // inputs of the cutoff per thread
     static_assert(TOUT % NT == 0, "flush mapping");
-    // the wave tiles hold fp64 sums in both modes: Acc is the precision of
+    // the tile holds fp64 sums in both modes: Acc is the precision of
     // the products (fp32 mode: the reference's fp32 products), and LDS fp64
     // atomic adds run many times faster than fp32 ones on this part
     using Tile = double;
-    __shared__ __align__(16) Tile tiles[NW * TSLOTS];   // the wave tiles
+    __shared__ __align__(16) Tile tiles[TSLOTS];   // the tile copies, then the staging copy
     // the search's scratch, then the selected rows
     constexpr int kSearchBytes = sizeof(SearchLds<NW>) > NT * 16 * 2 ? sizeof(SearchLds<NW>) : NT * 16 * 2;
     __shared__ __align__(16) uint4 s_search[(kSearchBytes + 15) / 16];
@@ -723,14 +725,15 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
             lsum = A[attn_lofs + ((tid * VPT) >> 7)];   // the head of the thread's inputs
         }
     }
-    // each wave clears its own tile while the loads are in flight
+    // the tile is cleared while the loads are in flight (the search's
+    // barriers order the clearing before the walk's adds)
     {
-        uint4* tz = reinterpret_cast<uint4*>(tiles + wave * TSLOTS);
+        uint4* tz = reinterpret_cast<uint4*>(tiles);
         constexpr int kTileVecs = TSLOTS * (int)sizeof(Tile) / 16;
         static_assert(TSLOTS * sizeof(Tile) % 16 == 0, "whole 16-byte stores");
 #pragma unroll
-        for (int i = 0; i < (kTileVecs + 63) / 64; i++)
-            if (i * 64 + lane < kTileVecs) tz[i * 64 + lane] = make_uint4(0u, 0u, 0u, 0u);
+        for (int i = 0; i < (kTileVecs + NT - 1) / NT; i++)
+            if (i * NT + tid < kTileVecs) tz[i * NT + tid] = make_uint4(0u, 0u, 0u, 0u);
     }
     // the block's slice and column tile (from the descriptor read through k)
     const int w = b;
@@ -813,7 +816,7 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
         const int nc = min(8, d.C - col0);
         const uint16_t* wb = d.W + (size_t)i0 * 16 * d.C + col0;
         const uint32_t tbase =
-            lds_offset(tiles) + (uint32_t)(wave * TSLOTS + (q % NCOPY) * CSLOTS + j) * (uint32_t)sizeof(Tile);
+            lds_offset(tiles) + (uint32_t)((q % NCOPY) * CSLOTS + j) * (uint32_t)sizeof(Tile);
         const int ng = (ns + RPI - 1) / RPI;
         // one instance of the loop per row load shape, so that no branch sits
         // in its steady state
@@ -896,14 +899,14 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     }
     __syncthreads();
 
-    // ---- flush: the wave tiles summed in wave order, read in slot order
+    // ---- flush: the tile copies summed in copy order, read in slot order
     // (free of bank conflicts), staged in LDS in output order (col*16 + pos,
     // the reference's output index, bucketMul.cl:442-445; one pad per 128
     // entries keeps the staging writes and the reads after them free of
     // conflicts too), then one atomic add per output and workgroup over
     // consecutive outputs.
     constexpr int OPT = TOUT / NT;
-    static_assert(NW * TSLOTS >= TOUT + TOUT / 128, "the staging copy fits the tiles");
+    static_assert(TSLOTS >= STAGE, "the staging copy fits the tiles");
     double* out = reinterpret_cast<double*>(d.acc) + (size_t)t * TOUT;
     const int nout = min(TOUT, (d.C - t * TC) * 16);
     {
@@ -914,10 +917,6 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
             Tile sv = tiles[sl];
 #pragma unroll
             for (int cc = 1; cc < NCOPY; cc++) sv += tiles[cc * CSLOTS + sl];
-#pragma unroll
-            for (int ww = 1; ww < NW; ww++)
-#pragma unroll
-                for (int cc = 0; cc < NCOPY; cc++) sv += tiles[ww * TSLOTS + cc * CSLOTS + sl];
             sum[k2] = sv;
         }
         __syncthreads();
