@@ -211,6 +211,44 @@ constexpr int kMaxAttnSplits = 128;   // max_ctx up to 8192
 // softmax sums, padded to 64 bytes
 __host__ __device__ constexpr int attn_part_stride(int rep) { return rep * 128 + 8; }
 
+// v + v of lane l ^ 8 (a DPP rotation by 8 within each row of 16 lanes)
+__device__ __forceinline__ double xsum8(double v) { return v + dpp_d<0x128>(v, v); }
+__device__ __forceinline__ float xsum8(float v) { return v + dpp_f<0x128>(v, v); }
+
+// v + v of lane l ^ M for M = 16 or 32: v_permlane{16,32}_swap with both
+// operands v returns (v of lane l & ~M, v of lane l | M) in every lane
+template <int M>
+__device__ __forceinline__ void swap_pair(uint32_t w, uint32_t& lo_lane, uint32_t& hi_lane)
+{
+    static_assert(M == 16 || M == 32, "16 or 32");
+    if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+        lo_lane = r[0];
+        hi_lane = r[1];
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+        lo_lane = r[0];
+        hi_lane = r[1];
+    }
+}
+template <int M>
+__device__ __forceinline__ double xsum_swap(double v)
+{
+    const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+    uint32_t l0, l1, h0, h1;
+    swap_pair<M>((uint32_t)b, l0, l1);
+    swap_pair<M>((uint32_t)(b >> 32), h0, h1);
+    return __longlong_as_double((long long)(((unsigned long long)h0 << 32) | l0)) +
+           __longlong_as_double((long long)(((unsigned long long)h1 << 32) | l1));
+}
+template <int M>
+__device__ __forceinline__ float xsum_swap(float v)
+{
+    uint32_t a, b;
+    swap_pair<M>(__float_as_uint(v), a, b);
+    return __uint_as_float(a) + __uint_as_float(b);
+}
+
 template <typename Acc>
 __device__ __forceinline__ Acc acc_exp(Acc x);
 template <>
@@ -327,9 +365,11 @@ __global__ __launch_bounds__(128 * kAttnMaxRep) void k_attn(AttnArgs a, Acc scal
     }
     sq[hr][hf * DH + lane] = (Acc)qv;
     __syncthreads();
-    // half dot product of position t0 + lane, then the two halves in order
+    // half dot product of position t0 + lane (four chains of 16 products,
+    // dimensions 4m + c in chain c, then added pairwise), then the two halves
+    // in order
     {
-        Acc sh = (Acc)0;
+        Acc sc[4] = {(Acc)0, (Acc)0, (Acc)0, (Acc)0};
         const uint4* kr = reinterpret_cast<const uint4*>(sk + min(lane, nt - 1) * RS + hf * DH);
 #pragma unroll
         for (int i = 0; i < DH / 8; i++) {
@@ -337,9 +377,10 @@ __global__ __launch_bounds__(128 * kAttnMaxRep) void k_attn(AttnArgs a, Acc scal
             const uint32_t w[4] = {kv.x, kv.y, kv.z, kv.w};
 #pragma unroll
             for (int e = 0; e < 8; e++)
-                sh = fma(sq[hr][hf * DH + i * 8 + e], (Acc)h2f((uint16_t)(w[e >> 1] >> ((e & 1) * 16))), sh);
+                sc[e & 3] = fma(sq[hr][hf * DH + i * 8 + e], (Acc)h2f((uint16_t)(w[e >> 1] >> ((e & 1) * 16))),
+                                sc[e & 3]);
         }
-        ss[hf][hr][lane] = sh;
+        ss[hf][hr][lane] = (sc[0] + sc[1]) + (sc[2] + sc[3]);
     }
     __syncthreads();
     const Acc s = (ss[0][hr][lane] + ss[1][hr][lane]) * scale;
@@ -366,11 +407,7 @@ __global__ __launch_bounds__(128 * kAttnMaxRep) void k_attn(AttnArgs a, Acc scal
         }
     }
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        o[e] += __shfl_xor(o[e], 8, 64);
-        o[e] += __shfl_xor(o[e], 16, 64);
-        o[e] += __shfl_xor(o[e], 32, 64);
-    }
+    for (int e = 0; e < 8; e++) o[e] = xsum_swap<32>(xsum_swap<16>(xsum8(o[e])));
     // the split's partial sums go to its own slot of the partials (no two
     // splits add to one address): lane (g, j) holds dimension
     // hf*64 + j*8 + g at slot position hr*128 + hf*64 + g*8 + j, so a wave
