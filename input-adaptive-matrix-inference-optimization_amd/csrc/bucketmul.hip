@@ -300,6 +300,17 @@ __device__ __forceinline__ int xcd_remap(int b, int nblocks)
     return xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
 }
 
+// 16 bytes of the weight stream, loaded non-temporally: read once per
+// launch, the rows would otherwise evict the small vectors every launch
+// reads first (inputs, probes, gains, stats, the KV cache) from L2 and the
+// Infinity Cache
+__device__ __forceinline__ uint4 load_stream(const uint16_t* p)
+{
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 r = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(r.x, r.y, r.z, r.w);
+}
+
 // LDS addresses as 32-bit byte offsets (a generic pointer into LDS makes the
 // compiler form every slot address with a 64-bit multiply-add)
 template <typename T>
@@ -836,14 +847,14 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
             for (int u = 0; u < UNR; u++) xc[u] = (Acc)(xl[u] * s_x[rl[u] >> 4]);
             if constexpr (WHOLE) {
 #pragma unroll
-                for (int u = 0; u < UNR; u++) v[u] = *reinterpret_cast<const uint4*>(wb + __umul24(rl[u], d.C));
+                for (int u = 0; u < UNR; u++) v[u] = load_stream(wb + __umul24(rl[u], d.C));
             } else {
 #pragma unroll
                 for (int u = 0; u < UNR; u++) {
                     const uint16_t* rp = wb + __umul24(rl[u], d.C);
                     uint32_t e[8];
 #pragma unroll
-                    for (int c = 0; c < 8; c++) e[c] = c < nc ? rp[c] : 0u;
+                    for (int c = 0; c < 8; c++) e[c] = c < nc ? (uint32_t)__builtin_nontemporal_load(rp + c) : 0u;
                     v[u] = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
                 }
             }
