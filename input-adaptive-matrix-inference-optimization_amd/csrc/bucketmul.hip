@@ -649,8 +649,10 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     // atomic adds run many times faster than fp32 ones on this part
     using Tile = double;
     __shared__ __align__(16) Tile tiles[TSLOTS];   // the tile copies, then the staging copy
-    // the search's scratch, then the selected rows
-    constexpr int kSearchBytes = sizeof(SearchLds<NW>) > NT * 16 * 2 ? sizeof(SearchLds<NW>) : NT * 16 * 2;
+    // the search's scratch (the windowed search's, or the radix search's
+    // when that one declines), then the selected rows
+    constexpr int kSearchA = sizeof(SearchLds<NW>) > sizeof(WindowLds<NW>) ? sizeof(SearchLds<NW>) : sizeof(WindowLds<NW>);
+    constexpr int kSearchBytes = kSearchA > NT * 16 * 2 ? kSearchA : NT * 16 * 2;
     __shared__ __align__(16) uint4 s_search[(kSearchBytes + 15) / 16];
     uint16_t* s_row = reinterpret_cast<uint16_t*>(s_search);
     __shared__ __align__(16) float s_x[NT];
@@ -660,6 +662,7 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     __shared__ float s_bv[NW];
     __shared__ int s_bi[NW];
     SearchLds<NW>& SL = *reinterpret_cast<SearchLds<NW>*>(s_search);
+    WindowLds<NW>& WL = *reinterpret_cast<WindowLds<NW>*>(s_search);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -746,6 +749,7 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
         for (int i = 0; i < (kTileVecs + NT - 1) / NT; i++)
             if (i * NT + tid < kTileVecs) tz[i * NT + tid] = make_uint4(0u, 0u, 0u, 0u);
     }
+    if (mode != kInCutoff) window_clear<NW>(WL);
     // the block's slice and column tile (from the descriptor read through k)
     const int w = b;
     const int p = w / d.T;
@@ -787,17 +791,29 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
         }
     }
 
-    // ---- cutoff, and the importances of the slice's rows (the waves that
-    // leave the search early compute theirs while wave 0 finishes it)
+    // ---- cutoff, and the importances of the slice's rows (computed while
+    // wave 0 finishes the search).  The windowed search leaves the cutoff in
+    // every wave, and each wave's last read of its scratch precedes the
+    // selection's first barrier, after which the scratch becomes the row
+    // list.  When it declines, the radix search runs.
     float imp[16];
     uint32_t vbits;
     if (mode != kInCutoff) {
         float v[VPT];
         importances<VPT>(xs, pw, v);
-        search_cutoff<NW>(v, quantile, SL);
-        select_prepare<NT>(ss, i0, ni, L, s_x, slice_regs, imp, vbits);
-        __syncthreads();   // wave 0 has stored the cutoff; the search scratch becomes the row list
-        cutoff = SL.cut;
+        if (!norm) __syncthreads();   // the window's histograms are clear (the norm's barrier orders them otherwise)
+        float cut_w;
+        const int found = search_window<NW>(v, quantile, WL, cut_w,
+                                             [&] { select_prepare<NT>(ss, i0, ni, L, s_x, slice_regs, imp, vbits); });
+        if (found == 1) {
+            cutoff = cut_w;
+        } else {
+            __syncthreads();   // every wave is done with the window's scratch
+            search_cutoff<NW>(v, quantile, SL);
+            if (found == 0) select_prepare<NT>(ss, i0, ni, L, s_x, slice_regs, imp, vbits);
+            __syncthreads();   // wave 0 has stored the cutoff; the search scratch becomes the row list
+            cutoff = SL.cut;
+        }
         if (w == 0 && tid == 0) d.cutoff[0] = cutoff;
     } else {
         select_prepare<NT>(ss, i0, ni, L, s_x, slice_regs, imp, vbits);

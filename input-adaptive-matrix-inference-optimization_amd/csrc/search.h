@@ -102,6 +102,62 @@ __device__ __forceinline__ void wave_low2(uint32_t& a1, uint32_t& a2)
     a2 = lane63(a2);
 }
 
+// The reference's rounds from U[o] = u_{t-2+o} (o = 0..4; -inf past the
+// numbers; U[0], U[1] unused where t-2, t-1 < 1) and the range of the
+// numbers, in every lane of the calling wave (whole waves only).
+__device__ __forceinline__ float replay_rounds(const float (&U)[5], int t, float gmin, float gmax)
+{
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const bool top_m1 = t - 1 < 1, top_m2 = t - 2 < 1;   // (U[0], U[1] unused then)
+
+    // the reference's rounds (bucketMul.cl:139-213): one chain of bounds,
+    // each round's side picked by U[2] > b (count >= target).  Each round's
+    // bound enters lane 0 of cb while the earlier ones move up a lane
+    // (whole-wave DPP shift), so after round 19 lane j holds round 19 - j's
+    // bound.  Both candidate next bounds are formed before the side is
+    // known, which leaves one select on the chain after the add and halving.
+    float lo = gmin, hi = gmax;
+    float b = midpoint(gmin, gmax);
+    float cb = 0.0f;
+#pragma unroll
+    for (int rd = 0; rd < 20; rd++) {
+        cb = dpp_f<0x138>(b, cb);            // wave_shr:1, lane 0 takes b
+        const bool g = U[2] > b;             // count >= target: min moves
+        float bu = midpoint(b, hi), bd = midpoint(lo, b);
+        asm volatile("" : "+v"(bu), "+v"(bd));
+        lo = g ? b : lo;
+        hi = g ? hi : b;
+        b = g ? bu : bd;
+    }
+    // lane j < 20 stands for round r = 19 - j: its decision, and the bracket
+    // of round r rebuilt from rounds 0 .. r (lanes j .. 19): the low end is
+    // the last tested bound whose count reached the target (else the
+    // minimum), the high end the last one whose count did not (else the
+    // maximum)
+    const bool act = lane < 20;
+    const uint32_t G = (uint32_t)__ballot(act && U[2] > cb);
+    const uint32_t upto = act ? 0xfffffu & ~((1u << lane) - 1u) : 0u;   // lanes j .. 19
+    const uint32_t gl = G & upto, gh = ~G & upto;
+    const float clo = gl ? __shfl(cb, __ffs(gl) - 1, 64) : gmin;
+    const float chi = gh ? __shfl(cb, __ffs(gh) - 1, 64) : gmax;
+    // (bitwise logic below: the tests are cheap and branches are not)
+    const bool cge = act & (((G >> (lane & 31)) & 1u) != 0u);
+    const bool cmi = gl == 0u;     // minB is still the minimum: its count is the reference's 4096 (:142)
+    // the stop tests of round r (bucketMul.cl:195-200)
+    const bool eq_t = cge & !(U[3] > cb);                         // count == target
+    const bool am1 = top_m1 | (U[1] > chi), am2 = top_m2 | (U[0] > chi);
+    const int dmax = am1 ? 1 : am2 ? 2 : 3;                       // target - maxCount (3: 3 or more)
+    const int dmin = !(U[3] > clo) ? 0 : !(U[4] > clo) ? 1 : 2;   // minCount - target (2: 2 or more)
+    const bool gap_min = (dmax <= 2) & (t - dmax >= IAM_PROBES_COUNT - 2);   // 4096 - maxCount < 3
+    const bool gap_small = cmi ? gap_min : dmin + dmax < 3;
+    const bool stop = act & (eq_t | (__fsub_rn(chi, clo) < 0.00001f) | gap_small);
+    const uint64_t sm = __ballot(stop);
+    // the first round that stops is the highest stopping lane; no stop: the
+    // untested midpoint after round 20 (:211-213)
+    return sm ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cb), 63 - __clzll((long long)sm))) : b;
+}
+
 // The cutoff of the 4096 importances held VPT = 4096 / (64 NW) per thread
 // (v: numbers >= +0 or NaN, as 1e5 * |x * probe| gives).  Wave 0 finishes
 // the search after its last barrier: its threads return the cutoff and lane
@@ -278,47 +334,339 @@ __device__ float search_cutoff(const float (&v)[IAM_PROBES_COUNT / (64 * NW)], i
 #pragma unroll
         for (int o = 0; o < 5; o++) U[o] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(uk), o));
     }
-    const bool top_m1 = t - 1 < 1, top_m2 = t - 2 < 1;   // (U[0], U[1] unused then)
-
-    // ---- 5. the reference's rounds (bucketMul.cl:139-213): one chain of
-    // bounds, each round's side picked by U[2] > b (count >= target); lane r
-    // keeps round r's tested bound and the decisions collect in a bit mask.
-    // Round r's bracket is then rebuilt per lane: its low end is the last
-    // tested bound at or before r whose count reached the target (else the
-    // minimum), its high end the last one whose count did not (else the
-    // maximum).
-    float lo = gmin, hi = gmax;
-    float b = midpoint(gmin, gmax);
-    float cb = 0.0f;
-    uint32_t gbits = 0u;
-#pragma unroll
-    for (int rd = 0; rd < 20; rd++) {
-        const bool g = U[2] > b;             // count >= target: min moves
-        cb = lane == rd ? b : cb;
-        gbits |= (g ? 1u : 0u) << rd;
-        lo = g ? b : lo;
-        hi = g ? hi : b;
-        b = midpoint(lo, hi);
-    }
-    const uint32_t upto = lane < 20 ? (2u << lane) - 1u : 0xfffffu;    // rounds 0 .. lane
-    const uint32_t gl = gbits & upto, gh = ~gbits & upto;
-    const float clo = gl ? __shfl(cb, 31 - __clz(gl), 64) : gmin;
-    const float chi = gh ? __shfl(cb, 31 - __clz(gh), 64) : gmax;
-    const bool cge = lane < 20 && ((gbits >> lane) & 1u);
-    const bool cmi = gl == 0u;     // minB is still the minimum: its count is the reference's 4096 (:142)
-    // lane r < 20: the stop tests of round r (bucketMul.cl:195-200)
-    const bool eq_t = cge && !(U[3] > cb);                        // count == target
-    const bool am1 = top_m1 || U[1] > chi, am2 = top_m2 || U[0] > chi;
-    const int dmax = am1 ? 1 : am2 ? 2 : 3;                       // target - maxCount (3: 3 or more)
-    const int dmin = !(U[3] > clo) ? 0 : !(U[4] > clo) ? 1 : 2;   // minCount - target (2: 2 or more)
-    const bool gap_small = cmi ? (dmax <= 2 && t - dmax >= IAM_PROBES_COUNT - 2)   // 4096 - maxCount < 3
-                               : dmin + dmax < 3;
-    const bool stop = lane < 20 && (eq_t || __fsub_rn(chi, clo) < 0.00001f || gap_small);
-    const uint64_t sm = __ballot(stop);
-    // no stop: the untested midpoint after round 20 (:211-213)
-    const float cut = sm ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cb), __ffsll((long long)sm) - 1)) : b;
+    const float cut = replay_rounds(U, t, gmin, gmax);
     if (lane == 0) L.cut = cut;
     return cut;
+}
+
+
+// ---------------------------------------------------------------------------
+// Windowed search: the same cutoff for the walk's workgroup in three
+// barriers, the serial tail done by wave 0 alone.  Importances are numbers
+// >= +0 (or NaN), whose order keys have the top bit set, so bits 30..20 of
+// a key (the float's exponent and its top three mantissa bits) give 2048
+// coarse bins of 1/8 binade in key order.
+//   A. every thread adds its keys to the coarse histogram; each wave
+//      reduces its key range (barrier);
+//   B. every wave finds the coarse bins holding ranks kmin = max(1, t-2)
+//      and kmax = min(n, t+2) (n numbers); the window is those bins and the
+//      ones between;
+//   C. a window of at most kSmallWindow keys is gathered into a list; a
+//      larger one goes into 1024 fine bins, each with its count and its
+//      largest and smallest key (barrier);
+//   D. wave 0 ranks the list, or reads the fine bins from the top of the
+//      16 that hold kmin: where kmax lies within 128 of them and no bin
+//      holding a rank kmin .. kmax has more than two keys, those keys are
+//      u_kmin .. u_kmax; otherwise the keys of those fine bins are gathered
+//      (two more barriers) and ranked.  Either way u_{t-2} .. u_{t+2} come
+//      out exactly, and wave 0 replays the reference's rounds from them
+//      while the other waves run the caller's `prep`; a barrier then hands
+//      the cutoff to all.
+// It declines (in every wave at the same step) when the importances hold no
+// number, a key below +0, or a list longer than kListCap; search_cutoff then
+// finds the cutoff.  Histograms are read with one lane per NB consecutive
+// bins (NB = 32 coarse, 16 fine), stored so that a wave's 16-byte reads are
+// contiguous.
+constexpr int kCoarseBins = 2048;
+constexpr int kFineBins = 1024;
+constexpr int kListCap = 64;
+constexpr int kSmallWindow = 32;   // a window of at most this many keys is listed outright
+
+// steps wave 0 hands on
+enum : int { kWinDecline = 0, kWinList = 1, kWinFine = 2, kWinDone = 3 };
+
+template <int NW>
+struct WindowLds {
+    uint32_t coarse[kCoarseBins];
+    uint32_t fine[kFineBins];
+    uint32_t fmax[kFineBins];   // per fine bin (at its count's slot): its largest key
+    uint32_t fminv[kFineBins];  // ~ its smallest key
+    uint32_t list[kListCap];
+    uint32_t ukey[8];           // keys of ranks t-2 .. t+2 (0: none)
+    uint32_t red[2][NW];        // per wave: min key - 1, max key
+    uint32_t nlist;
+    uint32_t nan_bin;           // the coarse adds of NaN keys (never read)
+    // wave 0's hand-over
+    int step, nl, above;
+    uint32_t rlo, rhi;
+    float cut;
+};
+
+// slot of bin b in a histogram read NB bins per lane: lane l's i-th 16-byte
+// read (at 1024 i + 16 l) holds bins NB l + 4i .. NB l + 4i + 3
+template <int NB>
+__device__ __forceinline__ int hist_slot(int b)
+{
+    return ((b >> 2) & (NB / 4 - 1)) * 256 + (b / NB) * 4 + (b & 3);
+}
+
+__device__ __forceinline__ int coarse_bin(uint32_t key) { return (int)((key >> 20) & (kCoarseBins - 1)); }
+
+// The zeroing of the histograms and the list counter, by all NT threads;
+// a barrier must separate it from search_window.
+template <int NW>
+__device__ __forceinline__ void window_clear(WindowLds<NW>& W)
+{
+    constexpr int NT = 64 * NW;
+    constexpr int kVecs = (kCoarseBins + 3 * kFineBins) / 4;
+    static_assert(offsetof(WindowLds<NW>, list) == (kCoarseBins + 3 * kFineBins) * 4, "the histograms first");
+    uint4* z = reinterpret_cast<uint4*>(W.coarse);
+#pragma unroll
+    for (int i = 0; i < (kVecs + NT - 1) / NT; i++)
+        if (i * NT + (int)threadIdx.x < kVecs) z[i * NT + threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
+    if (threadIdx.x == 0) W.nlist = 0u;
+}
+
+// One wave's scan of a histogram of 64 NB bins (keys counted in ascending
+// key order): lane sums, their prefix, and the number of keys above each
+// lane's bins.
+template <int NB>
+struct HistScan {
+    int tl, abl, total;
+};
+
+template <int NB>
+__device__ __forceinline__ HistScan<NB> hist_scan(const uint32_t* H)
+{
+    const int lane = threadIdx.x & 63;
+    const uint4* H4 = reinterpret_cast<const uint4*>(H);
+    uint4 h[NB / 4];
+#pragma unroll
+    for (int i = 0; i < NB / 4; i++) h[i] = H4[i * 64 + lane];
+    int tl = 0;
+#pragma unroll
+    for (int i = 0; i < NB / 4; i++) tl += (int)(h[i].x + h[i].y + h[i].z + h[i].w);
+    const int incl = wave_incl_sum(tl);
+    const int total = __builtin_amdgcn_readlane(incl, 63);
+    return HistScan<NB>{tl, total - incl, total};
+}
+
+// The bins d1 >= d2 of ranks 1 <= r1 <= r2 <= total (descending, 1-based),
+// the keys above each, and d2's count.  Lanes 0..31 resolve r1 within its
+// lane's NB bins, lanes 32..63 r2.
+template <int NB>
+__device__ __forceinline__ void hist_find2(const uint32_t* H, const HistScan<NB>& sc, int r1, int r2, int& d1,
+                                           int& ab1, int& d2, int& ab2, int& c2)
+{
+    static_assert(NB <= 32, "a half wave per rank");
+    const int lane = threadIdx.x & 63;
+    const int L1 = __ffsll((long long)__ballot(sc.abl < r1 && r1 <= sc.abl + sc.tl)) - 1;
+    const int L2 = __ffsll((long long)__ballot(sc.abl < r2 && r2 <= sc.abl + sc.tl)) - 1;
+    const int a1 = __builtin_amdgcn_readlane(sc.abl, L1);
+    const int a2 = __builtin_amdgcn_readlane(sc.abl, L2);
+    const bool hf = lane >= 32;
+    const int j = lane & 31;
+    const int c = j < NB ? (int)H[hist_slot<NB>((hf ? L2 : L1) * NB + j)] : 0;
+    const int inc = wave_incl_sum(c);
+    const int above = (hf ? __builtin_amdgcn_readlane(inc, 63) : __builtin_amdgcn_readlane(inc, 31)) - inc;
+    const int rb = hf ? r2 - a2 : r1 - a1;
+    const uint64_t bm = __ballot(j < NB && above < rb && rb <= above + c);
+    const int j1 = __ffsll((long long)(bm & 0xffffffffull)) - 1;
+    const int j2 = __ffsll((long long)(bm >> 32)) + 31;
+    d1 = L1 * NB + j1;
+    ab1 = a1 + __builtin_amdgcn_readlane(above, j1);
+    d2 = L2 * NB + (j2 - 32);
+    ab2 = a2 + __builtin_amdgcn_readlane(above, j2);
+    c2 = __builtin_amdgcn_readlane(c, j2);
+}
+
+// The keys of ranks t-2 .. t+2 read back from W.ukey (0: no such rank,
+// which compares like -inf)
+template <int NW>
+__device__ __forceinline__ void read_ukeys(const WindowLds<NW>& W, float (&U)[5])
+{
+    const uint4 q = *reinterpret_cast<const uint4*>(W.ukey);
+    const uint32_t k[5] = {q.x, q.y, q.z, q.w, W.ukey[4]};
+#pragma unroll
+    for (int o = 0; o < 5; o++) U[o] = k[o] ? key_float(k[o]) : -INFINITY;
+}
+
+// wave 0: u_{t-2} .. u_{t+2} from the nl listed keys: lane i's key holds
+// ranks above + gt + 1 .. above + ge
+template <int NW>
+__device__ __forceinline__ void rank_list(WindowLds<NW>& W, int nl, int above, int t, float (&U)[5])
+{
+    const int lane = threadIdx.x & 63;
+    const uint32_t lk = lane < nl ? W.list[lane] : 0u;
+    if (lane < 5) W.ukey[lane] = 0u;
+    int gt = above, ge = above;
+    for (int j = 0; j < nl; j++) {
+        const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)lk, j);
+        gt += kj > lk ? 1 : 0;
+        ge += kj >= lk ? 1 : 0;
+    }
+#pragma unroll
+    for (int o = 0; o < 5; o++) {
+        const int k = t - 2 + o;
+        if (lane < nl && gt < k && k <= ge) W.ukey[o] = lk;
+    }
+    read_ukeys(W, U);
+}
+
+// wave 0: the reference's rounds from U, the cutoff left in W.cut
+template <int NW>
+__device__ __forceinline__ void window_finish(WindowLds<NW>& W, const float (&U)[5], int t, uint32_t kmn, uint32_t kmx)
+{
+    // bucketMul.cl:98-99: min and max from 1e30 / -1e30 (fmin / fmax skip NaN)
+    const float gmin = fminf(1e30f, key_float(kmn));
+    const float gmax = fmaxf(-1e30f, key_float(kmx));
+    const float cut = replay_rounds(U, t, gmin, gmax);
+    if ((threadIdx.x & 63) == 0) {
+        W.cut = cut;
+        W.step = kWinDone;
+    }
+}
+
+// Returns 1 with the cutoff in every wave (prep has run in every wave), 0
+// when declined before prep ran, 2 when declined after it.
+template <int NW, typename Prep>
+__device__ int search_window(const float (&v)[IAM_PROBES_COUNT / (64 * NW)], int quantile, WindowLds<NW>& W,
+                             float& cut, Prep&& prep)
+{
+    static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+    constexpr int VPT = IAM_PROBES_COUNT / (64 * NW);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+
+    // ---- A. keys, the coarse histogram, the waves' key ranges
+    uint32_t key[VPT];
+    uint32_t kmn1 = 0xffffffffu, kmx = 0u;   // min of key - 1 (NaN keys wrap to the top), max
+#pragma unroll
+    for (int k = 0; k < VPT; k++) {
+        key[k] = order_key(v[k]);
+        kmn1 = min(kmn1, key[k] - 1u);
+        kmx = max(kmx, key[k]);
+        atomicAdd(key[k] != 0u ? W.coarse + hist_slot<32>(coarse_bin(key[k])) : &W.nan_bin, 1u);
+    }
+    kmn1 = wave_min_u32(kmn1);
+    kmx = wave_max_u32(kmx);
+    if (lane == 0) {
+        W.red[0][wave] = kmn1;
+        W.red[1][wave] = kmx;
+    }
+    __syncthreads();
+
+    // ---- B. the window, in every wave alike
+    kmn1 = 0xffffffffu;
+    kmx = 0u;
+#pragma unroll
+    for (int w = 0; w < NW; w++) {
+        kmn1 = min(kmn1, W.red[0][w]);
+        kmx = max(kmx, W.red[1][w]);
+    }
+    const uint32_t kmn = kmn1 + 1u;
+    if (kmx == 0u || kmn < 0x80000000u) return 0;    // no number, or one below +0
+    const int t = IAM_PROBES_COUNT - quantile;       // bucketMul.cl:81
+    const HistScan<32> cs = hist_scan<32>(W.coarse);
+    const int nv = cs.total;
+    const int kmin = max(1, t - 2), kmax = min(nv, t + 2);
+    if (kmin > kmax) return 0;
+    int dhi, ab_hi, dlo, ab_lo, c_lo;
+    hist_find2<32>(W.coarse, cs, kmin, kmax, dhi, ab_hi, dlo, ab_lo, c_lo);
+    const int nc = dhi - dlo + 1;
+    const int mc = ab_lo + c_lo - ab_hi;    // keys in the window
+    const uint32_t base = 0x80000000u + ((uint32_t)dlo << 20);
+    const uint32_t width = (uint32_t)nc << 20;
+    const int sf = 10 + (nc > 1 ? 32 - __clz(nc - 1) : 0);   // 1024 fine bins cover the window
+    const bool listed = mc <= kSmallWindow;
+
+    // ---- C. the window's list or its fine histogram
+    if (listed) {
+#pragma unroll
+        for (int k = 0; k < VPT; k++)
+            if (key[k] != 0u && key[k] - base < width) W.list[atomicAdd(&W.nlist, 1u)] = key[k];
+    } else {
+#pragma unroll
+        for (int k = 0; k < VPT; k++) {
+            const uint32_t rel = key[k] - base;
+            if (key[k] != 0u && rel < width) {
+                const int fs = hist_slot<16>((int)(rel >> sf));
+                atomicAdd(W.fine + fs, 1u);
+                atomicMax(W.fmax + fs, key[k]);
+                atomicMax(W.fminv + fs, ~key[k]);
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- D. wave 0: u_{t-2} .. u_{t+2} and the rounds
+    if (wave == 0) {
+        float U[5];
+        if (listed) {
+            rank_list(W, mc, ab_hi, t, U);
+            window_finish(W, U, t, kmn, kmx);
+        } else {
+            // the fine bins of window ranks r1 = kmin - ab_hi .. r2 = kmax - ab_hi:
+            // from the top bin of the lane whose 16 bins hold r1, lane l reads
+            // bins top - 2l and top - 2l - 1.  Where r2 lies within those 128
+            // bins and no bin holding a rank r1 .. r2 has more than two keys,
+            // their largest and smallest keys are u_kmin .. u_kmax.
+            const HistScan<16> fs = hist_scan<16>(W.fine);
+            const int r1 = kmin - ab_hi, r2 = kmax - ab_hi;
+            const int L1 = __ffsll((long long)__ballot(fs.abl < r1 && r1 <= fs.abl + fs.tl)) - 1;
+            const int top = 16 * L1 + 15;
+            const int a1 = __builtin_amdgcn_readlane(fs.abl, L1);    // window keys above bin top
+            const int f0 = top - 2 * lane, f1 = f0 - 1;
+            const int s0 = hist_slot<16>(max(f0, 0)), s1 = hist_slot<16>(max(f1, 0));
+            const int c0 = f0 >= 0 ? (int)W.fine[s0] : 0, c1 = f1 >= 0 ? (int)W.fine[s1] : 0;
+            const uint32_t x0 = W.fmax[s0], n0 = ~W.fminv[s0], x1 = W.fmax[s1], n1 = ~W.fminv[s1];
+            const int incl = wave_incl_sum(c0 + c1);
+            const int e0 = a1 + incl - c0 - c1, e1 = e0 + c0;      // window keys above bins f0, f1
+            const bool ov0 = c0 > 0 && e0 < r2 && e0 + c0 >= r1, ov1 = c1 > 0 && e1 < r2 && e1 + c1 >= r1;
+            const bool direct = __ballot((ov0 && c0 > 2) || (ov1 && c1 > 2)) == 0ull &&
+                                a1 + __builtin_amdgcn_readlane(incl, 63) >= r2;
+            if (direct) {
+                // each lane's keys go to the slots of their ranks: e0 + 1 (x0),
+                // e0 + 2 (n0), e1 + 1 (x1), e1 + 2 (n1), counted from t - 2
+                if (lane < 5) W.ukey[lane] = 0u;
+                const int o0 = ab_hi + e0 + 1 - (t - 2), o1 = ab_hi + e1 + 1 - (t - 2);
+                if (c0 >= 1 && (unsigned)o0 < 5u) W.ukey[o0] = x0;
+                if (c0 == 2 && (unsigned)(o0 + 1) < 5u) W.ukey[o0 + 1] = n0;
+                if (c1 >= 1 && (unsigned)o1 < 5u) W.ukey[o1] = x1;
+                if (c1 == 2 && (unsigned)(o1 + 1) < 5u) W.ukey[o1 + 1] = n1;
+                read_ukeys(W, U);
+                window_finish(W, U, t, kmn, kmx);
+            } else {   // list the keys of the fine bins flo .. fhi
+                int fhi, ab_f, flo, ab_flo, c_flo;
+                hist_find2<16>(W.fine, fs, r1, r2, fhi, ab_f, flo, ab_flo, c_flo);
+                if (lane == 0) {
+                    const int nl = ab_flo + c_flo - ab_f;
+                    W.step = nl > kListCap ? kWinDecline : kWinList;
+                    W.nl = nl;
+                    W.above = ab_hi + ab_f;
+                    W.rlo = (uint32_t)flo << sf;
+                    W.rhi = min((uint32_t)(fhi + 1) << sf, width);
+                }
+            }
+        }
+    }
+    prep();
+    __syncthreads();
+    const int step2 = W.step;
+    if (step2 == kWinDone) {
+        cut = W.cut;
+        return 1;
+    }
+    if (step2 == kWinDecline) return 2;
+    // the fine bins' keys, gathered (the list counter is still zero: the
+    // window was not listed)
+    {
+        const uint32_t rlo = W.rlo, rhi = W.rhi;
+#pragma unroll
+        for (int k = 0; k < VPT; k++) {
+            const uint32_t rel = key[k] - base;
+            if (key[k] != 0u && rel >= rlo && rel < rhi) W.list[atomicAdd(&W.nlist, 1u)] = key[k];
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float U[5];
+        rank_list(W, W.nl, W.above, t, U);
+        window_finish(W, U, t, kmn, kmx);
+    }
+    __syncthreads();
+    cut = W.cut;
+    return 1;
 }
 
 }  // namespace iam

@@ -91,6 +91,30 @@ __device__ __forceinline__ T wave_max_t(T v)
     return wave_reduce(v, [](T a, T b) { return a > b ? a : b; });
 }
 
+// min / max of unsigned values over the 64 lanes, in every lane: lanes
+// without a source see the identity, so each step is one min / max with a
+// DPP operand
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v)
+{
+    v = min(v, dpp_t<0x111>(0xffffffffu, v));
+    v = min(v, dpp_t<0x112>(0xffffffffu, v));
+    v = min(v, dpp_t<0x114>(0xffffffffu, v));
+    v = min(v, dpp_t<0x118>(0xffffffffu, v));
+    v = min(v, dpp_t<0x142, 0xA>(0xffffffffu, v));
+    v = min(v, dpp_t<0x143, 0xC>(0xffffffffu, v));
+    return lane63(v);
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
+{
+    v = max(v, dpp_t<0x111>(0u, v));
+    v = max(v, dpp_t<0x112>(0u, v));
+    v = max(v, dpp_t<0x114>(0u, v));
+    v = max(v, dpp_t<0x118>(0u, v));
+    v = max(v, dpp_t<0x142, 0xA>(0u, v));
+    v = max(v, dpp_t<0x143, 0xC>(0u, v));
+    return lane63(v);
+}
+
 // sum over the 64 lanes: lanes without a source add zero
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v)
