@@ -180,7 +180,7 @@ def test_cutoff_edge_paths(O, iam, ctx, pattern):
 def _search_input(kind, rng):
     """(x, probes) of one importance pattern of the search: heavy-tailed,
     skewed, tied, constant, an outlier, tiny, with infinities or NaNs,
-    overflowing midpoints, two adjacent floats, zero, bimodal."""
+    overflowing midpoints, two adjacent floats, zero, bimodal, quantized."""
     n = 4096
     p = rng.normal(0, 0.02, n).astype(np.float16).view(np.uint16)
     const_p = np.full(n, 0x2400, np.uint16)          # 2^-6
@@ -215,20 +215,26 @@ def _search_input(kind, rng):
         x[: 1 + int(rng.integers(0, 4))] = np.nan
     elif kind == "bimodal":
         x = (z + np.where(rng.random(n) < 0.5, 10.0, 0.0)).astype(np.float32)
+    elif kind == "quantized":      # about three equal keys per value near any rank
+        x, p = (np.round(z * 600) / 600).astype(np.float32), const_p
     return x, p
 
 
 _SEARCH_KINDS = ["normal", "skew", "ties", "constant", "outlier", "tiny", "inf", "nan", "huge",
-                 "adjacent", "zero", "all_nan", "nan_inf", "few_nans", "bimodal"]
+                 "adjacent", "zero", "all_nan", "nan_inf", "few_nans", "bimodal", "quantized"]
 
 
 @pytest.mark.parametrize("kind", _SEARCH_KINDS)
 def test_cutoff_search_kinds(O, iam, ctx, kind):
-    """The cutoff search bit-exact against the oracle on 15 importance
+    """The cutoff search bit-exact against the oracle on 16 importance
     patterns at efforts that give the quantiles 0..3, 4092..4095 and the
-    usual ones: the standalone cutoff kernel (4 waves) and the walk's own
-    search (8 waves) on 256 and 32000 outputs; the selected row count
-    matches too."""
+    usual ones: the standalone cutoff kernel (4 waves, radix search) and the
+    walk's own search (8 waves) on 256 and 32000 outputs; the selected row
+    count matches too.  On the walk's windowed search these patterns take
+    every route: a listed small window (e.g. normal at quantile 0), the fine
+    bins read directly (normal at 1023), the fine bins' keys gathered and
+    ranked (quantized at 1023), and the radix search after a decline at the
+    window (all_nan) or at the list (constant)."""
     rng = np.random.default_rng(100 + _SEARCH_KINDS.index(kind))
     x, p = _search_input(kind, rng)
     quants = [0, 1, 2, 3, 100, 1023, 2047, 3071, 3583, 3890, 4092, 4093, 4094, 4095]
