@@ -115,8 +115,8 @@ __device__ __forceinline__ float replay_rounds(const float (&U)[5], int t, float
     // each round's side picked by U[2] > b (count >= target).  Each round's
     // bound enters lane 0 of cb while the earlier ones move up a lane
     // (whole-wave DPP shift), so after round 19 lane j holds round 19 - j's
-    // bound.  Both candidate next bounds are formed before the side is
-    // known, which leaves one select on the chain after the add and halving.
+    // bound.  (One wave runs this chain alone, so its length is its
+    // instruction count: 7 per round.)
     float lo = gmin, hi = gmax;
     float b = midpoint(gmin, gmax);
     float cb = 0.0f;
@@ -124,11 +124,9 @@ __device__ __forceinline__ float replay_rounds(const float (&U)[5], int t, float
     for (int rd = 0; rd < 20; rd++) {
         cb = dpp_f<0x138>(b, cb);            // wave_shr:1, lane 0 takes b
         const bool g = U[2] > b;             // count >= target: min moves
-        float bu = midpoint(b, hi), bd = midpoint(lo, b);
-        asm volatile("" : "+v"(bu), "+v"(bd));
         lo = g ? b : lo;
         hi = g ? hi : b;
-        b = g ? bu : bd;
+        b = midpoint(lo, hi);
     }
     // lane j < 20 stands for round r = 19 - j: its decision, and the bracket
     // of round r rebuilt from rounds 0 .. r (lanes j .. 19): the low end is
