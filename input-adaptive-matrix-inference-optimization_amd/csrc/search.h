@@ -370,8 +370,9 @@ constexpr int kFineBins = 1024;
 constexpr int kListCap = 64;
 constexpr int kSmallWindow = 32;   // a window of at most this many keys is listed outright
 
-// steps wave 0 hands on
-enum : int { kWinDecline = 0, kWinList = 1, kWinFine = 2, kWinDone = 3 };
+// what wave 0 hands on after its tail: no cutoff (the radix search runs),
+// a list of the fine bins' keys to gather, or the cutoff
+enum : int { kWinDecline = 0, kWinList = 1, kWinDone = 3 };
 
 template <int NW>
 struct WindowLds {
