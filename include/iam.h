@@ -268,6 +268,32 @@ int iam_rope_kv_append(iam_ctx* ctx, const float* q_dev, const float* k_dev, con
 int iam_attention_decode(iam_ctx* ctx, const float* q_dev, const uint16_t* kcache_dev,
                          const uint16_t* vcache_dev, const int* pos_dev, int n_heads, int n_kv,
                          int head_dim, int max_ctx, float* out_dev);
+/* The reference's KV cache layout and fp32 attention, the parity mode of
+ * iam_rope_kv_append / iam_attention_decode: the caches hold K (after RoPE)
+ * and V repeated to every query head, fp32 [max_ctx][n_heads][head_dim] per
+ * layer (model.hpp:97-98).  RoPE of q and k, then K and V of KV head
+ * h*n_kv/n_heads stored for every query head h at *pos_dev (repeat4x32
+ * aux.cl:266-275, rope_mx :227-248, the copies of attention.hpp:281-309). */
+int iam_rope_kv_append_f32(iam_ctx* ctx, const float* q_dev, const float* k_dev, const float* v_dev,
+                           const float* table_dev, const int* pos_dev, int n_heads, int n_kv, int head_dim,
+                           int max_ctx, float* q_out_dev, float* kcache_dev, float* vcache_dev);
+/* Attention over positions 0..*pos_dev of those caches in the reference's
+ * fp32 arithmetic (dotSetScore2 aux.cl:497-540 with its work-group tree,
+ * sum_of_exps32_mx / softmax_add32_mx :204-225 with no maximum subtracted,
+ * sumScores32 :370-384; driver attention.hpp:311-404): one IEEE operation
+ * at a time, the sums of exp and of p*v in splits of 64 positions taken in
+ * order (the reference's float atomics have no fixed order).  A score above
+ * log(FLT_MAX) ~ 88.72 makes that head's outputs NaN, as in the reference. */
+int iam_attention_decode_f32(iam_ctx* ctx, const float* q_dev, const float* kcache_dev,
+                             const float* vcache_dev, const int* pos_dev, int n_heads, int head_dim,
+                             int max_ctx, float* out_dev);
+/* matmul16x32 (aux.cl:454-490), the reference's dense LM head (model.hpp:
+ * 207-227, 256 work-items per row): out[r] = the fp16 row r of W [rows][cols]
+ * times x, each row's products summed per work-item over the columns
+ * l, l+256, ... in order and then by the 256-way work-group tree, in fp32
+ * without contraction.  cols <= 16384. */
+int iam_matmul_f16_dense(iam_ctx* ctx, const uint16_t* w_dev, const float* x_dev, int rows, int cols,
+                         float* out_dev);
 /* fetchRow16to32 (aux.cl:442-452): out = (float) table[*token_dev][:]; a
  * token outside [0, vocab) yields zeros. */
 int iam_embed_gather(iam_ctx* ctx, const uint16_t* table_dev, int cols, int vocab,
@@ -341,6 +367,12 @@ int iam_model_decode(iam_model* m, int n_steps, float effort, int use_graph);
 int iam_model_set_position(iam_model* m, int pos);
 /* MistralModel::reset_caches (model.hpp:233-237); also rewinds the position. */
 int iam_model_reset_caches(iam_model* m);
+/* The LM head as the reference's dense fp16 product (matmul16x32 over
+ * lm_dense_dev [vocab][dim], a caller-owned device buffer that must outlive
+ * its use; model.hpp:207-227) instead of the bucket-layout one; NULL restores
+ * the bucket layout.  The step then runs the final norm, the dense product
+ * and the first-max pick as launches of their own. */
+int iam_model_set_lm_dense(iam_model* m, const uint16_t* lm_dense_dev);
 /* Per-channel fp32 factors applied to the gathered embedding before the
  * first layer (NULL restores plain fetchRow16to32).  Used for the skewed-
  * channel decode workload, which scales 1% of hidden channels. */

@@ -4,10 +4,12 @@
 // "_probes.bin" (1, in) and "_meta.txt".  Same structure and checks as the
 // reference reader (binary_loader.hpp:14-201); host vectors only, the caller
 // uploads.  Also the raw .npy skip-header reader of
-// transformer_layer.hpp:25-52 / model.hpp:54-81, with a header check.
+// transformer_layer.hpp:25-52 / model.hpp:54-81, with a header check, and
+// the reference's fp16 debugging helpers (binary_loader.hpp:203-241).
 #ifndef IAM_BINARY_LOADER_HPP
 #define IAM_BINARY_LOADER_HPP
 
+#include <cmath>
 #include <cstdint>
 #include <cstring>
 #include <fstream>
@@ -15,6 +17,8 @@
 #include <stdexcept>
 #include <string>
 #include <vector>
+
+#include "gpu.hpp"
 
 struct Shape3D {
     size_t dim0 = 0, dim1 = 0, dim2 = 0;
@@ -38,8 +42,12 @@ struct WeightMetadata {
     size_t bsize = 0;
 };
 
-// binary_loader.hpp:40-51 (host copies only)
+// binary_loader.hpp:40-51: the loader fills the host copies only; the device
+// handles stay null (the caller uploads), as in the reference
 struct BucketizedWeight {
+    void* buckets = nullptr;
+    void* stats = nullptr;
+    void* probes = nullptr;
     WeightMetadata meta;
     std::vector<uint16_t> buckets_host;
     std::vector<uint16_t> stats_host;
@@ -48,6 +56,9 @@ struct BucketizedWeight {
 
 class BinaryWeightLoader {
 public:
+    // binary_loader.hpp:137-139: the device is not used by the reader (it
+    // returns host vectors); it is kept for the reference's call sites
+    BinaryWeightLoader(Gpu* gpu, const std::string& base_path) : gpu(gpu), base_path(base_path) {}
     explicit BinaryWeightLoader(const std::string& base_path) : base_path(base_path) {}
 
     // binary_loader.hpp:59-102
@@ -164,7 +175,26 @@ public:
     }
 
 private:
+    Gpu* gpu = nullptr;
     std::string base_path;
 };
+
+// binary_loader.hpp:203-241: an fp16 value from its bits (subnormals, inf and
+// NaN included), and the position / value fields of a packed bucket entry
+// (value bits & 0xFFF0, position bits & 0xF; preprocess_layer_fixed_gpu.py:40-89)
+inline float fp16_to_float(uint16_t h)
+{
+    const int e = (h >> 10) & 0x1f;
+    const int m = h & 0x3ff;
+    float mag;
+    if (e == 0x1f) mag = m ? NAN : INFINITY;
+    else if (e == 0) mag = std::ldexp((float)m, -24);             // zero or subnormal: m * 2^-24
+    else mag = std::ldexp((float)(m | 0x400), e - 25);            // 1.m * 2^(e-15)
+    return (h & 0x8000) ? -mag : mag;
+}
+
+inline int extract_position(uint16_t packed_fp16) { return packed_fp16 & 0xf; }
+
+inline float extract_value(uint16_t packed_fp16) { return fp16_to_float((uint16_t)(packed_fp16 & 0xfff0)); }
 
 #endif

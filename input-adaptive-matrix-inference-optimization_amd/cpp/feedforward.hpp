@@ -15,7 +15,7 @@ public:
     FeedForward(Gpu* g, const std::string& weights_dir, int layer_idx, size_t hidden = 4096, size_t ffn = 14336)
         : gpu(g), hidden_dim(hidden), ffn_dim(ffn), layer_idx_(layer_idx)
     {
-        BinaryWeightLoader loader(weights_dir);
+        BinaryWeightLoader loader(gpu, weights_dir);
         const std::string prefix = "layer" + std::to_string(layer_idx);
         gate.reset(new BucketWeight(gpu, loader.load(prefix + "_gate_proj_bucketmul_fp16")));
         up.reset(new BucketWeight(gpu, loader.load(prefix + "_up_proj_bucketmul_fp16")));

@@ -1,12 +1,18 @@
 // iam_dropin - command-line driver over the drop-in C++ classes.
 //
 //   iam_dropin generate -d DIR -p 1,2,3 -n 16 [-e 0.25] [--eager] [--max-ctx N] [--theta T]
+//              [--lm dense|bucket] [--logits FILE]
 //       MistralModel greedy generation (test_generation.cpp:125-317 without the
 //       tokenizer: the prompt is a list of token ids); prints the new tokens
-//       and the prefill / generation rates.
+//       and the prefill / generation rates.  The LM head is the reference's
+//       dense product (default) or the bucket layout.  With --eager and
+//       --logits, the logits of every step after the prompt are appended to
+//       FILE (fp32).
 //   iam_dropin layer -d DIR -l L -e E --in h.f32 --out y.f32 [--pos P] [--max-ctx N] [--theta T]
+//              [--cache f16|f32]
 //       TransformerLayer::forward for positions 0..P with the same input
-//       (filling the KV cache), writes the output of the last position.
+//       (filling the KV cache), writes the output of the last position.  The
+//       caches are fp16 GQA (default) or the reference's fp32 layout.
 //   iam_dropin bucketmul -d DIR -w NAME -e E --in x.f32 --out y.f32
 //       BucketMul::calcDispatch + mul on one weight; writes y, prints the
 //       cutoff and the selected-row count.
@@ -26,7 +32,7 @@
 namespace {
 
 struct Args {
-    std::string cmd, dir, in, out, weight, prompt = "1";
+    std::string cmd, dir, in, out, weight, prompt = "1", lm = "dense", cache = "f16", logits;
     int n = 8, layer = 0, pos = 0, max_ctx = 2048;
     float effort = 1.0f;
     double theta = 1000000.0;
@@ -56,6 +62,9 @@ Args parse(int argc, char** argv)
         else if (s == "--max-ctx") a.max_ctx = std::stoi(next());
         else if (s == "--theta") a.theta = std::stod(next());
         else if (s == "--eager") a.eager = true;
+        else if (s == "--lm") a.lm = next();
+        else if (s == "--cache") a.cache = next();
+        else if (s == "--logits") a.logits = next();
         else throw std::runtime_error("unknown option " + s);
     }
     return a;
@@ -87,7 +96,11 @@ double now_ms()
 int cmd_generate(const Args& a)
 {
     Gpu gpu;
-    MistralModel model(&gpu, a.dir, a.max_ctx, a.theta);
+    if (a.lm != "dense" && a.lm != "bucket") throw std::runtime_error("--lm must be dense or bucket");
+    MistralModel model(&gpu, a.dir, a.max_ctx, a.theta, -1,
+                       a.lm == "dense" ? MistralModel::LmHead::Dense : MistralModel::LmHead::Bucket);
+    std::ofstream logf;
+    if (!a.logits.empty()) logf.open(a.logits, std::ios::binary);
     std::vector<int> prompt;
     std::stringstream ss(a.prompt);
     std::string tok;
@@ -101,12 +114,14 @@ int cmd_generate(const Args& a)
         std::vector<float> host(V);
         for (size_t i = 0; i < prompt.size(); i++) model.forward(prompt[i], (int)i, a.effort, &logits);
         gpu.readBuffer(logits.buffer, (size_t)V * 4, host.data());
+        if (logf) logf.write(reinterpret_cast<const char*>(host.data()), (std::streamsize)V * 4);
         int next = (int)(std::max_element(host.begin(), host.end()) - host.begin());
         for (int g = 0; g < a.n; g++) {
             out.push_back(next);
             if (g + 1 == a.n) break;
             model.forward(next, (int)prompt.size() + g, a.effort, &logits);
             gpu.readBuffer(logits.buffer, (size_t)V * 4, host.data());
+            if (logf) logf.write(reinterpret_cast<const char*>(host.data()), (std::streamsize)V * 4);
             next = (int)(std::max_element(host.begin(), host.end()) - host.begin());
         }
     } else {
@@ -126,17 +141,28 @@ int cmd_layer(const Args& a)
     const size_t D = TransformerLayer::HIDDEN_DIM;
     std::vector<float> h = read_f32(a.in);
     if (h.size() != D) throw std::runtime_error("layer: input must hold 4096 floats");
-    const size_t kv = (size_t)(a.layer + 1) * a.max_ctx * 8 * 128;
-    BufferWrapper<uint16_t> kc(&gpu, kv), vc(&gpu, kv);
-    kc.zero(&gpu);
-    vc.zero(&gpu);
+    if (a.cache != "f16" && a.cache != "f32") throw std::runtime_error("--cache must be f16 or f32");
     BufferWrapper<float> in(&gpu, D), hn(&gpu, D), xq(&gpu, D), xk(&gpu, 1024), xv(&gpu, 1024), xkr(&gpu, D),
         xqh(&gpu, D), xkh(&gpu, D), sc(&gpu, (size_t)32 * a.max_ctx), ao(&gpu, D), attn(&gpu, D), fxn(&gpu, D),
         ffn(&gpu, D), out(&gpu, D);
-    for (int p = 0; p <= a.pos; p++) {
-        in.setData(&gpu, h);
-        layer.forward(&in, a.layer, p, a.effort, &kc, &vc, &hn, &xq, &xk, &xv, &xkr, &xqh, &xkh, &sc, &ao, &attn,
-                      &fxn, &ffn, &out);
+    auto run = [&](auto* kc, auto* vc) {
+        kc->zero(&gpu);
+        vc->zero(&gpu);
+        for (int p = 0; p <= a.pos; p++) {
+            in.setData(&gpu, h);
+            layer.forward(&in, a.layer, p, a.effort, kc, vc, &hn, &xq, &xk, &xv, &xkr, &xqh, &xkh, &sc, &ao, &attn,
+                          &fxn, &ffn, &out);
+        }
+    };
+    if (a.cache == "f16") {
+        const size_t kv = (size_t)(a.layer + 1) * a.max_ctx * 8 * 128;
+        BufferWrapper<uint16_t> kc(&gpu, kv), vc(&gpu, kv);
+        run(&kc, &vc);
+    } else {
+        // the reference's layout: [layers][max_tokens][32][128] fp32 (model.hpp:97-98)
+        const size_t kv = (size_t)(a.layer + 1) * a.max_ctx * D;
+        BufferWrapper<float> kc(&gpu, kv), vc(&gpu, kv);
+        run(&kc, &vc);
     }
     write_f32(a.out, out.getData(&gpu));
     return 0;
@@ -145,7 +171,7 @@ int cmd_layer(const Args& a)
 int cmd_bucketmul(const Args& a)
 {
     Gpu gpu;
-    BinaryWeightLoader loader(a.dir);
+    BinaryWeightLoader loader(&gpu, a.dir);
     BucketizedWeight w = loader.load(a.weight);
     const size_t R = w.meta.stats_shape.dim1, C = w.meta.buckets_shape.dim2;
     BufferWrapper<uint16_t> buckets(&gpu, std::vector<size_t>{R, C}), stats(&gpu, std::vector<size_t>{R, 4}),

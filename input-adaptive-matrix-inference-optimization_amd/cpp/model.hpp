@@ -3,13 +3,17 @@
 //   layer{L}_{q,k,v,o,gate,up,down}_proj_bucketmul_fp16_{buckets,stats,probes}.bin + _meta.txt
 //   layer{L}_input_layernorm.npy, layer{L}_post_attention_layernorm.npy
 //   embed_tokens.npy, norm_weight.npy, lm_head.npy (dense fp16 [vocab][dim])
-// into one iam_model; the dense LM head is bucketized on the GPU at load so
-// the head runs through the same input-adaptive product.  forward() keeps
-// the reference's signature and ends with eval() (model.hpp:230).
+// into one iam_model.  The LM head is the reference's dense fp16 product
+// (matmul16x32, model.hpp:207-227) by default; LmHead::Bucket bucketizes
+// lm_head.npy on the GPU at load and runs the head through the same
+// input-adaptive product at the caller's effort (the decode workload's
+// head).  forward() keeps the reference's signature and ends with eval()
+// (model.hpp:230).
 #ifndef IAM_MODEL_HPP
 #define IAM_MODEL_HPP
 
 #include <fstream>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -18,9 +22,11 @@
 
 class MistralModel {
 public:
+    enum class LmHead { Dense, Bucket };
+
     MistralModel(Gpu* g, const std::string& weights_dir, int max_tokens = 2048, double rope_theta = 1000000.0,
-                 int n_layers = -1)
-        : gpu(g)
+                 int n_layers = -1, LmHead lm_head = LmHead::Dense)
+        : gpu(g), head(lm_head)
     {
         std::vector<size_t> eshape, lshape;
         auto embed = BinaryWeightLoader::loadNpyF16(weights_dir + "/embed_tokens.npy", &eshape);
@@ -28,7 +34,7 @@ public:
         auto lm = BinaryWeightLoader::loadNpyF16(weights_dir + "/lm_head.npy", &lshape);
         if (eshape.size() != 2 || lshape.size() != 2 || eshape[1] != lshape[1] || eshape[0] != lshape[0])
             throw std::runtime_error("MistralModel: embed_tokens and lm_head must both be [vocab][dim]");
-        BinaryWeightLoader loader(weights_dir);
+        BinaryWeightLoader loader(gpu, weights_dir);
         if (n_layers < 0) {
             n_layers = 0;
             while (std::ifstream(weights_dir + "/layer" + std::to_string(n_layers) +
@@ -69,17 +75,27 @@ public:
         }
         put("embed", embed);
         put("final_gain", norm);
-        // dense LM head -> bucket layout on the GPU (preprocess_layer_fixed_gpu.py:110-242)
-        BufferWrapper<uint16_t> dense(gpu, lm.size());
-        dense.setData(gpu, lm);
-        iam_cpp::check(iam_bucketize(gpu->ctx, dense.data(), cfg.vocab, cfg.dim, tensor("lm_head.buckets"),
-                                     tensor("lm_head.stats"), tensor("lm_head.probes")),
-                       "MistralModel: bucketize LM head");
-        compact("lm_head");
+        lm_dense.reset(new BufferWrapper<uint16_t>(gpu, lm.size()));
+        lm_dense->setData(gpu, lm);
+        if (head == LmHead::Bucket) {
+            // dense LM head -> bucket layout on the GPU (preprocess_layer_fixed_gpu.py:110-242)
+            iam_cpp::check(iam_bucketize(gpu->ctx, lm_dense->data(), cfg.vocab, cfg.dim, tensor("lm_head.buckets"),
+                                         tensor("lm_head.stats"), tensor("lm_head.probes")),
+                           "MistralModel: bucketize LM head");
+            compact("lm_head");
+            gpu->eval();
+            lm_dense.reset();
+        } else {
+            iam_cpp::check(iam_model_set_lm_dense(m, lm_dense->data()), "MistralModel: dense LM head");
+        }
         gpu->eval();
     }
 
-    ~MistralModel() { iam_model_destroy(m); }
+    ~MistralModel()
+    {
+        iam_model_destroy(m);
+        lm_dense.reset();
+    }
 
     MistralModel(const MistralModel&) = delete;
     MistralModel& operator=(const MistralModel&) = delete;
@@ -106,6 +122,7 @@ public:
     void reset_caches() { iam_cpp::check(iam_model_reset_caches(m), "MistralModel::reset_caches"); }
 
     const iam_model_config& config() const { return cfg; }
+    LmHead lm_head() const { return head; }
     iam_model* handle() const { return m; }
 
 private:
@@ -136,8 +153,10 @@ private:
     }
 
     Gpu* gpu;
+    LmHead head;
     iam_model* m = nullptr;
     iam_model_config cfg{};
+    std::unique_ptr<BufferWrapper<uint16_t>> lm_dense;   // the dense head's matrix (LmHead::Dense)
 };
 
 #endif

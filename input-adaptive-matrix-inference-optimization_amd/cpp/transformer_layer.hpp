@@ -1,12 +1,14 @@
 // transformer_layer.hpp - TransformerLayer of the reference
 // (transformer_layer.hpp:14-163) over the iam C ABI: pre-norm attention and
-// FFN blocks with residual adds.  Same constructor and forward() arguments
-// (the KV caches are fp16 GQA, see attention.hpp).
+// FFN blocks with residual adds.  Same constructor and forward() arguments;
+// forward() takes the reference's fp32 caches or the decode workload's fp16
+// GQA caches (see attention.hpp).
 #ifndef IAM_TRANSFORMER_LAYER_HPP
 #define IAM_TRANSFORMER_LAYER_HPP
 
 #include <memory>
 #include <string>
+#include <type_traits>
 
 #include "attention.hpp"
 #include "feedforward.hpp"
@@ -33,15 +35,18 @@ public:
         ffn_norm_weight->setData(gpu, f);
     }
 
-    // transformer_layer.hpp:75-122
-    void forward(BufferWrapper<float>* input, int layer_idx, int pos, float effort, BufferWrapper<uint16_t>* k_cache,
-                 BufferWrapper<uint16_t>* v_cache, BufferWrapper<float>* h_norm, BufferWrapper<float>* temp_xq,
+    // transformer_layer.hpp:75-122, over fp16 GQA caches or the reference's fp32 ones
+    template <typename CacheT>
+    void forward(BufferWrapper<float>* input, int layer_idx, int pos, float effort, BufferWrapper<CacheT>* k_cache,
+                 BufferWrapper<CacheT>* v_cache, BufferWrapper<float>* h_norm, BufferWrapper<float>* temp_xq,
                  BufferWrapper<float>* temp_xk, BufferWrapper<float>* temp_xv, BufferWrapper<float>* temp_xk_repeated,
                  BufferWrapper<float>* temp_xq_heads, BufferWrapper<float>* temp_xk_heads,
                  BufferWrapper<float>* temp_scores, BufferWrapper<float>* temp_attn_output,
                  BufferWrapper<float>* attn_out, BufferWrapper<float>* fxn, BufferWrapper<float>* ffn_out,
                  BufferWrapper<float>* output)
     {
+        static_assert(std::is_same<CacheT, float>::value || std::is_same<CacheT, uint16_t>::value,
+                      "caches are fp32 (the reference's layout) or fp16 (GQA)");
         rms_norm(input, attn_norm_weight.get(), h_norm);
         attention->forward(h_norm, layer_idx, pos, effort, k_cache, v_cache, temp_xq, temp_xk, temp_xv,
                            temp_xk_repeated, temp_xq_heads, temp_xk_heads, temp_scores, temp_attn_output, attn_out);

@@ -1115,10 +1115,10 @@ void plan_walk(int n, const MatOp* ops, float effort, WalkPlan* plan, int blk, i
 
 int walk_tiles(int bucket_cols) { return (bucket_cols + kTileColsNarrow - 1) / kTileColsNarrow; }
 
-int max_slices(int n, const MatOp* ops, float effort)
+int max_slices(int n, const MatOp* ops, float effort, int blk, int tc)
 {
     WalkPlan plan[kMaxMulti];
-    plan_walk(n, ops, effort, plan);
+    plan_walk(n, ops, effort, plan, blk, tc);
     int P = 1;
     for (int i = 0; i < n; i++) P = std::max(P, plan[i].P);
     return P;
@@ -1358,7 +1358,7 @@ static int walk_slots(Ctx* c, int n, const MatOp* ops, int in_mode, const float*
         wops[i].x = c->slots[i].x;
         wops[i].in_size = c->slots[i].in_size;
     }
-    const int P = max_slices(n, wops, g.effort);
+    const int P = max_slices(n, wops, g.effort, sel_block_for(c, g.effort), walk_tile_cols(g));
     for (int i = 0; i < n; i++) {
         const iam_bucket_matrix& M = ops[i].mat;
         const DispatchSlot& s = c->slots[i];

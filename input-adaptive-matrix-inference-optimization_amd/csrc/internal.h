@@ -107,6 +107,10 @@ struct Ctx {
     void* attn_acc = nullptr;
     size_t attn_acc_cap = 0;
     uint32_t* attn_ctr = nullptr;
+    // the fp32 attention over the reference's cache layout: exp(s) per head
+    // and position, the splits' sums and partial outputs
+    float* attn32 = nullptr;
+    size_t attn32_cap = 0;
     // bumped whenever a context-owned scratch buffer is reallocated:
     // captured graphs hold those addresses and must be re-captured
     uint64_t scratch_gen = 0;
@@ -204,15 +208,14 @@ enum WalkFin : int {
 // grid plan of one matrix in a walk launch
 struct WalkPlan {
     int NW;     // waves per workgroup (the same for every matrix of a launch)
-    int T;      // column tiles of 128 columns
+    int T;      // column tiles of tc columns
     int n_in;   // inputs walked
     int IPS;    // inputs per slice
     int P;      // slices
 };
-// blk: inputs per selection block (slices start at its multiples)
-// blk: inputs per selection block; tc: columns per tile (128 gives the
-// most slices, the bound the scratch is sized for)
-void plan_walk(int n, const MatOp* ops, float effort, WalkPlan* plan, int blk = 1, int tc = 128);
+// blk: inputs per selection block (slices start at its multiples); tc:
+// columns per tile (the launch's walk_tile_cols)
+void plan_walk(int n, const MatOp* ops, float effort, WalkPlan* plan, int blk, int tc);
 // the selection block size of a walk at this effort
 int sel_block_for(const Ctx* c, float effort);
 
@@ -272,18 +275,21 @@ struct WalkGroup {
 };
 // one walk launch of the group (plan from the matrices and effort)
 int walk_group(Ctx* c, const WalkGroup& g);
-// column tiles of a matrix in a walk launch
+// columns per tile of the group's walk launch (64 or 128)
+int walk_tile_cols(const WalkGroup& g);
 // column tiles of a matrix at the narrowest tile width (the most any launch
 // uses: the size of per-tile counters and candidates)
 int walk_tiles(int bucket_cols);
-// the largest slice count any plan gives a group of these matrices
-int max_slices(int n, const MatOp* ops, float effort);
+// the largest slice count of the plan a walk of these matrices runs with
+// (selection blocks of blk inputs, tiles of tc columns)
+int max_slices(int n, const MatOp* ops, float effort, int blk, int tc);
 
 // standalone calls: dispatch + walk with fp32 outputs (y), in_mode kInX or
 // kInNorm (the norm of h written to ops[0].x)
 int bucketmul_fused(Ctx* c, int n, const MatOp* ops, int expert_no, float effort, int in_mode, const float* h,
                     const uint16_t* gain, float eps);
 int ensure_attn_scratch(Ctx* c, size_t acc_words, int n_kv);
+int ensure_attn32_scratch(Ctx* c, size_t floats);
 
 int quantile_of(float effort);
 double est_rows(int rows, float effort);

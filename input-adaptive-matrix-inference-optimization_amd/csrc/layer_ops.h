@@ -51,8 +51,13 @@ size_t attention_part_words(int n_heads, int n_kv, int max_ctx);
 int resnorm(Ctx* c, const float* h, const void* delta_acc, float* h_out, const uint16_t* gain, int n, float eps,
             float* out);
 int embed(Ctx* c, const uint16_t* table, int cols, int vocab, const int* tok, float* out);
-// first-max argmax into out[0]; if pos_inc is non-null, *pos_inc += 1
-int argmax(Ctx* c, const float* v, int n, int* out, int* pos_inc);
+// first-max argmax into out[0]; if pos_inc is non-null, *pos_inc += 1 and,
+// when hist is non-null and the new position lies below hist_len,
+// hist[new position] = the index
+int argmax(Ctx* c, const float* v, int n, int* out, int* pos_inc, int* hist = nullptr, int hist_len = 0);
+// matmul16x32 (aux.cl:454-490): out[r] = fp16 row r of W [rows][cols] times x,
+// in the reference's work-group order (cols <= 16384)
+int matmul_f16_dense(Ctx* c, const uint16_t* W, const float* x, int rows, int cols, float* out);
 
 // synthetic data and the GPU bucketizer
 int gen_f16(Ctx* c, uint64_t seed, uint64_t tid, size_t count, double mean, double sigma, uint16_t* out);

@@ -194,16 +194,21 @@ __global__ void k_rope_kv(const float* __restrict__ q, const float* __restrict__
 // softmax_add32_mx, aux.cl:204-225: the reference's softmax has no maximum
 // subtracted, so the splits' sums add up directly); then lane (g, j)
 // accumulates 8 dimensions of the wave's half of sum p*V over every eighth
-// position.  The split adds sum p*V and sum p to the accumulators o and l
-// with atomics; out = o / l (sumScores32, aux.cl:370-384) is formed by the
-// consumer (the o projection's walk) or, for the standalone call, by the
-// last split of each KV head.  The split's K and V rows are loaded once per
-// workgroup, 16 bytes per thread, into LDS.  With the projection
-// accumulators as input the workgroup also applies RoPE to q and k (rope_mx,
-// aux.cl:227-248, table row of the position) and the split holding the
-// position appends the new K and V rows to the cache (attention.hpp:281-309)
-// and uses them from LDS.  Acc = double evaluates every product (exact:
-// fp32 x fp16), exponential and sum in fp64; Acc = float in fp32.
+// position.  Each split writes its sum p*V (rep heads x 128) and its sums
+// of p to its own slot of the partials with atomic exchanges, waits for
+// them to be performed and arrives at its KV head's counter; the last split
+// to arrive adds the slots in split order (no two splits add to one
+// address, so the sums do not depend on arrival order) and writes o and l
+// for the consumer (the o projection's walk, which divides x = o / l), or,
+// for the standalone call, out = o / l (sumScores32, aux.cl:370-384).  The
+// split's K and V rows are loaded once per workgroup, 16 bytes per thread,
+// into LDS.  With the projection accumulators as input the workgroup also
+// applies RoPE to q and k (rope_mx, aux.cl:227-248, table row of the
+// position) and the split holding the position appends the new K and V rows
+// to the cache (attention.hpp:281-309) and uses them from LDS.  Acc = double
+// evaluates every product (exact: fp32 x fp16), exponential and sum in fp64
+// (a score above log(DBL_MAX) ~ 709.78 overflows, as the reference's fp32
+// exp does above 88.72); Acc = float in fp32.
 constexpr int kAttnChunk = 64;
 constexpr int kAttnMaxRep = 8;
 constexpr int kMaxAttnSplits = 128;   // max_ctx up to 8192
@@ -488,7 +493,8 @@ __global__ void k_embed(const uint16_t* __restrict__ table, int cols, int vocab,
 // --------------------------------------------------------------- argmax ---
 // first index of the maximum (std::max_element, test_generation.cpp:235)
 __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ v, int n,
-                                                 int* __restrict__ out, int* __restrict__ pos_inc)
+                                                 int* __restrict__ out, int* __restrict__ pos_inc,
+                                                 int* __restrict__ hist, int hist_len)
 {
     __shared__ float sv[16];
     __shared__ int si[16];
@@ -521,8 +527,13 @@ __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ v, in
                 bv = sv[w];
                 bi = si[w];
             }
-        out[0] = bi < n ? bi : 0;
-        if (pos_inc) pos_inc[0] += 1;
+        const int tok = bi < n ? bi : 0;
+        out[0] = tok;
+        if (pos_inc) {
+            const int np = pos_inc[0] + 1;
+            if (hist && np >= 0 && np < hist_len) hist[np] = tok;
+            pos_inc[0] = np;
+        }
     }
 }
 
@@ -628,9 +639,9 @@ int embed(Ctx* c, const uint16_t* table, int cols, int vocab, const int* tok, fl
                   out);
 }
 
-int argmax(Ctx* c, const float* v, int n, int* out, int* pos_inc)
+int argmax(Ctx* c, const float* v, int n, int* out, int* pos_inc, int* hist, int hist_len)
 {
-    return launch(c, "argmax", k_argmax, dim3(1), dim3(1024), 0, v, n, out, pos_inc);
+    return launch(c, "argmax", k_argmax, dim3(1), dim3(1024), 0, v, n, out, pos_inc, hist, hist_len);
 }
 
 }  // namespace iam

@@ -56,6 +56,9 @@ struct iam_model {
     uint16_t* embed = nullptr;
     uint16_t* final_gain = nullptr;
     iam::Mat lm;
+    // the reference's dense fp16 LM head [vocab][dim] (caller-owned), used
+    // instead of the bucket-layout one when set
+    const uint16_t* lm_dense = nullptr;
     uint16_t* kcache = nullptr;
     uint16_t* vcache = nullptr;
     float* rope = nullptr;
@@ -304,6 +307,16 @@ static int step(iam_model* m, float effort, const float* hidden_override, float*
             g.zero_n[0] = D;
             IAM_TRY(walk_group(c, g));
         }
+    }
+    // ---- final norm + the reference's dense LM head (model.hpp:181-227,
+    // matmul16x32) + greedy pick
+    if (m->lm_dense) {
+        const float* hlast = m->hb + (size_t)(C.n_layers - 1) * D;
+        IAM_TRY(resnorm(c, hlast, m->acc_d, m->hidden, m->final_gain, D, C.norm_eps, m->hn));
+        IAM_TRY(matmul_f16_dense(c, m->lm_dense, m->hn, C.vocab, D, logits_out));
+        if (pick) IAM_TRY(argmax(c, logits_out, C.vocab, m->token, m->pos, m->hist, C.max_ctx + 1));
+        IAM_TRY(zero_async(c, m->acc_d, acc_bytes(D)));
+        return IAM_OK;
     }
     // ---- final norm + LM head (model.hpp:181-227) + greedy pick
     {
@@ -743,6 +756,17 @@ int iam_model_set_position(iam_model* m, int pos)
     IAM_TRY(launch(m->c, "set_int", k_set_int, dim3(1), dim3(1), 0, m->pos, pos));
     m->host_pos = pos;
     return IAM_OK;
+}
+
+int iam_model_set_lm_dense(iam_model* m, const uint16_t* lm_dense)
+{
+    if (!m) return fail(IAM_E_INVALID, "set_lm_dense: null model");
+    if (lm_dense) {
+        IAM_TRY(check_dev_range(m->c, lm_dense, (size_t)m->cfg.vocab * m->cfg.dim * 2, "set_lm_dense matrix"));
+        IAM_REQUIRE(((uintptr_t)lm_dense & 7) == 0, "set_lm_dense: the matrix must be 8-byte aligned");
+    }
+    m->lm_dense = lm_dense;
+    return drop_graph(m);   // the captured step depends on it
 }
 
 int iam_model_set_embed_scale(iam_model* m, const float* scale_host)

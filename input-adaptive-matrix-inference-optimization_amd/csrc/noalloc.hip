@@ -118,9 +118,10 @@ extern "C" int iam_bucketmul_fused_noalloc(iam_ctx* c, int n, const iam_bucket_m
     if (outputs > kNaOutputs)
         return fail(IAM_E_INVALID, "bucketmul_noalloc: " + std::to_string(outputs) +
                                        " outputs exceed the scratch limit of " + std::to_string(kNaOutputs));
-    WalkPlan plan[kMaxMulti];
-    plan_walk(n, ops, effort, plan);
-    for (int i = 0; i < n; i++) IAM_REQUIRE(plan[i].P <= kNaSlices, "bucketmul_noalloc: more than 1024 slices");
+    // the slices of the plan the launch runs (its selection blocks and tile width)
+    WalkGroup tg;
+    const int P = max_slices(n, ops, effort, sel_block_for(c, effort), walk_tile_cols(tg));
+    IAM_REQUIRE(P <= kNaSlices, "bucketmul_noalloc: more than 1024 slices");
     // the same argument checks as iam_bucketmul_fused
     for (int i = 0; i < n; i++) {
         const iam_bucket_matrix& M = mats[i];

@@ -151,6 +151,12 @@ class Ctx:
         dt = np.dtype(dtype)
         return DevBuf(self, max(n * dt.itemsize, 1), dt, (n,))
 
+    def mem_status(self):
+        """(bytes allocated through this context, usable bytes)."""
+        a, u = C.c_size_t(), C.c_size_t()
+        check(lib().iam_mem_status(self.h, C.byref(a), C.byref(u)))
+        return a.value, u.value
+
     def sync(self):
         check(lib().iam_sync(self.h))
 
@@ -316,6 +322,21 @@ class Ctx:
         check(lib().iam_attention_decode(self.h, _vp(q), _vp(kc), _vp(vc), _vp(pos_dev), n_heads,
                                          n_kv, head_dim, max_ctx, _vp(out)))
 
+    def rope_kv_append_f32(self, q, k, v, table, pos_dev, n_heads, n_kv, head_dim, max_ctx, q_out, kc, vc):
+        """RoPE + append into the reference's fp32 cache layout (K and V
+        repeated to every query head)."""
+        check(lib().iam_rope_kv_append_f32(self.h, _vp(q), _vp(k), _vp(v), _vp(table), _vp(pos_dev),
+                                           n_heads, n_kv, head_dim, max_ctx, _vp(q_out), _vp(kc), _vp(vc)))
+
+    def attention_f32(self, q, kc, vc, pos_dev, n_heads, head_dim, max_ctx, out):
+        """The reference's fp32 attention over its repeated-head fp32 caches."""
+        check(lib().iam_attention_decode_f32(self.h, _vp(q), _vp(kc), _vp(vc), _vp(pos_dev), n_heads,
+                                             head_dim, max_ctx, _vp(out)))
+
+    def matmul_f16_dense(self, w, x, rows, cols, out):
+        """matmul16x32: the reference's dense fp16 GEMV."""
+        check(lib().iam_matmul_f16_dense(self.h, _vp(w), _vp(x), rows, cols, _vp(out)))
+
     def embed(self, table, cols, vocab, token_dev, out):
         check(lib().iam_embed_gather(self.h, _vp(table), cols, vocab, _vp(token_dev), _vp(out)))
 
@@ -383,6 +404,11 @@ class Model:
 
     def set_position(self, pos):
         check(lib().iam_model_set_position(self.h, int(pos)))
+
+    def set_lm_dense(self, w_dev):
+        """The LM head as the reference's dense fp16 product over w_dev
+        ([vocab][dim] fp16 on the device); None: the bucket layout."""
+        check(lib().iam_model_set_lm_dense(self.h, None if w_dev is None else _vp(w_dev)))
 
     def set_embed_scale(self, scale):
         if scale is None:

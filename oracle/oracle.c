@@ -31,6 +31,16 @@
  *                                        one-hot x; x = 0
  *   orc_rmsnorm_gain, orc_silu_mul,
  *   orc_rope, orc_attention_f16kv ...... textbook numpy float64 forms
+ *   orc_attention_f32rep ............... one position (output = that V row
+ *                                        exactly), equal keys (the mean of V),
+ *                                        the textbook float64 form, dyadic
+ *                                        scores (exact tree sums), and the
+ *                                        overflow to NaN above 88.72
+ *   orc_rope_kv_rep32 .................. orc_rope + an index-wise repeat
+ *   orc_matmul_f16_dense ............... numpy float64 GEMV, exact sums on
+ *                                        dyadic inputs, one-hot x (a column
+ *                                        copy), and a reordering that a
+ *                                        wrong tree gives
  *   orc_rope_table ..................... numpy float32 cos/sin of the same
  *                                        angles (within 1 ulp)
  *   orc_argmax ......................... numpy argmax (first maximum)
@@ -639,8 +649,9 @@ void orc_add(const float* a, const float* b, int n, float* out)
 /* dotSetScore2 (aux.cl:497-540): s = q.k / sqrt(hd); sum_of_exps32_mx +
  * softmax_add32_mx (aux.cl:204-225): p = exp(s)/sum exp(s); sumScores32
  * (aux.cl:370-384): o = sum_t p v_t.  Query head h reads KV head
- * h / (n_heads/n_kv) (repeat4x32, aux.cl:266-275).  The max is subtracted
- * before exp, which leaves p unchanged in exact arithmetic. */
+ * h / (n_heads/n_kv) (repeat4x32, aux.cl:266-275).  Evaluated in fp64 with
+ * no maximum subtracted before exp, as the reference does (so a score above
+ * log(DBL_MAX) ~ 709.78 overflows to inf and the head's outputs are NaN). */
 void orc_attention_f16kv(const float* q, const uint16_t* kcache, const uint16_t* vcache,
                          int n_tok, int n_heads, int n_kv, int head_dim, float* out)
 {
@@ -652,17 +663,15 @@ void orc_attention_f16kv(const float* q, const uint16_t* kcache, const uint16_t*
         double* sc = (double*)malloc(sizeof(double) * (size_t)(n_tok > 0 ? n_tok : 1));
         int kv = h / rep;
         const float* qh = q + (size_t)h * head_dim;
-        double mx = -INFINITY;
         for (int t = 0; t < n_tok; t++) {
             const uint16_t* k = kcache + ((size_t)t * n_kv + kv) * head_dim;
             double d = 0.0;
             for (int j = 0; j < head_dim; j++) d += (double)qh[j] * (double)orc_f16_to_f32(k[j]);
             sc[t] = d * inv;
-            if (sc[t] > mx) mx = sc[t];
         }
         double den = 0.0;
         for (int t = 0; t < n_tok; t++) {
-            sc[t] = exp(sc[t] - mx);
+            sc[t] = exp(sc[t]);
             den += sc[t];
         }
         for (int j = 0; j < head_dim; j++) {
@@ -674,6 +683,109 @@ void orc_attention_f16kv(const float* q, const uint16_t* kcache, const uint16_t*
             out[(size_t)h * head_dim + j] = (float)(acc / den);
         }
         free(sc);
+    }
+}
+
+/* The reference's own attention path in fp32 over its cache layout: K and V
+ * repeated to every query head, [ctx][n_heads][head_dim] fp32 per layer
+ * (model.hpp:97-98, attention.hpp:281-309).
+ *   dotSetScore2 (aux.cl:497-540): the head_dim products q[d]*k[d] summed by
+ *     the work-group tree (stride head_dim/2 down to 1: p[i] += p[i+stride]),
+ *     then divided by sqrt((float)head_dim);
+ *   sum_of_exps32_mx (aux.cl:204-210): e_t = exp(s_t), no maximum
+ *     subtracted; the reference adds them with float atomics in whatever
+ *     order the work-items run.  Here the order is fixed: the positions in
+ *     splits of ORC_ATT32_SPLIT, each split summed in position order, then
+ *     the splits in order;
+ *   softmax_add32_mx (aux.cl:219-225): p_t = exp(s_t) / sum;
+ *   sumScores32 (aux.cl:370-384): o[d] = sum_t p_t * v_t[d] in fp32; the
+ *     reference runs one sequential loop, here each split's products are
+ *     summed in position order and the splits' sums added in split order.
+ * Every operation is one IEEE fp32 operation (no contraction); expf is the C
+ * library's.  A score above log(FLT_MAX) ~ 88.72 makes e_t inf and the
+ * head's outputs NaN, as in the reference. */
+void orc_attention_f32rep(const float* q, const float* kcache, const float* vcache, int n_tok,
+                          int n_heads, int head_dim, float* out)
+{
+    const float root = sqrtf((float)head_dim);
+    const int nsplit = (n_tok + ORC_ATT32_SPLIT - 1) / ORC_ATT32_SPLIT;
+    #pragma omp parallel for schedule(static)
+    for (int h = 0; h < n_heads; h++) {
+        float* e = (float*)malloc(sizeof(float) * (size_t)(n_tok > 0 ? n_tok : 1));
+        float* lp = (float*)malloc(sizeof(float) * (size_t)head_dim);
+        const float* qh = q + (size_t)h * head_dim;
+        for (int t = 0; t < n_tok; t++) {
+            const float* k = kcache + ((size_t)t * n_heads + h) * head_dim;
+            for (int d = 0; d < head_dim; d++) lp[d] = qh[d] * k[d];
+            for (int st = head_dim / 2; st > 0; st >>= 1)
+                for (int i = 0; i < st; i++) lp[i] = lp[i] + lp[i + st];
+            e[t] = expf(lp[0] / root);
+        }
+        float total = 0.0f;
+        for (int j = 0; j < nsplit; j++) {
+            float ss = 0.0f;
+            for (int t = j * ORC_ATT32_SPLIT; t < n_tok && t < (j + 1) * ORC_ATT32_SPLIT; t++) ss = ss + e[t];
+            total = total + ss;
+        }
+        for (int d = 0; d < head_dim; d++) {
+            float o = 0.0f;
+            for (int j = 0; j < nsplit; j++) {
+                float part = 0.0f;
+                for (int t = j * ORC_ATT32_SPLIT; t < n_tok && t < (j + 1) * ORC_ATT32_SPLIT; t++) {
+                    const float p = e[t] / total;
+                    const float pv = p * vcache[((size_t)t * n_heads + h) * head_dim + d];
+                    part = part + pv;
+                }
+                o = o + part;
+            }
+            out[(size_t)h * head_dim + d] = o;
+        }
+        free(e);
+        free(lp);
+    }
+}
+
+/* The reference's KV append for its own cache layout (attention.hpp:172-189,
+ * :281-309): RoPE of k (rope_mx on the repeated heads; every repeat of a KV
+ * head has the same values), then K and V of KV head h / rep stored for
+ * every query head h at position pos, fp32 [n_heads][head_dim]; q rotated
+ * into q_out. */
+void orc_rope_kv_rep32(const float* q, const float* k, const float* v, const float* table_row,
+                       int n_heads, int n_kv, int head_dim, float* q_out, float* k_row, float* v_row)
+{
+    int rep = n_heads / n_kv;
+    float* kr = (float*)malloc(sizeof(float) * (size_t)n_kv * head_dim);
+    orc_rope(q, table_row, n_heads, head_dim, q_out);
+    orc_rope(k, table_row, n_kv, head_dim, kr);
+    for (int h = 0; h < n_heads; h++) {
+        memcpy(k_row + (size_t)h * head_dim, kr + (size_t)(h / rep) * head_dim, sizeof(float) * (size_t)head_dim);
+        memcpy(v_row + (size_t)h * head_dim, v + (size_t)(h / rep) * head_dim, sizeof(float) * (size_t)head_dim);
+    }
+    free(kr);
+}
+
+/* matmul16x32 (aux.cl:454-490, called with 256 work-items per row at
+ * model.hpp:207-227): row r of the dense fp16 matrix times x.  Work-item l
+ * of the row sums w[l + 256k] * x[l + 256k] over k in order (a fp32 product,
+ * then a fp32 add: no contraction), then the 256 partial sums go through the
+ * work-group tree (stride 128 down to 1: p[l] += p[l + stride]). */
+void orc_matmul_f16_dense(const uint16_t* W, const float* x, int rows, int cols, float* out)
+{
+    #pragma omp parallel for schedule(static)
+    for (int r = 0; r < rows; r++) {
+        float part[ORC_DENSE_WG];
+        const uint16_t* w = W + (size_t)r * cols;
+        for (int l = 0; l < ORC_DENSE_WG; l++) {
+            float s = 0.0f;
+            for (int i = l; i < cols; i += ORC_DENSE_WG) {
+                const float pr = orc_f16_to_f32(w[i]) * x[i];
+                s = s + pr;
+            }
+            part[l] = s;
+        }
+        for (int st = ORC_DENSE_WG / 2; st > 0; st >>= 1)
+            for (int l = 0; l < st; l++) part[l] = part[l] + part[l + st];
+        out[r] = part[0];
     }
 }
 
@@ -744,8 +856,9 @@ void orc_layer_forward(const orc_model* m, int layer, int pos, float effort, flo
     free(att); free(o); free(g); free(u); free(s);
 }
 
-/* MistralModel::forward, model.hpp:152-231; the LM head goes through the
- * bucket layout at the same effort. */
+/* MistralModel::forward, model.hpp:152-231; the LM head is the reference's
+ * dense matmul16x32 when m->lm_dense is set, otherwise the bucket layout at
+ * the same effort. */
 void orc_model_forward(const orc_model* m, int token, int pos, float effort,
                        const float* hidden_in, float* logits)
 {
@@ -756,7 +869,8 @@ void orc_model_forward(const orc_model* m, int token, int pos, float effort,
     else orc_embed(m->embed, c->dim, token, h);
     for (int l = 0; l < c->n_layers; l++) orc_layer_forward(m, l, pos, effort, h);
     orc_rmsnorm_gain(h, m->final_gain, c->dim, c->norm_eps, hn);
-    mat_apply(&m->lm_head, hn, effort, logits);
+    if (m->lm_dense) orc_matmul_f16_dense(m->lm_dense, hn, c->vocab, c->dim, logits);
+    else mat_apply(&m->lm_head, hn, effort, logits);
     free(h);
     free(hn);
 }

@@ -115,9 +115,23 @@ void orc_embed(const uint16_t* table, int cols, int token, float* out);
 /* add32 (bucketMul.cl:517-520) */
 void orc_add(const float* a, const float* b, int n, float* out);
 /* decode attention (aux.cl:370-540; attention.hpp:311-404) over an fp16 GQA
- * cache K,V [ctx_cap][n_kv][hd] for positions 0..n_tok-1.  fp64 accumulation. */
+ * cache K,V [ctx_cap][n_kv][hd] for positions 0..n_tok-1.  fp64 evaluation,
+ * exp(s) with no maximum subtracted (as the reference). */
 void orc_attention_f16kv(const float* q, const uint16_t* kcache, const uint16_t* vcache,
                          int n_tok, int n_heads, int n_kv, int head_dim, float* out);
+/* the reference's fp32 attention over its repeated-head cache layout
+ * K, V [ctx_cap][n_heads][head_dim] fp32 (model.hpp:97-98) for positions
+ * 0..n_tok-1, in the fixed order of splits of ORC_ATT32_SPLIT positions */
+#define ORC_ATT32_SPLIT 64
+void orc_attention_f32rep(const float* q, const float* kcache, const float* vcache, int n_tok,
+                          int n_heads, int head_dim, float* out);
+/* RoPE of q and k, and the K/V rows of one position repeated to n_heads heads
+ * (attention.hpp:172-189, :281-309); k_row and v_row are [n_heads][head_dim] */
+void orc_rope_kv_rep32(const float* q, const float* k, const float* v, const float* table_row,
+                       int n_heads, int n_kv, int head_dim, float* q_out, float* k_row, float* v_row);
+/* matmul16x32 (aux.cl:454-490) with 256 work-items per row (model.hpp:207-227) */
+#define ORC_DENSE_WG 256
+void orc_matmul_f16_dense(const uint16_t* W, const float* x, int rows, int cols, float* out);
 /* argmax, first maximum (test_generation.cpp:235, 276) */
 int orc_argmax(const float* v, int n);
 
@@ -146,6 +160,8 @@ typedef struct {
     orc_matrix lm_head;         /* bucket layout */
     uint16_t *kcache, *vcache;  /* [n_layers][max_ctx][n_kv][hd] fp16 */
     float* rope;                /* [max_ctx][64][2] */
+    const uint16_t* lm_dense;   /* [vocab][dim] fp16: when set, the reference's dense
+                                   head (matmul16x32) instead of lm_head */
 } orc_model;
 
 /* one decode step; writes logits[vocab]; the KV cache at pos is written.

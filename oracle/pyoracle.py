@@ -50,7 +50,7 @@ class Layer(C.Structure):
 class Model(C.Structure):
     _fields_ = [("cfg", ModelConfig), ("layers", C.c_void_p), ("embed", C.c_void_p),
                 ("final_gain", C.c_void_p), ("lm_head", Matrix), ("kcache", C.c_void_p),
-                ("vcache", C.c_void_p), ("rope", C.c_void_p)]
+                ("vcache", C.c_void_p), ("rope", C.c_void_p), ("lm_dense", C.c_void_p)]
 
 
 def lib():
@@ -107,6 +107,9 @@ def lib():
     L.orc_embed.argtypes = [u16p, C.c_int, C.c_int, f32p]
     L.orc_add.argtypes = [f32p, f32p, C.c_int, f32p]
     L.orc_attention_f16kv.argtypes = [f32p, u16p, u16p, C.c_int, C.c_int, C.c_int, C.c_int, f32p]
+    L.orc_attention_f32rep.argtypes = [f32p, f32p, f32p, C.c_int, C.c_int, C.c_int, f32p]
+    L.orc_rope_kv_rep32.argtypes = [f32p, f32p, f32p, f32p, C.c_int, C.c_int, C.c_int, f32p, f32p, f32p]
+    L.orc_matmul_f16_dense.argtypes = [u16p, f32p, C.c_int, C.c_int, f32p]
     L.orc_argmax.restype = C.c_int
     L.orc_argmax.argtypes = [f32p, C.c_int]
     L.orc_set_selection_block.argtypes = [C.c_int, C.c_float]
@@ -278,6 +281,38 @@ def attention_f16kv(q, kcache, vcache, n_tok, n_heads, n_kv, head_dim):
     return out
 
 
+def attention_f32rep(q, kcache, vcache, n_tok, n_heads, head_dim):
+    """The reference's fp32 attention over K, V [ctx][n_heads][head_dim] fp32
+    (every query head's own copy of its KV head's rows)."""
+    out = np.empty(n_heads * head_dim, dtype=np.float32)
+    lib().orc_attention_f32rep(np.ascontiguousarray(q, np.float32),
+                               np.ascontiguousarray(kcache, np.float32).ravel(),
+                               np.ascontiguousarray(vcache, np.float32).ravel(), n_tok, n_heads, head_dim, out)
+    return out
+
+
+def rope_kv_rep32(q, k, v, table_row, n_heads, n_kv, head_dim):
+    """(q after RoPE, the K row and the V row of one position repeated to
+    n_heads heads), all fp32."""
+    qo = np.empty(n_heads * head_dim, np.float32)
+    kr = np.empty(n_heads * head_dim, np.float32)
+    vr = np.empty(n_heads * head_dim, np.float32)
+    lib().orc_rope_kv_rep32(np.ascontiguousarray(q, np.float32), np.ascontiguousarray(k, np.float32),
+                            np.ascontiguousarray(v, np.float32),
+                            np.ascontiguousarray(table_row, np.float32).ravel(), n_heads, n_kv, head_dim,
+                            qo, kr, vr)
+    return qo, kr, vr
+
+
+def matmul_f16_dense(W, x):
+    """matmul16x32: W uint16 (fp16 bits) [rows][cols] times x fp32 [cols]."""
+    W = np.ascontiguousarray(W, np.uint16)
+    rows, cols = W.shape
+    out = np.empty(rows, np.float32)
+    lib().orc_matmul_f16_dense(W.ravel(), np.ascontiguousarray(x, np.float32), rows, cols, out)
+    return out
+
+
 def argmax(v):
     return lib().orc_argmax(np.ascontiguousarray(v, np.float32), len(v))
 
@@ -291,7 +326,9 @@ class OracleModel:
 
     MATS = ["wq", "wk", "wv", "wo", "w1", "w3", "w2"]
 
-    def __init__(self, cfg, read):
+    def __init__(self, cfg, read, lm_dense=None):
+        """lm_dense: the dense fp16 LM head [vocab][dim] (uint16), used by the
+        forward instead of the bucket layout (matmul16x32)."""
         self.keep = []
         self.cfg = dict(cfg)
         c = self.cfg
@@ -313,15 +350,17 @@ class OracleModel:
         mod.layers = C.cast(layers, C.c_void_p)
         mod.embed = self._p(read("embed", np.uint16))
         mod.final_gain = self._p(read("final_gain", np.uint16))
-        mod.lm_head.buckets = self._p(read("lm_head.buckets", np.uint16))
-        mod.lm_head.stats = self._p(read("lm_head.stats", np.uint16))
-        mod.lm_head.probes = self._p(read("lm_head.probes", np.uint16))
+        if lm_dense is None:
+            mod.lm_head.buckets = self._p(read("lm_head.buckets", np.uint16))
+            mod.lm_head.stats = self._p(read("lm_head.stats", np.uint16))
+            mod.lm_head.probes = self._p(read("lm_head.probes", np.uint16))
         mod.lm_head.in_dim, mod.lm_head.out_dim = c["dim"], c["vocab"]
         kv = c["n_layers"] * c["max_ctx"] * c["n_kv_heads"] * c["head_dim"]
         self.kc = np.zeros(kv, np.uint16)
         self.vc = np.zeros(kv, np.uint16)
         mod.kcache, mod.vcache = self._p(self.kc), self._p(self.vc)
         mod.rope = self._p(rope_table(c["rope_theta"], c["head_dim"], c["max_ctx"]))
+        mod.lm_dense = None if lm_dense is None else self._p(np.ascontiguousarray(lm_dense, np.uint16))
         self.mod = mod
 
     def _p(self, a):

@@ -118,7 +118,9 @@ def test_generate_from_converted_checkpoint(O, converted):
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr
     toks = [int(v) for v in r.stdout.split("tokens:")[1].split("\n")[0].split()]
-    orc = O.OracleModel(CFG, lambda name, dtype: np.ascontiguousarray(t[name]).view(dtype).ravel())
+    # the drop-in model's default head: the reference's dense lm_head.npy (matmul16x32)
+    orc = O.OracleModel(CFG, lambda name, dtype: np.ascontiguousarray(t[name]).view(dtype).ravel(),
+                        lm_dense=f16["lm"].view(np.uint16))
     seq = list(prompt)
     for pos in range(len(prompt) + n_new - 1):
         lo = orc.forward(seq[pos], pos, 0.25)

@@ -9,7 +9,11 @@ cutoff bits, selected-row count and y (within 1 ulp); TransformerLayer
 (Attention then FeedForward) over six positions gives the oracle layer's
 output (within 1 ulp); MistralModel greedy
 generation (graph replay and eager host argmax) gives the oracle model's
-tokens, with the dense LM head bucketized on load."""
+tokens, with the reference's dense LM head and with it bucketized on load;
+and a caller written with the reference's own call sites
+(tests/dropin/reference_callsites.cpp: loader construction, BucketMul,
+fp32 caches of the reference's layout, TransformerLayer, MistralModel)
+checked stage by stage against the oracle."""
 import os
 import subprocess
 
@@ -20,6 +24,7 @@ pytestmark = pytest.mark.gpu
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 DROPIN = os.path.join(ROOT, "input-adaptive-matrix-inference-optimization_amd", "bin", "iam_dropin")
+CALLSITES = os.path.join(ROOT, "tests", "dropin", "reference_callsites")
 CFG = dict(n_layers=1, dim=4096, ffn_dim=4096, n_heads=32, n_kv_heads=8, head_dim=128, vocab=256,
            max_ctx=16, rope_theta=10000.0, norm_eps=1e-5)
 NAMES = {"wq": "q", "wk": "k", "wv": "v", "wo": "o", "w1": "gate", "w3": "up", "w2": "down"}
@@ -57,16 +62,25 @@ def weights(O, tmp_path_factory):
     np.save(os.path.join(d, "embed_tokens.npy"), t["embed"].view(np.float16).reshape(V, D))
     np.save(os.path.join(d, "norm_weight.npy"), t["final_gain"].view(np.float16))
     np.save(os.path.join(d, "lm_head.npy"), lm.view(np.float16))
+    t["lm_dense"] = lm
     lb, ls, lp = O.bucketize(lm)
     t["lm_head.buckets"], t["lm_head.stats"], t["lm_head.probes"] = lb, ls, lp
     return d, t
 
 
-def run(args):
-    assert os.path.exists(DROPIN), "bin/iam_dropin not built (run __graft_entry__.build())"
-    r = subprocess.run([DROPIN] + args, capture_output=True, text=True, timeout=120)
+def run(args, exe=DROPIN):
+    assert os.path.exists(exe), f"{exe} not built (run __graft_entry__.build())"
+    r = subprocess.run([exe] + args, capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr
     return r.stdout
+
+
+def ulps(a, b):
+    ia = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    ib = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    ia = np.where(ia < 0, -(ia & 0x7FFFFFFF), ia)
+    ib = np.where(ib < 0, -(ib & 0x7FFFFFFF), ib)
+    return np.abs(ia - ib)
 
 
 def test_bucketmul_from_reference_files(O, weights, tmp_path):
@@ -88,18 +102,22 @@ def test_bucketmul_from_reference_files(O, weights, tmp_path):
     assert np.abs(np.where(iy < 0, -(iy & 0x7FFFFFFF), iy) - np.where(io < 0, -(io & 0x7FFFFFFF), io)).max() <= 1
 
 
+@pytest.mark.parametrize("lm", ["dense", "bucket"])
 @pytest.mark.parametrize("eager", [False, True])
-def test_generate_from_reference_files(O, weights, eager):
+def test_generate_from_reference_files(O, weights, eager, lm):
+    """MistralModel greedy generation with the reference's dense LM head
+    (the default) or the bucket-layout head: the oracle model's tokens."""
     d, t = weights
     prompt = [3, 141, 59, 26]
     n_new = 6
     args = ["generate", "-d", d, "-p", ",".join(map(str, prompt)), "-n", str(n_new), "-e", "0.25",
-            "--max-ctx", str(CFG["max_ctx"]), "--theta", "10000"]
+            "--max-ctx", str(CFG["max_ctx"]), "--theta", "10000", "--lm", lm]
     if eager:
         args.append("--eager")
     out = run(args)
     toks = [int(v) for v in out.split("tokens:")[1].split("\n")[0].split()]
-    orc = O.OracleModel(CFG, lambda name, dtype: np.ascontiguousarray(t[name]).view(dtype).ravel())
+    orc = O.OracleModel(CFG, lambda name, dtype: np.ascontiguousarray(t[name]).view(dtype).ravel(),
+                        lm_dense=t["lm_dense"] if lm == "dense" else None)
     seq = list(prompt)
     for pos in range(len(prompt) + n_new - 1):
         lo = orc.forward(seq[pos], pos, 0.25)
@@ -127,3 +145,81 @@ def test_layer_from_reference_files(O, weights, tmp_path, effort):
     iy = y.view(np.int32).astype(np.int64)
     io = want.view(np.int32).astype(np.int64)
     assert np.abs(np.where(iy < 0, -(iy & 0x7FFFFFFF), iy) - np.where(io < 0, -(io & 0x7FFFFFFF), io)).max() <= 1
+
+
+def test_reference_callsites(O, weights, tmp_path):
+    """A program written with the reference's call sites verbatim
+    (BinaryWeightLoader(gpu, dir), loader->load, BufferWrapper uploads,
+    BucketMul::shared()->calcDispatch/mul, fp32 caches
+    [layers][2048][32][128], TransformerLayer::forward, MistralModel::forward
+    with a host argmax; the reference's defaults: 2048 positions, theta 1e6)
+    on reference-format files.  Layer 0 runs positions 0..5 on one input;
+    every stage of the last position is checked on the device's own
+    intermediates: q/k/v and o within 1 ulp of the oracle's bucketMul, RoPE
+    and the repeated-head cache rows bit-exact, the fp32 attention within
+    2e-6 (relative to its largest output), the FFN within 1 ulp, the
+    residual adds and norms bit-exact.  The model's greedy tokens (dense LM
+    head) equal the oracle model's."""
+    d, t = weights
+    P, effort = 5, 0.25
+    h = O.gen_f32(7, 660, 4096, 0.0, 1.0)
+    hin = str(tmp_path / "h.f32")
+    h.tofile(hin)
+    prefix = str(tmp_path / "rc")
+    out = run([d, str(effort), str(P), hin, prefix], exe=CALLSITES)
+    rd = lambda n: np.fromfile(f"{prefix}.{n}.bin", np.float32)
+
+    def bm(w, x):
+        y, _, _, _ = O.bucketmul(x, t[f"layer0.{w}.stats"], t[f"layer0.{w}.probes"], t[f"layer0.{w}.buckets"], effort)
+        return y
+
+    # fp16 helpers on the first 4096 packed entries of q_proj
+    vals = O.f16_to_f32(t["layer0.wq.buckets"].ravel()[:4096] & 0xFFF0).astype(np.float64)
+    pos_sum = int((t["layer0.wq.buckets"].ravel()[:4096] & 0xF).sum())
+    line = out.split("helpers:")[1].split("\n")[0].split()
+    assert np.isclose(float(line[0]), vals.sum(), rtol=1e-6) and int(line[1]) == pos_sum
+    # %.9g round-trips an fp32 value
+    assert np.float32(float(line[2])) == O.f16_to_f32(t["layer0.wq.probes"][:1])[0]
+    # BucketMul::shared(gpu)->calcDispatch + mul on the input itself
+    assert ulps(rd("q_proj"), bm("wq", h)).max() <= 1
+    # the layer's stages at position P
+    hn = O.rmsnorm_gain(h, t["layer0.attn_gain"], 1e-5)
+    for name, w in (("xq", "wq"), ("xk", "wk"), ("xv", "wv")):
+        assert ulps(rd(name), bm(w, hn)).max() <= 1, name
+    table = O.rope_table(1e6, 128, 2048)
+    qr, kr, vr = O.rope_kv_rep32(rd("xq"), rd("xk"), rd("xv"), table[P], 32, 8, 128)
+    kc = rd("kcache").reshape(P + 1, 32, 128)
+    vc = rd("vcache").reshape(P + 1, 32, 128)
+    assert np.array_equal(rd("xq_heads").view(np.uint32), qr.view(np.uint32))
+    assert np.array_equal(kc[P].ravel().view(np.uint32), kr.view(np.uint32))
+    assert np.array_equal(vc[P].ravel().view(np.uint32), vr.view(np.uint32))
+    for p in range(P):   # the same input at every position: the rows of earlier positions
+        _, kp, vp = O.rope_kv_rep32(rd("xq"), rd("xk"), rd("xv"), table[p], 32, 8, 128)
+        np.testing.assert_allclose(kc[p].ravel(), kp, rtol=2e-6, atol=1e-7)
+        np.testing.assert_allclose(vc[p].ravel(), vp, rtol=2e-6, atol=1e-7)
+    att = rd("attn_output")
+    want = O.attention_f32rep(rd("xq_heads"), kc, vc, P + 1, 32, 128)
+    assert np.abs(att - want).max() <= 2e-6 * np.abs(want).max()
+    assert ulps(rd("attn_out"), bm("wo", att)).max() <= 1
+    h_mid = (h + rd("attn_out")).astype(np.float32)
+    fxn = O.rmsnorm_gain(h_mid, t["layer0.ffn_gain"], 1e-5)
+    assert np.array_equal(rd("fxn").view(np.uint32), fxn.view(np.uint32))
+    dn = bm("w2", O.silu_mul(bm("w1", fxn), bm("w3", fxn)))
+    assert ulps(rd("ffn_out"), dn).max() <= 1
+    assert np.array_equal(rd("output").view(np.uint32), (h_mid + rd("ffn_out")).astype(np.float32).view(np.uint32))
+    # MistralModel(gpu, dir): dense LM head, greedy with a host argmax
+    toks = [int(v) for v in out.split("tokens:")[1].split("\n")[0].split()]
+    cfg = dict(CFG, max_ctx=2048, rope_theta=1e6)
+    orc = O.OracleModel(cfg, lambda name, dtype: np.ascontiguousarray(t[name]).view(dtype).ravel(),
+                        lm_dense=t["lm_dense"])
+    prompt = [3, 141, 59, 26]
+    seq = list(prompt)
+    logits = rd("logits").reshape(-1, CFG["vocab"])
+    worst = 0
+    for pos in range(len(prompt) + 4):
+        lo = orc.forward(seq[pos], pos, effort)
+        if pos >= len(prompt) - 1:
+            worst = max(worst, int(ulps(logits[pos - len(prompt) + 1], lo).max()))
+            seq.append(O.argmax(lo))
+    assert toks == seq[len(prompt):]
+    assert worst <= 4, worst

@@ -20,10 +20,17 @@ additions: at most 1 fp32 ulp (1 fp16 ulp for the K/V rows).
 
 Covered: greedy decode from a 512-token prompt to position ~4094 with the
 stages of layers 0, 15 and 31 checked near 512, at 2048 and near 4095
-(effort 0.25); the FFN block through the fused path at efforts 1.0, 0.5,
-0.25 and 0.125; the skew stress (1% of the hidden channels scaled 20x) at
+(effort 0.25), and the hidden state entering every layer checked at one
+position; the FFN block through the fused path at efforts 1.0, 0.5, 0.25
+and 0.125; the skew stress (1% of the hidden channels scaled 20x) at
 positions 4055-4094 over a KV cache filled with N(0,1) values, for 8 channel
-sets at efforts 0.05 and 1.0."""
+sets at efforts 0.05 and 1.0.
+
+Untethered: after a device prefill, the oracle model takes a copy of the
+device's KV cache and token and both sides decode greedily on their own for
+8 steps (test_generation.cpp:231-276) at efforts 0.25 and 1.0: the picked
+tokens must be identical at every step and the logits within 1 ulp of the
+oracle's."""
 import ctypes as C
 
 import numpy as np
@@ -158,6 +165,25 @@ def checked_step(st, effort, layers):
     return pos
 
 
+def test_fullsize_every_layer_input(O, iam, ctx, big):
+    """The hidden state entering each of the 32 layers at one position,
+    against the oracle layer run on the device's input of the layer before
+    (teacher forcing, layer by layer): within 1 ulp."""
+    st = Stages(O, iam, ctx, big)
+    big.reset_caches()
+    prompt = O.gen_tokens(0, 92, 40, CFG["vocab"])
+    big.generate(prompt, 1, 0.25, use_graph=True)
+    pos = checked_step(st, 0.25, [])
+    for L in range(CFG["n_layers"]):
+        h_in = big.read_tensor(f"layer{L}.h_in", np.float32)
+        h_mid = big.read_tensor(f"layer{L}.h_mid", np.float32)
+        out = big.read_tensor(f"layer{L + 1}.h_in" if L + 1 < CFG["n_layers"] else "hidden", np.float32)
+        want_mid = st.attention(L, pos, 0.25, h_in)[0]
+        assert ulps(h_mid, want_mid).max() <= 1, ("attention stage", L)
+        assert ulps(out, st.ffn(L, 0.25, h_mid)).max() <= 1, ("FFN stage", L)
+    print(f"  every layer checked at position {pos}", flush=True)
+
+
 def test_fullsize_synthesized_matrices_match_generator(O, big):
     """Spot check of the device synthesis at full size: layer 31's wk
     (buckets, stats, probes) equals the oracle generator + bucketizer."""
@@ -224,3 +250,40 @@ def test_fullsize_skew_stages(O, iam, ctx, big, effort):
             print(f"  sequence {seq} checked at positions {start}-{start + 1}", flush=True)
     finally:
         big.set_embed_scale(None)
+
+
+@pytest.mark.parametrize("effort", [0.25, 1.0])
+def test_fullsize_untethered_greedy(O, iam, ctx, big, effort):
+    """test_generation.cpp:231-276 at the benchmarked shape with both sides
+    running free: a device prefill of a 512-token prompt, then the oracle
+    model takes the device's KV cache and picked token, and device and
+    oracle each decode 8 greedy steps on their own intermediates.  Tokens
+    identical at every step; logits within 1 ulp."""
+    big.reset_caches()
+    prompt = O.gen_tokens(0, 93, 512, CFG["vocab"])
+    big.generate(prompt, 1, effort, use_graph=True)
+    ctx.sync()
+    pos = int(big.read_tensor("pos", np.int32)[0])
+    tok = int(big.read_tensor("token", np.int32)[0])
+    assert pos == 512
+    orc = O.OracleModel(CFG, big.read_tensor)
+    orc.kc[:] = big.read_tensor("kcache", np.uint16)
+    orc.vc[:] = big.read_tensor("vcache", np.uint16)
+    worst_ulps, worst_rel = 0, 0.0
+    for step in range(8):
+        lo = orc.forward(tok, pos, effort)
+        big.step_device(effort)
+        ctx.sync()
+        lg = big.read_tensor("logits", np.float32)
+        dtok = int(big.read_tensor("token", np.int32)[0])
+        otok = O.argmax(lo)
+        u = int(ulps(lg, lo).max())
+        r = float(np.abs(lg.astype(np.float64) - lo).max() / np.abs(lo).max())
+        worst_ulps, worst_rel = max(worst_ulps, u), max(worst_rel, r)
+        print(f"  effort {effort} position {pos}: token {dtok} (oracle {otok}), logits within {u} ulps, "
+              f"{r:.1e} of the largest", flush=True)
+        assert dtok == otok, (effort, pos)
+        assert u <= 1, (effort, pos, u, r)
+        tok = otok
+        pos += 1
+    print(f"  effort {effort}: 8 free-running steps, largest logit difference {worst_ulps} ulps", flush=True)

@@ -456,6 +456,137 @@ def test_attention_closed_form(O):
     np.testing.assert_allclose(got.reshape(n_heads, hd), want, rtol=1e-5, atol=1e-6)
 
 
+def test_attention_f16kv_has_no_max_subtraction(O):
+    """The reference's softmax exponentiates the scores as they are
+    (aux.cl:204-225): one score above log(DBL_MAX) ~ 709.78 overflows the
+    fp64 evaluation and that head's outputs are NaN (a max-subtracted softmax
+    would stay finite); just below, every output is finite."""
+    hd, n_tok = 128, 3
+    k = np.zeros((n_tok, 1, hd), np.float16)
+    k[1, 0, :] = 1.0
+    v = np.ones((n_tok, 1, hd), np.float16)
+    for qv, finite in ((62.0, True), (63.0, False)):   # s = 128 * qv / sqrt(128): 701.4, 712.7
+        q = np.full(2 * hd, qv, np.float32)
+        q[hd:] = 0.0                                    # head 1: all scores 0
+        got = O.attention_f16kv(q, k.view(np.uint16), v.view(np.uint16), n_tok, 2, 1, hd)
+        assert np.all(np.isfinite(got[:hd])) == finite
+        assert np.all(np.isnan(got[:hd])) == (not finite)
+        np.testing.assert_allclose(got[hd:], 1.0, rtol=1e-7)   # softmax of equal scores over equal rows
+
+
+def _att32_inputs(rng, n_tok, n_heads, hd, scale=1.0):
+    q = rng.normal(0, scale, n_heads * hd).astype(np.float32)
+    k = rng.normal(0, 1, (n_tok, n_heads, hd)).astype(np.float32)
+    v = rng.normal(0, 1, (n_tok, n_heads, hd)).astype(np.float32)
+    return q, k, v
+
+
+def test_attention_f32rep_textbook(O):
+    """Against softmax attention in float64 without a max subtracted, over
+    3 splits of positions (the fixed order of the fp32 sums changes only
+    roundings)."""
+    rng = np.random.default_rng(31)
+    n_heads, hd, n_tok = 4, 128, 150
+    q, k, v = _att32_inputs(rng, n_tok, n_heads, hd, 0.3)
+    got = O.attention_f32rep(q, k, v, n_tok, n_heads, hd).reshape(n_heads, hd)
+    for h in range(n_heads):
+        s = k[:, h].astype(np.float64) @ q[h * hd:(h + 1) * hd].astype(np.float64) / np.sqrt(hd)
+        p = np.exp(s) / np.exp(s).sum()
+        np.testing.assert_allclose(got[h], p @ v[:, h].astype(np.float64), rtol=2e-5, atol=2e-6)
+
+
+def test_attention_f32rep_one_position_and_equal_keys(O):
+    """One position: p = e/e = 1 exactly, so the output is that V row bit for
+    bit.  Equal keys at every position: equal scores, p = 1/n up to
+    rounding, the output is the mean of V."""
+    rng = np.random.default_rng(32)
+    n_heads, hd = 4, 128
+    q, k, v = _att32_inputs(rng, 1, n_heads, hd, 0.3)
+    got = O.attention_f32rep(q, k, v, 1, n_heads, hd)
+    assert np.array_equal(got.view(np.uint32), v.ravel().view(np.uint32))
+    n_tok = 200
+    q, k, v = _att32_inputs(rng, n_tok, n_heads, hd, 0.3)
+    k[:] = k[0]
+    got = O.attention_f32rep(q, k, v, n_tok, n_heads, hd).reshape(n_heads, hd)
+    np.testing.assert_allclose(got, v.astype(np.float64).mean(axis=0), rtol=1e-5, atol=1e-6)
+
+
+def test_attention_f32rep_score_tree_order(O):
+    """dotSetScore2 adds the products by the work-group tree (p[i] +=
+    p[i + stride] for stride 64 .. 1, aux.cl:519-525).  Products 2^27 at
+    d = 0, 1 at d = 64 and -2^27 at d = 1: the tree forms 2^27 + 1 = 2^27
+    first (an fp32 rounding) and ends at 0, where a sequential sum ends at 1.
+    With a zero V row for the other position the output is p * v, and
+    p = e0 / (e0 + e1) with e0 = exp(0) = 1 tells the score apart."""
+    hd = 128
+    q = np.zeros(hd, np.float32)
+    k = np.zeros((2, 1, hd), np.float32)
+    q[0], k[0, 0, 0] = 2.0 ** 14, 2.0 ** 13
+    q[64], k[0, 0, 64] = 1.0, 1.0
+    q[1], k[0, 0, 1] = -(2.0 ** 14), 2.0 ** 13
+    v = np.zeros((2, 1, hd), np.float32)
+    v[0, 0, :] = 1.0
+    got = O.attention_f32rep(q, k, v, 2, 1, hd)
+    # position 0 scores 0 (the tree), position 1 scores 0: p0 = 1 / 2 exactly
+    assert np.all(got == np.float32(0.5))
+
+
+def test_attention_f32rep_overflow_is_nan(O):
+    """No maximum is subtracted: a score above log(FLT_MAX) ~ 88.72 makes
+    exp(s) inf and the head's outputs NaN (inf / inf), as in the
+    reference; at 88.0 they are finite."""
+    hd = 128
+    for s_target, finite in ((88.0, True), (89.0, False)):
+        q = np.zeros(hd, np.float32)
+        q[0] = np.float32(s_target * np.sqrt(np.float32(hd)))   # q[0] * k[0] / sqrt(128) ~ s_target
+        k = np.zeros((2, 1, hd), np.float32)
+        k[0, 0, 0] = 1.0
+        v = np.ones((2, 1, hd), np.float32)
+        got = O.attention_f32rep(q, k, v, 2, 1, hd)
+        assert np.all(np.isfinite(got)) == finite
+        assert np.all(np.isnan(got)) == (not finite)
+
+
+def test_rope_kv_rep32(O):
+    """The appended row: RoPE of q and k, K and V repeated to every query
+    head by index (head h reads KV head h // rep, repeat4x32)."""
+    rng = np.random.default_rng(33)
+    n_heads, n_kv, hd = 32, 8, 128
+    t = O.rope_table(10000.0, hd, 8)
+    q = rng.normal(0, 1, n_heads * hd).astype(np.float32)
+    k = rng.normal(0, 1, n_kv * hd).astype(np.float32)
+    v = rng.normal(0, 1, n_kv * hd).astype(np.float32)
+    qo, kr, vr = O.rope_kv_rep32(q, k, v, t[5], n_heads, n_kv, hd)
+    assert np.array_equal(qo.view(np.uint32), O.rope(q, t[5], n_heads, hd).view(np.uint32))
+    kk = O.rope(k, t[5], n_kv, hd).reshape(n_kv, hd)
+    assert np.array_equal(kr.reshape(n_heads, hd), kk[np.arange(n_heads) // 4])
+    assert np.array_equal(vr.reshape(n_heads, hd), v.reshape(n_kv, hd)[np.arange(n_heads) // 4])
+
+
+def test_matmul_f16_dense(O):
+    """matmul16x32: against a float64 GEMV; one-hot x gives the column
+    exactly; and the order of the sums: work-item l adds its columns
+    l, l + 256, ... in order, then the 256-way tree (aux.cl:472-487).  Row
+    products 2^27 (column 0), 1 (column 256) and -2^27 (column 128): work-item
+    0 forms 2^27 + 1 = 2^27, the tree's first level cancels it: 0 (a
+    sequential sum over the columns gives 1)."""
+    rng = np.random.default_rng(34)
+    rows, cols = 48, 4096
+    W = rng.normal(0, 0.02, (rows, cols)).astype(np.float16)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    got = O.matmul_f16_dense(W.view(np.uint16), x)
+    np.testing.assert_allclose(got, W.astype(np.float64) @ x.astype(np.float64), rtol=1e-4, atol=1e-5)
+    e = np.zeros(cols, np.float32)
+    e[777] = 1.0
+    assert np.array_equal(O.matmul_f16_dense(W.view(np.uint16), e), W[:, 777].astype(np.float32))
+    W2 = np.zeros((1, 512), np.float16)
+    x2 = np.zeros(512, np.float32)
+    W2[0, 0], x2[0] = 2048.0, 2.0 ** 16
+    W2[0, 256], x2[256] = 1.0, 1.0
+    W2[0, 128], x2[128] = -2048.0, 2.0 ** 16
+    assert O.matmul_f16_dense(W2.view(np.uint16), x2)[0] == 0.0
+
+
 def test_argmax_first_max(O):
     v = np.array([1, 5, 3, 5, 5, -1], np.float32)
     assert O.argmax(v) == 1 == int(np.argmax(v))
