@@ -454,7 +454,8 @@ __device__ __forceinline__ uint4 load_early16(const void* p)
 // The slice input thread tid holds in the selection: waves 1.. take the
 // first ones and wave 0 the last, so that for slices of up to 64 * (NW - 1)
 // inputs the waves that leave the cutoff search early compute the rows'
-// importances while wave 0 finishes it.  Consecutive inputs stay in
+// importances, and list the rows certain to be selected, while wave 0
+// finishes it.  Consecutive inputs stay in
 // consecutive lanes of one wave (blocks of block mode included).
 template <int NT>
 __device__ __forceinline__ int sel_input(int tid)
@@ -553,44 +554,43 @@ __device__ __forceinline__ void select_prepare(const SelSrc& d, int i0, int ni, 
 // selected iff its importance >= cutoff (NaN never is), so the selected set
 // is the dispatch kernel's.  Block mode (blk > 1): rank k of every input of
 // a block is selected when rank k of any of them passes (block_select), rows
-// outside the expert excepted.  A scan over the waves in input order (waves
-// 1.., then 0) compacts the selected rows in ascending order into s_row
-// (slice-local ids input*16 + rank).  Ends with a barrier; returns the
-// number of selected rows.
-template <int NT>
-__device__ __forceinline__ uint32_t select_finish(float cutoff, const float (&imp)[16], uint32_t vbits,
-                                                  uint16_t* s_row, uint32_t* s_wsum, int blk)
+// outside the expert excepted.  The rows of the thread's input that are
+// selected and were not listed before (importance below `listed`: NaN when
+// none were), as a 16-bit mask (bit k: rank k).
+__device__ __forceinline__ uint32_t select_mask(float cutoff, float listed, const float (&imp)[16], uint32_t vbits,
+                                                int blk)
 {
-    constexpr int NW = NT / 64;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int li = sel_input<NT>(tid);
     uint32_t mask = 0;
 #pragma unroll
     for (int kk = 0; kk < 16; kk++)
-        if (imp[kk] >= cutoff) mask |= 1u << kk;   // bucketMul.cl:380
+        if (imp[kk] >= cutoff && !(imp[kk] >= listed)) mask |= 1u << kk;   // bucketMul.cl:380
     mask &= vbits;
     if (blk > 1) mask = block_select(mask, blk, vbits != 0u) & vbits;
-    const uint32_t cnt = (uint32_t)__popc(mask);
-    const uint32_t incl = (uint32_t)wave_incl_sum((int)cnt);
-    if (lane == 63) s_wsum[wave] = incl;
-    __syncthreads();
-    uint32_t off = incl - cnt;
-    uint32_t n_sel = 0;
-#pragma unroll
-    for (int w = 0; w < NW; w++) {
-        const uint32_t c = s_wsum[w];
-        if (w >= 1 && (w < wave || wave == 0)) off += c;   // waves before this one in input order
-        n_sel += c;
-    }
+    return mask;
+}
+
+// The wave's rows of `mask` (bit k: row rowb + k of the thread's input)
+// appended to the slice's row list: one LDS atomic reserves the wave's
+// slots, and each lane writes its rows there, ascending, after those of the
+// lanes before it (a DPP prefix sum), so that rows next to each other in the
+// weights stay together in the list and a walk load's rows share DRAM pages.
+// Where the waves' blocks stand in the list is free (each row's products are
+// added wherever it stands); its length is *cnt once every wave has
+// appended (after a barrier).
+__device__ __forceinline__ void wave_append_rows(uint32_t mask, uint32_t rowb, uint16_t* list, uint32_t* cnt)
+{
+    const int c = __popc(mask);
+    const int incl = wave_incl_sum(c);
+    const int total = __builtin_amdgcn_readlane(incl, 63);
+    if (total == 0) return;
+    uint32_t base = 0;
+    if ((threadIdx.x & 63) == 0) base = atomicAdd(cnt, (uint32_t)total);
+    uint32_t off = __builtin_amdgcn_readfirstlane(base) + (uint32_t)(incl - c);
     while (mask) {
         const int kk = __ffs(mask) - 1;
         mask &= mask - 1;
-        s_row[off++] = (uint16_t)(li * 16 + kk);
+        list[off++] = (uint16_t)(rowb | (uint32_t)kk);
     }
-    __syncthreads();
-    return n_sel;
 }
 
 // first maximum (test_generation.cpp:235, 276) of (value, index) pairs
@@ -650,14 +650,15 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     using Tile = double;
     __shared__ __align__(16) Tile tiles[TSLOTS];   // the tile copies, then the staging copy
     // the search's scratch (the windowed search's, or the radix search's
-    // when that one declines), then the selected rows
-    constexpr int kSearchA = sizeof(SearchLds<NW>) > sizeof(WindowLds<NW>) ? sizeof(SearchLds<NW>) : sizeof(WindowLds<NW>);
-    constexpr int kSearchBytes = kSearchA > NT * 16 * 2 ? kSearchA : NT * 16 * 2;
+    // when that one declines)
+    constexpr int kSearchBytes = sizeof(SearchLds<NW>) > sizeof(WindowLds<NW>) ? sizeof(SearchLds<NW>) : sizeof(WindowLds<NW>);
     __shared__ __align__(16) uint4 s_search[(kSearchBytes + 15) / 16];
-    uint16_t* s_row = reinterpret_cast<uint16_t*>(s_search);
+    // the slice's selected rows (slice-local ids input*16 + rank), in the
+    // order the waves append them, and their number
+    __shared__ __align__(16) uint16_t s_row[NT * 16];
+    __shared__ uint32_t s_nrow;
     __shared__ __align__(16) float s_x[NT];
     __shared__ float s_part[256];
-    __shared__ uint32_t s_wsum[NW];
     __shared__ int s_last;
     __shared__ float s_bv[NW];
     __shared__ int s_bi[NW];
@@ -750,6 +751,7 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
             if (i * NT + tid < kTileVecs) tz[i * NT + tid] = make_uint4(0u, 0u, 0u, 0u);
     }
     if (mode != kInCutoff) window_clear<NW>(WL);
+    if (tid == 0) s_nrow = 0u;
     // the block's slice and column tile (from the descriptor read through k)
     const int w = b;
     const int p = w / d.T;
@@ -791,36 +793,51 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
         }
     }
 
-    // ---- cutoff, and the importances of the slice's rows (computed while
-    // wave 0 finishes the search).  The windowed search leaves the cutoff in
-    // every wave, and each wave's last read of its scratch precedes the
-    // selection's first barrier, after which the scratch becomes the row
-    // list.  When it declines, the radix search runs.
+    // ---- cutoff, and the slice's rows.  While wave 0 finishes the windowed
+    // search, the other waves compute the importances of their inputs' rows
+    // and (per-row selection) append the rows certain to be selected, those
+    // whose importance reaches the window's upper bound hi > cutoff
+    // (cutoff_upper), to the row list; once the cutoff is known every wave
+    // appends its other selected rows, and one barrier publishes the list.
+    // When the windowed search declines, the radix search runs.
     float imp[16];
     uint32_t vbits;
+    float listed = __int_as_float(0x7fc00000);   // this wave's rows from this importance up are listed
+    const uint32_t rowb = (uint32_t)sel_input<NT>(tid) << 4;
     if (mode != kInCutoff) {
         float v[VPT];
         importances<VPT>(xs, pw, v);
         if (!norm) __syncthreads();   // the window's histograms are clear (the norm's barrier orders them otherwise)
         float cut_w;
-        const int found = search_window<NW>(v, quantile, WL, cut_w,
-                                             [&] { select_prepare<NT>(ss, i0, ni, L, s_x, slice_regs, imp, vbits); });
+        const int found = search_window<NW>(v, quantile, WL, cut_w, [&](float hi) {
+            select_prepare<NT>(ss, i0, ni, L, s_x, slice_regs, imp, vbits);
+            // wave 0 comes here at the end of the search: its rows wait for the cutoff
+            if (wave != 0 && a.sel_block == 1) {
+                uint32_t m = 0;
+#pragma unroll
+                for (int kk = 0; kk < 16; kk++)
+                    if (imp[kk] >= hi) m |= 1u << kk;
+                wave_append_rows(m & vbits, rowb, s_row, &s_nrow);
+                listed = hi;
+            }
+        });
         if (found == 1) {
             cutoff = cut_w;
         } else {
             __syncthreads();   // every wave is done with the window's scratch
             search_cutoff<NW>(v, quantile, SL);
             if (found == 0) select_prepare<NT>(ss, i0, ni, L, s_x, slice_regs, imp, vbits);
-            __syncthreads();   // wave 0 has stored the cutoff; the search scratch becomes the row list
+            __syncthreads();   // wave 0 has stored the cutoff
             cutoff = SL.cut;
         }
         if (w == 0 && tid == 0) d.cutoff[0] = cutoff;
     } else {
         select_prepare<NT>(ss, i0, ni, L, s_x, slice_regs, imp, vbits);
+        __syncthreads();   // the list's count is clear before any wave appends
     }
-
-    // ---- selection of the slice's rows
-    const int ns = (int)select_finish<NT>(cutoff, imp, vbits, s_row, s_wsum, a.sel_block);
+    wave_append_rows(select_mask(cutoff, listed, imp, vbits, a.sel_block), rowb, s_row, &s_nrow);
+    __syncthreads();
+    const int ns = (int)s_nrow;
     if (t == 0 && tid == 0) {
         d.slice_count[p] = (uint32_t)ns;
         if (a.counters) {

@@ -163,7 +163,7 @@ __device__ __forceinline__ float replay_rounds(const float (&U)[5], int t, float
 // needs the cutoff in every wave reads L.cut after a barrier.  The scratch
 // may be reused after that barrier.
 template <int NW>
-__device__ float search_cutoff(const float (&v)[IAM_PROBES_COUNT / (64 * NW)], int quantile, SearchLds<NW>& L)
+__device__ __forceinline__ float search_cutoff(const float (&v)[IAM_PROBES_COUNT / (64 * NW)], int quantile, SearchLds<NW>& L)
 {
 #pragma clang fp contract(off)
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
@@ -358,8 +358,10 @@ __device__ float search_cutoff(const float (&v)[IAM_PROBES_COUNT / (64 * NW)], i
 //      u_kmin .. u_kmax; otherwise the keys of those fine bins are gathered
 //      (two more barriers) and ranked.  Either way u_{t-2} .. u_{t+2} come
 //      out exactly, and wave 0 replays the reference's rounds from them
-//      while the other waves run the caller's `prep`; a barrier then hands
-//      the cutoff to all.
+//      while the other waves run the caller's `overlap(hi)` (wave 0 runs it
+//      after its tail) with hi > cutoff from the window of B (cutoff_upper),
+//      so that rows certain to be selected can be listed while the search
+//      finishes; a barrier then hands the cutoff to all.
 // It declines (in every wave at the same step) when the importances hold no
 // number, a key below +0, or a list longer than kListCap; search_cutoff then
 // finds the cutoff.  Histograms are read with one lane per NB consecutive
@@ -516,11 +518,41 @@ __device__ __forceinline__ void window_finish(WindowLds<NW>& W, const float (&U)
     }
 }
 
-// Returns 1 with the cutoff in every wave (prep has run in every wave), 0
-// when declined before prep ran, 2 when declined after it.
-template <int NW, typename Prep>
-__device__ int search_window(const float (&v)[IAM_PROBES_COUNT / (64 * NW)], int quantile, WindowLds<NW>& W,
-                             float& cut, Prep&& prep)
+// An upper bound of the cutoff known once the coarse bin dhi of rank
+// kmin = t - 2 is (t >= 3).  With u_j the j-th largest importance, gmin /
+// gmax their range and the bracket [min, max] of the rounds, the reference's
+// outcomes are (bucketMul.cl:131-213):
+//   count == t            returns b with u_{t+1} <= b < u_t;
+//   |maxCount-minCount|<3 returns b = the moved end: if max moved, count(b)
+//                         >= minCount - 2 >= t - 2, so b < u_{t-2}; if min
+//                         moved, count(b) >= t, so b < u_t;
+//   max - min < 1e-5      returns an end of a bracket holding u_t (min < u_t
+//                         <= max): b lies within 1e-5 (the fp32 test, so
+//                         within 1.0001e-5 exactly) of u_t;
+//   20 rounds             returns the midpoint of a bracket holding u_t
+//                         whose width is at most (gmax - gmin) 2^-20 +
+//                         ulp(gmax) (each fp32 midpoint rounds by at most
+//                         half an ulp of the sum).
+// With delta = max(1.0001e-5, (gmax - gmin) 2^-20 + gmax 2^-23) and
+// u_t <= u_{t-2}: cutoff < u_{t-2} + delta, and u_{t-2} lies below the upper
+// edge of bin dhi, so with the sum rounded up
+//   cutoff < edge(dhi + 1) + delta = hi,
+// and every row whose importance reaches hi is selected.  Where t < 3, or an
+// importance is infinite, there is no bound: hi = NaN, which no importance
+// reaches (not even +inf).
+__device__ __forceinline__ float cutoff_upper(int t, int dhi, uint32_t kmn, uint32_t kmx)
+{
+    if (t < 3 || kmx >= 0xff800000u) return __int_as_float(0x7fc00000);   // kmx: the key of +inf
+    const double gmn = (double)key_float(kmn), gmx = (double)key_float(kmx);
+    const double dl = fmax(1.0001e-5, (gmx - gmn) * 0x1p-20 + gmx * 0x1p-23);
+    return __double2float_ru((double)__uint_as_float((uint32_t)(dhi + 1) << 20) + dl);
+}
+
+// Returns 1 with the cutoff in every wave (overlap has run in every wave),
+// 0 when declined before it ran, 2 when declined after it.
+template <int NW, typename Overlap>
+__device__ __forceinline__ int search_window(const float (&v)[IAM_PROBES_COUNT / (64 * NW)], int quantile, WindowLds<NW>& W,
+                             float& cut, Overlap&& overlap)
 {
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     constexpr int VPT = IAM_PROBES_COUNT / (64 * NW);
@@ -639,7 +671,7 @@ __device__ int search_window(const float (&v)[IAM_PROBES_COUNT / (64 * NW)], int
             }
         }
     }
-    prep();
+    overlap(cutoff_upper(t, dhi, kmn, kmx));
     __syncthreads();
     const int step2 = W.step;
     if (step2 == kWinDone) {

@@ -1,0 +1,118 @@
+"""The walk lists the rows certain to be selected before the cutoff is known:
+those whose importance reaches an upper bound hi > cutoff taken from the
+coarse window of the cutoff search (cutoff_upper in csrc/search.h).  Here
+the bound is restated in numpy and checked against the oracle's bisection
+(bucketMul.cl:68-214) on adversarial importance vectors at quantiles across
+the range, edge ranks included: every cutoff lies strictly below hi.  The
+same bound with its slack term removed fails on some of these vectors, so
+the cases reach the bound's edge.  On the GPU the bucket-walk parity tests
+(selected count and outputs against the oracle) cover the device's use of
+it."""
+import numpy as np
+
+f32 = np.float32
+N = 4096   # importances per search (the probes)
+
+
+def keys(v):
+    """Order-preserving 32-bit keys of numbers >= +0; NaN -> 0."""
+    b = v.view(np.uint32).astype(np.uint64)
+    k = np.where(b >> 31, ~b & 0xFFFFFFFF, b | 0x80000000)
+    return np.where(np.isnan(v), 0, k).astype(np.uint64)
+
+
+def key_float(k):
+    k = int(k)
+    b = (k & 0x7FFFFFFF) if (k & 0x80000000) else (~k & 0xFFFFFFFF)
+    return float(np.uint32(b).view(np.float32))
+
+
+def round_up(x):
+    """double -> the smallest float >= x"""
+    f = f32(x)
+    return f if float(f) >= x else np.nextafter(f, f32(np.inf))
+
+
+def upper_bound(imp, t, slack=True):
+    """cutoff_upper: the coarse bin (bits 30..20 of the key) of rank
+    max(1, t - 2) among the numbers, its upper edge plus
+    delta = max(1.0001e-5, (gmax - gmin) 2^-20 + gmax 2^-23), rounded up.
+    None where the device's search declines (no number, a key below +0) or
+    gives no bound (t < 3, an infinite importance)."""
+    k = keys(imp)
+    nums = k[k != 0]
+    if len(nums) == 0 or nums.min() < 0x80000000:
+        return None
+    kmx = int(nums.max())
+    if t < 3 or kmx >= 0xFF800000:
+        return None
+    srt = np.sort(nums)[::-1]
+    kmin = max(1, t - 2)
+    if kmin > len(nums):
+        return None
+    dhi = int(srt[kmin - 1] >> 20) & 2047
+    gmn, gmx = key_float(int(nums.min())), key_float(kmx)
+    dl = max(1.0001e-5, (gmx - gmn) * 2.0**-20 + gmx * 2.0**-23) if slack else 0.0
+    return round_up(float(np.uint32((dhi + 1) << 20).view(np.float32)) + dl)
+
+
+def vectors(rng):
+    n = N
+    yield "normal", np.abs(rng.normal(0, 1, n)).astype(f32) * f32(1600)
+    yield "ties", np.round(np.abs(rng.normal(0, 3, n))).astype(f32)
+    yield "two values", np.where(rng.random(n) < 0.5, f32(1), f32(2)).astype(f32)
+    yield "constant", np.full(n, 5.0, f32)
+    yield "tiny", (np.abs(rng.normal(0, 1, n)) * 1e-30).astype(f32)
+    yield "huge", (np.abs(rng.normal(0, 1, n)) * 1e30).astype(f32)
+    yield "60 decades", (10.0 ** rng.uniform(-30, 30, n)).astype(f32)
+    yield "mostly zero", np.where(rng.random(n) < 0.7, f32(0), np.abs(rng.normal(0, 1, n)).astype(f32))
+    yield "adjacent floats", (f32(1000) + np.arange(n) * f32(2**-13)).astype(f32)
+    yield "eighths", (np.round(np.abs(rng.normal(0, 1, n)) * 8) / 8).astype(f32)
+    yield "bimodal", np.concatenate([np.abs(rng.normal(0, 1, n // 2)), 1e4 + np.abs(rng.normal(0, 1, n // 2))]).astype(f32)
+    yield "range 1e-5", (f32(1) + rng.random(n).astype(f32) * f32(1e-5)).astype(f32)
+    yield "subnormal", (rng.random(n) * 1e-40).astype(f32)
+    v = np.abs(rng.normal(0, 1, n)).astype(f32)
+    v[rng.random(n) < 0.1] = np.nan
+    yield "10% NaN", v
+    v = np.abs(rng.normal(0, 1, n)).astype(f32)
+    v[rng.random(n) < 0.99] = np.nan
+    yield "99% NaN", v
+
+
+def quantiles(rng):
+    fixed = [0, 1, 2, 3, 4, 100, 1000, 2047, 3071, 3583, 3890, 4090, 4092, 4093, 4094, 4095]
+    return sorted(set(fixed + [int(q) for q in rng.integers(0, N, 6)]))
+
+
+def test_certain_rows_bound_holds(O):
+    rng = np.random.default_rng(7)
+    checked, tightest = 0, np.inf
+    for rep in range(8):
+        for name, imp in vectors(rng):
+            rng.shuffle(imp)
+            for q in quantiles(rng):
+                hi = upper_bound(imp, N - q)
+                if hi is None:
+                    continue
+                c = O.find_cutoff_imp(imp, q)
+                assert np.isfinite(c), (name, q, c)
+                assert c < hi, (name, q, c, hi)
+                if c > 0:
+                    tightest = min(tightest, (float(hi) - float(c)) / float(c))
+                checked += 1
+    assert checked > 1500
+    print(f"  {checked} cases, smallest relative gap hi - cutoff: {tightest:.2e}")
+
+
+def test_bound_without_slack_fails_somewhere(O):
+    """The upper edge of the coarse bin alone is no bound: a cutoff can lie
+    up to the bisection's final bracket width above u_{t-2}."""
+    rng = np.random.default_rng(8)
+    broken = 0
+    for name, imp in vectors(rng):
+        rng.shuffle(imp)
+        for q in quantiles(rng):
+            hi = upper_bound(imp, N - q, slack=False)
+            if hi is not None and not (O.find_cutoff_imp(imp, q) < hi):
+                broken += 1
+    assert broken > 0
