@@ -194,13 +194,17 @@ __global__ void k_rope_kv(const float* __restrict__ q, const float* __restrict__
 // softmax_add32_mx, aux.cl:204-225: the reference's softmax has no maximum
 // subtracted, so the splits' sums add up directly); then lane (g, j)
 // accumulates 8 dimensions of the wave's half of sum p*V over every eighth
-// position.  Each split writes its sum p*V (rep heads x 128) and its sums
-// of p to its own slot of the partials with atomic exchanges, waits for
-// them to be performed and arrives at its KV head's counter; the last split
-// to arrive adds the slots in split order (no two splits add to one
-// address, so the sums do not depend on arrival order) and writes o and l
-// for the consumer (the o projection's walk, which divides x = o / l), or,
-// for the standalone call, out = o / l (sumScores32, aux.cl:370-384).  The
+// position.  The splits' sums p*V (rep heads x 128) and sums of p then
+// meet in o and l for the consumer (the o projection's walk, which divides
+// x = o / l), or, for the standalone call, out = o / l (sumScores32,
+// aux.cl:370-384).  In the model, while a KV head has at most
+// atomic_splits splits, each split adds its sums into o and l with fp64
+// atomics (the sums within an fp64 rounding of the exact ones, whatever the
+// order).  Otherwise each split writes its sums to its own slot of the
+// partials with atomic exchanges, waits for them to be performed and
+// arrives at its KV head's counter; the last split to arrive adds the slots
+// in split order (no two splits add to one address, so the sums do not
+// depend on arrival order) and writes o and l, or out.  The
 // split's K and V rows are loaded once per workgroup, 16 bytes per thread,
 // into LDS.  With the projection accumulators as input the workgroup also
 // applies RoPE to q and k (rope_mx, aux.cl:227-248, table row of the
@@ -276,11 +280,17 @@ struct AttnArgs {
     uint32_t* head_ctr;      // [n_kv] arrival counters, zero on entry (left zero)
     void* zero_p;            // accumulator words cleared by this launch
     int zero_n;
+    int atomic_splits;       // model: splits per KV head up to which o and l are added with atomics
 };
 
-// LDS copies of the split's K and V rows: 128 fp16 + 8 fp16 of padding, so
-// that lanes reading 16 bytes of consecutive rows start on different banks.
+// LDS copies of the split's K and V rows.  A 16-byte LDS access is served 16
+// lanes at a time over 64 banks of 4 bytes.  K rows are read one row per
+// lane (the dot products): 128 fp16 + 8 of padding (68 words) puts 16
+// consecutive rows on 16 disjoint groups of 4 banks.  V rows are read 8
+// lanes per row (p.V): 128 fp16 + 64 of padding (96 words, 32 banks apart)
+// puts the two rows of a 16-lane group on disjoint halves of the banks.
 constexpr int kAttnRowStride = 128 + 8;
+constexpr int kAttnVStride = 128 + 64;
 static_assert(kAttnChunk * kAttnRowStride * 2 >= kMaxAttnSplits * kAttnMaxRep * 8,
               "the K rows' LDS holds the softmax-sum partials of the last split");
 
@@ -288,9 +298,9 @@ template <typename Acc>
 __global__ __launch_bounds__(128 * kAttnMaxRep) void k_attn(AttnArgs a, Acc scale)
 {
 #pragma clang fp contract(off)
-    constexpr int HD = 128, RS = kAttnRowStride, DH = HD / 2;
+    constexpr int HD = 128, RS = kAttnRowStride, VS = kAttnVStride, DH = HD / 2;
     __shared__ __align__(16) uint16_t sk[kAttnChunk * RS];
-    __shared__ __align__(16) uint16_t sv[kAttnChunk * RS];
+    __shared__ __align__(16) uint16_t sv[kAttnChunk * VS];
     __shared__ Acc sq[kAttnMaxRep][HD];
     __shared__ Acc ss[2][kAttnMaxRep][kAttnChunk];          // half-dot products
     __shared__ Acc sp[2 * kAttnMaxRep][kAttnChunk];         // p, one copy per wave
@@ -343,9 +353,8 @@ __global__ __launch_bounds__(128 * kAttnMaxRep) void k_attn(AttnArgs a, Acc scal
         for (int u = 0; u < 4; u++) {
             const int idx = b0 + u * nthr + tid;
             if (idx < pieces && !(fresh && t0 + (idx >> 4) == pos)) {
-                const int o = (idx >> 4) * RS + (idx & 15) * 8;
-                *reinterpret_cast<uint4*>(sk + o) = kq[u];
-                *reinterpret_cast<uint4*>(sv + o) = vq[u];
+                *reinterpret_cast<uint4*>(sk + (idx >> 4) * RS + (idx & 15) * 8) = kq[u];
+                *reinterpret_cast<uint4*>(sv + (idx >> 4) * VS + (idx & 15) * 8) = vq[u];
             }
         }
     }
@@ -364,7 +373,7 @@ __global__ __launch_bounds__(128 * kAttnMaxRep) void k_attn(AttnArgs a, Acc scal
         uint16_t* crow = (r == 0 ? a.kc : a.vc) + ((size_t)pos * a.n_kv + kvh) * HD;
         crow[lane] = h0;
         crow[DH + lane] = h1;
-        uint16_t* lrow = (r == 0 ? sk : sv) + (pos - t0) * RS;
+        uint16_t* lrow = r == 0 ? sk + (pos - t0) * RS : sv + (pos - t0) * VS;
         lrow[lane] = h0;
         lrow[DH + lane] = h1;
     }
@@ -404,7 +413,7 @@ __global__ __launch_bounds__(128 * kAttnMaxRep) void k_attn(AttnArgs a, Acc scal
         const int i = g + 8 * u;
         if (i < nt) {
             const Acc pi = sp[r][i];
-            const uint4 vv = *reinterpret_cast<const uint4*>(sv + i * RS + hf * DH + j * 8);
+            const uint4 vv = *reinterpret_cast<const uint4*>(sv + i * VS + hf * DH + j * 8);
             const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
             for (int e = 0; e < 8; e++)
@@ -413,6 +422,19 @@ __global__ __launch_bounds__(128 * kAttnMaxRep) void k_attn(AttnArgs a, Acc scal
     }
 #pragma unroll
     for (int e = 0; e < 8; e++) o[e] = xsum_swap<32>(xsum_swap<16>(xsum8(o[e])));
+    Acc og = o[0];   // lane (g, j): dimension hf*64 + j*8 + g
+#pragma unroll
+    for (int e = 1; e < 8; e++) og = g == e ? o[e] : og;
+    const int ns = (n_tok + kAttnChunk - 1) / kAttnChunk;   // the KV head's splits
+    if (!a.out && ns <= a.atomic_splits) {
+        // few splits: each adds its sums into the accumulators (zero on
+        // entry) with fp64 atomics, which the launch's end makes visible to
+        // the o projection's walk; no partials, no arrival, no last split
+        double* O = reinterpret_cast<double*>(a.acc);
+        atomicAdd(O + (size_t)h * HD + hf * DH + j * 8 + g, (double)og);
+        if (hf == 0 && lane == 0) atomicAdd(O + (size_t)a.n_heads * HD + h, (double)l);
+        return;
+    }
     // the split's partial sums go to its own slot of the partials (no two
     // splits add to one address): lane (g, j) holds dimension
     // hf*64 + j*8 + g at slot position hr*128 + hf*64 + g*8 + j, so a wave
@@ -422,9 +444,6 @@ __global__ __launch_bounds__(128 * kAttnMaxRep) void k_attn(AttnArgs a, Acc scal
     const int PS = attn_part_stride(rep);
     double* part = reinterpret_cast<double*>(a.part);
     double* mine = part + ((size_t)kvh * gridDim.y + split) * PS;
-    Acc og = o[0];
-#pragma unroll
-    for (int e = 1; e < 8; e++) og = g == e ? o[e] : og;
     unsigned long long sink = __hip_atomic_exchange(
         reinterpret_cast<unsigned long long*>(mine + hr * HD + hf * DH + lane),
         (unsigned long long)__double_as_longlong((double)og), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -434,7 +453,6 @@ __global__ __launch_bounds__(128 * kAttnMaxRep) void k_attn(AttnArgs a, Acc scal
                                       __HIP_MEMORY_SCOPE_AGENT);
     asm volatile("" ::"v"(sink));
     __syncthreads();
-    const int ns = (n_tok + kAttnChunk - 1) / kAttnChunk;   // the KV head's splits
     if (tid == 0)
         s_last = __hip_atomic_fetch_add(a.head_ctr + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                  (uint32_t)(ns - 1);
@@ -628,6 +646,7 @@ int attention_launch(Ctx* c, const AttnLaunch& L)
     a.head_ctr = L.head_ctr;
     a.zero_p = L.zero_p;
     a.zero_n = L.zero_n;
+    a.atomic_splits = L.acc && !L.out ? L.atomic_splits : 0;
     const dim3 grid(L.n_kv, n_split), block(128 * (L.n_heads / L.n_kv));
     if (c->acc64) return launch(c, "attention", k_attn<double>, grid, block, 0, a, 1.0 / std::sqrt(128.0));
     return launch(c, "attention", k_attn<float>, grid, block, 0, a, 1.0f / std::sqrt(128.0f));

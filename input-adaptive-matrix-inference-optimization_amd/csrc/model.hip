@@ -251,6 +251,7 @@ static int step(iam_model* m, float effort, const float* hidden_override, float*
             A.head_ctr = m->att_ctr;
             A.zero_p = m->acc_d;
             A.zero_n = D;
+            A.atomic_splits = kAttnAtomicSplits;
             IAM_TRY(attention_launch(c, A));
         }
         // ---- o projection (attention.hpp:198-200)
@@ -292,6 +293,9 @@ static int step(iam_model* m, float effort, const float* hidden_override, float*
             }
             g.fin = kFinSilu;
             g.silu_out = m->s;
+            // the attention sums, read by the o walk: zero for the next layer's adds
+            g.zero_p[0] = m->acc_att;
+            g.zero_n[0] = (int)attention_acc_words(C.n_heads);
             IAM_TRY(walk_group(c, g));
         }
         // ---- down (feedforward.hpp:82-84)
