@@ -41,9 +41,10 @@ The default run also measures the other workloads of the path:
 (`--config1` and `--skew` run longer versions of configs 1 and 5 alone.)
 
 cpu_baseline: the C oracle on all host cores given to it (OpenMP threads),
-timed on a bounded sample (about 12 s: up to 1024 decoder layers at
-consecutive positions, and one LM head pass, of the same model at the same
-effort and context), scaled to tokens per second of the 32-layer model.
+timed on a bounded sample (about 12 s: decoder layers 0, 10, 21 and 31 of
+the same model, each on its own input and KV cache, at the positions of the
+timed GPU tokens and the same effort, and one LM head pass), scaled to
+tokens per second of the 32-layer model.
 
 Profiling modes (no JSON line): `--counter-probe` runs the workload the
 rocprofv3 counter passes read; `--counter-summary` and `--trace-summary`
@@ -181,46 +182,61 @@ def cpu_model():
     return "unknown"
 
 
-def cpu_baseline(model, cfg, pos, effort, budget_s=12.0):
-    """Time the oracle on a bounded sample of the same decode step."""
+CPU_LAYERS = (0, 10, 21, 31)
+
+
+def cpu_baseline(model, cfg, positions, effort, budget_s=12.0):
+    """Time the oracle on a bounded sample of the timed decode: layers 0, 10,
+    21 and 31, each as a one-layer oracle over that layer's weights and its KV
+    cache as the GPU filled it, fed that layer's input of the last GPU step,
+    at the positions [lo, hi) of the timed GPU tokens in turn; then one
+    final-norm + LM-head pass.  The per-layer median scaled to all layers,
+    plus the head, is the time per token."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle as O
 
     c1 = dict(cfg)
     c1["n_layers"] = 1
-
-    def read(name, dtype):
-        if name in ("embed",):
-            return np.zeros(16, dtype)          # unused: the sample feeds hidden states
-        return model.read_tensor(name, dtype)
-
-    orc = O.OracleModel(c1, read)
-    # layer 0's KV cache as filled on the GPU, so attention spans the real context
     kv = cfg["max_ctx"] * cfg["n_kv_heads"] * cfg["head_dim"]
-    orc.kc[:] = model.read_tensor("kcache", np.uint16)[:kv]
-    orc.vc[:] = model.read_tensor("vcache", np.uint16)[:kv]
-    h = model.read_tensor("hidden", np.float32)
-    t_layer = []
-    t0 = time.perf_counter()
-    k = 0
-    k_max = min(1024, cfg["max_ctx"] - pos - 2)   # positions pos .. pos + k stay in the cache
-    while time.perf_counter() - t0 < budget_s * 0.85 and k < k_max:
-        t = time.perf_counter()
-        h = orc.layer_forward(0, pos + k, effort, h)
-        t_layer.append(time.perf_counter() - t)
-        k += 1
-    t = time.perf_counter()
-    orc.forward(0, pos + k, effort, hidden_in=h)          # embed skipped, 1 layer + final norm + LM head
-    t_model1 = time.perf_counter() - t
+    kc_all = model.read_tensor("kcache", np.uint16)
+    vc_all = model.read_tensor("vcache", np.uint16)
+    lo, hi = positions
+    layers = [L for L in CPU_LAYERS if L < cfg["n_layers"]]
+    t_layer, calls = [], []
+    per_layer_s = budget_s * 0.85 / len(layers)
+    for L in layers:
+        def read(name, dtype, L=L):
+            if name == "embed":
+                return np.zeros(16, dtype)          # unused: the sample feeds hidden states
+            if name.startswith("layer0."):
+                name = f"layer{L}." + name[len("layer0."):]
+            return model.read_tensor(name, dtype)
+
+        orc = O.OracleModel(c1, read)
+        orc.kc[:] = kc_all[L * kv:(L + 1) * kv]
+        orc.vc[:] = vc_all[L * kv:(L + 1) * kv]
+        h = model.read_tensor(f"layer{L}.h_in", np.float32)
+        t0 = time.perf_counter()
+        k = 0
+        while time.perf_counter() - t0 < per_layer_s:
+            t = time.perf_counter()
+            orc.layer_forward(0, lo + k % (hi - lo), effort, h)
+            t_layer.append(time.perf_counter() - t)
+            k += 1
+        calls.append(k)
     tl = float(np.median(t_layer))
-    t_lm = max(t_model1 - tl, 0.0)
+    t = time.perf_counter()
+    orc.forward(0, hi - 1, effort, hidden_in=model.read_tensor("hidden", np.float32))   # 1 layer + norm + LM head
+    t_lm = max(time.perf_counter() - t - tl, 0.0)
     per_token = cfg["n_layers"] * tl + t_lm
     threads = O.threads()
     return {"value": round(1.0 / per_token, 4), "unit": "tok/s", "cores": threads, "kind": "port",
             "cpu_model": cpu_model(), "host_cpus": len(os.sched_getaffinity(0)),
-            "sample": f"C oracle, {threads} OpenMP threads: {k} decoder layers at positions {pos}..{pos + k - 1} "
-                      f"(median {tl * 1e3:.1f} ms/layer) + 1 final-norm/LM-head pass "
-                      f"({t_lm * 1e3:.1f} ms), effort {effort}, scaled to {cfg['n_layers']} layers"}
+            "sample": f"C oracle, {threads} OpenMP threads: decoder layers {', '.join(map(str, layers))} "
+                      f"({', '.join(map(str, calls))} calls) at the timed GPU tokens' positions {lo}..{hi - 1}, "
+                      f"each layer fed its own input of the last GPU step (median {tl * 1e3:.1f} ms/layer), "
+                      f"+ 1 final-norm/LM-head pass ({t_lm * 1e3:.1f} ms), effort {effort}, "
+                      f"scaled to {cfg['n_layers']} layers"}
 
 
 CONFIG1_COPIES = 40   # 40 x 32 MB of buckets: past the 256 MB Infinity Cache
@@ -814,7 +830,8 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         t = time.perf_counter()
-        cpu = cpu_baseline(model, cfg, pos_now, args.effort)
+        lo = args.prompt + args.warmup
+        cpu = cpu_baseline(model, cfg, (lo, lo + args.steps), args.effort)
         log(f"cpu baseline: {cpu['value']} tok/s ({time.perf_counter() - t:.1f} s)")
 
     configs = None
