@@ -101,9 +101,9 @@ struct Ctx {
     std::vector<hipEvent_t> event_pool;
     std::map<std::string, KernelStat> stats;
     DispatchSlot slots[kMaxMulti];
-    // attention: accumulators (o per head and dimension, then the softmax
-    // denominator per head; zero between calls) and per-KV-head arrival
-    // counters of the standalone entry point
+    // attention, standalone entry point: the splits' partial sums (o and
+    // the softmax sum per head and split) and the per-head arrival counters
+    // (zero between calls)
     void* attn_acc = nullptr;
     size_t attn_acc_cap = 0;
     uint32_t* attn_ctr = nullptr;
@@ -288,7 +288,7 @@ int max_slices(int n, const MatOp* ops, float effort, int blk, int tc);
 // kInNorm (the norm of h written to ops[0].x)
 int bucketmul_fused(Ctx* c, int n, const MatOp* ops, int expert_no, float effort, int in_mode, const float* h,
                     const uint16_t* gain, float eps);
-int ensure_attn_scratch(Ctx* c, size_t acc_words, int n_kv);
+int ensure_attn_scratch(Ctx* c, size_t acc_words, int n_heads);
 int ensure_attn32_scratch(Ctx* c, size_t floats);
 
 int quantile_of(float effort);

@@ -27,12 +27,12 @@ int silu_mul(Ctx* c, const float* g, const float* u, int n, float* out);
 int rope_kv(Ctx* c, const float* q, const float* k, const float* v, const float* table, const int* pos,
             int n_heads, int n_kv, int hd, int max_ctx, float* q_out, uint16_t* kc, uint16_t* vc);
 // one launch of the split-context attention (see k_attn)
-// Splits per KV head (64 positions each) up to which the model's attention
-// adds its sums with fp64 atomics.  Measured per attention launch (Mistral-7B
-// shape): at 9 splits 7.1 us against 8.3 us for the partials' exchange,
-// arrival and last split's serial sum, at 32 splits 12.9 against 13.5 us,
-// at 61 splits 19.9 against 19.0 us (the chains of adds to one address grow
-// with the splits).
+// Workgroups per head (each a run of consecutive 64-position chunks; at most
+// 16) up to which the model's attention adds its sums with fp64 atomics
+// rather than through partial slots and a last workgroup: 16 same-address
+// adds per output cost less than the exchange, the arrival and the serial
+// sum (measured per launch at 9 and 32 chains: 7.1 against 8.3 us and 12.9
+// against 13.5 us; at 61, 19.9 against 19.0 us).
 constexpr int kAttnAtomicSplits = 40;
 
 struct AttnLaunch {
@@ -44,13 +44,13 @@ struct AttnLaunch {
     const int* pos = nullptr;
     int n_heads = 0, n_kv = 0, max_ctx = 0;
     void* acc = nullptr;               // model: o then l (n_heads * 128 + n_heads doubles)
-    // model: with at most this many splits of the context per KV head, every
-    // split adds its o and l into acc (which must be zero on entry) with fp64
-    // atomics; with more, the last split of each KV head writes the sums
+    // model: with at most this many workgroups per head, every one adds its
+    // o and l into acc (which must be zero on entry) with fp64 atomics; with
+    // more, the last workgroup of each head writes the sums
     int atomic_splits = 0;
     void* part = nullptr;              // the splits' partial sums (attention_part_words doubles)
     float* out = nullptr;              // standalone: out = o / l
-    uint32_t* head_ctr = nullptr;      // [n_kv], zero on entry (left zero)
+    uint32_t* head_ctr = nullptr;      // [n_heads], zero on entry (left zero)
     void* zero_p = nullptr;
     int zero_n = 0;
 };

@@ -184,79 +184,47 @@ __global__ void k_rope_kv(const float* __restrict__ q, const float* __restrict__
 
 // ------------------------------------------------------------ attention ---
 // Decode attention over an fp16 GQA cache, split over the context.
-// Workgroup (kv head, split) handles kAttnChunk = 64 positions for the rep =
-// n_heads/n_kv query heads that read this KV head (repeat4x32,
-// aux.cl:266-275, without materialising the repeat): wave r is query head
-// kvh*rep + r % rep and half r / rep of the head dimension, lane i position
-// t0 + i.  Each lane computes its position's half dot product (dotSetScore2,
-// aux.cl:497-540, s = q.k / sqrt(hd)) with q broadcast from LDS, and the
-// halves are added through LDS; p = exp(s) (sum_of_exps32_mx /
+// Workgroup (query head h, split) handles kAttnChunk = 64 positions of one
+// query head; the heads that read one KV head (repeat4x32, aux.cl:266-275,
+// without materialising the repeat) sit in workgroups whose index is equal
+// modulo n_kv, so with 8 KV heads they run on one XCD and share the K and V
+// rows in its L2.  The split's K and V rows are loaded once per workgroup,
+// 16 bytes per thread, into LDS.  Dot products (dotSetScore2,
+// aux.cl:497-540, s = q.k / sqrt(hd)): lane = position, wave w adds the 16
+// dimensions 16w..16w+15 with q broadcast from LDS, and the waves' sums are
+// added in wave order; wave 0 takes p = exp(s) (sum_of_exps32_mx /
 // softmax_add32_mx, aux.cl:204-225: the reference's softmax has no maximum
-// subtracted, so the splits' sums add up directly); then lane (g, j)
-// accumulates 8 dimensions of the wave's half of sum p*V over every eighth
-// position.  The splits' sums p*V (rep heads x 128) and sums of p then
-// meet in o and l for the consumer (the o projection's walk, which divides
-// x = o / l), or, for the standalone call, out = o / l (sumScores32,
-// aux.cl:370-384).  In the model, while a KV head has at most
-// atomic_splits splits, each split adds its sums into o and l with fp64
-// atomics (the sums within an fp64 rounding of the exact ones, whatever the
-// order).  Otherwise each split writes its sums to its own slot of the
-// partials with atomic exchanges, waits for them to be performed and
-// arrives at its KV head's counter; the last split to arrive adds the slots
-// in split order (no two splits add to one address, so the sums do not
-// depend on arrival order) and writes o and l, or out.  The
-// split's K and V rows are loaded once per workgroup, 16 bytes per thread,
-// into LDS.  With the projection accumulators as input the workgroup also
-// applies RoPE to q and k (rope_mx, aux.cl:227-248, table row of the
-// position) and the split holding the position appends the new K and V rows
-// to the cache (attention.hpp:281-309) and uses them from LDS.  Acc = double
-// evaluates every product (exact: fp32 x fp16), exponential and sum in fp64
-// (a score above log(DBL_MAX) ~ 709.78 overflows, as the reference's fp32
-// exp does above 88.72); Acc = float in fp32.
+// subtracted, so the splits' sums add up directly) and their sum.  p.V:
+// lane l takes dimensions 2l and 2l+1 over the 8 positions 8w..8w+7, and the
+// waves' sums are added in wave order.  The splits' sums p*V and sums of p
+// then meet in o and l for the consumer (the o projection's walk, which
+// divides x = o / l), or, for the standalone call, out = o / l (sumScores32,
+// aux.cl:370-384).  In the model, while a head has at most atomic_splits
+// splits, each split adds its sums into o and l with fp64 atomics (the sums
+// within an fp64 rounding of the exact ones, whatever the order).
+// Otherwise each split writes its sums to its own slot of the partials with
+// atomic exchanges, waits for them to be performed and arrives at its
+// head's counter; the last split to arrive adds the slots in split order
+// (no two splits add to one address, so the sums do not depend on arrival
+// order) and writes o and l, or out.  With the projection accumulators as
+// input the workgroup also applies RoPE to q and k (rope_mx,
+// aux.cl:227-248, table row of the position), and the split holding the
+// position uses the new K and V rows from LDS; the workgroup of the KV
+// head's first query head appends them to the cache (attention.hpp:281-309).
+// Acc = double evaluates every product (exact: fp32 x fp16), exponential and
+// sum in fp64 (a score above log(DBL_MAX) ~ 709.78 overflows, as the
+// reference's fp32 exp does above 88.72); Acc = float in fp32.
 constexpr int kAttnChunk = 64;
 constexpr int kAttnMaxRep = 8;
 constexpr int kMaxAttnSplits = 128;   // max_ctx up to 8192
-// doubles per split and KV head in the partials: o of rep heads, the rep
-// softmax sums, padded to 64 bytes
-__host__ __device__ constexpr int attn_part_stride(int rep) { return rep * 128 + 8; }
-
-// v + v of lane l ^ 8 (a DPP rotation by 8 within each row of 16 lanes)
-__device__ __forceinline__ double xsum8(double v) { return v + dpp_d<0x128>(v, v); }
-__device__ __forceinline__ float xsum8(float v) { return v + dpp_f<0x128>(v, v); }
-
-// v + v of lane l ^ M for M = 16 or 32: v_permlane{16,32}_swap with both
-// operands v returns (v of lane l & ~M, v of lane l | M) in every lane
-template <int M>
-__device__ __forceinline__ void swap_pair(uint32_t w, uint32_t& lo_lane, uint32_t& hi_lane)
-{
-    static_assert(M == 16 || M == 32, "16 or 32");
-    if constexpr (M == 16) {
-        const auto r = __builtin_amdgcn_permlane16_swap(w, w, false, false);
-        lo_lane = r[0];
-        hi_lane = r[1];
-    } else {
-        const auto r = __builtin_amdgcn_permlane32_swap(w, w, false, false);
-        lo_lane = r[0];
-        hi_lane = r[1];
-    }
-}
-template <int M>
-__device__ __forceinline__ double xsum_swap(double v)
-{
-    const unsigned long long b = (unsigned long long)__double_as_longlong(v);
-    uint32_t l0, l1, h0, h1;
-    swap_pair<M>((uint32_t)b, l0, l1);
-    swap_pair<M>((uint32_t)(b >> 32), h0, h1);
-    return __longlong_as_double((long long)(((unsigned long long)h0 << 32) | l0)) +
-           __longlong_as_double((long long)(((unsigned long long)h1 << 32) | l1));
-}
-template <int M>
-__device__ __forceinline__ float xsum_swap(float v)
-{
-    uint32_t a, b;
-    swap_pair<M>(__float_as_uint(v), a, b);
-    return __uint_as_float(a) + __uint_as_float(b);
-}
+constexpr int kAttnThreads = 512;     // 8 waves
+constexpr int kAttnMaxHeads = 512;    // 64 KV heads x 8
+constexpr int kAttnGroups = 16;       // workgroups per head at most (runs of consecutive chunks)
+// workgroups per head of a launch over a context of up to max_ctx positions
+static int attn_runs(int max_ctx) { return std::min((max_ctx + kAttnChunk - 1) / kAttnChunk, kAttnGroups); }
+// doubles per split and query head in the partials: o (128), the softmax
+// sum, padded to 64 bytes
+constexpr int kAttnPartStride = 128 + 8;
 
 template <typename Acc>
 __device__ __forceinline__ Acc acc_exp(Acc x);
@@ -273,229 +241,239 @@ struct AttnArgs {
     uint16_t* vc;            // fp16 V rows, same layout
     const int* pos;
     int n_heads, n_kv, max_ctx;
-    void* acc;               // o [n_heads][128], then l [n_heads] (fp64): written by the last
-                             // split of each KV head (model mode)
-    void* part;              // the splits' partial sums [n_kv][splits][attn_part_stride(rep)] (fp64)
-    float* out;              // standalone: out = o / l, stored by the last split of each KV head
-    uint32_t* head_ctr;      // [n_kv] arrival counters, zero on entry (left zero)
+    void* acc;               // o [n_heads][128], then l [n_heads] (fp64) (model mode)
+    void* part;              // the splits' partial sums [n_heads][splits][kAttnPartStride] (fp64)
+    float* out;              // standalone: out = o / l, stored by the last split of each head
+    uint32_t* head_ctr;      // [n_heads] arrival counters, zero on entry (left zero)
     void* zero_p;            // accumulator words cleared by this launch
     int zero_n;
-    int atomic_splits;       // model: splits per KV head up to which o and l are added with atomics
+    int atomic_splits;       // model: splits per head up to which o and l are added with atomics
 };
 
-// LDS copies of the split's K and V rows.  A 16-byte LDS access is served 16
-// lanes at a time over 64 banks of 4 bytes.  K rows are read one row per
-// lane (the dot products): 128 fp16 + 8 of padding (68 words) puts 16
-// consecutive rows on 16 disjoint groups of 4 banks.  V rows are read 8
-// lanes per row (p.V): 128 fp16 + 64 of padding (96 words, 32 banks apart)
-// puts the two rows of a 16-lane group on disjoint halves of the banks.
+// LDS copies of the split's K and V rows: 128 fp16 + 8 of padding (68
+// words).  A 16-byte LDS access is served 16 lanes at a time over 64 banks
+// of 4 bytes: the dot products read one K row per lane, and 68-word rows
+// put 16 consecutive ones on 16 disjoint groups of 4 banks; p.V reads 4
+// bytes per lane of one V row (64 lanes, 64 banks).
 constexpr int kAttnRowStride = 128 + 8;
-constexpr int kAttnVStride = 128 + 64;
-static_assert(kAttnChunk * kAttnRowStride * 2 >= kMaxAttnSplits * kAttnMaxRep * 8,
-              "the K rows' LDS holds the softmax-sum partials of the last split");
 
 template <typename Acc>
-__global__ __launch_bounds__(128 * kAttnMaxRep) void k_attn(AttnArgs a, Acc scale)
+__global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a, Acc scale)
 {
 #pragma clang fp contract(off)
-    constexpr int HD = 128, RS = kAttnRowStride, VS = kAttnVStride, DH = HD / 2;
+    constexpr int HD = 128, RS = kAttnRowStride, DH = HD / 2, NW = kAttnThreads / 64;
     __shared__ __align__(16) uint16_t sk[kAttnChunk * RS];
-    __shared__ __align__(16) uint16_t sv[kAttnChunk * VS];
-    __shared__ Acc sq[kAttnMaxRep][HD];
-    __shared__ Acc ss[2][kAttnMaxRep][kAttnChunk];          // half-dot products
-    __shared__ Acc sp[2 * kAttnMaxRep][kAttnChunk];         // p, one copy per wave
-    __shared__ double sl[kAttnMaxRep];
+    __shared__ __align__(16) uint16_t sv[kAttnChunk * RS];
+    __shared__ __align__(16) Acc sq[HD];
+    __shared__ Acc ss[NW][kAttnChunk];      // the waves' dot products
+    __shared__ Acc sp[kAttnChunk];          // p
+    __shared__ __align__(16) Acc so[NW][HD];   // the waves' p.V
+    __shared__ double sl;
     __shared__ int s_last;
+    zero_share<double>(a.zero_p, a.zero_n, kAttnThreads);
     const int rep = a.n_heads / a.n_kv;
-    const int nthr = 128 * rep;
-    zero_share<double>(a.zero_p, a.zero_n, nthr);
-    const int kvh = blockIdx.x;
-    const int split = blockIdx.y;
+    const int kvh = blockIdx.x % a.n_kv;
+    const int r = blockIdx.x / a.n_kv;      // this head among the KV head's
+    const int h = kvh * rep + r;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int r = tid >> 6;
-    const int hr = r % rep, hf = r / rep;
+    const int w = tid >> 6;
     const int pos = *a.pos;
     const int n_tok = min(pos + 1, a.max_ctx);
-    const int t0 = split * kAttnChunk;
-    const int nt = min(kAttnChunk, max(0, n_tok - t0));
-    if (nt == 0) return;   // past the context: neither written nor counted
+    // the context's chunks of 64 positions, dealt to at most kAttnGroups
+    // workgroups per head in runs of G consecutive chunks
+    const int nch = (n_tok + kAttnChunk - 1) / kAttnChunk;
+    const int G = (nch + kAttnGroups - 1) / kAttnGroups;
+    const int ng = (nch + G - 1) / G;       // workgroups of this head with chunks
+    const int grp = blockIdx.y;
+    if (grp >= ng) return;                  // past the context: neither written nor counted
+    const int c0 = grp * G, c1 = min(nch, c0 + G);
     const bool pos_ok = pos >= 0 && pos < a.max_ctx;
-    const int h = kvh * rep + hr;
     const double* A = reinterpret_cast<const double*>(a.qkv_acc);
-    const bool fresh = A && pos_ok && pos >= t0 && pos < t0 + kAttnChunk;   // this split holds the new row
+    // waves 0 and 1: q of dimension w*64 + lane; with the accumulators, the
+    // rotation pair (lane, 64 + lane)
     float c = 1.0f, sn = 0.0f;
-    if (A && pos_ok) {
+    if (A && pos_ok && w < 4) {
         c = a.rope[(size_t)pos * HD + 2 * lane];
         sn = a.rope[(size_t)pos * HD + 2 * lane + 1];
     }
-    // q of dimension hf*64 + lane
-    float qv;
-    if (A) {
-        const float lo = (float)A[(size_t)h * HD + lane], hi = (float)A[(size_t)h * HD + DH + lane];
-        qv = hf == 0 ? __fsub_rn(__fmul_rn(lo, c), __fmul_rn(hi, sn))    // rope_mx: d < 64
-                     : __fadd_rn(__fmul_rn(hi, c), __fmul_rn(lo, sn));   // d >= 64
-    } else {
-        qv = a.q[(size_t)h * HD + hf * DH + lane];
-    }
-    // the split's K and V rows (the fresh row comes from the accumulators)
-    const int pieces = nt * (HD / 8);
-    for (int b0 = 0; b0 < pieces; b0 += 4 * nthr) {
-        uint4 kq[4], vq[4];
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int idx = min(b0 + u * nthr + tid, pieces - 1);
-            const size_t g = ((size_t)(t0 + (idx >> 4)) * a.n_kv + kvh) * HD + (idx & 15) * 8;
-            kq[u] = *reinterpret_cast<const uint4*>(a.kc + g);
-            vq[u] = *reinterpret_cast<const uint4*>(a.vc + g);
+    if (w < 2) {
+        float qv;
+        if (A) {
+            const float lo = (float)A[(size_t)h * HD + lane], hi = (float)A[(size_t)h * HD + DH + lane];
+            qv = w == 0 ? __fsub_rn(__fmul_rn(lo, c), __fmul_rn(hi, sn))    // rope_mx: d < 64
+                        : __fadd_rn(__fmul_rn(hi, c), __fmul_rn(lo, sn));   // d >= 64
+        } else {
+            qv = a.q[(size_t)h * HD + w * DH + lane];
         }
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int idx = b0 + u * nthr + tid;
-            if (idx < pieces && !(fresh && t0 + (idx >> 4) == pos)) {
-                *reinterpret_cast<uint4*>(sk + (idx >> 4) * RS + (idx & 15) * 8) = kq[u];
-                *reinterpret_cast<uint4*>(sv + (idx >> 4) * VS + (idx & 15) * 8) = vq[u];
-            }
-        }
+        sq[w * DH + lane] = (Acc)qv;
     }
-    if (fresh && r < 2) {
-        // wave 0: k after RoPE; wave 1: v; both rounded to fp16 into the
-        // cache row and the LDS row
+    // waves 2 and 3 of the run holding the new position: its k (after RoPE)
+    // and v from the accumulators, rounded to fp16; the KV head's first query
+    // head appends them to the cache
+    const bool fresh = A && pos_ok && pos >= c0 * kAttnChunk && pos < c1 * kAttnChunk;
+    uint16_t fr0 = 0, fr1 = 0;
+    if (fresh && w >= 2 && w < 4) {
+        const bool isk = w == 2;
         const int nq = a.n_heads * HD, nk = a.n_kv * HD;
-        const size_t base = (size_t)(r == 0 ? nq : nq + nk) + (size_t)kvh * HD;
+        const size_t base = (size_t)(isk ? nq : nq + nk) + (size_t)kvh * HD;
         const float lo = (float)A[base + lane], hi = (float)A[base + DH + lane];
         float o0 = lo, o1 = hi;
-        if (r == 0) {
+        if (isk) {
             o0 = __fsub_rn(__fmul_rn(lo, c), __fmul_rn(hi, sn));
             o1 = __fadd_rn(__fmul_rn(hi, c), __fmul_rn(lo, sn));
         }
-        const uint16_t h0 = __half_as_ushort(__float2half_rn(o0)), h1 = __half_as_ushort(__float2half_rn(o1));
-        uint16_t* crow = (r == 0 ? a.kc : a.vc) + ((size_t)pos * a.n_kv + kvh) * HD;
-        crow[lane] = h0;
-        crow[DH + lane] = h1;
-        uint16_t* lrow = r == 0 ? sk + (pos - t0) * RS : sv + (pos - t0) * VS;
-        lrow[lane] = h0;
-        lrow[DH + lane] = h1;
-    }
-    sq[hr][hf * DH + lane] = (Acc)qv;
-    __syncthreads();
-    // half dot product of position t0 + lane (four chains of 16 products,
-    // dimensions 4m + c in chain c, then added pairwise), then the two halves
-    // in order
-    {
-        Acc sc[4] = {(Acc)0, (Acc)0, (Acc)0, (Acc)0};
-        const uint4* kr = reinterpret_cast<const uint4*>(sk + min(lane, nt - 1) * RS + hf * DH);
-#pragma unroll
-        for (int i = 0; i < DH / 8; i++) {
-            const uint4 kv = kr[i];
-            const uint32_t w[4] = {kv.x, kv.y, kv.z, kv.w};
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-                sc[e & 3] = fma(sq[hr][hf * DH + i * 8 + e], (Acc)h2f((uint16_t)(w[e >> 1] >> ((e & 1) * 16))),
-                                sc[e & 3]);
-        }
-        ss[hf][hr][lane] = (sc[0] + sc[1]) + (sc[2] + sc[3]);
-    }
-    __syncthreads();
-    const Acc s = (ss[0][hr][lane] + ss[1][hr][lane]) * scale;
-    const Acc p = lane < nt ? acc_exp<Acc>(s) : (Acc)0;
-    const Acc l = wave_sum(p);
-    sp[r][lane] = p;   // read back by this wave only: no barrier
-    // sum of p * V over this half's dimensions: lane (g, j) takes dimensions
-    // hf*64 + 8j..8j+7 of the positions g, g + 8, ...; the eight g partials
-    // are added pairwise across lanes
-    const int g = lane >> 3, j = lane & 7;
-    Acc o[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) o[e] = (Acc)0;
-#pragma unroll
-    for (int u = 0; u < kAttnChunk / 8; u++) {
-        const int i = g + 8 * u;
-        if (i < nt) {
-            const Acc pi = sp[r][i];
-            const uint4 vv = *reinterpret_cast<const uint4*>(sv + i * VS + hf * DH + j * 8);
-            const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-                o[e] = fma(pi, (Acc)h2f((uint16_t)(w[e >> 1] >> ((e & 1) * 16))), o[e]);
+        fr0 = __half_as_ushort(__float2half_rn(o0));
+        fr1 = __half_as_ushort(__float2half_rn(o1));
+        if (r == 0) {
+            uint16_t* crow = (isk ? a.kc : a.vc) + ((size_t)pos * a.n_kv + kvh) * HD;
+            crow[lane] = fr0;
+            crow[DH + lane] = fr1;
         }
     }
+    // K and V pieces (16 bytes) of chunk ch: thread tid takes pieces tid and
+    // tid + 512 (row = piece / 16); pieces past the chunk re-read its last one
+    static_assert(kAttnChunk * (HD / 8) == 2 * kAttnThreads, "two pieces per thread");
+    uint4 ka, kb, va, vb;
+    auto load_chunk = [&](int ch) __attribute__((always_inline)) {
+        const int t0 = ch * kAttnChunk, nt = min(kAttnChunk, n_tok - t0), pieces = nt * (HD / 8);
+        const int i0 = min(tid, pieces - 1), i1 = min(kAttnThreads + tid, pieces - 1);
+        const size_t g0 = ((size_t)(t0 + (i0 >> 4)) * a.n_kv + kvh) * HD + (i0 & 15) * 8;
+        const size_t g1 = ((size_t)(t0 + (i1 >> 4)) * a.n_kv + kvh) * HD + (i1 & 15) * 8;
+        ka = *reinterpret_cast<const uint4*>(a.kc + g0);
+        kb = *reinterpret_cast<const uint4*>(a.kc + g1);
+        va = *reinterpret_cast<const uint4*>(a.vc + g0);
+        vb = *reinterpret_cast<const uint4*>(a.vc + g1);
+    };
+    load_chunk(c0);
+    Acc o0 = (Acc)0, o1 = (Acc)0;   // p.V of dimensions 2*lane, 2*lane + 1 over this wave's positions
+    Acc l = (Acc)0;                  // wave 0: the sum of p
+    for (int ch = c0; ch < c1; ch++) {
+        const int t0 = ch * kAttnChunk, nt = min(kAttnChunk, n_tok - t0), pieces = nt * (HD / 8);
+        // the chunk's rows into LDS (the new row from the accumulators), then
+        // the next chunk's loads go out
+        {
+            const int i0 = tid, i1 = kAttnThreads + tid;
+            if (i0 < pieces && !(fresh && t0 + (i0 >> 4) == pos)) {
+                const int o = (i0 >> 4) * RS + (i0 & 15) * 8;
+                *reinterpret_cast<uint4*>(sk + o) = ka;
+                *reinterpret_cast<uint4*>(sv + o) = va;
+            }
+            if (i1 < pieces && !(fresh && t0 + (i1 >> 4) == pos)) {
+                const int o = (i1 >> 4) * RS + (i1 & 15) * 8;
+                *reinterpret_cast<uint4*>(sk + o) = kb;
+                *reinterpret_cast<uint4*>(sv + o) = vb;
+            }
+        }
+        if (fresh && w >= 2 && w < 4 && pos >= t0 && pos < t0 + kAttnChunk) {
+            uint16_t* lrow = (w == 2 ? sk : sv) + (pos - t0) * RS;
+            lrow[lane] = fr0;
+            lrow[DH + lane] = fr1;
+        }
+        if (ch + 1 < c1) load_chunk(ch + 1);
+        __syncthreads();
+        // dot products: position t0 + lane over dimensions 16w..16w+15 (two
+        // chains, then added), then the waves' sums in wave order
+        {
+            Acc s0 = (Acc)0, s1 = (Acc)0;
+            const uint4* kr = reinterpret_cast<const uint4*>(sk + min(lane, nt - 1) * RS + w * 16);
 #pragma unroll
-    for (int e = 0; e < 8; e++) o[e] = xsum_swap<32>(xsum_swap<16>(xsum8(o[e])));
-    Acc og = o[0];   // lane (g, j): dimension hf*64 + j*8 + g
+            for (int i = 0; i < 2; i++) {
+                const uint4 kv = kr[i];
+                const uint32_t wd[4] = {kv.x, kv.y, kv.z, kv.w};
 #pragma unroll
-    for (int e = 1; e < 8; e++) og = g == e ? o[e] : og;
-    const int ns = (n_tok + kAttnChunk - 1) / kAttnChunk;   // the KV head's splits
-    if (!a.out && ns <= a.atomic_splits) {
-        // few splits: each adds its sums into the accumulators (zero on
-        // entry) with fp64 atomics, which the launch's end makes visible to
-        // the o projection's walk; no partials, no arrival, no last split
+                for (int e = 0; e < 8; e += 2) {
+                    s0 = fma(sq[w * 16 + i * 8 + e], (Acc)h2f((uint16_t)wd[e >> 1]), s0);
+                    s1 = fma(sq[w * 16 + i * 8 + e + 1], (Acc)h2f((uint16_t)(wd[e >> 1] >> 16)), s1);
+                }
+            }
+            ss[w][lane] = s0 + s1;
+        }
+        __syncthreads();
+        if (w == 0) {
+            Acc s = ss[0][lane];
+#pragma unroll
+            for (int v = 1; v < NW; v++) s += ss[v][lane];
+            const Acc p = lane < nt ? acc_exp<Acc>(s * scale) : (Acc)0;
+            sp[lane] = p;
+            l += wave_sum(p);
+        }
+        __syncthreads();
+        // p.V: dimensions 2*lane, 2*lane + 1 over positions t0 + 8w .. t0 + 8w + 7
+#pragma unroll
+        for (int u = 0; u < kAttnChunk / NW; u++) {
+            const int t = w * (kAttnChunk / NW) + u;
+            if (t < nt) {
+                const Acc pt = sp[t];
+                const uint32_t vw = *reinterpret_cast<const uint32_t*>(sv + t * RS + 2 * lane);
+                o0 = fma(pt, (Acc)h2f((uint16_t)vw), o0);
+                o1 = fma(pt, (Acc)h2f((uint16_t)(vw >> 16)), o1);
+            }
+        }
+        __syncthreads();   // the LDS rows and p are read no more in this chunk
+    }
+    so[w][2 * lane] = o0;
+    so[w][2 * lane + 1] = o1;
+    if (tid == 0) sl = (double)l;
+    __syncthreads();
+    // threads 0..127: dimension tid, the waves' sums in wave order
+    Acc ot = (Acc)0;
+    if (tid < HD) {
+        ot = so[0][tid];
+#pragma unroll
+        for (int v = 1; v < NW; v++) ot += so[v][tid];
+    }
+    if (!a.out && ng <= a.atomic_splits) {
+        // each run adds its sums into the accumulators (zero on entry) with
+        // fp64 atomics, which the launch's end makes visible to the o
+        // projection's walk; no partials, no arrival, no last run
         double* O = reinterpret_cast<double*>(a.acc);
-        atomicAdd(O + (size_t)h * HD + hf * DH + j * 8 + g, (double)og);
-        if (hf == 0 && lane == 0) atomicAdd(O + (size_t)a.n_heads * HD + h, (double)l);
+        if (tid < HD) atomicAdd(O + (size_t)h * HD + tid, (double)ot);
+        if (tid == HD) atomicAdd(O + (size_t)a.n_heads * HD + h, sl);
         return;
     }
-    // the split's partial sums go to its own slot of the partials (no two
-    // splits add to one address): lane (g, j) holds dimension
-    // hf*64 + j*8 + g at slot position hr*128 + hf*64 + g*8 + j, so a wave
-    // writes 64 consecutive values; then the softmax sums.  The exchanges
-    // return the old values and the split waits for them before it arrives,
-    // so all are performed where the last split's atomic loads read them.
-    const int PS = attn_part_stride(rep);
+    // the run's sums go to its own slot of the partials (no two runs add to
+    // one address): o at 0..127, the softmax sum at 128.  The exchanges
+    // return the old values and the run waits for them before it arrives, so
+    // all are performed where the last run's atomic loads read them.
+    constexpr int PS = kAttnPartStride;
     double* part = reinterpret_cast<double*>(a.part);
-    double* mine = part + ((size_t)kvh * gridDim.y + split) * PS;
-    unsigned long long sink = __hip_atomic_exchange(
-        reinterpret_cast<unsigned long long*>(mine + hr * HD + hf * DH + lane),
-        (unsigned long long)__double_as_longlong((double)og), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (hf == 0 && lane == 0)
-        sink += __hip_atomic_exchange(reinterpret_cast<unsigned long long*>(mine + rep * HD + hr),
-                                      (unsigned long long)__double_as_longlong((double)l), __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
-    asm volatile("" ::"v"(sink));
+    double* mine = part + ((size_t)h * gridDim.y + grp) * PS;
+    if (tid <= HD) {
+        const double v = tid < HD ? (double)ot : sl;
+        const unsigned long long sink = __hip_atomic_exchange(reinterpret_cast<unsigned long long*>(mine + tid),
+                                                              (unsigned long long)__double_as_longlong(v),
+                                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("" ::"v"(sink));
+    }
     __syncthreads();
     if (tid == 0)
-        s_last = __hip_atomic_fetch_add(a.head_ctr + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                 (uint32_t)(ns - 1);
+        s_last = __hip_atomic_fetch_add(a.head_ctr + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (uint32_t)(ng - 1);
     __syncthreads();
     if (!s_last) return;
-    // the last split of this KV head: the sums over the splits, in split
-    // order, of o (rep heads x 128: one value per thread, 16 splits' loads
-    // in flight) and l (thread t < rep * ns loads split t / rep's value of
-    // head t % rep into LDS, where the first threads add them up)
-    const double* first = part + (size_t)kvh * gridDim.y * PS;
-    const bool has_lp = tid < rep * ns;
-    const double lp = has_lp ? acc_peek(const_cast<double*>(first) + (size_t)(tid / rep) * PS + rep * HD + tid % rep)
-                             : 0.0;
+    // the last run of this head: the sums over the runs, in run order, of o
+    // (threads 0..127) and l (thread 128); at most kAttnGroups loads each
+    const double* first = part + (size_t)h * gridDim.y * PS;
     double to = 0.0;
-    for (int s0 = 0; s0 < ns; s0 += 16) {
-        double vo[16];
+    if (tid <= HD) {
+        double vo[kAttnGroups];
 #pragma unroll
-        for (int u = 0; u < 16; u++)
-            vo[u] = s0 + u < ns ? acc_peek(const_cast<double*>(first) + (size_t)(s0 + u) * PS + tid) : 0.0;
+        for (int u = 0; u < kAttnGroups; u++)
+            vo[u] = u < ng ? acc_peek(const_cast<double*>(first) + (size_t)u * PS + tid) : 0.0;
 #pragma unroll
-        for (int u = 0; u < 16; u++) to += vo[u];
+        for (int u = 0; u < kAttnGroups; u++) to += vo[u];
     }
-    double* s_lp = reinterpret_cast<double*>(sk);   // the K rows are read no more
-    if (has_lp) s_lp[tid] = lp;
-    __syncthreads();
-    if (tid < rep) {
-        double tl = 0.0;
-        for (int sp_ = 0; sp_ < ns; sp_++) tl += s_lp[sp_ * rep + tid];
-        sl[tid] = tl;
-    }
-    // slot position tid -> head and dimension
-    const int hh = tid / HD, pp = tid % HD;
-    const int d = (pp / DH) * DH + (pp % 8) * 8 + (pp % DH) / 8;
-    const size_t oi = (size_t)(kvh * rep + hh) * HD + d;
-    double* O = reinterpret_cast<double*>(a.acc);
+    if (tid == HD) sl = to;
     if (a.out) {
         __syncthreads();
-        a.out[oi] = (float)(to / sl[hh]);
+        if (tid < HD) a.out[(size_t)h * HD + tid] = (float)(to / sl);
     } else {
-        O[oi] = to;
-        if (tid < rep) O[(size_t)a.n_heads * HD + kvh * rep + tid] = sl[tid];
+        double* O = reinterpret_cast<double*>(a.acc);
+        if (tid < HD) O[(size_t)h * HD + tid] = to;
+        if (tid == HD) O[(size_t)a.n_heads * HD + h] = to;
     }
-    if (tid == 0) a.head_ctr[kvh] = 0u;
+    if (tid == 0) a.head_ctr[h] = 0u;
 }
 
 // ---------------------------------------------------------------- embed ---
@@ -622,7 +600,8 @@ size_t attention_acc_words(int n_heads) { return (size_t)n_heads * 128 + (size_t
 
 size_t attention_part_words(int n_heads, int n_kv, int max_ctx)
 {
-    return (size_t)n_kv * (size_t)((max_ctx + kAttnChunk - 1) / kAttnChunk) * attn_part_stride(n_heads / n_kv);
+    (void)n_kv;
+    return (size_t)n_heads * (size_t)attn_runs(max_ctx) * kAttnPartStride;
 }
 
 int attention_launch(Ctx* c, const AttnLaunch& L)
@@ -647,7 +626,8 @@ int attention_launch(Ctx* c, const AttnLaunch& L)
     a.zero_p = L.zero_p;
     a.zero_n = L.zero_n;
     a.atomic_splits = L.acc && !L.out ? L.atomic_splits : 0;
-    const dim3 grid(L.n_kv, n_split), block(128 * (L.n_heads / L.n_kv));
+    IAM_REQUIRE(L.n_heads <= kAttnMaxHeads, "attention: at most 512 query heads");
+    const dim3 grid(L.n_heads, attn_runs(L.max_ctx)), block(kAttnThreads);
     if (c->acc64) return launch(c, "attention", k_attn<double>, grid, block, 0, a, 1.0 / std::sqrt(128.0));
     return launch(c, "attention", k_attn<float>, grid, block, 0, a, 1.0f / std::sqrt(128.0f));
 }
@@ -790,7 +770,7 @@ int iam_attention_decode(iam_ctx* c, const float* q, const uint16_t* kc, const u
     IAM_TRY(check_dev_range(c, vc, (size_t)max_ctx * nk * 2, "attention vcache"));
     IAM_TRY(check_dev_range(c, out, (size_t)n_heads * head_dim * 4, "attention out"));
     IAM_TRY(check_dev_range(c, pos, 4, "attention pos"));
-    IAM_TRY(ensure_attn_scratch(c, attention_part_words(n_heads, n_kv, max_ctx), n_kv));
+    IAM_TRY(ensure_attn_scratch(c, attention_part_words(n_heads, n_kv, max_ctx), n_heads));
     AttnLaunch L{};
     L.q = q;
     L.kc = const_cast<uint16_t*>(kc);

@@ -75,7 +75,7 @@ struct iam_model {
     // accumulators (8 bytes per value): q|k|v, attention o|l, o, gate, up,
     // down, logits; zero between steps
     void* att_part = nullptr;       // attention: the splits' partial sums
-    uint32_t* att_ctr = nullptr;    // attention: arrival counters per KV head
+    uint32_t* att_ctr = nullptr;    // attention: arrival counters per query head
     void *acc_qkv = nullptr, *acc_att = nullptr, *acc_o = nullptr, *acc_g = nullptr, *acc_u = nullptr,
          *acc_d = nullptr, *acc_lm = nullptr;
     uint32_t* tile_ctr = nullptr;   // gate/up tiles, then LM head tiles, then the pick counter
@@ -546,7 +546,7 @@ int iam_model_create(iam_ctx* c, const iam_model_config* cfg, iam_model** out)
     T(alloc_owned(m, acc_bytes(D + 2 * KVD), &m->acc_qkv));
     T(alloc_owned(m, acc_bytes(attention_acc_words(C.n_heads)), &m->acc_att));
     T(alloc_owned(m, acc_bytes(attention_part_words(C.n_heads, C.n_kv_heads, C.max_ctx)), &m->att_part));
-    T(alloc_t(m, (size_t)C.n_kv_heads, &m->att_ctr));
+    T(alloc_t(m, (size_t)C.n_heads, &m->att_ctr));
     T(alloc_owned(m, acc_bytes(D), &m->acc_o));
     T(alloc_owned(m, acc_bytes(F), &m->acc_g));
     T(alloc_owned(m, acc_bytes(F), &m->acc_u));
@@ -636,7 +636,7 @@ int iam_model_reset_caches(iam_model* m)
     IAM_TRY(zero_async(m->c, m->acc_lm, acc_bytes(C.vocab)));
     const int T13 = walk_tiles(F / 16), Tlm = walk_tiles(C.vocab / 16);
     IAM_TRY(zero_async(m->c, m->tile_ctr, ((size_t)T13 + Tlm + 1) * 4));
-    IAM_TRY(zero_async(m->c, m->att_ctr, (size_t)C.n_kv_heads * 4));
+    IAM_TRY(zero_async(m->c, m->att_ctr, (size_t)C.n_heads * 4));
     IAM_CHECK_HIP(hipStreamSynchronize(m->c->stream));
     m->host_pos = 0;
     return IAM_OK;

@@ -115,12 +115,13 @@ int ensure_walk_scratch(Ctx* c, int slot, size_t m, size_t T, size_t P)
     return IAM_OK;
 }
 
-int ensure_attn_scratch(Ctx* c, size_t acc_words, int n_kv)
+int ensure_attn_scratch(Ctx* c, size_t acc_words, int n_heads)
 {
     IAM_TRY(grow_zeroed(c, &c->attn_acc, &c->attn_acc_cap, acc_words, 8, "attention accumulator"));
-    size_t cap = c->attn_ctr ? 64 : 0;
-    IAM_REQUIRE(n_kv <= 64, "attention: at most 64 KV heads");
-    return grow_zeroed(c, (void**)&c->attn_ctr, &cap, 64, sizeof(uint32_t), "attention counter");
+    constexpr size_t kCounters = 512;   // one per query head
+    size_t cap = c->attn_ctr ? kCounters : 0;
+    IAM_REQUIRE(n_heads <= (int)kCounters, "attention: at most 512 query heads");
+    return grow_zeroed(c, (void**)&c->attn_ctr, &cap, kCounters, sizeof(uint32_t), "attention counter");
 }
 
 int begin_launch(Ctx* c, const char* name, PendingEvent* ev)
