@@ -146,11 +146,14 @@ def test_rope_kv_append_and_attention(iam, O, ctx):
 
 
 def test_attention_long_context(iam, O, ctx):
-    """The split merge over every split a context of up to 8192 positions
-    has (128 splits of 64, two per lane of the merging wave), at positions
-    on and off split boundaries, with a 4-query-head GQA and a 1:1 layout."""
+    """Contexts of up to 8192 positions: the 64-position chunks dealt to at
+    most 16 runs per head (1 chunk per run up to 1024 positions, then 2, ...,
+    8 at 8192) and the last run's sum over the runs, at positions on and off
+    chunk and run-length boundaries, with a 4-query-head GQA and a 1:1
+    layout."""
     rng = np.random.default_rng(3)
-    for n_heads, n_kv, max_ctx, positions in ((32, 8, 8192, (4095, 4096, 8191)), (8, 8, 4160, (63, 4159))):
+    for n_heads, n_kv, max_ctx, positions in ((32, 8, 8192, (1023, 1024, 1088, 4095, 4096, 8191)),
+                                              (8, 8, 4160, (63, 4159))):
         hd = 128
         kc = rng.normal(0, 1, (max_ctx, n_kv, hd)).astype(np.float16)
         vc = rng.normal(0, 1, (max_ctx, n_kv, hd)).astype(np.float16)
@@ -164,6 +167,41 @@ def test_attention_long_context(iam, O, ctx):
             assert ulps(dout.read(), want).max() <= 1, (n_heads, n_kv, pos)
             dpos.free()
         for d_ in (dkc, dvc, dq, dout):
+            d_.free()
+
+
+def test_attention_overflow(O, ctx):
+    """No maximum is subtracted (aux.cl:204-225): evaluated in fp64, a score
+    above log(DBL_MAX) ~ 709.78 makes that head's outputs NaN and one just
+    below (701.4) gives the oracle's result; in fp32 (IAM_ACC_FP32) the limit
+    is log(FLT_MAX) ~ 88.72 (87.1 finite, 89.4 NaN).  The other head (all
+    scores 0 over equal V rows) is 1.0 either way."""
+    hd, n_tok, max_ctx = 128, 3, 64
+    k = np.zeros((max_ctx, 1, hd), np.float16)
+    k[1, 0, :] = 1.0
+    v = np.ones((max_ctx, 1, hd), np.float16)
+    dk, dv = ctx.upload(k.view(np.uint16)), ctx.upload(v.view(np.uint16))
+    dpos, dout = ctx.upload(np.array([n_tok - 1], np.int32)), ctx.empty(2 * hd, np.float32)
+    prev = ctx.get_accumulation()
+    try:
+        for acc, cases in (("fp64", ((62.0, True), (63.0, False))), ("fp32", ((7.7, True), (7.9, False)))):
+            ctx.set_accumulation(acc)
+            for qv, finite in cases:   # s = 128 qv / sqrt(128)
+                q = np.full(2 * hd, qv, np.float32)
+                q[hd:] = 0.0
+                dq = ctx.upload(q)
+                ctx.attention(dq, dk, dv, dpos, 2, 1, hd, max_ctx, dout)
+                got = dout.read()
+                assert np.all(np.isfinite(got[:hd])) == finite, (acc, qv)
+                assert np.all(np.isnan(got[:hd])) == (not finite), (acc, qv)
+                np.testing.assert_allclose(got[hd:], 1.0, rtol=1e-6)
+                if acc == "fp64" and finite:
+                    want = O.attention_f16kv(q, k.view(np.uint16), v.view(np.uint16), n_tok, 2, 1, hd)
+                    assert ulps(got, want).max() <= 1
+                dq.free()
+    finally:
+        ctx.set_accumulation(prev)
+        for d_ in (dk, dv, dpos, dout):
             d_.free()
 
 
