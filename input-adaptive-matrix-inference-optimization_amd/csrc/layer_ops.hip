@@ -257,64 +257,67 @@ struct AttnArgs {
 // bytes per lane of one V row (64 lanes, 64 banks).
 constexpr int kAttnRowStride = 128 + 8;
 
-template <typename Acc>
+template <typename Acc, int HPW>
 __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a, Acc scale)
 {
 #pragma clang fp contract(off)
     constexpr int HD = 128, RS = kAttnRowStride, DH = HD / 2, NW = kAttnThreads / 64;
+    static_assert(HPW == 1 || HPW == 2, "one or two query heads per workgroup");
     __shared__ __align__(16) uint16_t sk[kAttnChunk * RS];
     __shared__ __align__(16) uint16_t sv[kAttnChunk * RS];
-    __shared__ __align__(16) Acc sq[HD];
-    __shared__ Acc ss[NW][kAttnChunk];      // the waves' dot products
-    __shared__ Acc sp[kAttnChunk];          // p
-    __shared__ __align__(16) Acc so[NW][HD];   // the waves' p.V
-    __shared__ double sl;
+    __shared__ __align__(16) Acc sq[HPW][HD];
+    __shared__ Acc ss[HPW][NW][kAttnChunk];     // the waves' dot products
+    __shared__ Acc sp[HPW][kAttnChunk];         // p
+    __shared__ __align__(16) Acc so[NW][HPW][HD];   // the waves' p.V
+    __shared__ double sl[HPW];
     __shared__ int s_last;
     zero_share<double>(a.zero_p, a.zero_n, kAttnThreads);
     const int rep = a.n_heads / a.n_kv;
     const int kvh = blockIdx.x % a.n_kv;
-    const int r = blockIdx.x / a.n_kv;      // this head among the KV head's
-    const int h = kvh * rep + r;
+    const int r = blockIdx.x / a.n_kv;      // this workgroup's heads among the KV head's
+    const int h0 = kvh * rep + r * HPW;     // its first query head
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = tid >> 6;
     const int pos = *a.pos;
     const int n_tok = min(pos + 1, a.max_ctx);
     // the context's chunks of 64 positions, dealt to at most kAttnGroups
-    // workgroups per head in runs of G consecutive chunks
+    // workgroups per head group in runs of G consecutive chunks
     const int nch = (n_tok + kAttnChunk - 1) / kAttnChunk;
     const int G = (nch + kAttnGroups - 1) / kAttnGroups;
-    const int ng = (nch + G - 1) / G;       // workgroups of this head with chunks
+    const int ng = (nch + G - 1) / G;       // workgroups of these heads with chunks
     const int grp = blockIdx.y;
     if (grp >= ng) return;                  // past the context: neither written nor counted
     const int c0 = grp * G, c1 = min(nch, c0 + G);
     const bool pos_ok = pos >= 0 && pos < a.max_ctx;
     const double* A = reinterpret_cast<const double*>(a.qkv_acc);
-    // waves 0 and 1: q of dimension w*64 + lane; with the accumulators, the
-    // rotation pair (lane, 64 + lane)
+    // waves 0 .. 2*HPW-1: q of head h0 + w/2, dimension (w%2)*64 + lane; with
+    // the accumulators, the rotation pair (lane, 64 + lane)
+    constexpr int WK = 2 * HPW;             // the waves that form the new k and v
     float c = 1.0f, sn = 0.0f;
-    if (A && pos_ok && w < 4) {
+    if (A && pos_ok && w < WK + 2) {
         c = a.rope[(size_t)pos * HD + 2 * lane];
         sn = a.rope[(size_t)pos * HD + 2 * lane + 1];
     }
-    if (w < 2) {
+    if (w < 2 * HPW) {
+        const int hq = h0 + (w >> 1), hf = w & 1;
         float qv;
         if (A) {
-            const float lo = (float)A[(size_t)h * HD + lane], hi = (float)A[(size_t)h * HD + DH + lane];
-            qv = w == 0 ? __fsub_rn(__fmul_rn(lo, c), __fmul_rn(hi, sn))    // rope_mx: d < 64
-                        : __fadd_rn(__fmul_rn(hi, c), __fmul_rn(lo, sn));   // d >= 64
+            const float lo = (float)A[(size_t)hq * HD + lane], hi = (float)A[(size_t)hq * HD + DH + lane];
+            qv = hf == 0 ? __fsub_rn(__fmul_rn(lo, c), __fmul_rn(hi, sn))    // rope_mx: d < 64
+                         : __fadd_rn(__fmul_rn(hi, c), __fmul_rn(lo, sn));   // d >= 64
         } else {
-            qv = a.q[(size_t)h * HD + w * DH + lane];
+            qv = a.q[(size_t)hq * HD + hf * DH + lane];
         }
-        sq[w * DH + lane] = (Acc)qv;
+        sq[w >> 1][hf * DH + lane] = (Acc)qv;
     }
-    // waves 2 and 3 of the run holding the new position: its k (after RoPE)
-    // and v from the accumulators, rounded to fp16; the KV head's first query
-    // head appends them to the cache
+    // waves WK and WK + 1 of the run holding the new position: its k (after
+    // RoPE) and v from the accumulators, rounded to fp16; the workgroup of the
+    // KV head's first query head appends them to the cache
     const bool fresh = A && pos_ok && pos >= c0 * kAttnChunk && pos < c1 * kAttnChunk;
     uint16_t fr0 = 0, fr1 = 0;
-    if (fresh && w >= 2 && w < 4) {
-        const bool isk = w == 2;
+    if (fresh && w >= WK && w < WK + 2) {
+        const bool isk = w == WK;
         const int nq = a.n_heads * HD, nk = a.n_kv * HD;
         const size_t base = (size_t)(isk ? nq : nq + nk) + (size_t)kvh * HD;
         const float lo = (float)A[base + lane], hi = (float)A[base + DH + lane];
@@ -346,8 +349,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a, Acc scale)
         vb = *reinterpret_cast<const uint4*>(a.vc + g1);
     };
     load_chunk(c0);
-    Acc o0 = (Acc)0, o1 = (Acc)0;   // p.V of dimensions 2*lane, 2*lane + 1 over this wave's positions
-    Acc l = (Acc)0;                  // wave 0: the sum of p
+    Acc o[HPW][2];   // p.V of dimensions 2*lane, 2*lane + 1 over this wave's positions, per head
+#pragma unroll
+    for (int j = 0; j < HPW; j++) o[j][0] = o[j][1] = (Acc)0;
+    Acc l = (Acc)0;   // wave j < HPW: the sum of p of head h0 + j
     for (int ch = c0; ch < c1; ch++) {
         const int t0 = ch * kAttnChunk, nt = min(kAttnChunk, n_tok - t0), pieces = nt * (HD / 8);
         // the chunk's rows into LDS (the new row from the accumulators), then
@@ -355,27 +360,30 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a, Acc scale)
         {
             const int i0 = tid, i1 = kAttnThreads + tid;
             if (i0 < pieces && !(fresh && t0 + (i0 >> 4) == pos)) {
-                const int o = (i0 >> 4) * RS + (i0 & 15) * 8;
-                *reinterpret_cast<uint4*>(sk + o) = ka;
-                *reinterpret_cast<uint4*>(sv + o) = va;
+                const int oo = (i0 >> 4) * RS + (i0 & 15) * 8;
+                *reinterpret_cast<uint4*>(sk + oo) = ka;
+                *reinterpret_cast<uint4*>(sv + oo) = va;
             }
             if (i1 < pieces && !(fresh && t0 + (i1 >> 4) == pos)) {
-                const int o = (i1 >> 4) * RS + (i1 & 15) * 8;
-                *reinterpret_cast<uint4*>(sk + o) = kb;
-                *reinterpret_cast<uint4*>(sv + o) = vb;
+                const int oo = (i1 >> 4) * RS + (i1 & 15) * 8;
+                *reinterpret_cast<uint4*>(sk + oo) = kb;
+                *reinterpret_cast<uint4*>(sv + oo) = vb;
             }
         }
-        if (fresh && w >= 2 && w < 4 && pos >= t0 && pos < t0 + kAttnChunk) {
-            uint16_t* lrow = (w == 2 ? sk : sv) + (pos - t0) * RS;
+        if (fresh && w >= WK && w < WK + 2 && pos >= t0 && pos < t0 + kAttnChunk) {
+            uint16_t* lrow = (w == WK ? sk : sv) + (pos - t0) * RS;
             lrow[lane] = fr0;
             lrow[DH + lane] = fr1;
         }
         if (ch + 1 < c1) load_chunk(ch + 1);
         __syncthreads();
-        // dot products: position t0 + lane over dimensions 16w..16w+15 (two
-        // chains, then added), then the waves' sums in wave order
+        // dot products: position t0 + lane over dimensions 16w..16w+15, each
+        // K value converted once for the HPW heads (two chains per head, then
+        // added), then the waves' sums in wave order
         {
-            Acc s0 = (Acc)0, s1 = (Acc)0;
+            Acc s0[HPW], s1[HPW];
+#pragma unroll
+            for (int j = 0; j < HPW; j++) s0[j] = s1[j] = (Acc)0;
             const uint4* kr = reinterpret_cast<const uint4*>(sk + min(lane, nt - 1) * RS + w * 16);
 #pragma unroll
             for (int i = 0; i < 2; i++) {
@@ -383,19 +391,24 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a, Acc scale)
                 const uint32_t wd[4] = {kv.x, kv.y, kv.z, kv.w};
 #pragma unroll
                 for (int e = 0; e < 8; e += 2) {
-                    s0 = fma(sq[w * 16 + i * 8 + e], (Acc)h2f((uint16_t)wd[e >> 1]), s0);
-                    s1 = fma(sq[w * 16 + i * 8 + e + 1], (Acc)h2f((uint16_t)(wd[e >> 1] >> 16)), s1);
+                    const Acc k0 = (Acc)h2f((uint16_t)wd[e >> 1]), k1 = (Acc)h2f((uint16_t)(wd[e >> 1] >> 16));
+#pragma unroll
+                    for (int j = 0; j < HPW; j++) {
+                        s0[j] = fma(sq[j][w * 16 + i * 8 + e], k0, s0[j]);
+                        s1[j] = fma(sq[j][w * 16 + i * 8 + e + 1], k1, s1[j]);
+                    }
                 }
             }
-            ss[w][lane] = s0 + s1;
+#pragma unroll
+            for (int j = 0; j < HPW; j++) ss[j][w][lane] = s0[j] + s1[j];
         }
         __syncthreads();
-        if (w == 0) {
-            Acc s = ss[0][lane];
+        if (w < HPW) {   // wave j: head h0 + j
+            Acc s = ss[w][0][lane];
 #pragma unroll
-            for (int v = 1; v < NW; v++) s += ss[v][lane];
+            for (int v = 1; v < NW; v++) s += ss[w][v][lane];
             const Acc p = lane < nt ? acc_exp<Acc>(s * scale) : (Acc)0;
-            sp[lane] = p;
+            sp[w][lane] = p;
             l += wave_sum(p);
         }
         __syncthreads();
@@ -404,76 +417,91 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a, Acc scale)
         for (int u = 0; u < kAttnChunk / NW; u++) {
             const int t = w * (kAttnChunk / NW) + u;
             if (t < nt) {
-                const Acc pt = sp[t];
                 const uint32_t vw = *reinterpret_cast<const uint32_t*>(sv + t * RS + 2 * lane);
-                o0 = fma(pt, (Acc)h2f((uint16_t)vw), o0);
-                o1 = fma(pt, (Acc)h2f((uint16_t)(vw >> 16)), o1);
+                const Acc v0 = (Acc)h2f((uint16_t)vw), v1 = (Acc)h2f((uint16_t)(vw >> 16));
+#pragma unroll
+                for (int j = 0; j < HPW; j++) {
+                    const Acc pt = sp[j][t];
+                    o[j][0] = fma(pt, v0, o[j][0]);
+                    o[j][1] = fma(pt, v1, o[j][1]);
+                }
             }
         }
         __syncthreads();   // the LDS rows and p are read no more in this chunk
     }
-    so[w][2 * lane] = o0;
-    so[w][2 * lane + 1] = o1;
-    if (tid == 0) sl = (double)l;
-    __syncthreads();
-    // threads 0..127: dimension tid, the waves' sums in wave order
-    Acc ot = (Acc)0;
-    if (tid < HD) {
-        ot = so[0][tid];
 #pragma unroll
-        for (int v = 1; v < NW; v++) ot += so[v][tid];
+    for (int j = 0; j < HPW; j++) {
+        so[w][j][2 * lane] = o[j][0];
+        so[w][j][2 * lane + 1] = o[j][1];
+    }
+    if (lane == 0 && w < HPW) sl[w] = (double)l;
+    __syncthreads();
+    // threads 0 .. HPW*128 - 1: head h0 + tid/128, dimension tid%128, the
+    // waves' sums in wave order
+    const int oj = tid / HD, od = tid % HD;
+    Acc ot = (Acc)0;
+    if (tid < HPW * HD) {
+        ot = so[0][oj][od];
+#pragma unroll
+        for (int v = 1; v < NW; v++) ot += so[v][oj][od];
     }
     if (!a.out && ng <= a.atomic_splits) {
         // each run adds its sums into the accumulators (zero on entry) with
         // fp64 atomics, which the launch's end makes visible to the o
         // projection's walk; no partials, no arrival, no last run
         double* O = reinterpret_cast<double*>(a.acc);
-        if (tid < HD) atomicAdd(O + (size_t)h * HD + tid, (double)ot);
-        if (tid == HD) atomicAdd(O + (size_t)a.n_heads * HD + h, sl);
+        if (tid < HPW * HD) atomicAdd(O + (size_t)(h0 + oj) * HD + od, (double)ot);
+        if (tid >= HPW * HD && tid < HPW * HD + HPW)
+            atomicAdd(O + (size_t)a.n_heads * HD + h0 + (tid - HPW * HD), sl[tid - HPW * HD]);
         return;
     }
-    // the run's sums go to its own slot of the partials (no two runs add to
-    // one address): o at 0..127, the softmax sum at 128.  The exchanges
-    // return the old values and the run waits for them before it arrives, so
-    // all are performed where the last run's atomic loads read them.
+    // each head's sums of the run go to its own slot of the partials (no two
+    // runs add to one address): o at 0..127, the softmax sum at 128.  The
+    // exchanges return the old values and the run waits for them before it
+    // arrives (at the counter of its first head), so all are performed where
+    // the last run's atomic loads read them.
     constexpr int PS = kAttnPartStride;
     double* part = reinterpret_cast<double*>(a.part);
-    double* mine = part + ((size_t)h * gridDim.y + grp) * PS;
-    if (tid <= HD) {
-        const double v = tid < HD ? (double)ot : sl;
-        const unsigned long long sink = __hip_atomic_exchange(reinterpret_cast<unsigned long long*>(mine + tid),
+    if (tid < HPW * (HD + 1)) {
+        const int j = tid < HPW * HD ? oj : tid - HPW * HD, e = tid < HPW * HD ? od : HD;
+        const double v = tid < HPW * HD ? (double)ot : sl[j];
+        double* mine = part + ((size_t)(h0 + j) * gridDim.y + grp) * PS;
+        const unsigned long long sink = __hip_atomic_exchange(reinterpret_cast<unsigned long long*>(mine + e),
                                                               (unsigned long long)__double_as_longlong(v),
                                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         asm volatile("" ::"v"(sink));
     }
     __syncthreads();
     if (tid == 0)
-        s_last = __hip_atomic_fetch_add(a.head_ctr + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        s_last = __hip_atomic_fetch_add(a.head_ctr + h0, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                  (uint32_t)(ng - 1);
     __syncthreads();
     if (!s_last) return;
-    // the last run of this head: the sums over the runs, in run order, of o
-    // (threads 0..127) and l (thread 128); at most kAttnGroups loads each
-    const double* first = part + (size_t)h * gridDim.y * PS;
+    // the last run of these heads: the sums over the runs, in run order, of
+    // o (threads 0 .. HPW*128 - 1) and l (the next HPW threads); at most
+    // kAttnGroups loads each
     double to = 0.0;
-    if (tid <= HD) {
+    const bool has = tid < HPW * (HD + 1);
+    const int tj = tid < HPW * HD ? oj : tid - HPW * HD, te = tid < HPW * HD ? od : HD;
+    if (has) {
+        const double* first = part + (size_t)(h0 + tj) * gridDim.y * PS;
         double vo[kAttnGroups];
 #pragma unroll
         for (int u = 0; u < kAttnGroups; u++)
-            vo[u] = u < ng ? acc_peek(const_cast<double*>(first) + (size_t)u * PS + tid) : 0.0;
+            vo[u] = u < ng ? acc_peek(const_cast<double*>(first) + (size_t)u * PS + te) : 0.0;
 #pragma unroll
         for (int u = 0; u < kAttnGroups; u++) to += vo[u];
     }
-    if (tid == HD) sl = to;
+    if (has && te == HD) sl[tj] = to;
     if (a.out) {
         __syncthreads();
-        if (tid < HD) a.out[(size_t)h * HD + tid] = (float)(to / sl);
+        if (tid < HPW * HD) a.out[(size_t)(h0 + oj) * HD + od] = (float)(to / sl[oj]);
     } else {
         double* O = reinterpret_cast<double*>(a.acc);
-        if (tid < HD) O[(size_t)h * HD + tid] = to;
-        if (tid == HD) O[(size_t)a.n_heads * HD + h] = to;
+        if (tid < HPW * HD) O[(size_t)(h0 + oj) * HD + od] = to;
+        if (has && te == HD) O[(size_t)a.n_heads * HD + h0 + tj] = to;
     }
-    if (tid == 0) a.head_ctr[h] = 0u;
+    if (tid == 0) a.head_ctr[h0] = 0u;
 }
 
 // ---------------------------------------------------------------- embed ---
@@ -627,9 +655,17 @@ int attention_launch(Ctx* c, const AttnLaunch& L)
     a.zero_n = L.zero_n;
     a.atomic_splits = L.acc && !L.out ? L.atomic_splits : 0;
     IAM_REQUIRE(L.n_heads <= kAttnMaxHeads, "attention: at most 512 query heads");
-    const dim3 grid(L.n_heads, attn_runs(L.max_ctx)), block(kAttnThreads);
-    if (c->acc64) return launch(c, "attention", k_attn<double>, grid, block, 0, a, 1.0 / std::sqrt(128.0));
-    return launch(c, "attention", k_attn<float>, grid, block, 0, a, 1.0f / std::sqrt(128.0f));
+    // two query heads of one KV head per workgroup where the KV heads' query
+    // heads pair up: at most 16 runs x n_heads / 2 workgroups, one round on
+    // the CUs for 32 heads, and each K and V value converted once for both
+    const bool pair = (L.n_heads / L.n_kv) % 2 == 0;
+    const dim3 grid(L.n_heads / (pair ? 2 : 1), attn_runs(L.max_ctx)), block(kAttnThreads);
+    const double sd = 1.0 / std::sqrt(128.0);
+    const float sf = 1.0f / std::sqrt(128.0f);
+    if (c->acc64) return pair ? launch(c, "attention", k_attn<double, 2>, grid, block, 0, a, sd)
+                              : launch(c, "attention", k_attn<double, 1>, grid, block, 0, a, sd);
+    return pair ? launch(c, "attention", k_attn<float, 2>, grid, block, 0, a, sf)
+                : launch(c, "attention", k_attn<float, 1>, grid, block, 0, a, sf);
 }
 
 int embed(Ctx* c, const uint16_t* table, int cols, int vocab, const int* tok, float* out)
