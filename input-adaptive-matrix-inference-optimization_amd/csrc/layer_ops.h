@@ -28,11 +28,11 @@ int rope_kv(Ctx* c, const float* q, const float* k, const float* v, const float*
             int n_heads, int n_kv, int hd, int max_ctx, float* q_out, uint16_t* kc, uint16_t* vc);
 // one launch of the split-context attention (see k_attn)
 // Workgroups per head (each a run of consecutive 64-position chunks; at most
-// 16) up to which the model's attention adds its sums with fp64 atomics
-// rather than through partial slots and a last workgroup: 16 same-address
-// adds per output cost less than the exchange, the arrival and the serial
-// sum (measured per launch at 9 and 32 chains: 7.1 against 8.3 us and 12.9
-// against 13.5 us; at 61, 19.9 against 19.0 us).
+// 32) up to which the model's attention adds its sums with fp64 atomics
+// rather than through partial slots and a last workgroup: up to 32
+// same-address adds per output cost less than the exchange, the arrival and
+// the serial sum (measured per launch at 9 and 32 chains: 7.1 against 8.3 us
+// and 12.9 against 13.5 us; at 61, 19.9 against 19.0 us).
 constexpr int kAttnAtomicSplits = 40;
 
 struct AttnLaunch {

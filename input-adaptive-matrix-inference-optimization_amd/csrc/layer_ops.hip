@@ -219,7 +219,7 @@ constexpr int kAttnMaxRep = 8;
 constexpr int kMaxAttnSplits = 128;   // max_ctx up to 8192
 constexpr int kAttnThreads = 512;     // 8 waves
 constexpr int kAttnMaxHeads = 512;    // 64 KV heads x 8
-constexpr int kAttnGroups = 16;       // workgroups per head at most (runs of consecutive chunks)
+constexpr int kAttnGroups = 32;       // workgroups per head at most (runs of consecutive chunks)
 // workgroups per head of a launch over a context of up to max_ctx positions
 static int attn_runs(int max_ctx) { return std::min((max_ctx + kAttnChunk - 1) / kAttnChunk, kAttnGroups); }
 // doubles per split and query head in the partials: o (128), the softmax
@@ -656,8 +656,8 @@ int attention_launch(Ctx* c, const AttnLaunch& L)
     a.atomic_splits = L.acc && !L.out ? L.atomic_splits : 0;
     IAM_REQUIRE(L.n_heads <= kAttnMaxHeads, "attention: at most 512 query heads");
     // two query heads of one KV head per workgroup where the KV heads' query
-    // heads pair up: at most 16 runs x n_heads / 2 workgroups, one round on
-    // the CUs for 32 heads, and each K and V value converted once for both
+    // heads pair up (each K and V value converted once for both): for 32
+    // heads at most 32 runs x 16 workgroups, two resident per CU
     const bool pair = (L.n_heads / L.n_kv) % 2 == 0;
     const dim3 grid(L.n_heads / (pair ? 2 : 1), attn_runs(L.max_ctx)), block(kAttnThreads);
     const double sd = 1.0 / std::sqrt(128.0);

@@ -147,12 +147,12 @@ def test_rope_kv_append_and_attention(iam, O, ctx):
 
 def test_attention_long_context(iam, O, ctx):
     """Contexts of up to 8192 positions: the 64-position chunks dealt to at
-    most 16 runs per head (1 chunk per run up to 1024 positions, then 2, ...,
-    8 at 8192) and the last run's sum over the runs, at positions on and off
-    chunk and run-length boundaries, with a 4-query-head GQA and a 1:1
-    layout."""
+    most 32 runs per head (1 chunk per run up to 2048 positions, then 2, ...,
+    4 at 8192) and the last run's sum over the runs, at positions on and off
+    chunk and run-length boundaries, with a 4-query-head GQA (heads paired
+    per workgroup) and a 1:1 layout (one head per workgroup)."""
     rng = np.random.default_rng(3)
-    for n_heads, n_kv, max_ctx, positions in ((32, 8, 8192, (1023, 1024, 1088, 4095, 4096, 8191)),
+    for n_heads, n_kv, max_ctx, positions in ((32, 8, 8192, (1023, 2047, 2048, 2112, 4095, 4096, 8191)),
                                               (8, 8, 4160, (63, 4159))):
         hd = 128
         kc = rng.normal(0, 1, (max_ctx, n_kv, hd)).astype(np.float16)
