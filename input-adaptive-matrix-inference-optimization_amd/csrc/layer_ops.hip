@@ -183,34 +183,38 @@ __global__ void k_rope_kv(const float* __restrict__ q, const float* __restrict__
 }
 
 // ------------------------------------------------------------ attention ---
-// Decode attention over an fp16 GQA cache, split over the context.
-// Workgroup (query head h, split) handles kAttnChunk = 64 positions of one
-// query head; the heads that read one KV head (repeat4x32, aux.cl:266-275,
-// without materialising the repeat) sit in workgroups whose index is equal
-// modulo n_kv, so with 8 KV heads they run on one XCD and share the K and V
-// rows in its L2.  The split's K and V rows are loaded once per workgroup,
-// 16 bytes per thread, into LDS.  Dot products (dotSetScore2,
-// aux.cl:497-540, s = q.k / sqrt(hd)): lane = position, wave w adds the 16
-// dimensions 16w..16w+15 with q broadcast from LDS, and the waves' sums are
-// added in wave order; wave 0 takes p = exp(s) (sum_of_exps32_mx /
-// softmax_add32_mx, aux.cl:204-225: the reference's softmax has no maximum
-// subtracted, so the splits' sums add up directly) and their sum.  p.V:
-// lane l takes dimensions 2l and 2l+1 over the 8 positions 8w..8w+7, and the
-// waves' sums are added in wave order.  The splits' sums p*V and sums of p
+// Decode attention over an fp16 GQA cache, split over the context.  The
+// context is cut into chunks of 64 positions, dealt in runs of consecutive
+// chunks to at most kAttnGroups workgroups per head group.  Workgroup (head
+// group, run) takes HPW query heads of one KV head (2 where a KV head's
+// query heads pair up, else 1; repeat4x32, aux.cl:266-275, without
+// materialising the repeat); the head groups of one KV head sit in
+// workgroups whose index is equal modulo n_kv, so with 8 KV heads they run on
+// one XCD and share the K and V rows in its L2.  Each chunk's K and V rows
+// are loaded into LDS, 16 bytes per thread (the next chunk's loads in flight
+// during this one's arithmetic).  Dot products (dotSetScore2, aux.cl:497-540,
+// s = q.k / sqrt(hd)): lane = position, wave w adds dimensions 16w..16w+15
+// for every head of the group (each K value converted once) with q
+// broadcast from LDS, and the waves' sums are added in wave order; wave j
+// takes p = exp(s) of head j (sum_of_exps32_mx / softmax_add32_mx,
+// aux.cl:204-225: the reference's softmax has no maximum subtracted, so the
+// runs' sums add up directly) and their sum.  p.V: lane l takes dimensions 2l
+// and 2l+1 over the 8 positions 8w..8w+7 of each chunk, for every head, and
+// the waves' sums are added in wave order.  The runs' sums p*V and sums of p
 // then meet in o and l for the consumer (the o projection's walk, which
 // divides x = o / l), or, for the standalone call, out = o / l (sumScores32,
-// aux.cl:370-384).  In the model, while a head has at most atomic_splits
-// splits, each split adds its sums into o and l with fp64 atomics (the sums
-// within an fp64 rounding of the exact ones, whatever the order).
-// Otherwise each split writes its sums to its own slot of the partials with
-// atomic exchanges, waits for them to be performed and arrives at its
-// head's counter; the last split to arrive adds the slots in split order
-// (no two splits add to one address, so the sums do not depend on arrival
-// order) and writes o and l, or out.  With the projection accumulators as
-// input the workgroup also applies RoPE to q and k (rope_mx,
-// aux.cl:227-248, table row of the position), and the split holding the
-// position uses the new K and V rows from LDS; the workgroup of the KV
-// head's first query head appends them to the cache (attention.hpp:281-309).
+// aux.cl:370-384).  In the model, while a head group has at most
+// atomic_splits runs (always: at most kAttnGroups), each run adds its sums
+// into o and l with fp64 atomics (the sums within an fp64 rounding of the
+// exact ones, whatever the order).  Otherwise each run writes its sums to
+// its heads' slots of the partials with atomic exchanges, waits for them to
+// be performed and arrives at its head group's counter; the last run to
+// arrive adds the slots in run order (no two runs add to one address, so the
+// sums do not depend on arrival order) and writes o and l, or out.  With the
+// projection accumulators as input the workgroup also applies RoPE to q and
+// k (rope_mx, aux.cl:227-248, table row of the position), and the run holding
+// the position uses the new K and V rows from LDS; the workgroup of the KV
+// head's first query heads appends them to the cache (attention.hpp:281-309).
 // Acc = double evaluates every product (exact: fp32 x fp16), exponential and
 // sum in fp64 (a score above log(DBL_MAX) ~ 709.78 overflows, as the
 // reference's fp32 exp does above 88.72); Acc = float in fp32.
@@ -219,10 +223,10 @@ constexpr int kAttnMaxRep = 8;
 constexpr int kMaxAttnSplits = 128;   // max_ctx up to 8192
 constexpr int kAttnThreads = 512;     // 8 waves
 constexpr int kAttnMaxHeads = 512;    // 64 KV heads x 8
-constexpr int kAttnGroups = 32;       // workgroups per head at most (runs of consecutive chunks)
-// workgroups per head of a launch over a context of up to max_ctx positions
+constexpr int kAttnGroups = 32;       // workgroups per head group at most (runs of consecutive chunks)
+// workgroups per head group of a launch over a context of up to max_ctx positions
 static int attn_runs(int max_ctx) { return std::min((max_ctx + kAttnChunk - 1) / kAttnChunk, kAttnGroups); }
-// doubles per split and query head in the partials: o (128), the softmax
+// doubles per run and query head in the partials: o (128), the softmax
 // sum, padded to 64 bytes
 constexpr int kAttnPartStride = 128 + 8;
 
@@ -242,12 +246,13 @@ struct AttnArgs {
     const int* pos;
     int n_heads, n_kv, max_ctx;
     void* acc;               // o [n_heads][128], then l [n_heads] (fp64) (model mode)
-    void* part;              // the splits' partial sums [n_heads][splits][kAttnPartStride] (fp64)
-    float* out;              // standalone: out = o / l, stored by the last split of each head
-    uint32_t* head_ctr;      // [n_heads] arrival counters, zero on entry (left zero)
+    void* part;              // the runs' partial sums [n_heads][runs][kAttnPartStride] (fp64)
+    float* out;              // standalone: out = o / l, stored by the last run of each head group
+    uint32_t* head_ctr;      // [n_heads] arrival counters (a head group's first head's), zero on
+                             // entry (left zero)
     void* zero_p;            // accumulator words cleared by this launch
     int zero_n;
-    int atomic_splits;       // model: splits per head up to which o and l are added with atomics
+    int atomic_splits;       // model: runs per head group up to which o and l are added with atomics
 };
 
 // LDS copies of the split's K and V rows: 128 fp16 + 8 of padding (68
