@@ -340,6 +340,7 @@ struct WalkDesc {
     float* cutoff;
     uint32_t* slice_count;    // [P]: rows selected per slice (written by the tile-0 workgroups)
     void* acc;                // [16*C] accumulators
+    void* acc2;               // or null: the odd slices' accumulators (kFinNone)
     float* y;                 // kFinStore: outputs; kFinSilu: gate / up values (may be null)
     uint32_t* tile_ctr;       // [T] arrival counters (finalize modes)
     int quantile;
@@ -951,7 +952,7 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     // consecutive outputs.
     constexpr int OPT = TOUT / NT;
     static_assert(TSLOTS >= STAGE, "the staging copy fits the tiles");
-    double* out = reinterpret_cast<double*>(d.acc) + (size_t)t * TOUT;
+    double* out = reinterpret_cast<double*>((p & 1) && d.acc2 ? d.acc2 : d.acc) + (size_t)t * TOUT;
     const int nout = min(TOUT, (d.C - t * TC) * 16);
     {
         Tile sum[OPT];
@@ -1265,6 +1266,7 @@ int walk_group(Ctx* c, const WalkGroup& g)
         IAM_REQUIRE(wm.acc && wm.cutoff && wm.slice_count, "walk: missing scratch");
         IAM_REQUIRE(g.fin == kFinNone || wm.tile_ctr, "walk: missing tile counters");
         IAM_REQUIRE(g.fin != kFinStore || wm.y, "walk: missing outputs");
+        IAM_REQUIRE(!wm.acc2 || g.fin == kFinNone, "walk: a second accumulator only without a finalize");
         ops[i].mat = wm.mat;
         ops[i].in_size = wm.in_size;
         ops[i].x = wm.x;
@@ -1289,6 +1291,7 @@ int walk_group(Ctx* c, const WalkGroup& g)
         d.cutoff = wm.cutoff;
         d.slice_count = wm.slice_count;
         d.acc = wm.acc;
+        d.acc2 = wm.acc2;
         d.y = wm.y;
         d.tile_ctr = wm.tile_ctr;
         d.quantile = qv;

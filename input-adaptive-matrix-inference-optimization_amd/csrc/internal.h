@@ -231,6 +231,10 @@ struct WalkMat {
     float* cutoff;           // the search's result is stored here (kInCutoff: read from here)
     uint32_t* slice_count;   // [P]
     void* acc;               // [16 * bucket_cols] of the accumulator type
+    // a second accumulator of the same size (or null): the slices of odd
+    // index add there, halving the chains of adds to one address where one
+    // column tile takes every slice (kFinNone only; the consumer adds both)
+    void* acc2 = nullptr;
     uint32_t* tile_ctr;      // [T]
     float* y;                // kFinStore: outputs; kFinSilu: the gate / up values (may be null)
 };

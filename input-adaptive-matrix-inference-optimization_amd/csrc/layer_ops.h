@@ -38,6 +38,7 @@ constexpr int kAttnAtomicSplits = 40;
 struct AttnLaunch {
     const float* q = nullptr;          // queries after RoPE, or null: from qkv_acc (RoPE and KV append applied)
     const void* qkv_acc = nullptr;
+    int kv_copies = 1;                 // qkv_acc: 2 when k and v have second copies after v
     const float* rope = nullptr;
     uint16_t* kc = nullptr;
     uint16_t* vc = nullptr;

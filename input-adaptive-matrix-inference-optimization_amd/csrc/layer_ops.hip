@@ -253,6 +253,7 @@ struct AttnArgs {
     void* zero_p;            // accumulator words cleared by this launch
     int zero_n;
     int atomic_splits;       // model: runs per head group up to which o and l are added with atomics
+    int kv_copies;           // qkv_acc: 2 when k and v have second copies after v (added here)
 };
 
 // LDS copies of the split's K and V rows: 128 fp16 + 8 of padding (68
@@ -325,7 +326,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a, Acc scale)
         const bool isk = w == WK;
         const int nq = a.n_heads * HD, nk = a.n_kv * HD;
         const size_t base = (size_t)(isk ? nq : nq + nk) + (size_t)kvh * HD;
-        const float lo = (float)A[base + lane], hi = (float)A[base + DH + lane];
+        const size_t base2 = a.kv_copies > 1 ? base + 2 * (size_t)nk : base;   // the odd slices' copy
+        const double x0 = A[base + lane], x1 = A[base + DH + lane];
+        const float lo = (float)(a.kv_copies > 1 ? x0 + A[base2 + lane] : x0);
+        const float hi = (float)(a.kv_copies > 1 ? x1 + A[base2 + DH + lane] : x1);
         float o0 = lo, o1 = hi;
         if (isk) {
             o0 = __fsub_rn(__fmul_rn(lo, c), __fmul_rn(hi, sn));
@@ -659,6 +663,7 @@ int attention_launch(Ctx* c, const AttnLaunch& L)
     a.zero_p = L.zero_p;
     a.zero_n = L.zero_n;
     a.atomic_splits = L.acc && !L.out ? L.atomic_splits : 0;
+    a.kv_copies = L.kv_copies;
     IAM_REQUIRE(L.n_heads <= kAttnMaxHeads, "attention: at most 512 query heads");
     // two query heads of one KV head per workgroup where the KV heads' query
     // heads pair up (each K and V value converted once for both): for 32

@@ -194,6 +194,11 @@ static int step(iam_model* m, float effort, const float* hidden_override, float*
             g.m[0] = walk_mat(m, ly.wq, 0, D, qkv);
             g.m[1] = walk_mat(m, ly.wk, 1, D, qkv + acc_bytes(D));
             g.m[2] = walk_mat(m, ly.wv, 2, D, qkv + acc_bytes(D + KVD));
+            // k and v: one column tile each, so every slice adds into the
+            // same outputs; the odd slices use second copies (after v),
+            // which attention adds
+            g.m[1].acc2 = qkv + acc_bytes(D + 2 * KVD);
+            g.m[2].acc2 = qkv + acc_bytes(D + 3 * KVD);
             g.effort = effort;
             g.gain = ly.attn_gain;
             g.eps = C.norm_eps;
@@ -239,6 +244,7 @@ static int step(iam_model* m, float effort, const float* hidden_override, float*
         {
             AttnLaunch A{};
             A.qkv_acc = m->acc_qkv;
+            A.kv_copies = 2;
             A.rope = m->rope;
             A.kc = kc;
             A.vc = vc;
@@ -265,7 +271,7 @@ static int step(iam_model* m, float effort, const float* hidden_override, float*
             g.in_mode = kInAttn;
             g.attn_acc = m->acc_att;
             g.zero_p[0] = m->acc_qkv;
-            g.zero_n[0] = D + 2 * KVD;
+            g.zero_n[0] = D + 4 * KVD;
             IAM_TRY(walk_group(c, g));
         }
         // ---- gate and up (feedforward.hpp:60-78) with the residual add of o
@@ -543,7 +549,7 @@ int iam_model_create(iam_ctx* c, const iam_model_config* cfg, iam_model** out)
     T(alloc_t(m, (size_t)C.n_layers * D, &m->hb));
     for (float** p : {&m->hidden, &m->hn, &m->att_x, &m->hidden_in}) T(alloc_t(m, D, p));
     T(alloc_t(m, F, &m->s));
-    T(alloc_owned(m, acc_bytes(D + 2 * KVD), &m->acc_qkv));
+    T(alloc_owned(m, acc_bytes(D + 4 * KVD), &m->acc_qkv));   // q | k | v | k, v of the odd slices
     T(alloc_owned(m, acc_bytes(attention_acc_words(C.n_heads)), &m->acc_att));
     T(alloc_owned(m, acc_bytes(attention_part_words(C.n_heads, C.n_kv_heads, C.max_ctx)), &m->att_part));
     T(alloc_t(m, (size_t)C.n_heads, &m->att_ctr));
@@ -629,7 +635,7 @@ int iam_model_reset_caches(iam_model* m)
     // the accumulators and counters are zero between steps; clear them
     // anyway, so that a reset also recovers from an interrupted step
     const int D = C.dim, F = C.ffn_dim, KVD = C.n_kv_heads * C.head_dim;
-    IAM_TRY(zero_async(m->c, m->acc_qkv, acc_bytes(D + 2 * KVD)));
+    IAM_TRY(zero_async(m->c, m->acc_qkv, acc_bytes(D + 4 * KVD)));
     IAM_TRY(zero_async(m->c, m->acc_att, acc_bytes(attention_acc_words(C.n_heads))));
     for (void* p : {m->acc_o, m->acc_d}) IAM_TRY(zero_async(m->c, p, acc_bytes(D)));
     for (void* p : {m->acc_g, m->acc_u}) IAM_TRY(zero_async(m->c, p, acc_bytes(F)));
