@@ -203,6 +203,21 @@ int iam_walk_group_counters(iam_ctx* ctx, int group, uint64_t* weight_bytes, uin
  * Changing it re-captures the model's decode graph.  Not during capture.
  * No counterpart in the reference. */
 int iam_set_walk_counting(iam_ctx* ctx, int on);
+/* Hints for the walk's cutoff search (default off for the calls of this
+ * context; a model's decode steps always use them, one per matrix of each
+ * layer).  On, each iam_bucketmul_fused call starts the search of matrix
+ * slot i from the cutoff that slot found in the previous fused call: one
+ * pass over the importances counts those above the window [7/8, 8/7] of the
+ * hint and bins those inside it, which locates the cutoff's neighbourhood
+ * (ranks t-2 .. t+2) without the coarse histogram when the input changes
+ * little between calls, as from one decode step to the next; where the
+ * window misses those ranks the full search runs.  The cutoff, the selected
+ * rows and the outputs are the same either way.  iam_set_search_hint sets
+ * slot i's hint; any value is accepted (0, a negative, a non-finite one or
+ * one outside [1e-30, 1e30] means no hint).  Not during capture.  No
+ * counterpart in the reference. */
+int iam_set_search_hints(iam_ctx* ctx, int on);
+int iam_set_search_hint(iam_ctx* ctx, int slot, float value);
 /* Block-structured selection, the thesis's future work (THESIS p.42-43):
  * with block_inputs B > 1, the inputs are taken in blocks of B consecutive
  * ones, and rank k of every input of a block is selected when rank k of any

@@ -338,6 +338,9 @@ struct WalkDesc {
     const uint16_t* stats;    // row 0 of the expert
     const uint16_t* probes;   // probes of the expert
     float* cutoff;
+    // or null: the search's hint, the same matrix's cutoff of the previous
+    // step (read at the start, written by work item 0 once it has the cutoff)
+    float* hint;
     uint32_t* slice_count;    // [P]: rows selected per slice (written by the tile-0 workgroups)
     void* acc;                // [16*C] accumulators
     void* acc2;               // or null: the odd slices' accumulators (kFinNone)
@@ -722,9 +725,11 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     for (int k2 = 0; k2 < VPT / 2; k2++) pw[k2] = gw[k2] = ew[k2] = 0u;
     double lsum = 1.0;
     float cutoff = 0.0f;
+    float hint = 0.0f;   // thread 0: the search's hint (0: none)
     if (mode == kInCutoff) {
         cutoff = *d.cutoff;
     } else {
+        if (tid == 0 && d.hint) hint = load_early(d.hint);
         load_h16<VPT>(probes, pw);
         if (mode == kInX) load_f32<VPT>(dx, xs);
         if (mode == kInNorm || mode == kInResNorm) load_f32<VPT>(a_h, xs);
@@ -782,6 +787,9 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
         }
         if ((mode == kInResNorm || mode == kInEmbedNorm) && first && a.h_out) store_f32<VPT>(a.h_out, xs);
     }
+    // one value for the whole workgroup (work item 0 of the matrix may
+    // rewrite the hint meanwhile), published by the barrier before the search
+    if (tid == 0) WL.hint = hint;
     if (norm) block_rmsnorm4096<VPT>(xs, gw, a.eps, s_part);
     if (regs) {
         if (first && dx) store_f32<VPT>(dx, xs);
@@ -831,7 +839,10 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
             __syncthreads();   // wave 0 has stored the cutoff
             cutoff = SL.cut;
         }
-        if (w == 0 && tid == 0) d.cutoff[0] = cutoff;
+        if (w == 0 && tid == 0) {
+            d.cutoff[0] = cutoff;
+            if (d.hint) d.hint[0] = cutoff;
+        }
     } else {
         select_prepare<NT>(ss, i0, ni, L, s_x, slice_regs, imp, vbits);
         __syncthreads();   // the list's count is clear before any wave appends
@@ -1289,6 +1300,7 @@ int walk_group(Ctx* c, const WalkGroup& g)
         d.stats = M.stats + (size_t)g.expert_no * (size_t)M.expert_rows * M.stats_stride;
         d.probes = M.probes + (size_t)g.expert_no * kProbes;
         d.cutoff = wm.cutoff;
+        d.hint = wm.hint;
         d.slice_count = wm.slice_count;
         d.acc = wm.acc;
         d.acc2 = wm.acc2;
@@ -1404,6 +1416,7 @@ static int walk_slots(Ctx* c, int n, const MatOp* ops, int in_mode, const float*
         wm.in_size = s.in_size;
         wm.x = s.x;
         wm.cutoff = s.cutoff;
+        wm.hint = c->hints && in_mode != kInCutoff ? s.cutoff + 2 : nullptr;
         wm.slice_count = s.slice_count;
         wm.acc = s.acc;
         wm.tile_ctr = s.tile_ctr;

@@ -63,7 +63,7 @@ struct DispatchSlot {
     int expert_no = 0;
     float effort = 1.0f;
     bool valid = false;
-    float* cutoff = nullptr;     // device [2]: the search's value, the list kernel's value
+    float* cutoff = nullptr;     // device [4]: the search's value, the list kernel's value, the search's hint
     uint2* list = nullptr;       // [G][kChunkRows]
     uint32_t* counts = nullptr;  // [kMaxChunks]
     size_t cap_chunks = 0;
@@ -128,6 +128,9 @@ struct Ctx {
     // per-row selection), used for efforts below sel_below
     int sel_block = 1;
     float sel_below = 2.0f;
+    // fused calls start their cutoff search from the slot's hint, the
+    // slot's cutoff of the previous fused call (iam_set_search_hints)
+    bool hints = false;
 };
 
 int ctx_alloc(Ctx* c, size_t bytes, void** out);
@@ -229,6 +232,9 @@ struct WalkMat {
     const float* x;          // kInX / kInCutoff: the input; norm and attention modes: where block 0
                              // stores the computed input (may be null)
     float* cutoff;           // the search's result is stored here (kInCutoff: read from here)
+    // or null: the cutoff search's hint, this matrix's cutoff of the
+    // previous call (read, then rewritten by the walk); any value is safe
+    float* hint = nullptr;
     uint32_t* slice_count;   // [P]
     void* acc;               // [16 * bucket_cols] of the accumulator type
     // a second accumulator of the same size (or null): the slices of odd

@@ -81,6 +81,9 @@ struct iam_model {
     uint32_t* tile_ctr = nullptr;   // gate/up tiles, then LM head tiles, then the pick counter
     uint2* cand = nullptr;          // LM head tile maxima
     float* cut = nullptr;           // cutoffs of the last group [3]
+    // the cutoff searches' hints, each matrix's cutoff of the previous step:
+    // per layer q, k, v, o, w1, w3, w2 (8 slots), then the LM head
+    float* hints = nullptr;
     uint32_t* slice_counts = nullptr;   // [3][slice_cap]
     int slice_cap = 0;
     float* logits = nullptr;
@@ -194,6 +197,7 @@ static int step(iam_model* m, float effort, const float* hidden_override, float*
             g.m[0] = walk_mat(m, ly.wq, 0, D, qkv);
             g.m[1] = walk_mat(m, ly.wk, 1, D, qkv + acc_bytes(D));
             g.m[2] = walk_mat(m, ly.wv, 2, D, qkv + acc_bytes(D + KVD));
+            for (int j = 0; j < 3; j++) g.m[j].hint = m->hints + (size_t)L * 8 + j;
             // k and v: one column tile each, so every slice adds into the
             // same outputs; the odd slices use second copies (after v),
             // which attention adds
@@ -266,6 +270,7 @@ static int step(iam_model* m, float effort, const float* hidden_override, float*
             g.label = IAM_WALK_GROUP_O;
             g.n = 1;
             g.m[0] = walk_mat(m, ly.wo, 0, D, m->acc_o);
+            g.m[0].hint = m->hints + (size_t)L * 8 + 3;
             g.m[0].x = m->att_x;
             g.effort = effort;
             g.in_mode = kInAttn;
@@ -282,6 +287,8 @@ static int step(iam_model* m, float effort, const float* hidden_override, float*
             g.n = 2;
             g.m[0] = walk_mat(m, ly.w1, 0, D, m->acc_g);
             g.m[1] = walk_mat(m, ly.w3, 1, D, m->acc_u);
+            g.m[0].hint = m->hints + (size_t)L * 8 + 4;
+            g.m[1].hint = m->hints + (size_t)L * 8 + 5;
             g.m[0].tile_ctr = g.m[1].tile_ctr = m->tile_ctr;
             g.effort = effort;
             g.gain = ly.ffn_gain;
@@ -310,6 +317,7 @@ static int step(iam_model* m, float effort, const float* hidden_override, float*
             g.label = IAM_WALK_GROUP_FFN2;
             g.n = 1;
             g.m[0] = walk_mat(m, ly.w2, 0, F, m->acc_d);
+            g.m[0].hint = m->hints + (size_t)L * 8 + 6;
             g.m[0].x = m->s;
             g.effort = effort;
             g.in_mode = kInX;
@@ -335,6 +343,7 @@ static int step(iam_model* m, float effort, const float* hidden_override, float*
         g.label = IAM_WALK_GROUP_LM;
         g.n = 1;
         g.m[0] = walk_mat(m, m->lm, 0, D, m->acc_lm);
+        g.m[0].hint = m->hints + (size_t)C.n_layers * 8;
         g.m[0].tile_ctr = m->tile_ctr + T13;
         g.m[0].y = logits_out;
         g.m[0].x = m->hn;
@@ -562,6 +571,7 @@ int iam_model_create(iam_ctx* c, const iam_model_config* cfg, iam_model** out)
     T(alloc_t(m, (size_t)T13 + Tlm + 1, &m->tile_ctr));
     T(alloc_t(m, (size_t)Tlm, &m->cand));
     T(alloc_t(m, 3, &m->cut));
+    T(alloc_t(m, (size_t)C.n_layers * 8 + 1, &m->hints));
     m->slice_cap = std::max(D, F);   // a slice holds at least one input
     T(alloc_t(m, (size_t)3 * m->slice_cap, &m->slice_counts));
     T(alloc_t(m, C.vocab, &m->logits));
@@ -643,6 +653,8 @@ int iam_model_reset_caches(iam_model* m)
     const int T13 = walk_tiles(F / 16), Tlm = walk_tiles(C.vocab / 16);
     IAM_TRY(zero_async(m->c, m->tile_ctr, ((size_t)T13 + Tlm + 1) * 4));
     IAM_TRY(zero_async(m->c, m->att_ctr, (size_t)C.n_heads * 4));
+    // a new sequence starts without hints (0: the full search)
+    IAM_TRY(zero_async(m->c, m->hints, ((size_t)C.n_layers * 8 + 1) * 4));
     IAM_CHECK_HIP(hipStreamSynchronize(m->c->stream));
     m->host_pos = 0;
     return IAM_OK;

@@ -72,6 +72,7 @@ int ensure_slot(Ctx* c, int slot)
     if (!s.cutoff) {
         if (c->capturing) return fail(IAM_E_STATE, "dispatch buffer allocation during graph capture");
         IAM_TRY(ctx_alloc(c, 16, (void**)&s.cutoff));
+        IAM_TRY(zero_async(c, s.cutoff, 16));   // hint 0: none
         c->scratch_gen++;
     }
     return IAM_OK;
@@ -488,6 +489,28 @@ int iam_set_accumulation(iam_ctx* c, int mode)
         c->acc64 = f64;
         c->scratch_gen++;   // captured graphs hold kernels of the other mode
     }
+    return IAM_OK;
+}
+
+int iam_set_search_hints(iam_ctx* c, int on)
+{
+    if (!c) return fail(IAM_E_INVALID, "set_search_hints: null context");
+    IAM_REQUIRE(!c->capturing, "set_search_hints: not allowed during graph capture");
+    if ((on != 0) != c->hints) {
+        c->hints = on != 0;
+        c->scratch_gen++;   // captured graphs hold walk launches of the other setting
+    }
+    return IAM_OK;
+}
+
+int iam_set_search_hint(iam_ctx* c, int slot, float value)
+{
+    if (!c) return fail(IAM_E_INVALID, "set_search_hint: null context");
+    IAM_REQUIRE(slot >= 0 && slot < kMaxMulti, "set_search_hint: slot must be 0, 1 or 2");
+    IAM_REQUIRE(!c->capturing, "set_search_hint: not allowed during graph capture");
+    IAM_TRY(ensure_slot(c, slot));
+    IAM_CHECK_HIP(hipMemcpyAsync(c->slots[slot].cutoff + 2, &value, sizeof(float), hipMemcpyHostToDevice, c->stream));
+    IAM_CHECK_HIP(hipStreamSynchronize(c->stream));
     return IAM_OK;
 }
 

@@ -391,6 +391,9 @@ struct WindowLds {
     int step, nl, above;
     uint32_t rlo, rhi;
     float cut;
+    float hint;                 // the hinted window's centre (thread 0 stores it before a barrier)
+    // hinted pass, per wave: min key - 1, max key, keys above | keys in << 16, numbers
+    uint4 hsum[NW];
 };
 
 // slot of bin b in a histogram read NB bins per lane: lane l's i-th 16-byte
@@ -398,7 +401,8 @@ struct WindowLds {
 template <int NB>
 __device__ __forceinline__ int hist_slot(int b)
 {
-    return ((b >> 2) & (NB / 4 - 1)) * 256 + (b / NB) * 4 + (b & 3);
+    const uint32_t u = (uint32_t)b;   // b >= 0: unsigned shifts, no rounding fix-ups of a division
+    return (int)(((u >> 2) & (NB / 4 - 1)) * 256u + (u / NB) * 4u + (u & 3u));
 }
 
 __device__ __forceinline__ int coarse_bin(uint32_t key) { return (int)((key >> 20) & (kCoarseBins - 1)); }
@@ -518,10 +522,11 @@ __device__ __forceinline__ void window_finish(WindowLds<NW>& W, const float (&U)
     }
 }
 
-// An upper bound of the cutoff known once the coarse bin dhi of rank
-// kmin = t - 2 is (t >= 3).  With u_j the j-th largest importance, gmin /
-// gmax their range and the bracket [min, max] of the rounds, the reference's
-// outcomes are (bucketMul.cl:131-213):
+// An upper bound of the cutoff from an upper bound `edge` > u_{t-2} (t >= 3):
+// the upper edge of the coarse bin of rank kmin = t - 2, or the upper end of
+// a hinted window holding that rank.  With u_j the j-th largest importance,
+// gmin / gmax their range and the bracket [min, max] of the rounds, the
+// reference's outcomes are (bucketMul.cl:131-213):
 //   count == t            returns b with u_{t+1} <= b < u_t;
 //   |maxCount-minCount|<3 returns b = the moved end: if max moved, count(b)
 //                         >= minCount - 2 >= t - 2, so b < u_{t-2}; if min
@@ -534,91 +539,184 @@ __device__ __forceinline__ void window_finish(WindowLds<NW>& W, const float (&U)
 //                         ulp(gmax) (each fp32 midpoint rounds by at most
 //                         half an ulp of the sum).
 // With delta = max(1.0001e-5, (gmax - gmin) 2^-20 + gmax 2^-23) and
-// u_t <= u_{t-2}: cutoff < u_{t-2} + delta, and u_{t-2} lies below the upper
-// edge of bin dhi, so with the sum rounded up
-//   cutoff < edge(dhi + 1) + delta = hi,
+// u_t <= u_{t-2} < edge, with the sum rounded up
+//   cutoff < u_{t-2} + delta < edge + delta <= hi,
 // and every row whose importance reaches hi is selected.  Where t < 3, or an
 // importance is infinite, there is no bound: hi = NaN, which no importance
 // reaches (not even +inf).
-__device__ __forceinline__ float cutoff_upper(int t, int dhi, uint32_t kmn, uint32_t kmx)
+__device__ __forceinline__ float cutoff_upper(int t, float edge, uint32_t kmn, uint32_t kmx)
 {
     if (t < 3 || kmx >= 0xff800000u) return __int_as_float(0x7fc00000);   // kmx: the key of +inf
     const double gmn = (double)key_float(kmn), gmx = (double)key_float(kmx);
     const double dl = fmax(1.0001e-5, (gmx - gmn) * 0x1p-20 + gmx * 0x1p-23);
-    return __double2float_ru((double)__uint_as_float((uint32_t)(dhi + 1) << 20) + dl);
+    return __double2float_ru((double)edge + dl);
 }
+
+// A hint the windowed search takes: a positive normal float well inside the
+// float range (the cutoff of the same matrix in the previous decode step)
+__device__ __forceinline__ bool hint_usable(float h) { return h >= 1e-30f && h <= 1e30f; }
 
 // Returns 1 with the cutoff in every wave (overlap has run in every wave),
 // 0 when declined before it ran, 2 when declined after it.
+//
+// With a usable hint (the same value in every wave), one pass replaces
+// steps A to C: the window is [7/8 hint, 8/7 hint); each thread counts its
+// keys above it and its numbers, adds the keys inside it to the fine bins,
+// and a barrier sums the waves' counts and key ranges.  When the window
+// holds the ranks kmin .. kmax (fewer than kmin keys above it, at least
+// kmax down to its lower end), step D runs on it as on a window from B;
+// otherwise the fine bins are cleared and steps A to D run.  Either way the
+// keys u_{t-2} .. u_{t+2}, and so the cutoff, are the same: the hint only
+// picks which window finds them.
 template <int NW, typename Overlap>
 __device__ __forceinline__ int search_window(const float (&v)[IAM_PROBES_COUNT / (64 * NW)], int quantile, WindowLds<NW>& W,
                              float& cut, Overlap&& overlap)
 {
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
-    constexpr int VPT = IAM_PROBES_COUNT / (64 * NW);
+    constexpr int NT = 64 * NW;
+    constexpr int VPT = IAM_PROBES_COUNT / NT;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-
-    // ---- A. keys, the coarse histogram, the waves' key ranges
-    uint32_t key[VPT];
-    uint32_t kmn1 = 0xffffffffu, kmx = 0u;   // min of key - 1 (NaN keys wrap to the top), max
-#pragma unroll
-    for (int k = 0; k < VPT; k++) {
-        key[k] = order_key(v[k]);
-        kmn1 = min(kmn1, key[k] - 1u);
-        kmx = max(kmx, key[k]);
-        atomicAdd(key[k] != 0u ? W.coarse + hist_slot<32>(coarse_bin(key[k])) : &W.nan_bin, 1u);
-    }
-    kmn1 = wave_min_u32(kmn1);
-    kmx = wave_max_u32(kmx);
-    if (lane == 0) {
-        W.red[0][wave] = kmn1;
-        W.red[1][wave] = kmx;
-    }
-    __syncthreads();
-
-    // ---- B. the window, in every wave alike
-    kmn1 = 0xffffffffu;
-    kmx = 0u;
-#pragma unroll
-    for (int w = 0; w < NW; w++) {
-        kmn1 = min(kmn1, W.red[0][w]);
-        kmx = max(kmx, W.red[1][w]);
-    }
-    const uint32_t kmn = kmn1 + 1u;
-    if (kmx == 0u || kmn < 0x80000000u) return 0;    // no number, or one below +0
     const int t = IAM_PROBES_COUNT - quantile;       // bucketMul.cl:81
-    const HistScan<32> cs = hist_scan<32>(W.coarse);
-    const int nv = cs.total;
-    const int kmin = max(1, t - 2), kmax = min(nv, t + 2);
-    if (kmin > kmax) return 0;
-    int dhi, ab_hi, dlo, ab_lo, c_lo;
-    hist_find2<32>(W.coarse, cs, kmin, kmax, dhi, ab_hi, dlo, ab_lo, c_lo);
-    const int nc = dhi - dlo + 1;
-    const int mc = ab_lo + c_lo - ab_hi;    // keys in the window
-    const uint32_t base = 0x80000000u + ((uint32_t)dlo << 20);
-    const uint32_t width = (uint32_t)nc << 20;
-    const int sf = 10 + (nc > 1 ? 32 - __clz(nc - 1) : 0);   // 1024 fine bins cover the window
-    const bool listed = mc <= kSmallWindow;
 
-    // ---- C. the window's list or its fine histogram
-    if (listed) {
+    uint32_t key[VPT];
 #pragma unroll
-        for (int k = 0; k < VPT; k++)
-            if (key[k] != 0u && key[k] - base < width) W.list[atomicAdd(&W.nlist, 1u)] = key[k];
-    } else {
+    for (int k = 0; k < VPT; k++) key[k] = order_key(v[k]);
+
+    // the window of step D: its keys as a list (listed, mc keys) or in the
+    // fine bins (sf: bin shift) from key base over width key units, ab_hi
+    // keys above it; the ranks it holds, the key range, and the bound hi
+    uint32_t kmn, kmx, base, width;
+    int sf, ab_hi, kmin, kmax, mc = 0;
+    bool listed = false, ready = false;
+    float hi;
+
+    // ---- H. the hinted window
+    const float hint = W.hint;
+    if (hint_usable(hint)) {
+        const uint32_t klo = order_key(__fmul_rn(hint, 0.875f)), khi = order_key(__fmul_rn(hint, 1.142857142857f));
+        const uint32_t hw = khi - klo;
+        const int hsf = hw > (uint32_t)kFineBins ? 32 - __clz(hw - 1u) - 10 : 0;
+        // per thread: its keys' range, the keys above the window and the
+        // numbers (c_n), keys inside the window in the high half of c_ai
+        // (at most 1024 keys a wave: no carry between the halves)
+        uint32_t kmn1 = 0xffffffffu, kmx1 = 0u, c_ai = 0u, c_n = 0u;
 #pragma unroll
         for (int k = 0; k < VPT; k++) {
-            const uint32_t rel = key[k] - base;
-            if (key[k] != 0u && rel < width) {
-                const int fs = hist_slot<16>((int)(rel >> sf));
+            kmn1 = min(kmn1, key[k] - 1u);
+            kmx1 = max(kmx1, key[k]);
+            c_ai += key[k] >= khi ? 1u : 0u;
+            c_n += key[k] != 0u ? 1u : 0u;
+            const uint32_t rel = key[k] - klo;
+            if (key[k] != 0u && rel < hw) {
+                c_ai += 1u << 16;
+                const int fs = hist_slot<16>((int)(rel >> hsf));
                 atomicAdd(W.fine + fs, 1u);
                 atomicMax(W.fmax + fs, key[k]);
                 atomicMax(W.fminv + fs, ~key[k]);
             }
         }
+        kmn1 = wave_min_u32(kmn1);
+        kmx1 = wave_max_u32(kmx1);
+        c_ai = wave_sum(c_ai);
+        c_n = wave_sum(c_n);
+        if (lane == 0) W.hsum[wave] = make_uint4(kmn1, kmx1, c_ai, c_n);
+        __syncthreads();
+        kmn1 = 0xffffffffu;
+        kmx = 0u;
+        int na = 0, nw = 0, nv = 0;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const uint4 r = W.hsum[w];
+            kmn1 = min(kmn1, r.x);
+            kmx = max(kmx, r.y);
+            na += (int)(r.z & 0xffffu);
+            nw += (int)(r.z >> 16);
+            nv += (int)r.w;
+        }
+        kmn = kmn1 + 1u;
+        if (kmx == 0u || kmn < 0x80000000u) return 0;    // no number, or one below +0
+        kmin = max(1, t - 2);
+        kmax = min(nv, t + 2);
+        if (kmin > kmax) return 0;
+        if (na < kmin && na + nw >= kmax) {
+            ready = true;
+            base = klo;
+            width = hw;
+            sf = hsf;
+            ab_hi = na;
+            hi = cutoff_upper(t, key_float(khi), kmn, kmx);
+        } else {   // the fine bins cleared for the full search
+            uint4* z = reinterpret_cast<uint4*>(W.fine);
+#pragma unroll
+            for (int i = 0; i < (3 * kFineBins / 4 + NT - 1) / NT; i++)
+                if (i * NT + (int)threadIdx.x < 3 * kFineBins / 4) z[i * NT + threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
+            __syncthreads();
+        }
     }
-    __syncthreads();
+
+    if (!ready) {
+        // ---- A. the coarse histogram, the waves' key ranges
+        uint32_t kmn1 = 0xffffffffu;   // min of key - 1 (NaN keys wrap to the top)
+        kmx = 0u;
+#pragma unroll
+        for (int k = 0; k < VPT; k++) {
+            kmn1 = min(kmn1, key[k] - 1u);
+            kmx = max(kmx, key[k]);
+            atomicAdd(key[k] != 0u ? W.coarse + hist_slot<32>(coarse_bin(key[k])) : &W.nan_bin, 1u);
+        }
+        kmn1 = wave_min_u32(kmn1);
+        kmx = wave_max_u32(kmx);
+        if (lane == 0) {
+            W.red[0][wave] = kmn1;
+            W.red[1][wave] = kmx;
+        }
+        __syncthreads();
+
+        // ---- B. the window, in every wave alike
+        kmn1 = 0xffffffffu;
+        kmx = 0u;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            kmn1 = min(kmn1, W.red[0][w]);
+            kmx = max(kmx, W.red[1][w]);
+        }
+        kmn = kmn1 + 1u;
+        if (kmx == 0u || kmn < 0x80000000u) return 0;    // no number, or one below +0
+        const HistScan<32> cs = hist_scan<32>(W.coarse);
+        const int nv = cs.total;
+        kmin = max(1, t - 2);
+        kmax = min(nv, t + 2);
+        if (kmin > kmax) return 0;
+        int dhi, dlo, ab_lo, c_lo;
+        hist_find2<32>(W.coarse, cs, kmin, kmax, dhi, ab_hi, dlo, ab_lo, c_lo);
+        const int nc = dhi - dlo + 1;
+        mc = ab_lo + c_lo - ab_hi;    // keys in the window
+        base = 0x80000000u + ((uint32_t)dlo << 20);
+        width = (uint32_t)nc << 20;
+        sf = 10 + (nc > 1 ? 32 - __clz(nc - 1) : 0);   // 1024 fine bins cover the window
+        listed = mc <= kSmallWindow;
+
+        // ---- C. the window's list or its fine histogram
+        if (listed) {
+#pragma unroll
+            for (int k = 0; k < VPT; k++)
+                if (key[k] != 0u && key[k] - base < width) W.list[atomicAdd(&W.nlist, 1u)] = key[k];
+        } else {
+#pragma unroll
+            for (int k = 0; k < VPT; k++) {
+                const uint32_t rel = key[k] - base;
+                if (key[k] != 0u && rel < width) {
+                    const int fs = hist_slot<16>((int)(rel >> sf));
+                    atomicAdd(W.fine + fs, 1u);
+                    atomicMax(W.fmax + fs, key[k]);
+                    atomicMax(W.fminv + fs, ~key[k]);
+                }
+            }
+        }
+        __syncthreads();
+        hi = cutoff_upper(t, __uint_as_float((uint32_t)(dhi + 1) << 20), kmn, kmx);
+    }
 
     // ---- D. wave 0: u_{t-2} .. u_{t+2} and the rounds
     if (wave == 0) {
@@ -671,7 +769,7 @@ __device__ __forceinline__ int search_window(const float (&v)[IAM_PROBES_COUNT /
             }
         }
     }
-    overlap(cutoff_upper(t, dhi, kmn, kmx));
+    overlap(hi);
     __syncthreads();
     const int step2 = W.step;
     if (step2 == kWinDone) {

@@ -255,6 +255,15 @@ class Ctx:
         """Count the walk's selected rows (default on; off shortens each reduce)."""
         check(lib().iam_set_walk_counting(self.h, 1 if on else 0))
 
+    def set_search_hints(self, on):
+        """Start each fused call's cutoff search from the slot's previous
+        cutoff (same results; default off)."""
+        check(lib().iam_set_search_hints(self.h, 1 if on else 0))
+
+    def set_search_hint(self, slot, value):
+        """Set matrix slot `slot`'s search hint (any float; unusable ones mean none)."""
+        check(lib().iam_set_search_hint(self.h, int(slot), C.c_float(value)))
+
     def set_selection_block(self, block_inputs, below_effort=2.0):
         """Block-structured selection: blocks of `block_inputs` consecutive
         inputs share each rank's selection, for efforts below `below_effort`

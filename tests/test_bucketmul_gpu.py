@@ -272,6 +272,56 @@ def test_cutoff_search_kinds(O, iam, ctx, kind):
     dx.free()
 
 
+_HINT_KINDS = ["normal", "skew", "ties", "constant", "outlier", "tiny", "inf", "nan", "huge",
+               "adjacent", "zero", "few_nans", "bimodal", "quantized"]
+
+
+@pytest.mark.parametrize("kind", _HINT_KINDS)
+def test_search_hints(O, iam, ctx, kind):
+    """The walk's search started from a hint finds the oracle's cutoff bit
+    for bit, whatever the hint: the exact cutoff and its neighbouring float
+    (the window's centre on a key), 10% off (inside the window or at its
+    edge), a factor 8 off (the window misses: the full search runs), and
+    hints that are no hint (0, negative, NaN, +inf, -inf, tiny, huge); also
+    the hint the previous call left, from a scaled input (as the next decode
+    step finds it).  The selected row count and the walk's count match
+    too."""
+    rng = np.random.default_rng(300 + _HINT_KINDS.index(kind))
+    x, p = _search_input(kind, rng)
+    quants = [0, 3, 1023, 3071, 3890, 4092, 4095]
+    efforts = sorted({float(np.float32(1.0 - (q + 0.5) / 4095.0)) for q in quants} | {0.25})
+    b, s, _ = make_matrix(O, 256, 4096, tid=9)
+    R, C = b.shape
+    db, ds, dp = ctx.upload(b), ctx.upload(s), ctx.upload(p)
+    dy = ctx.empty(16 * C, np.float32)
+    mat = iam.BucketMatrix(db.ptr, ds.ptr, dp.ptr, R, C, 4, 3)
+    ctx.set_search_hints(True)
+    try:
+        with np.errstate(all="ignore"):
+            for scale in (1.0, 1.03):
+                xs = (x * np.float32(scale)).astype(np.float32)
+                dx = ctx.upload(xs)
+                for effort in efforts:
+                    q = O.effort_quantile(effort)
+                    ocut = np.float32(O.find_cutoff(xs, p, q))
+                    _, oS = O.select_rows(xs, s, ocut, R, R // 16)
+                    hints = [None, ocut, np.nextafter(ocut, np.float32(np.inf)), ocut * np.float32(1.1),
+                             ocut * np.float32(0.9), ocut * np.float32(8), ocut / np.float32(8), 0.0, -1.0,
+                             np.nan, np.inf, -np.inf, 1e-31, 2e30]
+                    for h in hints:
+                        if h is not None:      # None: the hint the previous call left
+                            ctx.set_search_hint(0, float(h))
+                        ctx.fused([mat], dx, R // 16, [dy], effort)
+                        cut, S = ctx.dispatch_info(0)
+                        assert np.float32(cut).view(np.uint32) == ocut.view(np.uint32), (kind, scale, effort, h, cut, ocut)
+                        assert S == oS and ctx.walk_count(0) == S, (kind, scale, effort, h, S, oS)
+                dx.free()
+    finally:
+        ctx.set_search_hints(False)
+    for d in (db, ds, dp, dy):
+        d.free()
+
+
 @pytest.mark.parametrize("in_dim", [4096, 8192])
 def test_fused_norm_input(O, iam, ctx, in_dim):
     """iam_bucketmul_fused with a norm input: x = RMSNorm(h) * gain is the

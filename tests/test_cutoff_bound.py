@@ -3,7 +3,9 @@ those whose importance reaches an upper bound hi > cutoff taken from the
 coarse window of the cutoff search (cutoff_upper in csrc/search.h).  Here
 the bound is restated in numpy and checked against the oracle's bisection
 (bucketMul.cl:68-214) on adversarial importance vectors at quantiles across
-the range, edge ranks included: every cutoff lies strictly below hi.  The
+the range, edge ranks included: every cutoff lies strictly below hi; also
+for the hinted window (the previous decode step's cutoff of the matrix),
+where hi comes from the window's upper end.  The
 same bound with its slack term removed fails on some of these vectors, so
 the cases reach the bound's edge.  On the GPU the bucket-walk parity tests
 (selected count and outputs against the oracle) cover the device's use of
@@ -116,3 +118,50 @@ def test_bound_without_slack_fails_somewhere(O):
             if hi is not None and not (O.find_cutoff_imp(imp, q) < hi):
                 broken += 1
     assert broken > 0
+
+
+def hinted_upper(imp, t, hint):
+    """cutoff_upper of a hinted window: None where the device would not use
+    the hint or the window [7/8 hint, 8/7 hint) misses ranks t-2 .. t+2;
+    else the window's upper end plus delta, rounded up."""
+    if not (1e-30 <= hint <= 1e30):
+        return None
+    k = keys(imp)
+    nums = k[k != 0]
+    if len(nums) == 0 or nums.min() < 0x80000000:
+        return None
+    kmx = int(nums.max())
+    if t < 3 or kmx >= 0xFF800000:
+        return None
+    klo = int(keys(np.array([f32(hint) * f32(0.875)], f32))[0])
+    khi = int(keys(np.array([f32(hint) * f32(1.142857142857)], f32))[0])
+    above = int(np.count_nonzero(nums >= khi))
+    inside = int(np.count_nonzero((nums >= klo) & (nums < khi)))
+    kmin, kmax = max(1, t - 2), min(len(nums), t + 2)
+    if not (above < kmin and above + inside >= kmax):
+        return None
+    gmn, gmx = key_float(int(nums.min())), key_float(kmx)
+    dl = max(1.0001e-5, (gmx - gmn) * 2.0**-20 + gmx * 2.0**-23)
+    return round_up(key_float(khi) + dl)
+
+
+def test_hinted_window_bound_holds(O):
+    """The same bound from a hinted window (the previous step's cutoff of
+    the matrix): wherever the window holds ranks t-2 .. t+2, every cutoff
+    lies strictly below its upper end plus delta."""
+    rng = np.random.default_rng(9)
+    checked = 0
+    for rep in range(4):
+        for name, imp in vectors(rng):
+            rng.shuffle(imp)
+            for q in quantiles(rng):
+                c = O.find_cutoff_imp(imp, q)
+                if not np.isfinite(c) or c <= 0:
+                    continue
+                for f in (1.0, 1.0 + 2.0**-23, 1.05, 0.95, 1.12, 0.89, 1.14, 0.876):
+                    hi = hinted_upper(imp, N - q, float(f32(c) * f32(f)))
+                    if hi is None:
+                        continue
+                    assert c < hi, (name, q, f, c, hi)
+                    checked += 1
+    assert checked > 1000
