@@ -1091,6 +1091,9 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
 
 int quantile_of(float effort) { return (int)((double)(kProbes - 1) * (1.0 - (double)effort)); }
 
+// ranks within this many of either end of the importances take no search hint
+constexpr int kHintEdge = 64;
+
 // Expected fraction of selected rows (N(0,1) inputs, N(0, 0.02^2) weights),
 // used only to size the walk grid.
 static double est_fraction(float effort)
@@ -1300,7 +1303,13 @@ int walk_group(Ctx* c, const WalkGroup& g)
         d.stats = M.stats + (size_t)g.expert_no * (size_t)M.expert_rows * M.stats_stride;
         d.probes = M.probes + (size_t)g.expert_no * kProbes;
         d.cutoff = wm.cutoff;
-        d.hint = wm.hint;
+        // a hint only for order statistics away from the ends: the few
+        // smallest or largest importances (efforts near 1 or 0) move too much
+        // between decode steps for a window around the previous one (about
+        // half of them missed at effort 1.0, each miss costing the hinted
+        // pass on top of the full search)
+        const int t_rank = kProbes - qv;
+        d.hint = t_rank >= kHintEdge && t_rank <= kProbes - kHintEdge ? wm.hint : nullptr;
         d.slice_count = wm.slice_count;
         d.acc = wm.acc;
         d.acc2 = wm.acc2;

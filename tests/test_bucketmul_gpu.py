@@ -288,7 +288,8 @@ def test_search_hints(O, iam, ctx, kind):
     too."""
     rng = np.random.default_rng(300 + _HINT_KINDS.index(kind))
     x, p = _search_input(kind, rng)
-    quants = [0, 3, 1023, 3071, 3890, 4092, 4095]
+    # ranks t = 4096 - quantile; the walk takes a hint for 64 <= t <= 4032
+    quants = [0, 3, 64, 65, 1023, 3071, 3890, 4031, 4032, 4092, 4095]
     efforts = sorted({float(np.float32(1.0 - (q + 0.5) / 4095.0)) for q in quants} | {0.25})
     b, s, _ = make_matrix(O, 256, 4096, tid=9)
     R, C = b.shape
