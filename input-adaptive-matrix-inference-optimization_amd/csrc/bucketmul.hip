@@ -789,7 +789,7 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     }
     // one value for the whole workgroup (work item 0 of the matrix may
     // rewrite the hint meanwhile), published by the barrier before the search
-    if (tid == 0) WL.hint = hint;
+    if (tid == 0 && d.hint) WL.hint = hint;
     if (norm) block_rmsnorm4096<VPT>(xs, gw, a.eps, s_part);
     if (regs) {
         if (first && dx) store_f32<VPT>(dx, xs);
@@ -818,7 +818,7 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
         importances<VPT>(xs, pw, v);
         if (!norm) __syncthreads();   // the window's histograms are clear (the norm's barrier orders them otherwise)
         float cut_w;
-        const int found = search_window<NW>(v, quantile, WL, cut_w, [&](float hi) {
+        const int found = search_window<NW>(v, quantile, d.hint != nullptr, WL, cut_w, [&](float hi) {
             select_prepare<NT>(ss, i0, ni, L, s_x, slice_regs, imp, vbits);
             // wave 0 comes here at the end of the search: its rows wait for the cutoff
             if (wave != 0 && a.sel_block == 1) {

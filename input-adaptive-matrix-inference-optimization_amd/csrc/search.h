@@ -559,7 +559,7 @@ __device__ __forceinline__ bool hint_usable(float h) { return h >= 1e-30f && h <
 // Returns 1 with the cutoff in every wave (overlap has run in every wave),
 // 0 when declined before it ran, 2 when declined after it.
 //
-// With a usable hint (the same value in every wave), one pass replaces
+// With a usable hint in W.hint (hinted; the same value in every wave), one pass replaces
 // steps A to C: the window is [7/8 hint, 8/7 hint); each thread counts its
 // keys above it and its numbers, adds the keys inside it to the fine bins,
 // and a barrier sums the waves' counts and key ranges.  When the window
@@ -569,8 +569,8 @@ __device__ __forceinline__ bool hint_usable(float h) { return h >= 1e-30f && h <
 // keys u_{t-2} .. u_{t+2}, and so the cutoff, are the same: the hint only
 // picks which window finds them.
 template <int NW, typename Overlap>
-__device__ __forceinline__ int search_window(const float (&v)[IAM_PROBES_COUNT / (64 * NW)], int quantile, WindowLds<NW>& W,
-                             float& cut, Overlap&& overlap)
+__device__ __forceinline__ int search_window(const float (&v)[IAM_PROBES_COUNT / (64 * NW)], int quantile, bool hinted,
+                             WindowLds<NW>& W, float& cut, Overlap&& overlap)
 {
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     constexpr int NT = 64 * NW;
@@ -591,8 +591,9 @@ __device__ __forceinline__ int search_window(const float (&v)[IAM_PROBES_COUNT /
     bool listed = false, ready = false;
     float hi;
 
-    // ---- H. the hinted window
-    const float hint = W.hint;
+    // ---- H. the hinted window (hinted: the launch has a hint, uniform; its
+    // value is read from LDS only then)
+    const float hint = hinted ? W.hint : 0.0f;
     if (hint_usable(hint)) {
         const uint32_t klo = order_key(__fmul_rn(hint, 0.875f)), khi = order_key(__fmul_rn(hint, 1.142857142857f));
         const uint32_t hw = khi - klo;
