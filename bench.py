@@ -134,6 +134,9 @@ def group_table(ctx, cfg, ctx_len):
         us = ms * 1e3 / calls
         out[g] = {"launches": calls, "weight_bytes": round(wb / calls), "bytes": round(b),
                   "us": round(us, 2), "GBs": round(b / us / 1e3, 1), "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+        tries, hits = ctx.walk_group_hints(g)
+        if tries:   # matrices whose cutoff search started from the previous step's cutoff, and held
+            out[g]["hint_hits"] = round(hits / tries, 4)
     ms, calls = ctx.kernel_stat("attention")
     if calls:
         b = kv_bytes(cfg, ctx_len)

@@ -196,6 +196,12 @@ int iam_walk_counters(iam_ctx* ctx, uint64_t* weight_bytes, uint64_t* rows, uint
 #define IAM_WALK_GROUP_LM 5
 int iam_walk_group_counters(iam_ctx* ctx, int group, uint64_t* weight_bytes, uint64_t* rows,
                             uint64_t* matrices);
+/* Of the group's walks since the last reset: the matrices whose cutoff
+ * search started from a hint (tries; see iam_set_search_hints) and those
+ * whose hinted window held the cutoff's ranks (hits; the others ran the
+ * full search).  Counted with the counters above (iam_set_walk_counting).
+ * Blocking.  No counterpart in the reference. */
+int iam_walk_group_hints(iam_ctx* ctx, int group, uint64_t* tries, uint64_t* hits);
 /* Counting of the walk's selected rows (default on): the first column tile
  * of each input slice adds its row count to the counters above (three
  * 64-bit atomics per slice).  Off, the counters are not updated.  The

@@ -813,12 +813,13 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     uint32_t vbits;
     float listed = __int_as_float(0x7fc00000);   // this wave's rows from this importance up are listed
     const uint32_t rowb = (uint32_t)sel_input<NT>(tid) << 4;
+    bool hint_hit = false;   // the search's hinted window held the cutoff's ranks
     if (mode != kInCutoff) {
         float v[VPT];
         importances<VPT>(xs, pw, v);
         if (!norm) __syncthreads();   // the window's histograms are clear (the norm's barrier orders them otherwise)
         float cut_w;
-        const int found = search_window<NW>(v, quantile, d.hint != nullptr, WL, cut_w, [&](float hi) {
+        const int found = search_window<NW>(v, quantile, d.hint != nullptr, WL, cut_w, hint_hit, [&](float hi) {
             select_prepare<NT>(ss, i0, ni, L, s_x, slice_regs, imp, vbits);
             // wave 0 comes here at the end of the search: its rows wait for the cutoff
             if (wave != 0 && a.sel_block == 1) {
@@ -857,6 +858,8 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
             atomicAdd(cr + 0, (unsigned long long)ns * (unsigned long long)d.C * 2ull);
             atomicAdd(cr + 1, (unsigned long long)ns);
             if (p == 0) atomicAdd(cr + 2, 1ull);
+            // hinted searches (high half) and those whose window held (low half)
+            if (p == 0 && d.hint && mode != kInCutoff) atomicAdd(cr + 3, (1ull << 32) | (hint_hit ? 1ull : 0ull));
         }
     }
 

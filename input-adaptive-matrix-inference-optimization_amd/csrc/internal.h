@@ -115,7 +115,8 @@ struct Ctx {
     // captured graphs hold those addresses and must be re-captured
     uint64_t scratch_gen = 0;
     // device walk counters, one block per walk label (kWalkLabels), each of
-    // kCounterLanes rows of {weight bytes, rows, matrices, pad}: each walk
+    // kCounterLanes rows of {weight bytes, rows, matrices, hinted searches
+    // << 32 | their hits}: each walk
     // adds to row (slice % kCounterLanes) of its label's block, so the
     // additions of one launch do not queue on one address
     unsigned long long* counters = nullptr;

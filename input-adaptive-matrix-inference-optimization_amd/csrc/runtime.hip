@@ -458,6 +458,25 @@ static int read_counters(Ctx* c, int g0, int g1, uint64_t* bytes, uint64_t* rows
     return IAM_OK;
 }
 
+int iam_walk_group_hints(iam_ctx* c, int group, uint64_t* tries, uint64_t* hits)
+{
+    if (!c) return fail(IAM_E_INVALID, "walk_group_hints: null context");
+    if (group < 0 || group >= kWalkLabels)
+        return fail(IAM_E_INVALID, "walk_group_hints: group must be one of IAM_WALK_GROUP_*");
+    std::vector<unsigned long long> h(kCounterWords);
+    IAM_CHECK_HIP(hipMemcpyAsync(h.data(), c->counters, kCounterWords * sizeof(unsigned long long),
+                                 hipMemcpyDeviceToHost, c->stream));
+    IAM_CHECK_HIP(hipStreamSynchronize(c->stream));
+    unsigned long long t = 0, k = 0;
+    for (int l = group * kCounterLanes; l < (group + 1) * kCounterLanes; l++) {
+        t += h[(size_t)l * 4 + 3] >> 32;
+        k += h[(size_t)l * 4 + 3] & 0xffffffffull;
+    }
+    if (tries) *tries = t;
+    if (hits) *hits = k;
+    return IAM_OK;
+}
+
 int iam_walk_counters(iam_ctx* c, uint64_t* bytes, uint64_t* rows, uint64_t* mats, int reset)
 {
     if (!c) return fail(IAM_E_INVALID, "walk_counters: null context");

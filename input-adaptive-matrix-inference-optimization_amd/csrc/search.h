@@ -557,7 +557,8 @@ __device__ __forceinline__ float cutoff_upper(int t, float edge, uint32_t kmn, u
 __device__ __forceinline__ bool hint_usable(float h) { return h >= 1e-30f && h <= 1e30f; }
 
 // Returns 1 with the cutoff in every wave (overlap has run in every wave),
-// 0 when declined before it ran, 2 when declined after it.
+// 0 when declined before it ran, 2 when declined after it; hint_hit: the
+// hinted window held the cutoff's ranks (in every wave).
 //
 // With a usable hint in W.hint (hinted; the same value in every wave), one pass replaces
 // steps A to C: the window is [7/8 hint, 8/7 hint); each thread counts its
@@ -570,7 +571,7 @@ __device__ __forceinline__ bool hint_usable(float h) { return h >= 1e-30f && h <
 // picks which window finds them.
 template <int NW, typename Overlap>
 __device__ __forceinline__ int search_window(const float (&v)[IAM_PROBES_COUNT / (64 * NW)], int quantile, bool hinted,
-                             WindowLds<NW>& W, float& cut, Overlap&& overlap)
+                             WindowLds<NW>& W, float& cut, bool& hint_hit, Overlap&& overlap)
 {
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     constexpr int NT = 64 * NW;
@@ -590,6 +591,7 @@ __device__ __forceinline__ int search_window(const float (&v)[IAM_PROBES_COUNT /
     int sf, ab_hi, kmin, kmax, mc = 0;
     bool listed = false, ready = false;
     float hi;
+    hint_hit = false;
 
     // ---- H. the hinted window (hinted: the launch has a hint, uniform; its
     // value is read from LDS only then)
@@ -642,6 +644,7 @@ __device__ __forceinline__ int search_window(const float (&v)[IAM_PROBES_COUNT /
         if (kmin > kmax) return 0;
         if (na < kmin && na + nw >= kmax) {
             ready = true;
+            hint_hit = true;
             base = klo;
             width = hw;
             sf = hsf;

@@ -255,6 +255,13 @@ class Ctx:
         """Count the walk's selected rows (default on; off shortens each reduce)."""
         check(lib().iam_set_walk_counting(self.h, 1 if on else 0))
 
+    def walk_group_hints(self, group):
+        """(hinted cutoff searches, hits) of a walk group ('qkv', 'o', ...)
+        since the counters' reset."""
+        t, k = C.c_uint64(), C.c_uint64()
+        check(lib().iam_walk_group_hints(self.h, self.WALK_GROUPS[group], C.byref(t), C.byref(k)))
+        return t.value, k.value
+
     def set_search_hints(self, on):
         """Start each fused call's cutoff search from the slot's previous
         cutoff (same results; default off)."""

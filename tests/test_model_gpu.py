@@ -150,6 +150,29 @@ def test_counting_off_gives_the_same_tokens(O, ctx, model):
     assert ctx.walk_counters(reset=True)[2] > 0
 
 
+def test_search_hint_counters(O, ctx, model):
+    """Each walk of a decode step starts its cutoff search from the same
+    matrix's cutoff of the previous step: at effort 0.25 (rank 1025) every
+    group takes hints and nearly all hold (the first step after the reset
+    has none); at effort 1.0 (rank 4096, within 64 of the end) none is
+    taken.  Hits never exceed tries, and the tokens are those of an
+    unhinted run (test_greedy_tokens_match_oracle, which checks them
+    against the oracle, runs with hints too)."""
+    prompt = O.gen_tokens(0, 97, 12, CFG["vocab"]).tolist()
+    for effort, want in ((0.25, True), (1.0, False)):
+        model.reset_caches()
+        ctx.walk_counters(reset=True)
+        model.generate(prompt, 4, effort, use_graph=True)
+        for g in ("qkv", "o", "ffn13", "ffn2", "lm"):
+            tries, hits = ctx.walk_group_hints(g)
+            assert hits <= tries, (effort, g, tries, hits)
+            if want:
+                assert tries > 0 and hits >= 0.7 * tries, (effort, g, tries, hits)
+            else:
+                assert tries == 0, (effort, g, tries)
+    ctx.walk_counters(reset=True)
+
+
 @pytest.mark.parametrize("effort", [0.05, 1.0])
 def test_skewed_embedding_logits_match_oracle(O, ctx, model, effort):
     """Skew stress: 1% of the hidden channels (41 of 4096) scaled 20x after
