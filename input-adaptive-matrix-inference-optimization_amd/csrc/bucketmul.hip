@@ -1114,9 +1114,12 @@ double est_rows(int rows, float effort) { return std::max(1.0, rows * est_fracti
 // Walk launch shape: 8-wave workgroups (each CU holds one: 128 KB of fp64
 // tiles), about IAM_WALK_WGS of them, shared among the matrices in
 // proportion to their expected weight bytes (at least one slice each), so
-// that no CU holds more work than another.
+// that no CU holds more work than another.  IAM_WALK_UNR loads of RPI rows
+// form a batch, two batches in flight per wave: with 2, each batch's LDS
+// adds reach the tile in shorter bursts than with 4 (434.8 against 421.6
+// tokens/s in decode), while 1 leaves too little in flight (411).
 #ifndef IAM_WALK_UNR
-#define IAM_WALK_UNR 4
+#define IAM_WALK_UNR 2
 #endif
 #ifndef IAM_WALK_WGS
 #define IAM_WALK_WGS 256
