@@ -556,9 +556,10 @@ __device__ __forceinline__ float cutoff_upper(int t, float edge, uint32_t kmn, u
 // float range (the cutoff of the same matrix in the previous decode step)
 __device__ __forceinline__ bool hint_usable(float h) { return h >= 1e-30f && h <= 1e30f; }
 
-// Returns 1 with the cutoff in every wave (overlap has run in every wave),
-// 0 when declined before it ran, 2 when declined after it; hint_hit: the
-// hinted window held the cutoff's ranks (in every wave).
+// Returns 1 with the cutoff in every wave (overlap has run in every wave,
+// wave 0's with hi = NaN), 0 when declined before it ran, 2 when declined
+// after it; hint_hit: the hinted window held the cutoff's ranks (in every
+// wave).
 //
 // With a usable hint in W.hint (hinted; the same value in every wave), one pass replaces
 // steps A to C: the window is [7/8 hint, 8/7 hint); each thread counts its
@@ -649,7 +650,9 @@ __device__ __forceinline__ int search_window(const float (&v)[IAM_PROBES_COUNT /
             width = hw;
             sf = hsf;
             ab_hi = na;
-            hi = cutoff_upper(t, key_float(khi), kmn, kmx);
+            // (wave 0, whose tail is the search's critical path, does not
+            // list rows early: it skips the bound's fp64 arithmetic)
+            hi = wave != 0 ? cutoff_upper(t, key_float(khi), kmn, kmx) : __int_as_float(0x7fc00000);
         } else {   // the fine bins cleared for the full search
             uint4* z = reinterpret_cast<uint4*>(W.fine);
 #pragma unroll
@@ -719,7 +722,8 @@ __device__ __forceinline__ int search_window(const float (&v)[IAM_PROBES_COUNT /
             }
         }
         __syncthreads();
-        hi = cutoff_upper(t, __uint_as_float((uint32_t)(dhi + 1) << 20), kmn, kmx);
+        hi = wave != 0 ? cutoff_upper(t, __uint_as_float((uint32_t)(dhi + 1) << 20), kmn, kmx)
+                       : __int_as_float(0x7fc00000);
     }
 
     // ---- D. wave 0: u_{t-2} .. u_{t+2} and the rounds
