@@ -992,16 +992,34 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     // workgroup waits for all of them before it arrives at the tile
     // counter: every addition is then performed, at the one place where all
     // atomics on that address are ordered, before the last workgroup to
-    // arrive takes the sums there with atomic exchanges.
-    const bool ret = a.fin != kFinNone;
-    double sink = 0.0;
+    // arrive takes the sums there with atomic exchanges.  The two modes
+    // keep loops of their own: within one loop the compiler merges the two
+    // additions into a returning one and waits for each return in turn, a
+    // round trip per addition in both modes; here the non-returning
+    // additions are issued back to back, and the returning ones are all
+    // issued before the first wait.
+    // The staged sums are all read before the first addition goes out
+    // (an LDS read after it may reuse its registers and wait for it).
+    Tile sv[OPT];
 #pragma unroll
     for (int k2 = 0; k2 < OPT; k2++) {
-        const int o = tid + k2 * NT;                      // col_local*16 + pos
-        const Tile sv = tiles[o + (o >> 7)];
-        if (o < nout && sv != (Tile)0) {
-            if (ret) sink += __hip_atomic_fetch_add(out + o, (double)sv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            else acc_add(out + o, (double)sv);
+        const int o = tid + k2 * NT;                          // col_local*16 + pos
+        sv[k2] = tiles[o + (o >> 7)];
+    }
+    double got[OPT];
+    if (a.fin != kFinNone) {
+#pragma unroll
+        for (int k2 = 0; k2 < OPT; k2++) {
+            const int o = tid + k2 * NT;
+            got[k2] = 0.0;
+            if (o < nout && sv[k2] != (Tile)0)
+                got[k2] = __hip_atomic_fetch_add(out + o, (double)sv[k2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    } else {
+#pragma unroll
+        for (int k2 = 0; k2 < OPT; k2++) {
+            const int o = tid + k2 * NT;
+            if (o < nout && sv[k2] != (Tile)0) acc_add(out + o, (double)sv[k2]);
         }
     }
     // accumulators of earlier launches that are read no more (after the
@@ -1011,7 +1029,8 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     if (a.fin == kFinNone) return;
 
     // ---- finalize: the last workgroup to flush into tile t
-    asm volatile("" ::"v"(sink));   // the returned values are in: every addition is performed
+#pragma unroll
+    for (int k2 = 0; k2 < OPT; k2++) asm volatile("" ::"v"(got[k2]));   // the returned values are in: every addition is performed
     __syncthreads();
     if (tid == 0)
         s_last = __hip_atomic_fetch_add(d.tile_ctr + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
@@ -1022,8 +1041,27 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     if (a.fin == kFinSilu) {
         double* g_acc = reinterpret_cast<double*>(a.d[0].acc) + (size_t)t * TOUT;
         double* u_acc = reinterpret_cast<double*>(a.d[1].acc) + (size_t)t * TOUT;
-        for (int o = tid; o < nout; o += NT) {
-            const float gv = (float)acc_take(g_acc + o), uv = (float)acc_take(u_acc + o);
+        // every exchange goes out before the first value is used
+        double gt[OPT], ut[OPT];
+#pragma unroll
+        for (int k2 = 0; k2 < OPT; k2++) {
+            const int o = tid + k2 * NT;
+            gt[k2] = ut[k2] = 0.0;
+            if (o < nout) {
+                gt[k2] = acc_take(g_acc + o);
+                ut[k2] = acc_take(u_acc + o);
+            }
+        }
+        // the values' first use, pinned after the last exchange (the
+        // compiler would otherwise convert each one inside its branch and
+        // wait there)
+#pragma unroll
+        for (int k2 = 0; k2 < OPT; k2++) asm volatile("" : "+v"(gt[k2]), "+v"(ut[k2]));
+#pragma unroll
+        for (int k2 = 0; k2 < OPT; k2++) {
+            const int o = tid + k2 * NT;
+            if (o >= nout) break;
+            const float gv = (float)gt[k2], uv = (float)ut[k2];
             const size_t oo = (size_t)t * TOUT + o;
             if (a.d[0].y) a.d[0].y[oo] = gv;
             if (a.d[1].y) a.d[1].y[oo] = uv;
@@ -1035,8 +1073,19 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     // kFinStore
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int o = tid; o < nout; o += NT) {
-        const float yv = (float)acc_take(out + o);
+    double yt[OPT];
+#pragma unroll
+    for (int k2 = 0; k2 < OPT; k2++) {
+        const int o = tid + k2 * NT;
+        yt[k2] = o < nout ? acc_take(out + o) : 0.0;
+    }
+#pragma unroll
+    for (int k2 = 0; k2 < OPT; k2++) asm volatile("" : "+v"(yt[k2]));   // as above: the waits after the last exchange
+#pragma unroll
+    for (int k2 = 0; k2 < OPT; k2++) {
+        const int o = tid + k2 * NT;
+        if (o >= nout) break;
+        const float yv = (float)yt[k2];
         const int oo = t * TOUT + o;
         d.y[oo] = yv;
         take_max(bv, bi, yv, oo);
