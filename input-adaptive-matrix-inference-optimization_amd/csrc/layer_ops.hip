@@ -327,9 +327,12 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnArgs a, Acc scale)
         const int nq = a.n_heads * HD, nk = a.n_kv * HD;
         const size_t base = (size_t)(isk ? nq : nq + nk) + (size_t)kvh * HD;
         const size_t base2 = a.kv_copies > 1 ? base + 2 * (size_t)nk : base;   // the odd slices' copy
+        // all four loads unconditional (a single copy re-reads its own
+        // values), so they go out together and share one wait
         const double x0 = A[base + lane], x1 = A[base + DH + lane];
-        const float lo = (float)(a.kv_copies > 1 ? x0 + A[base2 + lane] : x0);
-        const float hi = (float)(a.kv_copies > 1 ? x1 + A[base2 + DH + lane] : x1);
+        const double y0 = A[base2 + lane], y1 = A[base2 + DH + lane];
+        const float lo = (float)(a.kv_copies > 1 ? x0 + y0 : x0);
+        const float hi = (float)(a.kv_copies > 1 ? x1 + y1 : x1);
         float o0 = lo, o1 = hi;
         if (isk) {
             o0 = __fsub_rn(__fmul_rn(lo, c), __fmul_rn(hi, sn));
