@@ -710,22 +710,19 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     const bool norm = mode == kInNorm || mode == kInResNorm || mode == kInEmbedNorm;
     const bool regs = norm || mode == kInAttn;           // x[0:4096] computed in registers
 
-    // ---- prologue: every global load is issued before any is used
+    // ---- prologue: every global load is issued before any is used.
+    // Each array is read only in the modes that load it, and none has a
+    // default: the compiler cannot tell the modes apart, and a default it
+    // sets on the other modes' path (where that path merges with the
+    // loading one) makes those modes wait there for every load in flight.
     float xs[VPT];
-    double ra[VPT];
+    double ra[VPT], rt[VPT];   // the residual delta; the attention sums (apart: see below)
     uint32_t pw[VPT / 2], gw[VPT / 2], ew[VPT / 2];
     float sc[VPT];
-#pragma unroll
-    for (int k2 = 0; k2 < VPT; k2++) {
-        xs[k2] = 0.0f;
-        ra[k2] = 0.0;
-        sc[k2] = 1.0f;
-    }
-#pragma unroll
-    for (int k2 = 0; k2 < VPT / 2; k2++) pw[k2] = gw[k2] = ew[k2] = 0u;
-    double lsum = 1.0;
+    double lsum;
+    bool tok_ok = false;
     float cutoff = 0.0f;
-    float hint = 0.0f;   // thread 0: the search's hint (0: none)
+    float hint;   // thread 0, with a hint: the search's hint
     if (mode == kInCutoff) {
         cutoff = *d.cutoff;
     } else {
@@ -736,13 +733,17 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
         if (mode == kInResNorm && a_res) load_f64<VPT>(reinterpret_cast<const double*>(a_res), ra);
         if (mode == kInEmbedNorm) {
             const int tok = *a.token;
-            if (tok >= 0 && tok < a.vocab) load_h16<VPT>(a.embed + (size_t)tok * kProbes, ew);
+            tok_ok = tok >= 0 && tok < a.vocab;
+            if (tok_ok) load_h16<VPT>(a.embed + (size_t)tok * kProbes, ew);
             if (a.embed_scale) load_f32<VPT>(a.embed_scale, sc);
         }
         if (norm) load_h16<VPT>(a_gain, gw);
         if (mode == kInAttn) {
             const double* A = reinterpret_cast<const double*>(a_attn);
-            load_f64<VPT>(A, ra);
+            // into registers of their own: loads into ra here would first
+            // wait for the residual mode's (the compiler cannot tell the
+            // modes apart), and with them for every load in flight
+            load_f64<VPT>(A, rt);
             lsum = A[attn_lofs + ((tid * VPT) >> 7)];   // the head of the thread's inputs
         }
     }
@@ -779,11 +780,12 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
         }
         if (mode == kInEmbedNorm) {   // fetchRow16to32 (aux.cl:442-452), then the optional channel scale
 #pragma unroll
-            for (int k2 = 0; k2 < VPT; k2++) xs[k2] = __fmul_rn(half_at<VPT>(ew, k2), sc[k2]);
+            for (int k2 = 0; k2 < VPT; k2++)
+                xs[k2] = __fmul_rn(tok_ok ? half_at<VPT>(ew, k2) : 0.0f, a.embed_scale ? sc[k2] : 1.0f);
         }
         if (mode == kInAttn) {
 #pragma unroll
-            for (int k2 = 0; k2 < VPT; k2++) xs[k2] = (float)(ra[k2] / lsum);
+            for (int k2 = 0; k2 < VPT; k2++) xs[k2] = (float)(rt[k2] / lsum);
         }
         if ((mode == kInResNorm || mode == kInEmbedNorm) && first && a.h_out) store_f32<VPT>(a.h_out, xs);
     }
