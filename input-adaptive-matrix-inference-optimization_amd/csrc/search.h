@@ -341,9 +341,10 @@ __device__ __forceinline__ float search_cutoff(const float (&v)[IAM_PROBES_COUNT
 // ---------------------------------------------------------------------------
 // Windowed search: the same cutoff for the walk's workgroup in three
 // barriers, the serial tail done by wave 0 alone.  Importances are numbers
-// >= +0 (or NaN), whose order keys have the top bit set, so bits 30..20 of
-// a key (the float's exponent and its top three mantissa bits) give 2048
-// coarse bins of 1/8 binade in key order.
+// >= +0 (or NaN) with the sign bit clear; their keys are their bits with
+// the top bit set, so bits 30..20 of a key (the float's exponent and its
+// top three mantissa bits) give 2048 coarse bins of 1/8 binade in key
+// order, and a NaN's key lies above +inf's.
 //   A. every thread adds its keys to the coarse histogram; each wave
 //      reduces its key range (barrier);
 //   B. every wave finds the coarse bins holding ranks kmin = max(1, t-2)
@@ -362,13 +363,13 @@ __device__ __forceinline__ float search_cutoff(const float (&v)[IAM_PROBES_COUNT
 //      after its tail) with hi > cutoff from the window of B (cutoff_upper),
 //      so that rows certain to be selected can be listed while the search
 //      finishes; a barrier then hands the cutoff to all.
-// It declines (in every wave at the same step) when the importances hold no
-// number, a key below +0, or a list longer than kListCap; search_cutoff then
-// finds the cutoff.  Histograms are read with one lane per NB consecutive
+// It declines (in every wave at the same step) when an importance is NaN or
+// a list would be longer than kListCap; search_cutoff then finds the cutoff.  Histograms are read with one lane per NB consecutive
 // bins (NB = 32 coarse, 16 fine), stored so that a wave's 16-byte reads are
 // contiguous.
 constexpr int kCoarseBins = 2048;
 constexpr int kFineBins = 1024;
+constexpr uint32_t kKeyInf = 0xff800000u;   // the window search's key of +inf (NaN keys lie above)
 constexpr int kListCap = 64;
 constexpr int kSmallWindow = 32;   // a window of at most this many keys is listed outright
 
@@ -386,14 +387,13 @@ struct WindowLds {
     uint32_t ukey[8];           // keys of ranks t-2 .. t+2 (0: none)
     uint32_t red[2][NW];        // per wave: min key - 1, max key
     uint32_t nlist;
-    uint32_t nan_bin;           // the coarse adds of NaN keys (never read)
     // wave 0's hand-over
     int step, nl, above;
     uint32_t rlo, rhi;
     float cut;
     float hint;                 // the hinted window's centre (thread 0 stores it before a barrier)
-    // hinted pass, per wave: min key - 1, max key, keys above | keys in << 16, numbers
-    uint4 hsum[NW];
+    // hinted pass, per wave: min key, max key, keys above | keys in << 16
+    uint3 hsum[NW];
 };
 
 // slot of bin b in a histogram read NB bins per lane: lane l's i-th 16-byte
@@ -402,10 +402,24 @@ template <int NB>
 __device__ __forceinline__ int hist_slot(int b)
 {
     const uint32_t u = (uint32_t)b;   // b >= 0: unsigned shifts, no rounding fix-ups of a division
+    if constexpr (NB == 16)           // the same for b < 1024, as three bit fields
+        return (int)(((u & 0xcu) << 6) | ((u >> 2) & 0xfcu) | (u & 3u));
     return (int)(((u >> 2) & (NB / 4 - 1)) * 256u + (u / NB) * 4u + (u & 3u));
 }
 
 __device__ __forceinline__ int coarse_bin(uint32_t key) { return (int)((key >> 20) & (kCoarseBins - 1)); }
+
+// A key added to fine bin b < kFineBins (its count, largest and smallest
+// key).  The byte offset of hist_slot<16>(b) as three bit fields: bits 0-1
+// of b move to 2-3, bits 2-3 to 10-11, bits 4-9 stay.
+template <int NW>
+__device__ __forceinline__ void fine_add(WindowLds<NW>& W, uint32_t b, uint32_t key)
+{
+    const uint32_t off = (b & 0x3f0u) | ((b << 2) & 0xcu) | ((b << 8) & 0xc00u);
+    atomicAdd(reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(W.fine) + off), 1u);
+    atomicMax(reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(W.fmax) + off), key);
+    atomicMax(reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(W.fminv) + off), ~key);
+}
 
 // The zeroing of the histograms and the list counter, by all NT threads;
 // a barrier must separate it from search_window.
@@ -581,9 +595,14 @@ __device__ __forceinline__ int search_window(const float (&v)[IAM_PROBES_COUNT /
     const int wave = threadIdx.x >> 6;
     const int t = IAM_PROBES_COUNT - quantile;       // bucketMul.cl:81
 
+    // The importances are >= +0 or NaN with the sign bit clear (1e5 * |x *
+    // probe|), so their keys are their bits with the top bit set: one
+    // instruction instead of order_key's four.  A NaN's key then lies above
+    // +inf's, and the window search declines on seeing one (the radix
+    // search maps NaN below every number); +0's key is not zero.
     uint32_t key[VPT];
 #pragma unroll
-    for (int k = 0; k < VPT; k++) key[k] = order_key(v[k]);
+    for (int k = 0; k < VPT; k++) key[k] = __float_as_uint(v[k]) | 0x80000000u;
 
     // the window of step D: its keys as a list (listed, mc keys) or in the
     // fine bins (sf: bin shift) from key base over width key units, ab_hi
@@ -601,47 +620,40 @@ __device__ __forceinline__ int search_window(const float (&v)[IAM_PROBES_COUNT /
         const uint32_t klo = order_key(__fmul_rn(hint, 0.875f)), khi = order_key(__fmul_rn(hint, 1.142857142857f));
         const uint32_t hw = khi - klo;
         const int hsf = hw > (uint32_t)kFineBins ? 32 - __clz(hw - 1u) - 10 : 0;
-        // per thread: its keys' range, the keys above the window and the
-        // numbers (c_n), keys inside the window in the high half of c_ai
-        // (at most 1024 keys a wave: no carry between the halves)
-        uint32_t kmn1 = 0xffffffffu, kmx1 = 0u, c_ai = 0u, c_n = 0u;
+        // per thread: its keys' range, the keys above the window, and the
+        // keys inside it in the high half of c_ai (at most 1024 keys a wave:
+        // no carry between the halves)
+        uint32_t kmn1 = 0xffffffffu, kmx1 = 0u, c_ai = 0u;
 #pragma unroll
         for (int k = 0; k < VPT; k++) {
-            kmn1 = min(kmn1, key[k] - 1u);
+            kmn1 = min(kmn1, key[k]);
             kmx1 = max(kmx1, key[k]);
             c_ai += key[k] >= khi ? 1u : 0u;
-            c_n += key[k] != 0u ? 1u : 0u;
             const uint32_t rel = key[k] - klo;
-            if (key[k] != 0u && rel < hw) {
+            if (rel < hw) {
                 c_ai += 1u << 16;
-                const int fs = hist_slot<16>((int)(rel >> hsf));
-                atomicAdd(W.fine + fs, 1u);
-                atomicMax(W.fmax + fs, key[k]);
-                atomicMax(W.fminv + fs, ~key[k]);
+                fine_add(W, rel >> hsf, key[k]);
             }
         }
         kmn1 = wave_min_u32(kmn1);
         kmx1 = wave_max_u32(kmx1);
         c_ai = wave_sum(c_ai);
-        c_n = wave_sum(c_n);
-        if (lane == 0) W.hsum[wave] = make_uint4(kmn1, kmx1, c_ai, c_n);
+        if (lane == 0) W.hsum[wave] = make_uint3(kmn1, kmx1, c_ai);
         __syncthreads();
-        kmn1 = 0xffffffffu;
+        kmn = 0xffffffffu;
         kmx = 0u;
-        int na = 0, nw = 0, nv = 0;
+        int na = 0, nw = 0;
 #pragma unroll
         for (int w = 0; w < NW; w++) {
-            const uint4 r = W.hsum[w];
-            kmn1 = min(kmn1, r.x);
+            const uint3 r = W.hsum[w];
+            kmn = min(kmn, r.x);
             kmx = max(kmx, r.y);
             na += (int)(r.z & 0xffffu);
             nw += (int)(r.z >> 16);
-            nv += (int)r.w;
         }
-        kmn = kmn1 + 1u;
-        if (kmx == 0u || kmn < 0x80000000u) return 0;    // no number, or one below +0
+        if (kmx > kKeyInf) return 0;   // a NaN
         kmin = max(1, t - 2);
-        kmax = min(nv, t + 2);
+        kmax = min(IAM_PROBES_COUNT, t + 2);   // every key is a number
         if (kmin > kmax) return 0;
         if (na < kmin && na + nw >= kmax) {
             ready = true;
@@ -663,14 +675,15 @@ __device__ __forceinline__ int search_window(const float (&v)[IAM_PROBES_COUNT /
     }
 
     if (!ready) {
-        // ---- A. the coarse histogram, the waves' key ranges
-        uint32_t kmn1 = 0xffffffffu;   // min of key - 1 (NaN keys wrap to the top)
+        // ---- A. the coarse histogram, the waves' key ranges (a NaN's key
+        // lands in a bin above +inf's, and the search declines below)
+        uint32_t kmn1 = 0xffffffffu;
         kmx = 0u;
 #pragma unroll
         for (int k = 0; k < VPT; k++) {
-            kmn1 = min(kmn1, key[k] - 1u);
+            kmn1 = min(kmn1, key[k]);
             kmx = max(kmx, key[k]);
-            atomicAdd(key[k] != 0u ? W.coarse + hist_slot<32>(coarse_bin(key[k])) : &W.nan_bin, 1u);
+            atomicAdd(W.coarse + hist_slot<32>(coarse_bin(key[k])), 1u);
         }
         kmn1 = wave_min_u32(kmn1);
         kmx = wave_max_u32(kmx);
@@ -688,12 +701,11 @@ __device__ __forceinline__ int search_window(const float (&v)[IAM_PROBES_COUNT /
             kmn1 = min(kmn1, W.red[0][w]);
             kmx = max(kmx, W.red[1][w]);
         }
-        kmn = kmn1 + 1u;
-        if (kmx == 0u || kmn < 0x80000000u) return 0;    // no number, or one below +0
+        kmn = kmn1;
+        if (kmx > kKeyInf) return 0;   // a NaN
         const HistScan<32> cs = hist_scan<32>(W.coarse);
-        const int nv = cs.total;
         kmin = max(1, t - 2);
-        kmax = min(nv, t + 2);
+        kmax = min(IAM_PROBES_COUNT, t + 2);   // every key is a number
         if (kmin > kmax) return 0;
         int dhi, dlo, ab_lo, c_lo;
         hist_find2<32>(W.coarse, cs, kmin, kmax, dhi, ab_hi, dlo, ab_lo, c_lo);
@@ -708,17 +720,12 @@ __device__ __forceinline__ int search_window(const float (&v)[IAM_PROBES_COUNT /
         if (listed) {
 #pragma unroll
             for (int k = 0; k < VPT; k++)
-                if (key[k] != 0u && key[k] - base < width) W.list[atomicAdd(&W.nlist, 1u)] = key[k];
+                if (key[k] - base < width) W.list[atomicAdd(&W.nlist, 1u)] = key[k];
         } else {
 #pragma unroll
             for (int k = 0; k < VPT; k++) {
                 const uint32_t rel = key[k] - base;
-                if (key[k] != 0u && rel < width) {
-                    const int fs = hist_slot<16>((int)(rel >> sf));
-                    atomicAdd(W.fine + fs, 1u);
-                    atomicMax(W.fmax + fs, key[k]);
-                    atomicMax(W.fminv + fs, ~key[k]);
-                }
+                if (rel < width) fine_add(W, rel >> sf, key[k]);
             }
         }
         __syncthreads();
@@ -792,7 +799,7 @@ __device__ __forceinline__ int search_window(const float (&v)[IAM_PROBES_COUNT /
 #pragma unroll
         for (int k = 0; k < VPT; k++) {
             const uint32_t rel = key[k] - base;
-            if (key[k] != 0u && rel >= rlo && rel < rhi) W.list[atomicAdd(&W.nlist, 1u)] = key[k];
+            if (rel >= rlo && rel < rhi) W.list[atomicAdd(&W.nlist, 1u)] = key[k];
         }
     }
     __syncthreads();
