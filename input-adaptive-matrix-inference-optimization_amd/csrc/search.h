@@ -385,15 +385,16 @@ struct WindowLds {
     uint32_t fminv[kFineBins];  // ~ its smallest key
     uint32_t list[kListCap];
     uint32_t ukey[8];           // keys of ranks t-2 .. t+2 (0: none)
-    uint32_t red[2][NW];        // per wave: min key - 1, max key
+    uint32_t red[2][NW];        // per wave: min key, max key
     uint32_t nlist;
     // wave 0's hand-over
     int step, nl, above;
     uint32_t rlo, rhi;
     float cut;
     float hint;                 // the hinted window's centre (thread 0 stores it before a barrier)
-    // hinted pass, per wave: min key, max key, keys above | keys in << 16
-    uint3 hsum[NW];
+    // hinted pass, over the waves (LDS atomics): min key, max key, keys above
+    // | keys in << 16
+    uint32_t hred[3];
 };
 
 // slot of bin b in a histogram read NB bins per lane: lane l's i-th 16-byte
@@ -433,7 +434,12 @@ __device__ __forceinline__ void window_clear(WindowLds<NW>& W)
 #pragma unroll
     for (int i = 0; i < (kVecs + NT - 1) / NT; i++)
         if (i * NT + (int)threadIdx.x < kVecs) z[i * NT + threadIdx.x] = make_uint4(0u, 0u, 0u, 0u);
-    if (threadIdx.x == 0) W.nlist = 0u;
+    if (threadIdx.x == 0) {
+        W.nlist = 0u;
+        W.hred[0] = 0xffffffffu;
+        W.hred[1] = 0u;
+        W.hred[2] = 0u;
+    }
 }
 
 // One wave's scan of a histogram of 64 NB bins (keys counted in ascending
@@ -553,17 +559,26 @@ __device__ __forceinline__ void window_finish(WindowLds<NW>& W, const float (&U)
 //                         ulp(gmax) (each fp32 midpoint rounds by at most
 //                         half an ulp of the sum).
 // With delta = max(1.0001e-5, (gmax - gmin) 2^-20 + gmax 2^-23) and
-// u_t <= u_{t-2} < edge, with the sum rounded up
+// u_t <= u_{t-2} < edge,
 //   cutoff < u_{t-2} + delta < edge + delta <= hi,
-// and every row whose importance reaches hi is selected.  Where t < 3, or an
-// importance is infinite, there is no bound: hi = NaN, which no importance
-// reaches (not even +inf).
+// and every row whose importance reaches hi is selected.  hi is formed in
+// fp32, every operation rounded to nearest (relative error at most 2^-24
+// each; the scalings by powers of two are exact): the difference, the sum
+// of the two terms and the sum with edge lose at most a factor
+// (1 - 2^-24)^3 > 1 - 2^-22 together, 1.0002e-5f exceeds 1.0001e-5, and
+// the last product by 1 + 2^-20 (itself rounded, another 1 - 2^-24) more
+// than makes up for them, so hi >= edge + delta exactly.  All terms are
+// >= 0 and the sum is at least 1e-5 (no denormal); an overflow gives
+// +inf, which no importance reaches here (kmx is below +inf's key).  Where
+// t < 3, or an importance is infinite, there is no bound: hi = NaN, which
+// no importance reaches (not even +inf).
 __device__ __forceinline__ float cutoff_upper(int t, float edge, uint32_t kmn, uint32_t kmx)
 {
+#pragma clang fp contract(off)
     if (t < 3 || kmx >= 0xff800000u) return __int_as_float(0x7fc00000);   // kmx: the key of +inf
-    const double gmn = (double)key_float(kmn), gmx = (double)key_float(kmx);
-    const double dl = fmax(1.0001e-5, (gmx - gmn) * 0x1p-20 + gmx * 0x1p-23);
-    return __double2float_ru((double)edge + dl);
+    const float gmn = key_float(kmn), gmx = key_float(kmx);
+    const float dl = fmaxf(1.0002e-5f, __fadd_rn(__fmul_rn(__fsub_rn(gmx, gmn), 0x1p-20f), __fmul_rn(gmx, 0x1p-23f)));
+    return __fmul_rn(__fadd_rn(edge, dl), 1.0f + 0x1p-20f);
 }
 
 // A hint the windowed search takes: a positive normal float well inside the
@@ -638,19 +653,16 @@ __device__ __forceinline__ int search_window(const float (&v)[IAM_PROBES_COUNT /
         kmn1 = wave_min_u32(kmn1);
         kmx1 = wave_max_u32(kmx1);
         c_ai = wave_sum(c_ai);
-        if (lane == 0) W.hsum[wave] = make_uint3(kmn1, kmx1, c_ai);
-        __syncthreads();
-        kmn = 0xffffffffu;
-        kmx = 0u;
-        int na = 0, nw = 0;
-#pragma unroll
-        for (int w = 0; w < NW; w++) {
-            const uint3 r = W.hsum[w];
-            kmn = min(kmn, r.x);
-            kmx = max(kmx, r.y);
-            na += (int)(r.z & 0xffffu);
-            nw += (int)(r.z >> 16);
+        if (lane == 0) {
+            atomicMin(&W.hred[0], kmn1);
+            atomicMax(&W.hred[1], kmx1);
+            atomicAdd(&W.hred[2], c_ai);   // at most 4096 keys each half: no carry between them
         }
+        __syncthreads();
+        kmn = W.hred[0];
+        kmx = W.hred[1];
+        const uint32_t cw = W.hred[2];
+        const int na = (int)(cw & 0xffffu), nw = (int)(cw >> 16);
         if (kmx > kKeyInf) return 0;   // a NaN
         kmin = max(1, t - 2);
         kmax = min(IAM_PROBES_COUNT, t + 2);   // every key is a number

@@ -29,18 +29,24 @@ def key_float(k):
     return float(np.uint32(b).view(np.float32))
 
 
-def round_up(x):
-    """double -> the smallest float >= x"""
-    f = f32(x)
-    return f if float(f) >= x else np.nextafter(f, f32(np.inf))
+def bound_hi(edge, gmn, gmx):
+    """cutoff_upper's fp32 formula, every operation rounded to nearest:
+    (edge + max(1.0002e-5, (gmax - gmin) 2^-20 + gmax 2^-23)) (1 + 2^-20)"""
+    d = f32(f32(gmx) - f32(gmn))
+    s = f32(f32(d * f32(2.0**-20)) + f32(f32(gmx) * f32(2.0**-23)))
+    dl = max(f32(1.0002e-5), s)
+    return f32(f32(f32(edge) + dl) * f32(1.0 + 2.0**-20))
 
 
 def upper_bound(imp, t, slack=True):
     """cutoff_upper: the coarse bin (bits 30..20 of the key) of rank
     max(1, t - 2) among the numbers, its upper edge plus
-    delta = max(1.0001e-5, (gmax - gmin) 2^-20 + gmax 2^-23), rounded up.
-    None where the device's search declines (no number, a key below +0) or
-    gives no bound (t < 3, an infinite importance)."""
+    delta = max(1.0001e-5, (gmax - gmin) 2^-20 + gmax 2^-23), formed in fp32
+    as the device does (bound_hi); without the slack, the edge alone.  None
+    where the device's window search declines (a NaN importance) or gives
+    no bound (t < 3, an infinite importance)."""
+    if np.isnan(imp).any():
+        return None
     k = keys(imp)
     nums = k[k != 0]
     if len(nums) == 0 or nums.min() < 0x80000000:
@@ -54,8 +60,8 @@ def upper_bound(imp, t, slack=True):
         return None
     dhi = int(srt[kmin - 1] >> 20) & 2047
     gmn, gmx = key_float(int(nums.min())), key_float(kmx)
-    dl = max(1.0001e-5, (gmx - gmn) * 2.0**-20 + gmx * 2.0**-23) if slack else 0.0
-    return round_up(float(np.uint32((dhi + 1) << 20).view(np.float32)) + dl)
+    edge = np.uint32((dhi + 1) << 20).view(np.float32)
+    return bound_hi(edge, gmn, gmx) if slack else f32(edge)
 
 
 def vectors(rng):
@@ -84,6 +90,25 @@ def vectors(rng):
 def quantiles(rng):
     fixed = [0, 1, 2, 3, 4, 100, 1000, 2047, 3071, 3583, 3890, 4090, 4092, 4093, 4094, 4095]
     return sorted(set(fixed + [int(q) for q in rng.integers(0, N, 6)]))
+
+
+def test_bound_hi_exceeds_exact_sum():
+    """bound_hi (the device's fp32 formula) is at least the exact edge + delta
+    (in exact rational arithmetic), also where every rounding goes down."""
+    from fractions import Fraction as Fr
+    rng = np.random.default_rng(11)
+    cases = 0
+    for _ in range(20000):
+        gmx = f32(10.0 ** rng.uniform(-30, 30))
+        gmn = f32(float(gmx) * rng.choice([0.0, rng.random(), 1.0]))
+        edge = f32(float(gmx) * rng.uniform(0.0, 1.5))
+        hi = bound_hi(edge, gmn, gmx)
+        if not np.isfinite(hi):
+            continue
+        dl = max(Fr(10001, 10**9), (Fr(float(gmx)) - Fr(float(gmn))) * Fr(1, 2**20) + Fr(float(gmx)) * Fr(1, 2**23))
+        assert Fr(float(hi)) >= Fr(float(edge)) + dl, (edge, gmn, gmx, hi)
+        cases += 1
+    assert cases > 15000
 
 
 def test_certain_rows_bound_holds(O):
@@ -122,9 +147,10 @@ def test_bound_without_slack_fails_somewhere(O):
 
 def hinted_upper(imp, t, hint):
     """cutoff_upper of a hinted window: None where the device would not use
-    the hint or the window [7/8 hint, 8/7 hint) misses ranks t-2 .. t+2;
-    else the window's upper end plus delta, rounded up."""
-    if not (1e-30 <= hint <= 1e30):
+    the hint, declines (a NaN importance) or the window [7/8 hint, 8/7 hint)
+    misses ranks t-2 .. t+2; else the window's upper end plus delta, formed
+    as the device does (bound_hi)."""
+    if not (1e-30 <= hint <= 1e30) or np.isnan(imp).any():
         return None
     k = keys(imp)
     nums = k[k != 0]
@@ -141,8 +167,7 @@ def hinted_upper(imp, t, hint):
     if not (above < kmin and above + inside >= kmax):
         return None
     gmn, gmx = key_float(int(nums.min())), key_float(kmx)
-    dl = max(1.0001e-5, (gmx - gmn) * 2.0**-20 + gmx * 2.0**-23)
-    return round_up(key_float(khi) + dl)
+    return bound_hi(f32(key_float(khi)), gmn, gmx)
 
 
 def test_hinted_window_bound_holds(O):
