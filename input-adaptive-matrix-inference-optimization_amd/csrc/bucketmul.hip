@@ -1118,22 +1118,36 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     }
     __syncthreads();
     if (!s_last) return;
-    if (tid == 0) {
+    if (wave == 0) {
         if (a.token_out) {
+            // the tiles' candidates, one per lane (first maximum: a larger
+            // value, or an equal one at a smaller index, wins; candidates are
+            // never NaN, so the order of the combinations does not matter)
             float v = -INFINITY;
             int idx = 0x7fffffff;
-            for (int tt = 0; tt < d.T; tt++) {
-                const unsigned long long cw = __hip_atomic_load(reinterpret_cast<unsigned long long*>(a.tile_cand + tt),
-                                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                take_max(v, idx, __uint_as_float((uint32_t)cw), (int)(cw >> 32));
+            for (int t0 = 0; t0 < d.T; t0 += 64) {
+                const int tt = t0 + lane;
+                if (tt < d.T) {
+                    const unsigned long long cw = __hip_atomic_load(
+                        reinterpret_cast<unsigned long long*>(a.tile_cand + tt), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    take_max(v, idx, __uint_as_float((uint32_t)cw), (int)(cw >> 32));
+                }
             }
-            const int tok = idx < d.C * 16 ? idx : 0;
-            a.token_out[0] = tok;
-            const int ps = a.pos[0];
-            if (ps + 1 >= 0 && ps + 1 < a.hist_len) a.hist[ps + 1] = tok;
-            a.pos[0] = ps + 1;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const float ov = __shfl_xor(v, o, 64);
+                const int oi = __shfl_xor(idx, o, 64);
+                take_max(v, idx, ov, oi);
+            }
+            if (lane == 0) {
+                const int tok = idx < d.C * 16 ? idx : 0;
+                a.token_out[0] = tok;
+                const int ps = a.pos[0];
+                if (ps + 1 >= 0 && ps + 1 < a.hist_len) a.hist[ps + 1] = tok;
+                a.pos[0] = ps + 1;
+            }
         }
-        a.pick_ctr[0] = 0u;
+        if (lane == 0) a.pick_ctr[0] = 0u;
     }
     if (a.final_zero) {
         double* fz = reinterpret_cast<double*>(a.final_zero);
