@@ -47,6 +47,15 @@ struct Layer {
     uint16_t* ffn_gain = nullptr;
 };
 
+// a captured run of decode steps at one effort
+struct StepGraph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    float effort = -1.0f;
+    uint64_t gen = 0;   // Ctx::scratch_gen at capture
+};
+constexpr int kGraphSteps = 8;
+
 }  // namespace iam
 
 struct iam_model {
@@ -91,12 +100,10 @@ struct iam_model {
     int* pos = nullptr;
     int* hist = nullptr;            // token history [max_ctx + 1]
     int host_pos = 0;               // the position the next step computes
-    // captured step
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t exec = nullptr;
-    float graph_effort = -1.0f;
-    bool graph_override = false;
-    uint64_t graph_gen = 0;          // Ctx::scratch_gen at capture
+    // captured decode steps: one step, and kGraphSteps consecutive ones (the
+    // decode loops launch the latter while that many remain, so the gap
+    // between two graph launches comes once per kGraphSteps steps)
+    iam::StepGraph one, multi;
     std::vector<void*> owned;
 };
 
@@ -377,37 +384,71 @@ static int step(iam_model* m, float effort, const float* hidden_override, float*
     return IAM_OK;
 }
 
+static void drop_one(StepGraph& G)
+{
+    if (G.exec) (void)hipGraphExecDestroy(G.exec);
+    if (G.graph) (void)hipGraphDestroy(G.graph);
+    G = StepGraph{};
+}
+
 static int drop_graph(iam_model* m)
 {
-    if (m->exec) (void)hipGraphExecDestroy(m->exec);
-    if (m->graph) (void)hipGraphDestroy(m->graph);
-    m->exec = nullptr;
-    m->graph = nullptr;
-    m->graph_effort = -1.0f;
+    drop_one(m->one);
+    drop_one(m->multi);
     return IAM_OK;
 }
 
-static int capture_step(iam_model* m, float effort, bool override_hidden)
+// The captured graph of `steps` consecutive decode steps (1 or kGraphSteps)
+// at this effort, captured where it is missing or stale (another effort, or
+// a context scratch buffer reallocated since: the graph holds addresses).
+static int step_graph(iam_model* m, float effort, int steps, hipGraphExec_t* out)
 {
     Ctx* c = m->c;
-    IAM_TRY(drop_graph(m));
-    IAM_CHECK_HIP(hipStreamSynchronize(c->stream));
-    IAM_CHECK_HIP(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-    c->capturing = true;
-    int rc = step(m, effort, override_hidden ? m->hidden_in : nullptr, m->logits, true);
-    c->capturing = false;
-    hipGraph_t g = nullptr;
-    hipError_t e = hipStreamEndCapture(c->stream, &g);
-    if (rc != IAM_OK) {
-        if (g) (void)hipGraphDestroy(g);
-        return rc;
+    StepGraph& G = steps == 1 ? m->one : m->multi;
+    if (G.exec && (G.effort != effort || G.gen != c->scratch_gen)) drop_one(G);
+    if (!G.exec) {
+        IAM_CHECK_HIP(hipStreamSynchronize(c->stream));
+        IAM_CHECK_HIP(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+        c->capturing = true;
+        int rc = IAM_OK;
+        for (int s = 0; s < steps && rc == IAM_OK; s++) rc = step(m, effort, nullptr, m->logits, true);
+        c->capturing = false;
+        hipGraph_t g = nullptr;
+        hipError_t e = hipStreamEndCapture(c->stream, &g);
+        if (rc != IAM_OK) {
+            if (g) (void)hipGraphDestroy(g);
+            return rc;
+        }
+        if (e != hipSuccess) return fail(IAM_E_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(e));
+        G.graph = g;
+        IAM_CHECK_HIP(hipGraphInstantiate(&G.exec, g, nullptr, nullptr, 0));
+        G.effort = effort;
+        G.gen = c->scratch_gen;
     }
-    if (e != hipSuccess) return fail(IAM_E_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(e));
-    m->graph = g;
-    IAM_CHECK_HIP(hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
-    m->graph_effort = effort;
-    m->graph_override = override_hidden;
-    m->graph_gen = c->scratch_gen;
+    *out = G.exec;
+    return IAM_OK;
+}
+
+// n decode steps from the device's token and position: graph launches of
+// kGraphSteps steps while that many remain, then single steps.  Both graphs
+// are made current before the first launch (a capture records and
+// instantiates, it runs nothing), so a later call with more steps finds its
+// graph ready.
+static int run_steps(iam_model* m, int n, float effort, bool use_graph)
+{
+    if (!use_graph) {
+        for (int t = 0; t < n; t++) IAM_TRY(step(m, effort, nullptr, m->logits, true));
+        return IAM_OK;
+    }
+    if (n == 0) return IAM_OK;
+    hipGraphExec_t x1 = nullptr, xk = nullptr;
+    IAM_TRY(step_graph(m, effort, 1, &x1));
+    IAM_TRY(step_graph(m, effort, kGraphSteps, &xk));
+    for (int t = 0; t < n;) {
+        const bool many = n - t >= kGraphSteps;
+        IAM_CHECK_HIP(hipGraphLaunch(many ? xk : x1, m->c->stream));
+        t += many ? kGraphSteps : 1;
+    }
     return IAM_OK;
 }
 
@@ -703,24 +744,14 @@ int iam_model_generate(iam_model* m, const int* prompt, int n_prompt, int n_new,
     Ctx* c = m->c;
     IAM_TRY(launch(c, "set_int", k_set_int, dim3(1), dim3(1), 0, m->pos, 0));
     m->host_pos = 0;
-    if (use_graph && (m->exec == nullptr || m->graph_effort != effort || m->graph_override ||
-                      m->graph_gen != c->scratch_gen))
-        IAM_TRY(capture_step(m, effort, false));
-    auto one = [&]() -> int {
-        if (use_graph) {
-            IAM_CHECK_HIP(hipGraphLaunch(m->exec, c->stream));
-            return IAM_OK;
-        }
-        return step(m, effort, nullptr, m->logits, true);
-    };
     // prefill token by token through the decode path (test_generation.cpp:202-210)
     for (int i = 0; i < n_prompt; i++) {
         IAM_TRY(launch(c, "set_int", k_set_int, dim3(1), dim3(1), 0, m->token, prompt[i]));
-        IAM_TRY(one());
+        IAM_TRY(run_steps(m, 1, effort, use_graph));
     }
     // the pick of the last prompt step is the first new token; each further
     // step consumes the token the previous step picked
-    for (int t = 1; t < n_new; t++) IAM_TRY(one());
+    if (n_new > 1) IAM_TRY(run_steps(m, n_new - 1, effort, use_graph));
     m->host_pos = n_prompt + std::max(n_new - 1, 0);
     if (n_new > 0) {
         std::vector<int> hist(C.max_ctx + 1);
@@ -736,17 +767,10 @@ int iam_model_decode(iam_model* m, int n_steps, float effort, int use_graph)
     if (!m) return fail(IAM_E_INVALID, "decode: null model");
     IAM_REQUIRE(n_steps >= 0, "decode: negative step count");
     IAM_REQUIRE(!std::isnan(effort), "decode: effort is NaN");
-    Ctx* c = m->c;
     // positions host_pos .. host_pos + n_steps - 1 must fit the KV cache
     IAM_REQUIRE(m->host_pos >= 0 && (int64_t)m->host_pos + n_steps <= m->cfg.max_ctx,
                 "decode: the steps would pass the KV capacity");
-    if (use_graph && (m->exec == nullptr || m->graph_effort != effort || m->graph_override ||
-                      m->graph_gen != c->scratch_gen))
-        IAM_TRY(capture_step(m, effort, false));
-    for (int t = 0; t < n_steps; t++) {
-        if (use_graph) IAM_CHECK_HIP(hipGraphLaunch(m->exec, c->stream));
-        else IAM_TRY(step(m, effort, nullptr, m->logits, true));
-    }
+    IAM_TRY(run_steps(m, n_steps, effort, use_graph != 0));
     m->host_pos += n_steps;
     return IAM_OK;
 }
@@ -794,13 +818,16 @@ int iam_model_set_lm_dense(iam_model* m, const uint16_t* lm_dense)
 int iam_model_set_embed_scale(iam_model* m, const float* scale_host)
 {
     if (!m) return fail(IAM_E_INVALID, "set_embed_scale: null model");
+    const bool was = m->use_scale;
     if (!scale_host) {
         m->use_scale = false;
     } else {
         IAM_TRY(iam_write(m->c, m->embed_scale, 0, scale_host, (size_t)m->cfg.dim * 4));
         m->use_scale = true;
     }
-    return drop_graph(m);   // the captured step depends on it
+    // the captured steps read the scale buffer (or none): new contents need
+    // no new capture, switching it on or off does
+    return was != m->use_scale ? drop_graph(m) : IAM_OK;
 }
 
 }  // extern "C"

@@ -102,9 +102,10 @@ def test_lm_head_teacher_forced_every_step(O, ctx, model, effort):
 
 
 def test_generate_graph_equals_eager_and_picks_argmax(O, ctx, model):
-    """Greedy generation: graph-replayed steps give the eager steps' tokens,
-    in both accumulation modes, and every picked token is the first maximum
-    of the oracle LM head on the GPU's own hidden state."""
+    """Greedy generation: graph-replayed steps (9 new steps: one graph of 8
+    captured steps, then a one-step graph) give the eager steps' tokens, in
+    both accumulation modes, and every picked token is the first maximum of
+    the oracle LM head on the GPU's own hidden state."""
     prompt = O.gen_tokens(0, 98, 5, CFG["vocab"]).tolist()
     n_new = 10
     for mode in ("fp32", "fp64"):
