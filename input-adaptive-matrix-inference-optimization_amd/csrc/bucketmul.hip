@@ -661,6 +661,7 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     // order the waves append them, and their number
     __shared__ __align__(16) uint16_t s_row[NT * 16];
     __shared__ uint32_t s_nrow;
+    __shared__ uint32_t s_met;   // waves 1.. that have listed their certain rows
     __shared__ __align__(16) float s_x[NT];
     __shared__ float s_part[256];
     __shared__ int s_last;
@@ -758,7 +759,10 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
             if (i * NT + tid < kTileVecs) tz[i * NT + tid] = make_uint4(0u, 0u, 0u, 0u);
     }
     if (mode != kInCutoff) window_clear<NW>(WL);
-    if (tid == 0) s_nrow = 0u;
+    if (tid == 0) {
+        s_nrow = 0u;
+        s_met = 0u;
+    }
     // the block's slice and column tile (from the descriptor read through k)
     const int w = b;
     const int p = w / d.T;
@@ -804,6 +808,47 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
         }
     }
 
+    // The walk's lane geometry (lane = q*LPR + j reads 16 bytes, columns
+    // 8j..8j+7, of row q of each group of RPI rows), and the first batch of
+    // a wave, loaded before the cutoff where the rows certain to be selected
+    // fill every wave's first batch (below).
+    const int j = lane % LPR;
+    const int q = lane / LPR;
+    const int col0 = t * TC + j * 8;
+    const bool whole = (d.C & 7) == 0;
+    const uint16_t* wb = d.W + (size_t)i0 * 16 * d.C + col0;
+    uint4 pva[UNR];
+    Acc pxa[UNR];
+    bool pre = false;
+    // After waves 1.. have listed their certain rows (they then meet at an
+    // LDS counter; a bounded wait), the list's first UNR*NW*RPI entries are
+    // final when that many rows are listed: every wave's first batch (rows
+    // (wave + u*NW)*RPI + q) is among them, so its loads go out now instead
+    // of after the list barrier.  They are the loads the walk issues first,
+    // unchanged; x = 1 * s_x of their inputs (written before the listing).
+    auto prefetch = [&]() {
+        if (!whole || a.sel_block != 1) return;
+        bool met = false;
+        for (int spin = 0; spin < 4096; spin++) {
+            if (__hip_atomic_load(&s_met, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= (uint32_t)(NW - 1)) {
+                met = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");   // the entries after the count
+        const int na = (int)__hip_atomic_load(&s_nrow, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (!met || na < UNR * NW * RPI) return;
+        pre = true;
+        if (col0 >= d.C) return;
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            const int rl = s_row[(wave + u * NW) * RPI + q];
+            pxa[u] = (Acc)s_x[rl >> 4];
+            pva[u] = load_stream(wb + __umul24(rl, d.C));
+        }
+    };
+
     // ---- cutoff, and the slice's rows.  While wave 0 finishes the windowed
     // search, the other waves compute the importances of their inputs' rows
     // and (per-row selection) append the rows certain to be selected, those
@@ -831,7 +876,10 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
                     if (imp[kk] >= hi) m |= 1u << kk;
                 wave_append_rows(m & vbits, rowb, s_row, &s_nrow);
                 listed = hi;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");   // the list entries, then the count
+                if (lane == 0) atomicAdd(&s_met, 1u);
             }
+            prefetch();
         });
         if (found == 1) {
             cutoff = cut_w;
@@ -866,16 +914,11 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
     }
 
     // ---- walk of the selected rows
-    const int j = lane % LPR;
-    const int q = lane / LPR;
-    const int col0 = t * TC + j * 8;
     if (col0 < d.C) {
-        // C % 8 == 0: one 16-byte load per row; otherwise (rows only 2-byte
-        // aligned, a lane's last columns may lie past C) eight 2-byte loads,
-        // zero past C (they land in slots the flush does not store)
-        const bool whole = (d.C & 7) == 0;
+        // C % 8 == 0 (whole): one 16-byte load per row; otherwise (rows only
+        // 2-byte aligned, a lane's last columns may lie past C) eight 2-byte
+        // loads, zero past C (they land in slots the flush does not store)
         const int nc = min(8, d.C - col0);
-        const uint16_t* wb = d.W + (size_t)i0 * 16 * d.C + col0;
         const uint32_t tbase =
             lds_offset(tiles) + (uint32_t)((q % NCOPY) * CSLOTS + j) * (uint32_t)sizeof(Tile);
         const int ng = (ns + RPI - 1) / RPI;
@@ -932,8 +975,20 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
         uint4 va[UNR], vb[UNR];
         Acc xa[UNR], xb[UNR];
         int g = wave;
+        // the first batch: loaded before the cutoff (pre: ng >= UNR*NW > g), or now
+        auto first = [&]() {
+            if (pre) {
+#pragma unroll
+                for (int u = 0; u < UNR; u++) {
+                    va[u] = pva[u];
+                    xa[u] = pxa[u];
+                }
+            } else {
+                issue(g, va, xa);
+            }
+        };
         if (g + 3 * GSTRIDE < ng) {
-            issue(g, va, xa);
+            first();
             issue(g + GSTRIDE, vb, xb);
             do {
                 consume(va, xa);
@@ -947,7 +1002,7 @@ __global__ __launch_bounds__(64 * NW) void k_walk(WalkArgs a)
                 g += 2 * GSTRIDE;
             } while (g + 3 * GSTRIDE < ng);
         } else {
-            if (g < ng) issue(g, va, xa);
+            if (g < ng) first();
             if (g + GSTRIDE < ng) issue(g + GSTRIDE, vb, xb);
         }
         if (g < ng) consume(va, xa);
