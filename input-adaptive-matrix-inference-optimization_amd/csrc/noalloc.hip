@@ -105,11 +105,13 @@ extern "C" int iam_bucketmul_fused_noalloc(iam_ctx* c, int n, const iam_bucket_m
     // the limits first: shapes beyond them are refused before anything else
     MatOp ops[kMaxMulti];
     size_t outputs = 0;
+    WalkGroup tg;                           // the launch's tile width
+    const int tc = walk_tile_cols(tg);
     for (int i = 0; i < n; i++) {
         const iam_bucket_matrix& M = mats[i];
         IAM_REQUIRE(M.expert_rows > 0 && M.bucket_cols > 0, "bucketmul_noalloc: empty matrix");
         outputs += (size_t)M.bucket_cols * 16;
-        IAM_REQUIRE(walk_tiles(M.bucket_cols) <= kNaTiles, "bucketmul_noalloc: more than 256 column tiles");
+        IAM_REQUIRE((M.bucket_cols + tc - 1) / tc <= kNaTiles, "bucketmul_noalloc: more than 256 column tiles");
         ops[i].mat = M;
         ops[i].x = x;
         ops[i].in_size = in_size;
@@ -119,8 +121,7 @@ extern "C" int iam_bucketmul_fused_noalloc(iam_ctx* c, int n, const iam_bucket_m
         return fail(IAM_E_INVALID, "bucketmul_noalloc: " + std::to_string(outputs) +
                                        " outputs exceed the scratch limit of " + std::to_string(kNaOutputs));
     // the slices of the plan the launch runs (its selection blocks and tile width)
-    WalkGroup tg;
-    const int P = max_slices(n, ops, effort, sel_block_for(c, effort), walk_tile_cols(tg));
+    const int P = max_slices(n, ops, effort, sel_block_for(c, effort), tc);
     IAM_REQUIRE(P <= kNaSlices, "bucketmul_noalloc: more than 1024 slices");
     // the same argument checks as iam_bucketmul_fused
     for (int i = 0; i < n; i++) {
