@@ -102,6 +102,42 @@ __device__ __forceinline__ void wave_low2(uint32_t& a1, uint32_t& a2)
     a2 = lane63(a2);
 }
 
+// the three smallest of {a1 <= a2 <= a3} and {b1 <= b2 <= b3}: the k-th
+// smallest of two sorted lists is the least max(a_i, b_j) over i + j = k
+// (a_0 = b_0 below everything)
+__device__ __forceinline__ void merge_low3(uint32_t& a1, uint32_t& a2, uint32_t& a3, uint32_t b1, uint32_t b2,
+                                           uint32_t b3)
+{
+    const uint32_t n3 = min(min(a3, b3), min(max(a1, b2), max(a2, b1)));
+    const uint32_t n2 = min(min(a2, b2), max(a1, b1));
+    a1 = min(a1, b1);
+    a2 = n2;
+    a3 = n3;
+}
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ void dpp_low3(uint32_t& a1, uint32_t& a2, uint32_t& a3)
+{
+    const uint32_t o1 = dpp_t<CTRL, ROW_MASK>(0xffffffffu, a1);
+    const uint32_t o2 = dpp_t<CTRL, ROW_MASK>(0xffffffffu, a2);
+    const uint32_t o3 = dpp_t<CTRL, ROW_MASK>(0xffffffffu, a3);
+    merge_low3(a1, a2, a3, o1, o2, o3);
+}
+
+// the three smallest of the wave's triples, in every lane
+__device__ __forceinline__ void wave_low3(uint32_t& a1, uint32_t& a2, uint32_t& a3)
+{
+    dpp_low3<0x111>(a1, a2, a3);
+    dpp_low3<0x112>(a1, a2, a3);
+    dpp_low3<0x114>(a1, a2, a3);
+    dpp_low3<0x118>(a1, a2, a3);
+    dpp_low3<0x142, 0xA>(a1, a2, a3);
+    dpp_low3<0x143, 0xC>(a1, a2, a3);
+    a1 = lane63(a1);
+    a2 = lane63(a2);
+    a3 = lane63(a3);
+}
+
 // The reference's rounds from U[o] = u_{t-2+o} (o = 0..4; -inf past the
 // numbers; U[0], U[1] unused where t-2, t-1 < 1) and the range of the
 // numbers, in every lane of the calling wave (whole waves only).
@@ -626,12 +662,58 @@ __device__ __forceinline__ int search_window(const float (&v)[IAM_PROBES_COUNT /
     int sf, ab_hi, kmin, kmax, mc = 0;
     bool listed = false, ready = false;
     float hi;
+    float U[5];   // wave 0: u_{t-2} .. u_{t+2}
     hint_hit = false;
+
+    // ---- E. the last rank (t = 4096, effort 1): u_{t-2} .. u_t are the
+    // three smallest keys and u_{t+1}, u_{t+2} lie past the numbers.  Each
+    // thread keeps its three smallest, the waves merge theirs by DPP, and
+    // after one barrier every wave merges the waves' triples: wave 0 replays
+    // the rounds, the others list the rows above the bound from the key just
+    // above u_{t-2}.
+    const bool last = t == IAM_PROBES_COUNT;
+    if (last) {
+        uint32_t a1 = 0xffffffffu, a2 = 0xffffffffu, a3 = 0xffffffffu, mx = 0u;
+#pragma unroll
+        for (int k = 0; k < VPT; k++) {
+            merge_low3(a1, a2, a3, key[k], 0xffffffffu, 0xffffffffu);
+            mx = max(mx, key[k]);
+        }
+        wave_low3(a1, a2, a3);
+        mx = wave_max_u32(mx);
+        if (lane == 0) {
+            W.list[3 * wave] = a1;
+            W.list[3 * wave + 1] = a2;
+            W.list[3 * wave + 2] = a3;
+            W.red[1][wave] = mx;
+        }
+        __syncthreads();
+        kmx = W.red[1][0];
+#pragma unroll
+        for (int w = 1; w < NW; w++) kmx = max(kmx, W.red[1][w]);
+        if (kmx > kKeyInf) return 0;   // a NaN
+        uint32_t b1 = 0xffffffffu, b2 = 0xffffffffu, b3 = 0xffffffffu;
+        if (lane < NW) {
+            b1 = W.list[3 * lane];
+            b2 = W.list[3 * lane + 1];
+            b3 = W.list[3 * lane + 2];
+        }
+        wave_low3(b1, b2, b3);
+        U[0] = key_float(b3);
+        U[1] = key_float(b2);
+        U[2] = key_float(b1);
+        U[3] = U[4] = -INFINITY;
+        kmn = b1;
+        // (b3 + 1 is the key of the next float up; where b3 is +inf's key,
+        // so is kmx, and there is no bound)
+        hi = wave != 0 ? cutoff_upper(t, key_float(b3 + 1u), b1, kmx) : __int_as_float(0x7fc00000);
+        ready = true;
+    }
 
     // ---- H. the hinted window (hinted: the launch has a hint, uniform; its
     // value is read from LDS only then)
     const float hint = hinted ? W.hint : 0.0f;
-    if (hint_usable(hint)) {
+    if (!last && hint_usable(hint)) {
         const uint32_t klo = order_key(__fmul_rn(hint, 0.875f)), khi = order_key(__fmul_rn(hint, 1.142857142857f));
         const uint32_t hw = khi - klo;
         const int hsf = hw > (uint32_t)kFineBins ? 32 - __clz(hw - 1u) - 10 : 0;
@@ -745,12 +827,12 @@ __device__ __forceinline__ int search_window(const float (&v)[IAM_PROBES_COUNT /
                        : __int_as_float(0x7fc00000);
     }
 
-    // ---- D. wave 0: u_{t-2} .. u_{t+2} and the rounds
+    // ---- D. wave 0: u_{t-2} .. u_{t+2} (E has them) and the rounds
     if (wave == 0) {
-        float U[5];
-        if (listed) {
+        bool rounds = true;
+        if (last) {
+        } else if (listed) {
             rank_list(W, mc, ab_hi, t, U);
-            window_finish(W, U, t, kmn, kmx);
         } else {
             // the fine bins of window ranks r1 = kmin - ab_hi .. r2 = kmax - ab_hi:
             // from the top bin of the lane whose 16 bins hold r1, lane l reads
@@ -781,8 +863,8 @@ __device__ __forceinline__ int search_window(const float (&v)[IAM_PROBES_COUNT /
                 if (c1 >= 1 && (unsigned)o1 < 5u) W.ukey[o1] = x1;
                 if (c1 == 2 && (unsigned)(o1 + 1) < 5u) W.ukey[o1 + 1] = n1;
                 read_ukeys(W, U);
-                window_finish(W, U, t, kmn, kmx);
             } else {   // list the keys of the fine bins flo .. fhi
+                rounds = false;
                 int fhi, ab_f, flo, ab_flo, c_flo;
                 hist_find2<16>(W.fine, fs, r1, r2, fhi, ab_f, flo, ab_flo, c_flo);
                 if (lane == 0) {
@@ -795,6 +877,7 @@ __device__ __forceinline__ int search_window(const float (&v)[IAM_PROBES_COUNT /
                 }
             }
         }
+        if (rounds) window_finish(W, U, t, kmn, kmx);
     }
     overlap(hi);
     __syncthreads();

@@ -231,7 +231,8 @@ def test_cutoff_search_kinds(O, iam, ctx, kind):
     usual ones: the standalone cutoff kernel (4 waves, radix search) and the
     walk's own search (8 waves) on 256 and 32000 outputs; the selected row
     count matches too.  On the walk's windowed search these patterns take
-    every route: a listed small window (e.g. normal at quantile 0), the fine
+    every route: the three smallest keys (quantile 0, effort 1), a listed
+    small window (e.g. normal at the other extreme quantiles), the fine
     bins read directly (normal at 1023), the fine bins' keys gathered and
     ranked (quantized at 1023), and the radix search after a decline at the
     window (all_nan) or at the list (constant)."""
